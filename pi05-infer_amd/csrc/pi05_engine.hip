@@ -1,0 +1,771 @@
+// Host side of the gfx950 denoise engine: the C ABI declared in include/pi05_denoise.h.
+//
+// A context owns every device buffer of one shape signature (B, P, num_steps) and replays the
+// whole Euler loop as one hipGraph, so the graph's kernel arguments (all context-owned device
+// addresses) never change between predicts.  All argument validation happens before the first
+// HIP call of an entry point.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pi05_denoise.h"
+#include "pi05_device.h"
+#include "pi05_kernels.h"
+
+using namespace pi05;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct LayerBind {
+  const void* wq = nullptr;
+  const void* wk = nullptr;
+  const void* wv = nullptr;
+  const void* wo = nullptr;
+  const void* wgate = nullptr;
+  const void* wup = nullptr;
+  const void* wdown = nullptr;
+  const float* ln1_w = nullptr;
+  const float* ln1_b = nullptr;
+  const float* ln2_w = nullptr;
+  const float* ln2_b = nullptr;
+  bool set = false;
+};
+
+struct HeadBind {
+  const float* norm_w = nullptr;
+  const float* norm_b = nullptr;
+  const float* in_w = nullptr;
+  const float* in_b = nullptr;
+  const float* out_w = nullptr;
+  const float* out_b = nullptr;
+  const float* tin_w = nullptr;
+  const float* tin_b = nullptr;
+  const float* tout_w = nullptr;
+  const float* tout_b = nullptr;
+  bool set = false;
+};
+
+// Device buffer plan of one signature (sizes in bytes).
+struct Plan {
+  int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1;
+  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, kv = 0, valid = 0, rope = 0, pos = 0;
+  size_t h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0, ptrs = 0, invf = 0;
+  size_t total() const {
+    return wpack + table + temb + 2 * cond + heads + 2 * kv + valid + 2 * rope + pos + h + rowss + q + o + act + part +
+           2 * partml + x + trace + ptrs + invf;
+  }
+};
+
+// Split-KV factor: about 8 key blocks (256 keys) per workgroup.
+int choose_nsplit(int s_pad) {
+  const int nkb = s_pad / 32;
+  int ns = (nkb + 7) / 8;
+  if (ns < 1) ns = 1;
+  if (ns > 16) ns = 16;
+  return ns;
+}
+
+Plan make_plan(const pi05_dims& d) {
+  Plan p;
+  p.M = d.batch * kHorizon;
+  p.S = d.prefix_len + kHorizon;
+  p.s_pad = (p.S + 31) / 32 * 32;
+  p.n_norms = 2 * d.depth + 1;
+  p.rows = p.M * kHeads;
+  p.nsplit = choose_nsplit(p.s_pad);
+  p.wpack = (size_t)d.depth * kLayerElems * 2;
+  p.table = (size_t)d.num_steps * p.n_norms * kModW * 4;
+  p.temb = (size_t)d.num_steps * kWidth * 4;
+  p.cond = (size_t)d.num_steps * kWidth * 4;
+  p.heads = ((size_t)kWidth * kActDim * 2 + kWidth + kActDim) * 4;
+  p.kv = (size_t)d.depth * d.batch * p.s_pad * kHeadDim * 2;
+  p.valid = (size_t)d.batch * p.s_pad;
+  p.rope = (size_t)p.M * kHeadDim * 2;
+  p.pos = (size_t)p.M * 4;
+  p.h = (size_t)p.M * kWidth * 2;
+  p.rowss = (size_t)kRowSlots * p.M * 4;
+  p.q = (size_t)p.M * kHeads * kHeadDim * 2;
+  p.o = p.q;
+  p.act = (size_t)p.M * kMlp * 2;
+  p.part = p.nsplit > 1 ? (size_t)p.nsplit * p.rows * kHeadDim * 4 : 0;
+  p.partml = p.nsplit > 1 ? (size_t)p.nsplit * p.rows * 4 : 0;
+  p.x = (size_t)p.M * kActDim * 4;
+  p.trace = (size_t)d.num_steps * p.M * kActDim * 4;
+  p.ptrs = (size_t)2 * d.depth * sizeof(void*);
+  p.invf = (size_t)kHalfDim * 4;
+  return p;
+}
+
+bool check_dims_msg(const pi05_dims* d, std::string* msg) {
+  char buf[256];
+  if (!d) {
+    *msg = "dims is NULL";
+    return false;
+  }
+#define REQ(cond, ...)                          \
+  do {                                          \
+    if (!(cond)) {                              \
+      snprintf(buf, sizeof buf, __VA_ARGS__);   \
+      *msg = buf;                               \
+      return false;                             \
+    }                                           \
+  } while (0)
+  REQ(d->width == kWidth, "width %d unsupported (engine is compiled for %d)", d->width, kWidth);
+  REQ(d->num_heads == kHeads, "num_heads %d unsupported (compiled for %d)", d->num_heads, kHeads);
+  REQ(d->num_kv_heads == 1, "num_kv_heads %d unsupported (compiled for 1)", d->num_kv_heads);
+  REQ(d->head_dim == kHeadDim, "head_dim %d unsupported (compiled for %d)", d->head_dim, kHeadDim);
+  REQ(d->mlp_dim == kMlp, "mlp_dim %d unsupported (compiled for %d)", d->mlp_dim, kMlp);
+  REQ(d->action_dim == kActDim, "action_dim %d unsupported (compiled for %d)", d->action_dim, kActDim);
+  REQ(d->action_horizon == kHorizon, "action_horizon %d unsupported (compiled for %d)", d->action_horizon, kHorizon);
+  REQ(d->depth >= 1 && d->depth <= 64, "depth %d out of range [1, 64]", d->depth);
+  REQ(d->batch >= 1 && d->batch <= 64, "batch %d out of range [1, 64]", d->batch);
+  REQ(d->prefix_len >= 1 && d->prefix_len <= 16384, "prefix_len %d out of range [1, 16384]", d->prefix_len);
+  REQ(d->num_steps >= 1 && d->num_steps <= kMaxSteps, "num_steps %d out of range [1, %d]", d->num_steps, kMaxSteps);
+  REQ(std::isfinite(d->rms_eps) && d->rms_eps > 0.f, "rms_eps must be a positive finite float");
+  REQ(std::isfinite(d->rope_theta) && d->rope_theta > 1.f, "rope_theta must be > 1");
+  REQ(std::isfinite(d->time_min_period) && d->time_min_period > 0.f && std::isfinite(d->time_max_period) &&
+          d->time_max_period > d->time_min_period,
+      "time periods must satisfy 0 < min_period < max_period");
+#undef REQ
+  return true;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Euler schedule linspace(1, 1/N, N) ++ [0] as the elementwise fp32 GPU linspace evaluates it
+// (engine.py:425-426): step = (end - start) / (N - 1); i < N/2: start + step*i, else
+// end - step*(N - 1 - i).
+std::vector<float> euler_schedule(int n) {
+  std::vector<float> ts(n + 1, 0.f);
+  const float start = 1.0f;
+  const float end = (float)(1.0 / n);
+  if (n == 1) {
+    ts[0] = start;
+  } else {
+    const float step = (end - start) / (float)(n - 1);
+    const int half = n / 2;
+    for (int i = 0; i < n; ++i) ts[i] = i < half ? start + step * (float)i : end - step * (float)(n - i - 1);
+  }
+  ts[n] = 0.f;
+  return ts;
+}
+
+// Sinusoidal timestep embedding in float64, cast to fp32 (pi0_pytorch.py:29-46; the fraction is
+// the f64 GPU linspace(0, 1, dim/2)).
+void sinusoid(float t, int dim, double min_p, double max_p, float* out) {
+  const int half = dim / 2;
+  const double step = (1.0 - 0.0) / (double)(half - 1);
+  for (int i = 0; i < half; ++i) {
+    const double frac = i < half / 2 ? 0.0 + step * (double)i : 1.0 - step * (double)(half - i - 1);
+    const double period = min_p * std::pow(max_p / min_p, frac);
+    const double scaling = 1.0 / period * 2.0 * M_PI;
+    const double arg = scaling * (double)t;
+    out[i] = (float)std::sin(arg);
+    out[half + i] = (float)std::cos(arg);
+  }
+}
+
+// RoPE inverse frequencies as transformers computes them in fp32:
+// 1 / (theta ** (arange(0, D, 2) / D)), the power rounded to fp32, then the fp32 reciprocal.
+void rope_inv_freq(float theta, float* out) {
+  for (int i = 0; i < kHalfDim; ++i) {
+    const float ex = (float)(2 * i) / (float)kHeadDim;
+    const float pw = (float)std::pow((double)theta, (double)ex);
+    out[i] = 1.0f / pw;
+  }
+}
+
+}  // namespace
+
+struct pi05_ctx {
+  pi05_dims d{};
+  Plan plan;
+  int device = -1;
+  std::vector<LayerBind> layers;
+  HeadBind heads;
+  std::vector<float> ts;
+  std::vector<const void*> kv_host_ptrs;
+
+  u16* wpack = nullptr;
+  float* table = nullptr;
+  float* temb = nullptr;
+  float* cond1 = nullptr;
+  float* cond = nullptr;
+  float* heads_buf = nullptr;  // in_w [W,a] | out_w [a,W] | in_b [W] | out_b [a]
+  u16* kcache = nullptr;
+  u16* vcache = nullptr;
+  uint8_t* valid = nullptr;
+  u16* cos_tab = nullptr;
+  u16* sin_tab = nullptr;
+  int32_t* positions = nullptr;
+  u16* h = nullptr;
+  float* rowss = nullptr;
+  u16* q = nullptr;
+  u16* o = nullptr;
+  u16* act = nullptr;
+  float* part = nullptr;
+  float* part_m = nullptr;
+  float* part_l = nullptr;
+  float* x = nullptr;
+  float* trace = nullptr;
+  const void** kv_ptrs = nullptr;
+  float* inv_freq = nullptr;
+
+  hipStream_t cap = nullptr;
+  hipGraphExec_t exec[2] = {nullptr, nullptr};
+  bool weights_ready = false;
+  bool primed = false;
+  std::string err;
+
+  int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    err = buf;
+    return code;
+  }
+  int hip_fail(hipError_t e, const char* what) {
+    return fail(PI05_E_HIP, "%s failed: %s", what, hipGetErrorString(e));
+  }
+};
+
+#define HIPCHK(ctx, expr)                            \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return (ctx)->hip_fail(e_, #expr); \
+  } while (0)
+
+namespace {
+
+float* heads_in_w(pi05_ctx* c) { return c->heads_buf; }
+float* heads_out_w(pi05_ctx* c) { return c->heads_buf + (size_t)kWidth * kActDim; }
+float* heads_in_b(pi05_ctx* c) { return c->heads_buf + (size_t)kWidth * kActDim * 2; }
+float* heads_out_b(pi05_ctx* c) { return heads_in_b(c) + kWidth; }
+
+void free_all(pi05_ctx* c) {
+  for (auto& e : c->exec)
+    if (e) {
+      (void)hipGraphExecDestroy(e);
+      e = nullptr;
+    }
+  void* bufs[] = {c->wpack, c->table, c->temb, c->cond1, c->cond, c->heads_buf, c->kcache, c->vcache, c->valid,
+                  c->cos_tab, c->sin_tab, c->positions, c->h, c->rowss, c->q, c->o, c->act, c->part, c->part_m,
+                  c->part_l, c->x, c->trace, (void*)c->kv_ptrs, c->inv_freq};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (c->cap) (void)hipStreamDestroy(c->cap);
+  c->cap = nullptr;
+}
+
+template <typename T>
+hipError_t dalloc(T** p, size_t bytes) {
+  if (bytes == 0) {
+    *p = nullptr;
+    return hipSuccess;
+  }
+  void* v = nullptr;
+  hipError_t e = hipMalloc(&v, bytes);
+  if (e != hipSuccess) return e;
+  e = hipMemset(v, 0, bytes);
+  *p = reinterpret_cast<T*>(v);
+  return e;
+}
+
+// Enqueue the full num_steps loop (what the graph records).
+int enqueue_loop(pi05_ctx* c, hipStream_t st, bool with_trace) {
+  const pi05_dims& d = c->d;
+  const Plan& p = c->plan;
+  const size_t kv_block = (size_t)d.batch * p.s_pad * kHeadDim;
+  for (int s = 0; s <= d.num_steps; ++s) {
+    StepIoArgs io{};
+    io.rowss = c->rowss;
+    io.h = c->h;
+    io.x = c->x;
+    io.in_w = heads_in_w(c);
+    io.in_b = heads_in_b(c);
+    io.out_w = heads_out_w(c);
+    io.out_b = heads_out_b(c);
+    io.eps = d.rms_eps;
+    io.M = p.M;
+    io.has_prev = s > 0;
+    io.has_next = s < d.num_steps;
+    if (s > 0) {
+      const int ps = s - 1;
+      const float t = c->ts[ps];
+      const float delta = c->ts[ps] - c->ts[ps + 1];
+      io.t = t;
+      io.one_minus_t = 1.0f - t;
+      io.x1_weight = t - delta;
+      io.x0_weight = 1.0f - io.x1_weight;
+      io.final_mod = c->table + ((size_t)ps * p.n_norms + (p.n_norms - 1)) * kModW;
+      io.trace = with_trace ? c->trace + (size_t)ps * p.M * kActDim : nullptr;
+    }
+    HIPCHK(c, launch_step_io(io, st));
+    if (s == d.num_steps) break;
+    const float* mod_step = c->table + (size_t)s * p.n_norms * kModW;
+    for (int l = 0; l < d.depth; ++l) {
+      const u16* wl = c->wpack + (size_t)l * kLayerElems;
+      const float* mod1 = mod_step + (size_t)(2 * l) * kModW;
+      const float* mod2 = mod_step + (size_t)(2 * l + 1) * kModW;
+      QkvArgs qa{};
+      qa.w = wl + kOffQkv;
+      qa.h = c->h;
+      qa.rowss = c->rowss;
+      qa.mod = mod1;
+      qa.cos_tab = c->cos_tab;
+      qa.sin_tab = c->sin_tab;
+      qa.q = c->q;
+      qa.kcache = c->kcache + (size_t)l * kv_block;
+      qa.vcache = c->vcache + (size_t)l * kv_block;
+      qa.eps = d.rms_eps;
+      qa.M = p.M;
+      qa.prefix_len = d.prefix_len;
+      qa.s_pad = p.s_pad;
+      HIPCHK(c, launch_qkv_rope(qa, st));
+
+      AttnArgs aa{};
+      aa.q = c->q;
+      aa.kcache = qa.kcache;
+      aa.vcache = qa.vcache;
+      aa.valid = c->valid;
+      aa.out = c->o;
+      aa.part = c->part;
+      aa.part_m = c->part_m;
+      aa.part_l = c->part_l;
+      aa.rows = p.rows;
+      aa.s_pad = p.s_pad;
+      aa.nsplit = p.nsplit;
+      HIPCHK(c, launch_attention(aa, st));
+
+      ResidualArgs ra{};
+      ra.w = wl + kOffO;
+      ra.act = c->o;
+      ra.mod_gate = mod1 + 2 * kWidth;
+      ra.h = c->h;
+      ra.rowss = c->rowss;
+      ra.M = p.M;
+      HIPCHK(c, launch_o_proj(ra, st));
+
+      GateUpArgs ga{};
+      ga.wgate = wl + kOffGate;
+      ga.wup = wl + kOffUp;
+      ga.h = c->h;
+      ga.rowss = c->rowss;
+      ga.mod = mod2;
+      ga.act = c->act;
+      ga.eps = d.rms_eps;
+      ga.M = p.M;
+      HIPCHK(c, launch_gate_up(ga, st));
+
+      ResidualArgs da{};
+      da.w = wl + kOffDown;
+      da.act = c->act;
+      da.mod_gate = mod2 + 2 * kWidth;
+      da.h = c->h;
+      da.rowss = c->rowss;
+      da.M = p.M;
+      HIPCHK(c, launch_down(da, st));
+    }
+  }
+  return PI05_OK;
+}
+
+int ensure_graph(pi05_ctx* c, bool with_trace) {
+  hipGraphExec_t& ex = c->exec[with_trace ? 1 : 0];
+  if (ex) return PI05_OK;
+  HIPCHK(c, hipStreamBeginCapture(c->cap, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_loop(c, c->cap, with_trace);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(c->cap, &g);
+  if (rc != PI05_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return c->hip_fail(e, "hipStreamEndCapture");
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) {
+    ex = nullptr;
+    return c->hip_fail(e, "hipGraphInstantiate");
+  }
+  return PI05_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pi05_abi_version(void) { return PI05_ABI_VERSION; }
+
+void pi05_default_dims(pi05_dims* d) {
+  if (!d) return;
+  d->width = kWidth;
+  d->depth = 18;
+  d->num_heads = kHeads;
+  d->num_kv_heads = 1;
+  d->head_dim = kHeadDim;
+  d->mlp_dim = kMlp;
+  d->action_dim = kActDim;
+  d->action_horizon = kHorizon;
+  d->batch = 1;
+  d->prefix_len = 968;
+  d->num_steps = 10;
+  d->rms_eps = 1e-6f;
+  d->rope_theta = 10000.0f;
+  d->time_min_period = 4e-3f;
+  d->time_max_period = 4.0f;
+}
+
+int pi05_check_dims(const pi05_dims* dims) {
+  std::string msg;
+  if (!check_dims_msg(dims, &msg)) {
+    g_last_error = msg;
+    return PI05_E_INVALID;
+  }
+  return PI05_OK;
+}
+
+size_t pi05_ctx_device_bytes(const pi05_dims* dims) {
+  std::string msg;
+  if (!check_dims_msg(dims, &msg)) return 0;
+  return make_plan(*dims).total();
+}
+
+const char* pi05_last_error(const pi05_ctx* ctx) { return ctx ? ctx->err.c_str() : g_last_error.c_str(); }
+
+int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
+  if (!out) {
+    g_last_error = "out is NULL";
+    return PI05_E_INVALID;
+  }
+  *out = nullptr;
+  std::string msg;
+  if (!check_dims_msg(dims, &msg)) {
+    g_last_error = msg;
+    return PI05_E_INVALID;
+  }
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    g_last_error = std::string("no HIP device: ") + hipGetErrorString(e);
+    return PI05_E_NODEVICE;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    g_last_error = std::string("device is not gfx950 (MI355X): ") + (e == hipSuccess ? prop.gcnArchName : hipGetErrorString(e));
+    return PI05_E_NODEVICE;
+  }
+  pi05_ctx* c = new pi05_ctx();
+  c->d = *dims;
+  c->device = dev;
+  c->plan = make_plan(*dims);
+  c->layers.resize(dims->depth);
+  c->ts = euler_schedule(dims->num_steps);
+  c->kv_host_ptrs.assign(2 * dims->depth, nullptr);
+  const Plan& p = c->plan;
+  hipError_t ae = hipSuccess;
+#define ALLOC(field, bytes) \
+  if (ae == hipSuccess) ae = dalloc(&c->field, bytes)
+  ALLOC(wpack, p.wpack);
+  ALLOC(table, p.table);
+  ALLOC(temb, p.temb);
+  ALLOC(cond1, p.cond);
+  ALLOC(cond, p.cond);
+  ALLOC(heads_buf, p.heads);
+  ALLOC(kcache, p.kv);
+  ALLOC(vcache, p.kv);
+  ALLOC(valid, p.valid);
+  ALLOC(cos_tab, p.rope);
+  ALLOC(sin_tab, p.rope);
+  ALLOC(positions, p.pos);
+  ALLOC(h, p.h);
+  ALLOC(rowss, p.rowss);
+  ALLOC(q, p.q);
+  ALLOC(o, p.o);
+  ALLOC(act, p.act);
+  ALLOC(part, p.part);
+  ALLOC(part_m, p.partml);
+  ALLOC(part_l, p.partml);
+  ALLOC(x, p.x);
+  ALLOC(trace, p.trace);
+  ALLOC(kv_ptrs, p.ptrs);
+  ALLOC(inv_freq, p.invf);
+#undef ALLOC
+  if (ae == hipSuccess) ae = hipStreamCreateWithFlags(&c->cap, hipStreamNonBlocking);
+  if (ae == hipSuccess) {
+    std::vector<float> invf(kHalfDim);
+    rope_inv_freq(dims->rope_theta, invf.data());
+    ae = hipMemcpy(c->inv_freq, invf.data(), p.invf, hipMemcpyHostToDevice);
+  }
+  if (ae == hipSuccess) {
+    std::vector<float> temb((size_t)dims->num_steps * kWidth);
+    for (int s = 0; s < dims->num_steps; ++s)
+      sinusoid(c->ts[s], kWidth, (double)dims->time_min_period, (double)dims->time_max_period, &temb[(size_t)s * kWidth]);
+    ae = hipMemcpy(c->temb, temb.data(), p.temb, hipMemcpyHostToDevice);
+  }
+  if (ae != hipSuccess) {
+    g_last_error = std::string("context allocation failed: ") + hipGetErrorString(ae);
+    const int code = (ae == hipErrorOutOfMemory) ? PI05_E_NOMEM : PI05_E_HIP;
+    free_all(c);
+    delete c;
+    return code;
+  }
+  *out = c;
+  return PI05_OK;
+}
+
+int pi05_ctx_destroy(pi05_ctx* ctx) {
+  if (!ctx) return PI05_OK;
+  (void)hipDeviceSynchronize();
+  free_all(ctx);
+  delete ctx;
+  return PI05_OK;
+}
+
+int pi05_bind_layer(pi05_ctx* c, int layer, const void* wq, const void* wk, const void* wv, const void* wo,
+                    const void* wgate, const void* wup, const void* wdown, const float* ln1_w, const float* ln1_b,
+                    const float* ln2_w, const float* ln2_b) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (layer < 0 || layer >= c->d.depth) return c->fail(PI05_E_INVALID, "layer %d out of range [0, %d)", layer, c->d.depth);
+  const void* ptrs[] = {wq, wk, wv, wo, wgate, wup, wdown, ln1_w, ln1_b, ln2_w, ln2_b};
+  const char* names[] = {"wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "ln1_w", "ln1_b", "ln2_w", "ln2_b"};
+  for (int i = 0; i < 11; ++i) {
+    if (!ptrs[i]) return c->fail(PI05_E_INVALID, "layer %d: %s is NULL", layer, names[i]);
+    if (!aligned16(ptrs[i])) return c->fail(PI05_E_INVALID, "layer %d: %s is not 16-byte aligned", layer, names[i]);
+  }
+  LayerBind& b = c->layers[layer];
+  b.wq = wq;
+  b.wk = wk;
+  b.wv = wv;
+  b.wo = wo;
+  b.wgate = wgate;
+  b.wup = wup;
+  b.wdown = wdown;
+  b.ln1_w = ln1_w;
+  b.ln1_b = ln1_b;
+  b.ln2_w = ln2_w;
+  b.ln2_b = ln2_b;
+  b.set = true;
+  c->weights_ready = false;
+  return PI05_OK;
+}
+
+int pi05_bind_heads(pi05_ctx* c, const float* norm_w, const float* norm_b, const float* in_w, const float* in_b,
+                    const float* out_w, const float* out_b, const float* tin_w, const float* tin_b, const float* tout_w,
+                    const float* tout_b) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  const void* ptrs[] = {norm_w, norm_b, in_w, in_b, out_w, out_b, tin_w, tin_b, tout_w, tout_b};
+  const char* names[] = {"norm_w", "norm_b", "in_w", "in_b", "out_w", "out_b", "tin_w", "tin_b", "tout_w", "tout_b"};
+  for (int i = 0; i < 10; ++i) {
+    if (!ptrs[i]) return c->fail(PI05_E_INVALID, "heads: %s is NULL", names[i]);
+    if (!aligned16(ptrs[i])) return c->fail(PI05_E_INVALID, "heads: %s is not 16-byte aligned", names[i]);
+  }
+  HeadBind& h = c->heads;
+  h.norm_w = norm_w;
+  h.norm_b = norm_b;
+  h.in_w = in_w;
+  h.in_b = in_b;
+  h.out_w = out_w;
+  h.out_b = out_b;
+  h.tin_w = tin_w;
+  h.tin_b = tin_b;
+  h.tout_w = tout_w;
+  h.tout_b = tout_b;
+  h.set = true;
+  c->weights_ready = false;
+  return PI05_OK;
+}
+
+int pi05_refresh_weights(pi05_ctx* c, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  for (int l = 0; l < c->d.depth; ++l)
+    if (!c->layers[l].set) return c->fail(PI05_E_STATE, "layer %d weights are not bound", l);
+  if (!c->heads.set) return c->fail(PI05_E_STATE, "head weights (norm/action/time) are not bound");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const Plan& p = c->plan;
+  for (int l = 0; l < c->d.depth; ++l) {
+    const LayerBind& b = c->layers[l];
+    u16* wl = c->wpack + (size_t)l * kLayerElems;
+    HIPCHK(c, launch_pack_weight(b.wq, wl + kOffQkv, kHeads * kHeadDim, kWidth, st));
+    HIPCHK(c, launch_pack_weight(b.wk, wl + kOffQkv + wfrag_offset(128, 0, 32), kHeadDim, kWidth, st));
+    HIPCHK(c, launch_pack_weight(b.wv, wl + kOffQkv + wfrag_offset(144, 0, 32), kHeadDim, kWidth, st));
+    HIPCHK(c, launch_pack_weight(b.wo, wl + kOffO, kWidth, kHeads * kHeadDim, st));
+    HIPCHK(c, launch_pack_weight(b.wgate, wl + kOffGate, kMlp, kWidth, st));
+    HIPCHK(c, launch_pack_weight(b.wup, wl + kOffUp, kMlp, kWidth, st));
+    HIPCHK(c, launch_pack_weight(b.wdown, wl + kOffDown, kWidth, kMlp, st));
+  }
+  const HeadBind& hb = c->heads;
+  HIPCHK(c, hipMemcpyAsync(heads_in_w(c), hb.in_w, (size_t)kWidth * kActDim * 4, hipMemcpyDeviceToDevice, st));
+  HIPCHK(c, hipMemcpyAsync(heads_out_w(c), hb.out_w, (size_t)kWidth * kActDim * 4, hipMemcpyDeviceToDevice, st));
+  HIPCHK(c, hipMemcpyAsync(heads_in_b(c), hb.in_b, (size_t)kWidth * 4, hipMemcpyDeviceToDevice, st));
+  HIPCHK(c, hipMemcpyAsync(heads_out_b(c), hb.out_b, (size_t)kActDim * 4, hipMemcpyDeviceToDevice, st));
+  // adaRMS modulation table (engine.py:578-599): cond = silu(W2 silu(W1 temb + b1) + b2),
+  // table[s][n] = dense_n(cond[s]).
+  const int S = c->d.num_steps;
+  GemvArgs g1{hb.tin_w, hb.tin_b, c->temb, c->cond1, kWidth, kWidth, S, kWidth, 0, 1};
+  HIPCHK(c, launch_gemv_rows(g1, st));
+  GemvArgs g2{hb.tout_w, hb.tout_b, c->cond1, c->cond, kWidth, kWidth, S, kWidth, 0, 1};
+  HIPCHK(c, launch_gemv_rows(g2, st));
+  for (int n = 0; n < p.n_norms; ++n) {
+    const float* w;
+    const float* b;
+    if (n == p.n_norms - 1) {
+      w = hb.norm_w;
+      b = hb.norm_b;
+    } else {
+      const LayerBind& lb = c->layers[n / 2];
+      w = (n & 1) ? lb.ln2_w : lb.ln1_w;
+      b = (n & 1) ? lb.ln2_b : lb.ln1_b;
+    }
+    GemvArgs gd{w, b, c->cond, c->table, kModW, kWidth, S, p.n_norms * kModW, n * kModW, 0};
+    HIPCHK(c, launch_gemv_rows(gd, st));
+  }
+  c->weights_ready = true;
+  return PI05_OK;
+}
+
+int pi05_get_adarms_table(pi05_ctx* c, float* table_out, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (!table_out) return c->fail(PI05_E_INVALID, "table_out is NULL");
+  if (!c->weights_ready) return c->fail(PI05_E_STATE, "weights not refreshed");
+  HIPCHK(c, hipMemcpyAsync(table_out, c->table, c->plan.table, hipMemcpyDeviceToDevice, reinterpret_cast<hipStream_t>(stream)));
+  return PI05_OK;
+}
+
+int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* const* v_layers, int64_t kv_batch_stride,
+                      int64_t kv_row_stride, const uint8_t* prefix_pad, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  const pi05_dims& d = c->d;
+  if (!k_layers || !v_layers) return c->fail(PI05_E_INVALID, "k_layers / v_layers is NULL");
+  if (!prefix_pad) return c->fail(PI05_E_INVALID, "prefix_pad is NULL");
+  if (kv_row_stride < kHeadDim || kv_row_stride % 8) return c->fail(PI05_E_INVALID, "kv_row_stride %lld must be >= %d and a multiple of 8", (long long)kv_row_stride, kHeadDim);
+  if (d.batch > 1 && (kv_batch_stride < (int64_t)d.prefix_len * kv_row_stride || kv_batch_stride % 8))
+    return c->fail(PI05_E_INVALID, "kv_batch_stride %lld too small or not a multiple of 8", (long long)kv_batch_stride);
+  for (int l = 0; l < d.depth; ++l) {
+    if (!k_layers[l] || !v_layers[l]) return c->fail(PI05_E_INVALID, "layer %d K/V pointer is NULL", l);
+    if (!aligned16(k_layers[l]) || !aligned16(v_layers[l])) return c->fail(PI05_E_INVALID, "layer %d K/V pointer is not 16-byte aligned", l);
+    c->kv_host_ptrs[l] = k_layers[l];
+    c->kv_host_ptrs[d.depth + l] = v_layers[l];
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the pointer table is tiny; a synchronous copy keeps the host vector's lifetime trivial
+  HIPCHK(c, hipMemcpy(c->kv_ptrs, c->kv_host_ptrs.data(), c->plan.ptrs, hipMemcpyHostToDevice));
+  PrimeKvArgs ka{};
+  ka.k_ptrs = c->kv_ptrs;
+  ka.v_ptrs = c->kv_ptrs + d.depth;
+  ka.batch_stride = kv_batch_stride;
+  ka.row_stride = kv_row_stride;
+  ka.kcache = c->kcache;
+  ka.vcache = c->vcache;
+  ka.batch = d.batch;
+  ka.prefix_len = d.prefix_len;
+  ka.s_pad = c->plan.s_pad;
+  HIPCHK(c, launch_prime_kv(ka, d.depth, st));
+  PrimeTablesArgs ta{};
+  ta.prefix_pad = prefix_pad;
+  ta.inv_freq = c->inv_freq;
+  ta.positions = c->positions;
+  ta.valid = c->valid;
+  ta.cos_tab = c->cos_tab;
+  ta.sin_tab = c->sin_tab;
+  ta.prefix_len = d.prefix_len;
+  ta.s_pad = c->plan.s_pad;
+  HIPCHK(c, launch_prime_tables(ta, d.batch, st));
+  c->primed = true;
+  return PI05_OK;
+}
+
+int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (!x_inout) return c->fail(PI05_E_INVALID, "x_inout is NULL");
+  if (!c->weights_ready) return c->fail(PI05_E_STATE, "weights not bound/refreshed (call pi05_refresh_weights)");
+  if (!c->primed) return c->fail(PI05_E_STATE, "prefix not primed (call pi05_prime_prefix)");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool with_trace = v_trace != nullptr;
+  int rc = ensure_graph(c, with_trace);
+  if (rc != PI05_OK) return rc;
+  HIPCHK(c, hipMemcpyAsync(c->x, x_inout, c->plan.x, hipMemcpyDeviceToDevice, st));
+  HIPCHK(c, hipGraphLaunch(c->exec[with_trace ? 1 : 0], st));
+  HIPCHK(c, hipMemcpyAsync(x_inout, c->x, c->plan.x, hipMemcpyDeviceToDevice, st));
+  if (with_trace) HIPCHK(c, hipMemcpyAsync(v_trace, c->trace, c->plan.trace, hipMemcpyDeviceToDevice, st));
+  return PI05_OK;
+}
+
+int pi05_release_graph(pi05_ctx* c) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  for (auto& e : c->exec)
+    if (e) {
+      HIPCHK(c, hipGraphExecDestroy(e));
+      e = nullptr;
+    }
+  return PI05_OK;
+}
+
+int pi05_launches_per_step(const pi05_ctx* c) {
+  if (!c) return 0;
+  return 1 + c->d.depth * (c->plan.nsplit > 1 ? 6 : 5);
+}
+
+int pi05_euler_schedule(int num_steps, float* ts_host) {
+  if (num_steps < 1 || num_steps > kMaxSteps || !ts_host) {
+    g_last_error = "num_steps out of range or ts_host is NULL";
+    return PI05_E_INVALID;
+  }
+  const std::vector<float> ts = euler_schedule(num_steps);
+  memcpy(ts_host, ts.data(), ts.size() * sizeof(float));
+  return PI05_OK;
+}
+
+int pi05_time_embedding(const pi05_dims* dims, float t, float* out_host) {
+  if (pi05_check_dims(dims) != PI05_OK) return PI05_E_INVALID;
+  if (!out_host) {
+    g_last_error = "out_host is NULL";
+    return PI05_E_INVALID;
+  }
+  sinusoid(t, kWidth, (double)dims->time_min_period, (double)dims->time_max_period, out_host);
+  return PI05_OK;
+}
+
+int pi05_rope_inv_freq(const pi05_dims* dims, float* out_host) {
+  if (pi05_check_dims(dims) != PI05_OK) return PI05_E_INVALID;
+  if (!out_host) {
+    g_last_error = "out_host is NULL";
+    return PI05_E_INVALID;
+  }
+  rope_inv_freq(dims->rope_theta, out_host);
+  return PI05_OK;
+}
+
+}  // extern "C"

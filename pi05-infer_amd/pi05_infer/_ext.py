@@ -1,0 +1,292 @@
+"""ctypes binding of ``libpi05_denoise.so`` (the C ABI in ``include/pi05_denoise.h``).
+
+The shared library is built in-tree next to this file (``build_lib.py``).  There is no fallback:
+if the library is missing or fails to load, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+
+LIB_NAME = "libpi05_denoise.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+PI05_OK = 0
+ERROR_NAMES = {-1: "PI05_E_INVALID", -2: "PI05_E_STATE", -3: "PI05_E_HIP", -4: "PI05_E_NOMEM", -5: "PI05_E_NODEVICE"}
+
+# every exported symbol of include/pi05_denoise.h
+EXPORTED_SYMBOLS = (
+    "pi05_abi_version",
+    "pi05_default_dims",
+    "pi05_check_dims",
+    "pi05_ctx_device_bytes",
+    "pi05_ctx_create",
+    "pi05_ctx_destroy",
+    "pi05_last_error",
+    "pi05_bind_layer",
+    "pi05_bind_heads",
+    "pi05_refresh_weights",
+    "pi05_get_adarms_table",
+    "pi05_prime_prefix",
+    "pi05_denoise",
+    "pi05_release_graph",
+    "pi05_launches_per_step",
+    "pi05_euler_schedule",
+    "pi05_time_embedding",
+    "pi05_rope_inv_freq",
+)
+
+
+class Pi05Error(RuntimeError):
+    """A non-zero status from the engine's C ABI."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+class Pi05Dims(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("mlp_dim", ctypes.c_int32),
+        ("action_dim", ctypes.c_int32),
+        ("action_horizon", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("prefix_len", ctypes.c_int32),
+        ("num_steps", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("time_min_period", ctypes.c_float),
+        ("time_max_period", ctypes.c_float),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and type the engine library; raises if it is absent or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{LIB_NAME} not found at {path}; build it first (python pi05-infer_amd/build_lib.py). "
+            "There is no fallback implementation."
+        )
+    lib = ctypes.CDLL(path)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    dims_p = ctypes.POINTER(Pi05Dims)
+    sig = {
+        "pi05_abi_version": (i32, []),
+        "pi05_default_dims": (None, [dims_p]),
+        "pi05_check_dims": (i32, [dims_p]),
+        "pi05_ctx_device_bytes": (ctypes.c_size_t, [dims_p]),
+        "pi05_ctx_create": (i32, [dims_p, ctypes.POINTER(vp)]),
+        "pi05_ctx_destroy": (i32, [vp]),
+        "pi05_last_error": (ctypes.c_char_p, [vp]),
+        "pi05_bind_layer": (i32, [vp, i32] + [vp] * 11),
+        "pi05_bind_heads": (i32, [vp] + [vp] * 10),
+        "pi05_refresh_weights": (i32, [vp, vp]),
+        "pi05_get_adarms_table": (i32, [vp, vp, vp]),
+        "pi05_prime_prefix": (i32, [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp, vp]),
+        "pi05_denoise": (i32, [vp, vp, vp, vp]),
+        "pi05_release_graph": (i32, [vp]),
+        "pi05_launches_per_step": (i32, [vp]),
+        "pi05_euler_schedule": (i32, [i32, vp]),
+        "pi05_time_embedding": (i32, [dims_p, ctypes.c_float, vp]),
+        "pi05_rope_inv_freq": (i32, [dims_p, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.pi05_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_NAME} ABI {lib.pi05_abi_version()} != expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def _check(lib: ctypes.CDLL, rc: int, ctx: Optional[int]) -> None:
+    if rc != PI05_OK:
+        msg = lib.pi05_last_error(ctx)
+        raise Pi05Error(rc, msg.decode() if msg else "")
+
+
+def default_dims() -> Pi05Dims:
+    lib = load_library()
+    d = Pi05Dims()
+    lib.pi05_default_dims(ctypes.byref(d))
+    return d
+
+
+def make_dims(geometry, batch: int, prefix_len: int, num_steps: int) -> Pi05Dims:
+    g = geometry
+    return Pi05Dims(
+        g.width, g.depth, g.num_heads, g.num_kv_heads, g.head_dim, g.mlp_dim, g.action_dim, g.action_horizon,
+        batch, prefix_len, num_steps, g.rms_eps, g.rope_theta, g.time_min_period, g.time_max_period,
+    )
+
+
+def check_dims(dims: Pi05Dims) -> None:
+    """Validate dims without touching a GPU; raises Pi05Error(PI05_E_INVALID)."""
+    lib = load_library()
+    _check(lib, lib.pi05_check_dims(ctypes.byref(dims)), None)
+
+
+def device_bytes(dims: Pi05Dims) -> int:
+    return int(load_library().pi05_ctx_device_bytes(ctypes.byref(dims)))
+
+
+def euler_schedule(num_steps: int) -> torch.Tensor:
+    """Host-side Euler schedule of the engine ``[num_steps + 1]`` fp32."""
+    lib = load_library()
+    out = torch.empty(num_steps + 1, dtype=torch.float32)
+    _check(lib, lib.pi05_euler_schedule(num_steps, out.data_ptr()), None)
+    return out
+
+
+def time_embedding(dims: Pi05Dims, t: float) -> torch.Tensor:
+    """Host-side sinusoidal timestep embedding ``[width]`` fp32."""
+    lib = load_library()
+    out = torch.empty(dims.width, dtype=torch.float32)
+    _check(lib, lib.pi05_time_embedding(ctypes.byref(dims), t, out.data_ptr()), None)
+    return out
+
+
+def rope_inv_freq(dims: Pi05Dims) -> torch.Tensor:
+    """Host-side RoPE inverse frequencies ``[head_dim / 2]`` fp32."""
+    lib = load_library()
+    out = torch.empty(dims.head_dim // 2, dtype=torch.float32)
+    _check(lib, lib.pi05_rope_inv_freq(ctypes.byref(dims), out.data_ptr()), None)
+    return out
+
+
+def _ptr(t: torch.Tensor, dtype: torch.dtype, name: str, device: torch.device) -> int:
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name}: expected device {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    return t.data_ptr()
+
+
+def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+class DenoiseContext:
+    """One engine context: a (batch, prefix_len, num_steps) signature on the current device."""
+
+    def __init__(self, geometry, batch: int, prefix_len: int, num_steps: int, device: torch.device):
+        self.lib = load_library()
+        self.geometry = geometry
+        self.dims = make_dims(geometry, batch, prefix_len, num_steps)
+        self.device = torch.device(device)
+        _check(self.lib, self.lib.pi05_check_dims(ctypes.byref(self.dims)), None)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _check(self.lib, self.lib.pi05_ctx_create(ctypes.byref(self.dims), ctypes.byref(handle)), None)
+        self.handle = handle.value
+        self._keepalive: list = []
+
+    @property
+    def signature(self) -> tuple[int, int, int]:
+        return (self.dims.batch, self.dims.prefix_len, self.dims.num_steps)
+
+    def _call(self, rc: int) -> None:
+        _check(self.lib, rc, self.handle)
+
+    def bind_layer(self, i: int, wq, wk, wv, wo, wgate, wup, wdown, ln1_w, ln1_b, ln2_w, ln2_b) -> None:
+        bf, f32, dev = torch.bfloat16, torch.float32, self.device
+        ptrs = [
+            _ptr(wq, bf, "wq", dev), _ptr(wk, bf, "wk", dev), _ptr(wv, bf, "wv", dev), _ptr(wo, bf, "wo", dev),
+            _ptr(wgate, bf, "wgate", dev), _ptr(wup, bf, "wup", dev), _ptr(wdown, bf, "wdown", dev),
+            _ptr(ln1_w, f32, "ln1_w", dev), _ptr(ln1_b, f32, "ln1_b", dev),
+            _ptr(ln2_w, f32, "ln2_w", dev), _ptr(ln2_b, f32, "ln2_b", dev),
+        ]
+        self._call(self.lib.pi05_bind_layer(self.handle, i, *ptrs))
+
+    def bind_heads(self, norm_w, norm_b, in_w, in_b, out_w, out_b, tin_w, tin_b, tout_w, tout_b) -> None:
+        f32, dev = torch.float32, self.device
+        names = ("norm_w", "norm_b", "in_w", "in_b", "out_w", "out_b", "tin_w", "tin_b", "tout_w", "tout_b")
+        ts = (norm_w, norm_b, in_w, in_b, out_w, out_b, tin_w, tin_b, tout_w, tout_b)
+        self._call(self.lib.pi05_bind_heads(self.handle, *[_ptr(t, f32, n, dev) for t, n in zip(ts, names)]))
+
+    def refresh_weights(self, stream=None) -> None:
+        self._call(self.lib.pi05_refresh_weights(self.handle, _stream_ptr(stream)))
+
+    def adarms_table(self, stream=None) -> torch.Tensor:
+        d = self.dims
+        out = torch.empty((d.num_steps, 2 * d.depth + 1, 3 * d.width), dtype=torch.float32, device=self.device)
+        self._call(self.lib.pi05_get_adarms_table(self.handle, out.data_ptr(), _stream_ptr(stream)))
+        return out
+
+    def prime_prefix(self, k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.Tensor],
+                     prefix_pad: torch.Tensor, stream=None) -> None:
+        """k_layers/v_layers: per layer bf16 [B, 1, P, D] (or any view whose last dim is contiguous
+        and whose batch/position strides are uniform across layers)."""
+        d = self.dims
+        if len(k_layers) != d.depth or len(v_layers) != d.depth:
+            raise ValueError(f"expected {d.depth} K and V layers, got {len(k_layers)} / {len(v_layers)}")
+        ref = k_layers[0]
+        if ref.dim() != 4 or tuple(ref.shape) != (d.batch, 1, d.prefix_len, d.head_dim):
+            raise ValueError(f"K layer shape {tuple(ref.shape)} != {(d.batch, 1, d.prefix_len, d.head_dim)}")
+        bstride, rstride = ref.stride(0), ref.stride(2)
+        for name, layers in (("K", k_layers), ("V", v_layers)):
+            for i, t in enumerate(layers):
+                if t.dtype != torch.bfloat16 or t.device != self.device:
+                    raise TypeError(f"{name}[{i}] must be bf16 on {self.device}")
+                if tuple(t.shape) != tuple(ref.shape) or t.stride(0) != bstride or t.stride(2) != rstride or t.stride(3) != 1:
+                    raise ValueError(f"{name}[{i}] shape/strides differ from layer 0")
+        pad = prefix_pad
+        if pad.dtype == torch.bool:
+            pad = pad.to(torch.uint8)
+        if pad.dtype != torch.uint8 or tuple(pad.shape) != (d.batch, d.prefix_len):
+            raise ValueError(f"prefix_pad must be bool/uint8 [{d.batch}, {d.prefix_len}]")
+        pad = pad.to(self.device).contiguous()
+        karr = (ctypes.c_void_p * d.depth)(*[t.data_ptr() for t in k_layers])
+        varr = (ctypes.c_void_p * d.depth)(*[t.data_ptr() for t in v_layers])
+        self._keepalive = [pad]
+        self._call(self.lib.pi05_prime_prefix(self.handle, karr, varr, bstride, rstride, pad.data_ptr(), _stream_ptr(stream)))
+
+    def denoise(self, x: torch.Tensor, trace: Optional[torch.Tensor] = None, stream=None) -> None:
+        """In place: x [B, A, a] fp32 noise -> actions.  trace [steps, B, A, a] fp32 or None."""
+        d = self.dims
+        if tuple(x.shape) != (d.batch, d.action_horizon, d.action_dim):
+            raise ValueError(f"x shape {tuple(x.shape)} != {(d.batch, d.action_horizon, d.action_dim)}")
+        xp = _ptr(x, torch.float32, "x", self.device)
+        tp = None
+        if trace is not None:
+            if tuple(trace.shape) != (d.num_steps, d.batch, d.action_horizon, d.action_dim):
+                raise ValueError("trace shape mismatch")
+            tp = _ptr(trace, torch.float32, "trace", self.device)
+        self._call(self.lib.pi05_denoise(self.handle, xp, tp, _stream_ptr(stream)))
+
+    def release_graph(self) -> None:
+        self._call(self.lib.pi05_release_graph(self.handle))
+
+    def launches_per_step(self) -> int:
+        return int(self.lib.pi05_launches_per_step(self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.pi05_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

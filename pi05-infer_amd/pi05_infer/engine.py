@@ -1,0 +1,277 @@
+"""pi0.5 inference engine whose denoise loop runs on hand-written gfx950 kernels.
+
+Drop-in for the reference's ``pi05_infer.engine`` on the denoise path: ``OpenPi0Inference``
+keeps ``sample_actions(observation, noise=None) -> {"actions"}`` (engine.py:344-406),
+``capture_cuda_graph`` / ``is_cuda_graph_enabled`` / ``release_cuda_graph`` (engine.py:831-860,
+_vendored/base_policy.py:96-107), ``enable_torch_compile`` (a no-op here: there is nothing to
+compile, engine.py:1003-1059), ``invalidate_weight_derived_caches`` (engine.py:526-554) and
+``predict_action_batch`` (engine.py:321-342).
+
+Every denoise computation happens in ``libpi05_denoise.so``; PyTorch only provides device
+memory, streams and the random noise draw.  The prefix (SigLIP + PaliGemma prefill,
+engine.py:770-794) is not built here: an observation carries the prefix KV cache and pad mask
+that ``_build_prefix_cache`` would produce (the reference's frozen-prefix mode,
+tools/bitexact_compiled_toggles.py:354-376).
+"""
+
+from __future__ import annotations
+
+import logging
+from dataclasses import dataclass, field
+from typing import Any, Optional, Sequence
+
+import torch
+
+from . import _ext
+from .synthetic import BF16_KEYS, HEAD_PARAM_NAMES, ExpertGeometry, layer_param_names
+
+logger = logging.getLogger(__name__)
+
+
+@dataclass(frozen=True)
+class OpenPi0InferConfig:
+    """Inference config: the pi0.5 fields of openpi's ``Pi0Config`` that the denoise path reads
+    plus the reference's inference extras (engine.py:120-140)."""
+
+    config_name: str = "pi05_libero"
+    pi05: bool = True
+    action_dim: int = 32
+    action_horizon: int = 50
+    max_token_len: int = 200
+    dtype: str = "bfloat16"
+    paligemma_variant: str = "gemma_2b"
+    action_expert_variant: str = "gemma_300m"
+    num_images_in_input: int = 2
+    noise_method: str = "flow_sde"
+    noise_level: float = 0.5
+    action_chunk: int = 5
+    action_env_dim: int = 7
+    num_steps: int = 10
+    train_expert_only: bool = False
+
+
+@dataclass
+class Observation:
+    """What ``sample_actions`` consumes: the prefix KV cache of ``_build_prefix_cache`` (per layer
+    K and V bf16 ``[B, 1, P, D]``, or stacked ``[B, L, P, D]``), its pad mask ``[B, P]`` and the
+    robot state (unused by pi0.5's suffix, pi0_pytorch.py:269-287)."""
+
+    prefix_k: Any
+    prefix_v: Any
+    prefix_pad_masks: torch.Tensor
+    state: Optional[torch.Tensor] = None
+    extra: dict = field(default_factory=dict)
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "Observation":
+        if "past_key_values" in d:
+            kv = d["past_key_values"]
+            ks = [p[0] for p in kv]
+            vs = [p[1] for p in kv]
+        else:
+            ks, vs = d["prefix_k"], d["prefix_v"]
+        return cls(ks, vs, d["prefix_pad_masks"], d.get("state"))
+
+
+def _split_layers(t: Any, depth: int) -> list[torch.Tensor]:
+    if isinstance(t, torch.Tensor):
+        if t.dim() != 4:
+            raise ValueError("stacked prefix K/V must be [B, L, P, D]")
+        return [t[:, i : i + 1] for i in range(depth)]
+    return list(t)
+
+
+class OpenPi0Inference:
+    """pi0.5 action prediction with the gfx950 denoise engine."""
+
+    def __init__(self, config: OpenPi0InferConfig, geometry: ExpertGeometry = ExpertGeometry()):
+        if not config.pi05:
+            raise NotImplementedError("only pi0.5 (adaRMS action expert) is implemented")
+        if config.action_horizon != geometry.action_horizon or config.action_dim != geometry.action_dim:
+            raise ValueError("config action_horizon/action_dim must match the expert geometry")
+        self.config = config
+        self.geometry = geometry
+        self.params: dict[str, torch.Tensor] = {}
+        self.device = torch.device("cpu")
+        self.logger = logger
+        self._contexts: dict[tuple, _ext.DenoiseContext] = {}
+        self._stale_contexts: set = set()
+        self.cuda_graph_manager = None
+        self.torch_compile_enabled = False
+        self._torch_compile_mode = None
+        self.training = False
+
+    # ------------------------------------------------------------------ parameters
+    def expected_parameters(self) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
+        from .synthetic import parameter_specs
+
+        return {n: (s, torch.bfloat16 if bf else torch.float32) for n, s, bf in parameter_specs(self.geometry)}
+
+    def load_state_dict(self, state_dict: dict, strict: bool = False):
+        """Copy matching tensors in (dtype policy of gemma_pytorch.py:84-104 applied); returns
+        (missing, unexpected) like ``nn.Module.load_state_dict``."""
+        spec = self.expected_parameters()
+        missing = [n for n in spec if n not in state_dict]
+        unexpected = [n for n in state_dict if n not in spec]
+        if strict and (missing or unexpected):
+            raise KeyError(f"missing={missing[:5]} unexpected={unexpected[:5]}")
+        for name, (shape, dtype) in spec.items():
+            if name not in state_dict:
+                continue
+            t = state_dict[name]
+            if tuple(t.shape) != tuple(shape):
+                raise ValueError(f"{name}: shape {tuple(t.shape)} != {shape}")
+            t = t.to(device=self.device, dtype=dtype).contiguous()
+            if name in self.params:
+                self.params[name].copy_(t)  # in place: keeps addresses for bound contexts
+            else:
+                self.params[name] = t
+        self._mark_weights_changed()
+        return missing, unexpected
+
+    def state_dict(self) -> dict[str, torch.Tensor]:
+        return dict(self.params)
+
+    def parameters(self):
+        return iter(self.params.values())
+
+    def to(self, device=None, dtype=None):
+        if dtype is not None:
+            raise ValueError("the engine keeps the reference dtype policy; dtype cannot be changed")
+        if device is not None:
+            device = torch.device(device)
+            if device.type == "cuda" and device.index is None:
+                device = torch.device("cuda", torch.cuda.current_device())
+            self.params = {k: v.to(device).contiguous() for k, v in self.params.items()}
+            self.device = device
+            self._drop_contexts()
+        return self
+
+    def eval(self):
+        self.training = False
+        return self
+
+    def train(self, mode: bool = True):
+        if mode:
+            raise NotImplementedError("inference-only engine")
+        return self
+
+    # ------------------------------------------------------------------ engine contexts
+    def _drop_contexts(self) -> None:
+        for c in self._contexts.values():
+            c.close()
+        self._contexts.clear()
+        self._stale_contexts.clear()
+
+    def _mark_weights_changed(self) -> None:
+        self._stale_contexts = set(self._contexts)
+
+    def _bind(self, ctx: _ext.DenoiseContext) -> None:
+        p = self.params
+        for i in range(self.geometry.depth):
+            n = layer_param_names(i)
+            ctx.bind_layer(i, *(p[n[k]] for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown",
+                                                    "ln1_w", "ln1_b", "ln2_w", "ln2_b")))
+        h = HEAD_PARAM_NAMES
+        ctx.bind_heads(*(p[h[k]] for k in ("norm_w", "norm_b", "in_w", "in_b", "out_w", "out_b",
+                                            "tin_w", "tin_b", "tout_w", "tout_b")))
+
+    def _context(self, batch: int, prefix_len: int, num_steps: int) -> _ext.DenoiseContext:
+        if self.device.type != "cuda":
+            raise RuntimeError("the denoise engine runs on a gfx950 GPU; call .to('cuda') first")
+        key = (batch, prefix_len, num_steps)
+        ctx = self._contexts.get(key)
+        if ctx is None:
+            missing = [n for n in self.expected_parameters() if n not in self.params]
+            if missing:
+                raise RuntimeError(f"weights not loaded: {missing[:3]} ...")
+            ctx = _ext.DenoiseContext(self.geometry, batch, prefix_len, num_steps, self.device)
+            self._bind(ctx)
+            ctx.refresh_weights()
+            self._contexts[key] = ctx
+        elif key in self._stale_contexts:
+            ctx.refresh_weights()
+            self._stale_contexts.discard(key)
+        return ctx
+
+    # ------------------------------------------------------------------ reference API
+    def sample_noise(self, shape, device):
+        """pi0_pytorch.py:176-183."""
+        return torch.normal(mean=0.0, std=1.0, size=shape, dtype=torch.float32, device=device)
+
+    @torch.no_grad()
+    def sample_actions(self, observation, noise: Optional[torch.Tensor] = None) -> dict:
+        """Prefix KV + ``num_steps`` flow_ode Euler steps (engine.py:344-406) -> ``{"actions"}``."""
+        actions, _ = self._run(observation, noise, trace=False)
+        return {"actions": actions}
+
+    @torch.no_grad()
+    def sample_actions_with_velocities(self, observation, noise: Optional[torch.Tensor] = None):
+        """Like ``sample_actions`` but also returns every step's velocity ``[steps, B, A, a]``
+        (the reference's per-step ``v_t``, engine.py:659-661); for parity checks."""
+        return self._run(observation, noise, trace=True)
+
+    def _run(self, observation, noise, trace: bool):
+        obs = Observation.from_dict(observation) if isinstance(observation, dict) else observation
+        ks = _split_layers(obs.prefix_k, self.geometry.depth)
+        vs = _split_layers(obs.prefix_v, self.geometry.depth)
+        pad = obs.prefix_pad_masks
+        bsize, plen = pad.shape
+        device = self.device
+        cfg = self.config
+        if noise is None:
+            noise = self.sample_noise((bsize, cfg.action_horizon, cfg.action_dim), device)
+        x = noise.to(device=device, dtype=torch.float32).clone().contiguous()
+        ctx = self._context(bsize, plen, cfg.num_steps)
+        ctx.prime_prefix(ks, vs, pad.to(device))
+        tr = None
+        if trace:
+            tr = torch.empty((cfg.num_steps, bsize, cfg.action_horizon, cfg.action_dim), dtype=torch.float32, device=device)
+        ctx.denoise(x, tr)
+        return x, tr
+
+    def capture_cuda_graph(self, train_batch_size: int, eval_batch_size: int):
+        """The engine always replays its whole Euler loop as one hipGraph, captured lazily per
+        (B, P, num_steps) signature; this only records that graph use was requested."""
+        self.cuda_graph_manager = {"eval_batch_size": eval_batch_size}
+
+    def is_cuda_graph_enabled(self) -> bool:
+        return self.cuda_graph_manager is not None
+
+    def release_cuda_graph(self):
+        for c in self._contexts.values():
+            c.release_graph()
+        self.cuda_graph_manager = None
+
+    def enable_torch_compile(self, mode: str = "max-autotune"):
+        """Compatibility shim: the denoise path is hand-written HIP, so there is nothing to compile."""
+        self.torch_compile_enabled = True
+        self._torch_compile_mode = mode
+
+    def invalidate_weight_derived_caches(self):
+        """Re-pack weights and rebuild the adaRMS table in place after an in-place weight update
+        (engine.py:526-554); device addresses stay stable, so captured graphs stay valid."""
+        for key, ctx in self._contexts.items():
+            ctx.refresh_weights()
+        self._stale_contexts.clear()
+
+    def output_transform(self, outputs: dict) -> dict:
+        """Slice to ``action_chunk`` (engine.py:282); the openpi unnormalize transforms are not part
+        of this engine."""
+        out = dict(outputs)
+        out["actions"] = outputs["actions"][:, : self.config.action_chunk]
+        return out
+
+    def predict_action_batch(self, env_obs, **kwargs) -> torch.Tensor:
+        """Observation with a prefix cache -> actions ``[B, action_chunk, a]`` (engine.py:321-342)."""
+        outputs = self.sample_actions(env_obs, kwargs.get("noise"))
+        return self.output_transform(outputs)["actions"]
+
+    def close(self) -> None:
+        self._drop_contexts()
+
+
+Engine = OpenPi0Inference
+EngineConfig = OpenPi0InferConfig
+
+__all__ = ["Engine", "EngineConfig", "Observation", "OpenPi0Inference", "OpenPi0InferConfig"]
