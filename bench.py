@@ -1,0 +1,209 @@
+#!/usr/bin/env python3
+"""Benchmark of the pi0.5 action-expert denoise loop on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4] [--no-cpu-baseline]
+
+One bench "step" is one predict's denoise: the 10-step flow-matching Euler loop of the 18-layer
+expert over a static prefix KV cache (one hipGraph replay), with weights, KV and noise already
+resident in HBM.  Random-init weights (seed 0), N(0,1) bf16 prefix KV (seed 1), N(0,1) noise
+(seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "pi05-infer_amd"))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    "c1": dict(batch=1, prefix_len=968),
+    "c2": dict(batch=1, prefix_len=456),
+    "c3": dict(batch=8, prefix_len=968),
+    "c4": dict(batch=1, prefix_len=3272),
+}
+METRIC = "denoise ms/predict (10 steps, bs=1, 968 prefix) + % peak HBM GB/s"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def algorithmic_bytes_per_predict(depth: int, batch: int, prefix_len: int, steps: int) -> int:
+    """Compulsory HBM bytes of one predict: per step the bf16 expert weights, the KV cache of
+    prefix + suffix keys, one modulation-table slice, the fp32 action in/out weights and x in/out."""
+    W, H, D, I, A, a = 1024, 8, 256, 4096, 50, 32
+    weights = depth * ((H + 2) * D * W + W * H * D + 2 * I * W + W * I) * 2
+    kv = depth * batch * (prefix_len + A) * D * 2 * 2
+    mod = (2 * depth + 1) * 3 * W * 4
+    heads = (W * a * 2 + W + a) * 4
+    x = batch * A * a * 4 * 2
+    return steps * (weights + kv + mod + heads + x)
+
+
+def gate_up_bytes(batch: int) -> int:
+    """Algorithmic bytes of one gate_up launch: gate + up bf16 weights, the residual rows it
+    normalises, its modulation scale/shift and the GeGLU output."""
+    M = 50 * batch
+    return 2 * 4096 * 1024 * 2 + M * 1024 * 2 + 2 * 1024 * 4 + M * 4096 * 2
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/)."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-predicts", type=int, default=3, help="predicts in the CPU-baseline sample")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this engine runs the denoise loop on one GPU; runs with --gpus > 1 are not "
+              "supported (data-parallel sharding over samples needs no communication, see DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from pi05_infer import synthetic as S
+    from pi05_infer.builder import build_model
+    from pi05_infer.engine import Observation
+
+    cfg = CONFIGS[args.config]
+    B, P, steps = cfg["batch"], cfg["prefix_len"], 10
+    g = S.ExpertGeometry()
+    model = build_model("random:0", "pi05_libero", num_steps=steps)
+    model.to("cuda")
+    k, v = S.make_prefix_kv(g, P, B)
+    x1 = S.make_noise(g, B).cuda()
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(P, B).cuda())
+    model.sample_actions(obs, x1)  # builds the context, primes the prefix, captures the graph
+    ctx = model._context(B, P, steps)
+    stream = torch.cuda.current_stream()
+    xs = [x1.clone() for _ in range(args.warmup + args.steps)]
+
+    for i in range(args.warmup):
+        ctx.denoise(xs[i])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        ctx.denoise(xs[args.warmup + i])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_predict = e0.elapsed_time(e1) / args.steps
+
+    # dominant kernel (gate_up, the largest weight stream), timed with events on its stream
+    kiters = 200
+    ctx.bench_kernel("gate_up", 0, 10)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    ctx.bench_kernel("gate_up", 0, kiters)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gu_us = e0.elapsed_time(e1) * 1e3 / kiters
+    gu_bytes = gate_up_bytes(B)
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+
+    pred_bytes = algorithmic_bytes_per_predict(g.depth, B, P, steps)
+    pred_gbs = pred_bytes / (ms_per_predict * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import denoise_oracle as O
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        w = {n: t.cpu() for n, t in model.params.items()}
+        og = O.geometry_from(g)
+        table = O.adarms_table(w, og, steps)
+        pad = S.full_prefix_pad(P, B)
+        times = []
+        for _ in range(args.cpu_predicts):
+            t0 = time.perf_counter()
+            O.sample_actions(w, og, k, v, pad, x1.cpu(), steps, table)
+            times.append((time.perf_counter() - t0) * 1e3)
+        cpu = {
+            "value": round(statistics.median(times), 3),
+            "unit": "ms/predict",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{args.cpu_predicts} full predicts ({steps} steps, B={B}, P={P}) of the fp32 CPU oracle, median; "
+                      f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}",
+        }
+
+    traffic = read_traffic("gate_up_c1_traffic.txt") if args.config == "c1" else None
+    out = {
+        "metric": METRIC,
+        "value": round(ms_per_predict, 4),
+        "unit": "ms/predict",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_predict, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights seed 0, N(0,1) bf16 prefix KV seed 1, N(0,1) noise seed 2)",
+        "config": {
+            "workload": f"pi0.5 action-expert {steps}-step flow-matching denoise, depth 18, bs={B}, {P}-token prefix KV",
+            "batch": B,
+            "prefix_len": P,
+            "num_steps": steps,
+            "launches_per_step": ctx.launches_per_step(),
+        },
+        "roofline": {
+            "kernel": "gate_up (adaRMSNorm + gate|up GEMM + GeGLU)",
+            "bound": "hbm",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "avg_launch_us": round(gu_us, 3),
+            "algorithmic_bytes_per_launch": gu_bytes,
+        },
+        "predict_roofline": {
+            "achieved": round(pred_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(pred_gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_predict": pred_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

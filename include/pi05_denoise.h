@@ -64,8 +64,8 @@ typedef struct pi05_dims {
   int32_t num_steps;      /* Euler steps (10) */
   float rms_eps;          /* 1e-6 (GemmaRMSNorm eps, modeling_gemma.py:66) */
   float rope_theta;       /* 10000 (transformers default rope) */
-  float time_min_period;  /* 4e-3 (pi0_pytorch.py:298) */
-  float time_max_period;  /* 4.0 */
+  double time_min_period; /* 4e-3 (pi0_pytorch.py:298; a Python float, hence double) */
+  double time_max_period; /* 4.0 */
 } pi05_dims;
 
 typedef struct pi05_ctx pi05_ctx;
@@ -147,6 +147,14 @@ int pi05_release_graph(pi05_ctx* ctx);
 
 /* Number of kernel launches in one denoise step (for profiling). */
 int pi05_launches_per_step(const pi05_ctx* ctx);
+
+/* Profiling hook: enqueue `iters` back-to-back launches of one kernel of the denoise step with the
+ * arguments the graph uses for Euler step 0 and decoder layer `layer`, on `stream`.  kernel_id:
+ * 0 step boundary (final norm + action_out_proj + Euler + action_in_proj), 1 qkv_rope,
+ * 2 attention, 3 o_proj, 4 gate_up, 5 down_proj.  It overwrites the context's activations, so
+ * call pi05_denoise again afterwards for a meaningful result.  No counterpart in the reference
+ * (its tools/ time kernels from nsys traces); it lets a benchmark time one kernel with events. */
+int pi05_bench_kernel(pi05_ctx* ctx, int kernel_id, int layer, int iters, void* stream);
 
 /* ---- host-only helpers (no GPU needed; what the context computes on the host) ---- */
 

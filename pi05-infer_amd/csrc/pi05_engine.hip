@@ -10,7 +10,9 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -55,7 +57,7 @@ struct HeadBind {
 
 // Device buffer plan of one signature (sizes in bytes).
 struct Plan {
-  int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1;
+  int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1, mgroups = 1;
   size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, kv = 0, valid = 0, rope = 0, pos = 0;
   size_t h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0, ptrs = 0, invf = 0;
   size_t total() const {
@@ -64,14 +66,16 @@ struct Plan {
   }
 };
 
-// Split-KV factor: about 8 key blocks (256 keys) per workgroup.
+// Split-KV factor: one 32-key block per wave (4 per workgroup) up to kMaxAttnSplits splits;
+// longer prefixes give each wave several blocks instead.
 int choose_nsplit(int s_pad) {
   const int nkb = s_pad / 32;
-  int ns = (nkb + 7) / 8;
+  int ns = (nkb + 3) / 4;
   if (ns < 1) ns = 1;
-  if (ns > 16) ns = 16;
+  if (ns > kMaxAttnSplits) ns = kMaxAttnSplits;
   return ns;
 }
+
 
 Plan make_plan(const pi05_dims& d) {
   Plan p;
@@ -97,6 +101,7 @@ Plan make_plan(const pi05_dims& d) {
   p.act = (size_t)p.M * kMlp * 2;
   p.part = p.nsplit > 1 ? (size_t)p.nsplit * p.rows * kHeadDim * 4 : 0;
   p.partml = p.nsplit > 1 ? (size_t)p.nsplit * p.rows * 4 : 0;
+  p.mgroups = (p.M + 63) / 64;
   p.x = (size_t)p.M * kActDim * 4;
   p.trace = (size_t)d.num_steps * p.M * kActDim * 4;
   p.ptrs = (size_t)2 * d.depth * sizeof(void*);
@@ -131,7 +136,7 @@ bool check_dims_msg(const pi05_dims* d, std::string* msg) {
   REQ(d->num_steps >= 1 && d->num_steps <= kMaxSteps, "num_steps %d out of range [1, %d]", d->num_steps, kMaxSteps);
   REQ(std::isfinite(d->rms_eps) && d->rms_eps > 0.f, "rms_eps must be a positive finite float");
   REQ(std::isfinite(d->rope_theta) && d->rope_theta > 1.f, "rope_theta must be > 1");
-  REQ(std::isfinite(d->time_min_period) && d->time_min_period > 0.f && std::isfinite(d->time_max_period) &&
+  REQ(std::isfinite(d->time_min_period) && d->time_min_period > 0.0 && std::isfinite(d->time_max_period) &&
           d->time_max_period > d->time_min_period,
       "time periods must satisfy 0 < min_period < max_period");
 #undef REQ
@@ -281,100 +286,127 @@ hipError_t dalloc(T** p, size_t bytes) {
   return e;
 }
 
-// Enqueue the full num_steps loop (what the graph records).
-int enqueue_loop(pi05_ctx* c, hipStream_t st, bool with_trace) {
+// Kernel ids of one denoise step (pi05_bench_kernel).
+enum { kKStepIo = 0, kKQkv = 1, kKAttn = 2, kKOProj = 3, kKGateUp = 4, kKDown = 5, kKCount = 6 };
+
+int enqueue_step_io(pi05_ctx* c, hipStream_t st, int s, bool with_trace) {
+  const pi05_dims& d = c->d;
+  const Plan& p = c->plan;
+  StepIoArgs io{};
+  io.rowss = c->rowss;
+  io.h = c->h;
+  io.x = c->x;
+  io.in_w = heads_in_w(c);
+  io.in_b = heads_in_b(c);
+  io.out_w = heads_out_w(c);
+  io.out_b = heads_out_b(c);
+  io.eps = d.rms_eps;
+  io.M = p.M;
+  io.has_prev = s > 0;
+  io.has_next = s < d.num_steps;
+  if (s > 0) {
+    const int ps = s - 1;
+    const float t = c->ts[ps];
+    const float delta = c->ts[ps] - c->ts[ps + 1];
+    io.t = t;
+    io.one_minus_t = 1.0f - t;
+    io.x1_weight = t - delta;
+    io.x0_weight = 1.0f - io.x1_weight;
+    io.final_mod = c->table + ((size_t)ps * p.n_norms + (p.n_norms - 1)) * kModW;
+    io.trace = with_trace ? c->trace + (size_t)ps * p.M * kActDim : nullptr;
+  }
+  HIPCHK(c, launch_step_io(io, st));
+  return PI05_OK;
+}
+
+// Enqueue the kernels of decoder layer l at Euler step s whose bit is set in `mask`.
+int enqueue_layer(pi05_ctx* c, hipStream_t st, int s, int l, unsigned mask) {
   const pi05_dims& d = c->d;
   const Plan& p = c->plan;
   const size_t kv_block = (size_t)d.batch * p.s_pad * kHeadDim;
+  const float* mod_step = c->table + (size_t)s * p.n_norms * kModW;
+  const u16* wl = c->wpack + (size_t)l * kLayerElems;
+  const float* mod1 = mod_step + (size_t)(2 * l) * kModW;
+  const float* mod2 = mod_step + (size_t)(2 * l + 1) * kModW;
+  u16* kc_l = c->kcache + (size_t)l * kv_block;
+  u16* vc_l = c->vcache + (size_t)l * kv_block;
+  if (mask & (1u << kKQkv)) {
+    GemmArgs qa{};
+    qa.w = wl + kOffQkv;
+    qa.h = c->h;
+    qa.rowss = c->rowss;
+    qa.mod = mod1;
+    qa.cos_tab = c->cos_tab;
+    qa.sin_tab = c->sin_tab;
+    qa.q = c->q;
+    qa.kcache = kc_l;
+    qa.vcache = vc_l;
+    qa.eps = d.rms_eps;
+    qa.M = p.M;
+    qa.prefix_len = d.prefix_len;
+    qa.s_pad = p.s_pad;
+    HIPCHK(c, launch_qkv_rope(qa, st));
+  }
+  if (mask & (1u << kKAttn)) {
+    AttnArgs aa{};
+    aa.q = c->q;
+    aa.kcache = kc_l;
+    aa.vcache = vc_l;
+    aa.valid = c->valid;
+    aa.out = c->o;
+    aa.part = c->part;
+    aa.part_m = c->part_m;
+    aa.part_l = c->part_l;
+    aa.rows = p.rows;
+    aa.s_pad = p.s_pad;
+    aa.nsplit = p.nsplit;
+    HIPCHK(c, launch_attention(aa, st));
+  }
+  if (mask & (1u << kKOProj)) {
+    GemmArgs oa{};
+    oa.w = wl + kOffO;
+    oa.act = c->o;
+    oa.mod = mod1;
+    oa.h_out = c->h;
+    oa.rowss = c->rowss;
+    oa.M = p.M;
+    HIPCHK(c, launch_o_proj(oa, st));
+  }
+  if (mask & (1u << kKGateUp)) {
+    GemmArgs ga{};
+    ga.w = wl + kOffGate;
+    ga.w2 = wl + kOffUp;
+    ga.h = c->h;
+    ga.rowss = c->rowss;
+    ga.mod = mod2;
+    ga.out = c->act;
+    ga.eps = d.rms_eps;
+    ga.M = p.M;
+    HIPCHK(c, launch_gate_up(ga, st));
+  }
+  if (mask & (1u << kKDown)) {
+    GemmArgs da{};
+    da.w = wl + kOffDown;
+    da.act = c->act;
+    da.mod = mod2;
+    da.h_out = c->h;
+    da.rowss = c->rowss;
+    da.M = p.M;
+    HIPCHK(c, launch_down(da, st));
+  }
+  return PI05_OK;
+}
+
+// Enqueue the full num_steps loop (what the graph records).
+int enqueue_loop(pi05_ctx* c, hipStream_t st, bool with_trace) {
+  const pi05_dims& d = c->d;
   for (int s = 0; s <= d.num_steps; ++s) {
-    StepIoArgs io{};
-    io.rowss = c->rowss;
-    io.h = c->h;
-    io.x = c->x;
-    io.in_w = heads_in_w(c);
-    io.in_b = heads_in_b(c);
-    io.out_w = heads_out_w(c);
-    io.out_b = heads_out_b(c);
-    io.eps = d.rms_eps;
-    io.M = p.M;
-    io.has_prev = s > 0;
-    io.has_next = s < d.num_steps;
-    if (s > 0) {
-      const int ps = s - 1;
-      const float t = c->ts[ps];
-      const float delta = c->ts[ps] - c->ts[ps + 1];
-      io.t = t;
-      io.one_minus_t = 1.0f - t;
-      io.x1_weight = t - delta;
-      io.x0_weight = 1.0f - io.x1_weight;
-      io.final_mod = c->table + ((size_t)ps * p.n_norms + (p.n_norms - 1)) * kModW;
-      io.trace = with_trace ? c->trace + (size_t)ps * p.M * kActDim : nullptr;
-    }
-    HIPCHK(c, launch_step_io(io, st));
+    int rc = enqueue_step_io(c, st, s, with_trace);
+    if (rc != PI05_OK) return rc;
     if (s == d.num_steps) break;
-    const float* mod_step = c->table + (size_t)s * p.n_norms * kModW;
     for (int l = 0; l < d.depth; ++l) {
-      const u16* wl = c->wpack + (size_t)l * kLayerElems;
-      const float* mod1 = mod_step + (size_t)(2 * l) * kModW;
-      const float* mod2 = mod_step + (size_t)(2 * l + 1) * kModW;
-      QkvArgs qa{};
-      qa.w = wl + kOffQkv;
-      qa.h = c->h;
-      qa.rowss = c->rowss;
-      qa.mod = mod1;
-      qa.cos_tab = c->cos_tab;
-      qa.sin_tab = c->sin_tab;
-      qa.q = c->q;
-      qa.kcache = c->kcache + (size_t)l * kv_block;
-      qa.vcache = c->vcache + (size_t)l * kv_block;
-      qa.eps = d.rms_eps;
-      qa.M = p.M;
-      qa.prefix_len = d.prefix_len;
-      qa.s_pad = p.s_pad;
-      HIPCHK(c, launch_qkv_rope(qa, st));
-
-      AttnArgs aa{};
-      aa.q = c->q;
-      aa.kcache = qa.kcache;
-      aa.vcache = qa.vcache;
-      aa.valid = c->valid;
-      aa.out = c->o;
-      aa.part = c->part;
-      aa.part_m = c->part_m;
-      aa.part_l = c->part_l;
-      aa.rows = p.rows;
-      aa.s_pad = p.s_pad;
-      aa.nsplit = p.nsplit;
-      HIPCHK(c, launch_attention(aa, st));
-
-      ResidualArgs ra{};
-      ra.w = wl + kOffO;
-      ra.act = c->o;
-      ra.mod_gate = mod1 + 2 * kWidth;
-      ra.h = c->h;
-      ra.rowss = c->rowss;
-      ra.M = p.M;
-      HIPCHK(c, launch_o_proj(ra, st));
-
-      GateUpArgs ga{};
-      ga.wgate = wl + kOffGate;
-      ga.wup = wl + kOffUp;
-      ga.h = c->h;
-      ga.rowss = c->rowss;
-      ga.mod = mod2;
-      ga.act = c->act;
-      ga.eps = d.rms_eps;
-      ga.M = p.M;
-      HIPCHK(c, launch_gate_up(ga, st));
-
-      ResidualArgs da{};
-      da.w = wl + kOffDown;
-      da.act = c->act;
-      da.mod_gate = mod2 + 2 * kWidth;
-      da.h = c->h;
-      da.rowss = c->rowss;
-      da.M = p.M;
-      HIPCHK(c, launch_down(da, st));
+      rc = enqueue_layer(c, st, s, l, 0xffffffffu);
+      if (rc != PI05_OK) return rc;
     }
   }
   return PI05_OK;
@@ -422,8 +454,8 @@ void pi05_default_dims(pi05_dims* d) {
   d->num_steps = 10;
   d->rms_eps = 1e-6f;
   d->rope_theta = 10000.0f;
-  d->time_min_period = 4e-3f;
-  d->time_max_period = 4.0f;
+  d->time_min_period = 4e-3;
+  d->time_max_period = 4.0;
 }
 
 int pi05_check_dims(const pi05_dims* dims) {
@@ -511,7 +543,7 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   if (ae == hipSuccess) {
     std::vector<float> temb((size_t)dims->num_steps * kWidth);
     for (int s = 0; s < dims->num_steps; ++s)
-      sinusoid(c->ts[s], kWidth, (double)dims->time_min_period, (double)dims->time_max_period, &temb[(size_t)s * kWidth]);
+      sinusoid(c->ts[s], kWidth, dims->time_min_period, dims->time_max_period, &temb[(size_t)s * kWidth]);
     ae = hipMemcpy(c->temb, temb.data(), p.temb, hipMemcpyHostToDevice);
   }
   if (ae != hipSuccess) {
@@ -738,6 +770,23 @@ int pi05_launches_per_step(const pi05_ctx* c) {
   return 1 + c->d.depth * (c->plan.nsplit > 1 ? 6 : 5);
 }
 
+int pi05_bench_kernel(pi05_ctx* c, int kernel_id, int layer, int iters, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (kernel_id < 0 || kernel_id >= kKCount) return c->fail(PI05_E_INVALID, "kernel_id %d out of range [0, %d)", kernel_id, kKCount);
+  if (layer < 0 || layer >= c->d.depth) return c->fail(PI05_E_INVALID, "layer %d out of range", layer);
+  if (iters < 1 || iters > 100000) return c->fail(PI05_E_INVALID, "iters %d out of range [1, 100000]", iters);
+  if (!c->weights_ready || !c->primed) return c->fail(PI05_E_STATE, "weights and prefix must be ready");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (int i = 0; i < iters; ++i) {
+    const int rc = kernel_id == kKStepIo ? enqueue_step_io(c, st, 1, false) : enqueue_layer(c, st, 0, layer, 1u << kernel_id);
+    if (rc != PI05_OK) return rc;
+  }
+  return PI05_OK;
+}
+
 int pi05_euler_schedule(int num_steps, float* ts_host) {
   if (num_steps < 1 || num_steps > kMaxSteps || !ts_host) {
     g_last_error = "num_steps out of range or ts_host is NULL";
@@ -754,7 +803,7 @@ int pi05_time_embedding(const pi05_dims* dims, float t, float* out_host) {
     g_last_error = "out_host is NULL";
     return PI05_E_INVALID;
   }
-  sinusoid(t, kWidth, (double)dims->time_min_period, (double)dims->time_max_period, out_host);
+  sinusoid(t, kWidth, dims->time_min_period, dims->time_max_period, out_host);
   return PI05_OK;
 }
 

@@ -39,7 +39,7 @@ struct GemvArgs {
 };
 
 struct StepIoArgs {
-  float* rowss;            // [64][M] partial sums of squares of h rows (read, then rewritten)
+  float* rowss;            // [M][64] partial sums of squares of h rows (read, then rewritten)
   u16* h;                  // [M, W] bf16 residual stream
   float* x;                // [M, a] actions (in/out)
   float* trace;            // [M, a] velocity of the previous step (nullable)
@@ -52,39 +52,26 @@ struct StepIoArgs {
   int M, has_prev, has_next;
 };
 
-struct QkvArgs {
-  const u16* w;          // packed q|k|v tiles of this layer
-  const u16* h;          // [M, W]
-  const float* rowss;    // [64][M]
-  const float* mod;      // input_layernorm modulation row [3W] of this step
-  const u16* cos_tab;    // [M, D]
+// One argument block for the GEMM family (fields unused by a mode are ignored).
+struct GemmArgs {
+  const u16* w;          // packed weight tiles (q|k|v, gate, o_proj or down)
+  const u16* w2;         // packed up_proj tiles (gate_up)
+  const u16* act;        // [M, K] bf16 A operand (residual mode)
+  const u16* h;          // [M, W] residual stream read by the adaRMSNorm prologue
+  u16* h_out;            // [M, W] residual stream updated by the residual epilogue
+  float* rowss;          // [M][64] row sums of squares: read by the prologue, written by the residual epilogue
+  const float* mod;      // modulation row [3W] of this norm and step: scale | shift | gate
+  const u16* cos_tab;    // [M, D] bf16 RoPE tables
   const u16* sin_tab;
   u16* q;                // [M, H*D]
   u16* kcache;           // this layer's [B] fragment-major K blocks
   u16* vcache;
+  u16* out;              // [M, I] GeGLU output
   float eps;
   int M, prefix_len, s_pad;
 };
 
-struct ResidualArgs {
-  const u16* w;         // packed [W/16 tiles][K/32] fragments
-  const u16* act;       // [M, K] bf16 GEMM input
-  const float* mod_gate;  // gate third of the modulation row [W]
-  u16* h;               // [M, W] residual stream (updated in place)
-  float* rowss;         // [64][M] partial sums of squares (written)
-  int M;
-};
-
-struct GateUpArgs {
-  const u16* wgate;
-  const u16* wup;
-  const u16* h;
-  const float* rowss;
-  const float* mod;     // post_attention_layernorm modulation row [3W]
-  u16* act;             // [M, I]
-  float eps;
-  int M;
-};
+constexpr int kMaxAttnSplits = 8;
 
 struct AttnArgs {
   const u16* q;        // [rows, D] (rows = M * H)
@@ -103,10 +90,10 @@ hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);
 hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t st);
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st);
 hipError_t launch_step_io(const StepIoArgs& a, hipStream_t st);
-hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t st);
-hipError_t launch_o_proj(const ResidualArgs& a, hipStream_t st);
-hipError_t launch_down(const ResidualArgs& a, hipStream_t st);
-hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st);
+hipError_t launch_qkv_rope(const GemmArgs& a, hipStream_t st);
+hipError_t launch_gate_up(const GemmArgs& a, hipStream_t st);
+hipError_t launch_o_proj(const GemmArgs& a, hipStream_t st);
+hipError_t launch_down(const GemmArgs& a, hipStream_t st);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 
 }  // namespace pi05

@@ -141,95 +141,132 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs a) {
 
 // =============================================================================================
 // step boundary: final norm + action_out_proj + Euler (previous step), action_in_proj (this step)
+// One workgroup per token row; every global load is issued before the first dependent use.
 // =============================================================================================
 
 __global__ __launch_bounds__(256) void step_io_kernel(StepIoArgs a) {
   const int m = blockIdx.x;  // token row (b * A + t)
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
+  const int j = tid >> 3, part = tid & 7;  // action_out_proj: 8 threads per output, 128 k each
+  const int c0 = tid * 4;                  // 4 hidden columns per thread
   __shared__ float s_n[kWidth];
   __shared__ float s_x[kActDim];
-  __shared__ float s_ss;
+  __shared__ float s_rstd;
+
+  // ---- loads
+  float4 rs = {0.f, 0.f, 0.f, 0.f};
+  u16x4 hv = {0, 0, 0, 0};
+  float4 sc = {0.f, 0.f, 0.f, 0.f}, sh = {0.f, 0.f, 0.f, 0.f};
+  float4 wo[32];
+  float xj = 0.f, bo = 0.f;
+  if (a.has_prev) {
+    if (tid < 16) rs = *reinterpret_cast<const float4*>(a.rowss + (size_t)m * kRowSlots + tid * 4);
+    hv = *reinterpret_cast<const u16x4*>(a.h + (size_t)m * kWidth + c0);
+    sc = *reinterpret_cast<const float4*>(a.final_mod + c0);
+    sh = *reinterpret_cast<const float4*>(a.final_mod + kWidth + c0);
+#pragma unroll
+    for (int q = 0; q < 32; ++q) wo[q] = *reinterpret_cast<const float4*>(a.out_w + (size_t)j * kWidth + part * 128 + q * 4);
+    if (part == 0) {
+      xj = a.x[(size_t)m * kActDim + j];
+      bo = a.out_b[j];
+    }
+  } else if (tid < kActDim) {
+    s_x[tid] = a.x[(size_t)m * kActDim + tid];
+  }
+  float4 wi[4][8];
+  float4 bi = {0.f, 0.f, 0.f, 0.f};
+  if (a.has_next) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) wi[q][k] = *reinterpret_cast<const float4*>(a.in_w + (size_t)(c0 + q) * kActDim + k * 4);
+    bi = *reinterpret_cast<const float4*>(a.in_b + c0);
+  }
 
   if (a.has_prev) {
-    // final adaRMSNorm (model.norm, modeling_gemma.py:782-783) of h[m]
-    if (tid < 64) {
-      float v = a.rowss[(size_t)tid * a.M + m];
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-      if (tid == 0) s_ss = v;
+    // final adaRMSNorm (model.norm, modeling_gemma.py:782-783)
+    if (tid < 16) {
+      float v = (rs.x + rs.y) + (rs.z + rs.w);
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      if (tid == 0) s_rstd = 1.0f / sqrtf(fadd(v * (1.0f / kWidth), a.eps));
     }
     __syncthreads();
-    const float rstd = 1.0f / sqrtf(fadd(s_ss * (1.0f / kWidth), a.eps));
-    const u16* hrow = a.h + (size_t)m * kWidth;
-    for (int c = tid; c < kWidth; c += 256) {
-      const float hv = bf2f(hrow[c]);
-      const float sc = a.final_mod[c];
-      const float sh = a.final_mod[kWidth + c];
-      s_n[c] = round_bf(fadd(fmul(fmul(hv, rstd), fadd(1.0f, sc)), sh));
-    }
+    const float rstd = s_rstd;
+    const float scs[4] = {sc.x, sc.y, sc.z, sc.w};
+    const float shs[4] = {sh.x, sh.y, sh.z, sh.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s_n[c0 + q] = round_bf(fadd(fmul(fmul(bf2f(hv[q]), rstd), fadd(1.0f, scs[q])), shs[q]));
     __syncthreads();
-    // v = action_out_proj(n) fp32 (engine.py:767): 8 threads per output, 128 k each
-    const int j = tid >> 3;
-    const int part = tid & 7;
-    const float* wr = a.out_w + (size_t)j * kWidth + part * 128;
+    // v = action_out_proj(n) in fp32 (engine.py:767)
     float acc = 0.f;
-    for (int k = 0; k < 128; k += 4) {
-      const float4 w4 = *reinterpret_cast<const float4*>(wr + k);
-      acc += w4.x * s_n[part * 128 + k] + w4.y * s_n[part * 128 + k + 1] + w4.z * s_n[part * 128 + k + 2] +
-             w4.w * s_n[part * 128 + k + 3];
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const float* n = s_n + part * 128 + q * 4;
+      acc += wo[q].x * n[0] + wo[q].y * n[1] + wo[q].z * n[2] + wo[q].w * n[3];
     }
     acc += __shfl_xor(acc, 1);
     acc += __shfl_xor(acc, 2);
     acc += __shfl_xor(acc, 4);
     if (part == 0) {
-      const float v = acc + a.out_b[j];
-      const float x = a.x[(size_t)m * kActDim + j];
-      // flow_ode mean, reference op order (engine.py:664-675)
-      const float x0_pred = fsub(x, fmul(v, a.t));
-      const float x1_pred = fadd(x, fmul(v, a.one_minus_t));
+      const float v = acc + bo;
+      // flow_ode mean in the reference's op order (engine.py:664-675)
+      const float x0_pred = fsub(xj, fmul(v, a.t));
+      const float x1_pred = fadd(xj, fmul(v, a.one_minus_t));
       const float xn = fadd(fmul(x0_pred, a.x0_weight), fmul(x1_pred, a.x1_weight));
       a.x[(size_t)m * kActDim + j] = xn;
       s_x[j] = xn;
       if (a.trace) a.trace[(size_t)m * kActDim + j] = v;
     }
-  } else if (tid < kActDim) {
-    s_x[tid] = a.x[(size_t)m * kActDim + tid];
   }
   __syncthreads();
 
   if (a.has_next) {
     // h = bf16(action_in_proj(x)) (pi0_pytorch.py:303-306; modeling_gemma.py:724-725)
-    const int c0 = tid * 4;
+    const float bis[4] = {bi.x, bi.y, bi.z, bi.w};
     float ss = 0.f;
-    u16 hv[4];
+    u16x4 h4;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float* wr = a.in_w + (size_t)(c0 + q) * kActDim;
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < kActDim; k += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(wr + k);
-        acc += w4.x * s_x[k] + w4.y * s_x[k + 1] + w4.z * s_x[k + 2] + w4.w * s_x[k + 3];
-      }
-      hv[q] = f2bf(acc + a.in_b[c0 + q]);
-      const float hf = bf2f(hv[q]);
+      for (int k = 0; k < 8; ++k)
+        acc += wi[q][k].x * s_x[4 * k] + wi[q][k].y * s_x[4 * k + 1] + wi[q][k].z * s_x[4 * k + 2] + wi[q][k].w * s_x[4 * k + 3];
+      h4[q] = f2bf(acc + bis[q]);
+      const float hf = bf2f(h4[q]);
       ss += hf * hf;
     }
-    u16x4 h4 = {hv[0], hv[1], hv[2], hv[3]};
     *reinterpret_cast<u16x4*>(a.h + (size_t)m * kWidth + c0) = h4;
     // per-16-column partial sums of squares (4 threads per 16-column tile)
     ss += __shfl_xor(ss, 1);
     ss += __shfl_xor(ss, 2);
-    if ((lane & 3) == 0) a.rowss[(size_t)(c0 >> 4) * a.M + m] = ss;
+    if ((tid & 3) == 0) a.rowss[(size_t)m * kRowSlots + (c0 >> 4)] = ss;
   }
 }
 
 // =============================================================================================
-// GEMM family (small M, weight streaming on MFMA)
+// GEMM family: small-M weight streaming on MFMA 16x16x32 bf16
+//
+// A workgroup owns NT 16-column weight tiles over the whole K; its 8 waves split K into KSW
+// k-steps each.  Each wave issues its activation loads first and its weight fragments
+// (nontemporal) right after, all before the first MFMA, so a kernel pays about one memory round
+// trip; per-workgroup operands shared by all lanes (modulation rows) are staged once in LDS.
+// The waves' partial sums meet in LDS and are added in fixed wave order, so results do not
+// depend on timing.  No workgroup ever waits for another one.
+//   norm_gemm_kernel<kModeQkv>    : adaRMSNorm prologue, RoPE epilogue (q; k/v into the cache)
+//   norm_gemm_kernel<kModeGateUp> : adaRMSNorm prologue, GeGLU epilogue
+//   residual_gemm_kernel          : plain A operand, gated-residual epilogue + row statistics
+// Epilogue mapping: thread T < 256 owns m-tile T/64 and MFMA lane T%64, i.e. output column
+// T%16 of the tile and rows mt*16 + ((T%64)/16)*4 + i, i < 4 (the MFMA D layout).
 // =============================================================================================
 
-// Weight fragments of this wave: NT tiles x KSW k-steps, issued up front (nontemporal: the
-// weights are read once per step and must not evict the activations from L2).
+enum GemmMode { kModeQkv = 0, kModeGateUp = 1 };
+
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = kGemmWaves * 64;
+
 template <int NT, int KSW>
 __device__ __forceinline__ void load_weights(bf16x8 (&w)[NT][KSW], const u16* const (&tile)[NT], int ks0, int lane) {
 #pragma unroll
@@ -241,39 +278,7 @@ __device__ __forceinline__ void load_weights(bf16x8 (&w)[NT][KSW], const u16* co
     }
 }
 
-// adaRMSNorm applied while forming the MFMA A fragment: 8 consecutive k of row `row`
-// (modeling_gemma.py:82-116): bf16((h * rstd) * (1 + scale) + shift).
-__device__ __forceinline__ bf16x8 norm_frag(const u16* __restrict__ h, int row, int k, float rstd,
-                                            const float* __restrict__ scale, const float* __restrict__ shift) {
-  const u16x8 hv = *reinterpret_cast<const u16x8*>(h + (size_t)row * kWidth + k);
-  const float4 s0 = *reinterpret_cast<const float4*>(scale + k);
-  const float4 s1 = *reinterpret_cast<const float4*>(scale + k + 4);
-  const float4 t0 = *reinterpret_cast<const float4*>(shift + k);
-  const float4 t1 = *reinterpret_cast<const float4*>(shift + k + 4);
-  const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  const float sh[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
-  u16x8 o;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = f2bf(fadd(fmul(fmul(bf2f(hv[j]), rstd), fadd(1.0f, sc[j])), sh[j]));
-  return as_bf16x8(o);
-}
-
-// rstd of 64 rows starting at m0 from the per-tile sum-of-squares partials.
-__device__ __forceinline__ void row_rstd(float* s_rstd, const float* __restrict__ rowss, int M, int m0, float eps) {
-  const int t = threadIdx.x;
-  if (t < 64) {
-    const int m = m0 + t;
-    float ss = 0.f;
-    if (m < M) {
-      for (int s = 0; s < kRowSlots; ++s) ss += rowss[(size_t)s * M + m];
-    }
-    s_rstd[t] = 1.0f / sqrtf(fadd(ss * (1.0f / kWidth), eps));
-  }
-}
-
-// Cross-wave K reduction through LDS.  Wave w stores acc[mt][t] (lane-major f32x4), then each
-// output (row r in 0..63, col c in 0..15) is summed over waves in fixed order.
-template <int NW, int NT>
+template <int NT>
 __device__ __forceinline__ void store_partials(float* red, const f32x4 (&acc)[4][NT], int wave, int lane) {
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -282,174 +287,17 @@ __device__ __forceinline__ void store_partials(float* red, const f32x4 (&acc)[4]
       *reinterpret_cast<f32x4*>(red + ((((size_t)wave * 4 + mt) * NT + t) * 64 + lane) * 4) = acc[mt][t];
 }
 
-template <int NW, int NT>
-__device__ __forceinline__ float reduced(const float* red, int r, int c, int t) {
-  const int mt = r >> 4, g = (r & 15) >> 2, i = r & 3;
-  const int lane = g * 16 + c;
-  float v = 0.f;
+// Sum over the 8 waves, in wave order, of the D fragment (m-tile mt, lane) of tile t.
+template <int NT>
+__device__ __forceinline__ f32x4 reduce_waves(const float* red, int mt, int lane, int t) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(red + (((size_t)mt * NT + t) * 64 + lane) * 4);
 #pragma unroll
-  for (int w = 0; w < NW; ++w) v += red[((((size_t)w * 4 + mt) * NT + t) * 64 + lane) * 4 + i];
+  for (int w = 1; w < kGemmWaves; ++w) v += *reinterpret_cast<const f32x4*>(red + ((((size_t)w * 4 + mt) * NT + t) * 64 + lane) * 4);
   return v;
 }
 
-// ---------------------------------------------------------------------------------------------
-// qkv_rope: 80 workgroups x 4 waves.  WG p < 72 owns a RoPE pair of 16-column tiles of one
-// rotated head (8 q heads + the k head): dims [dt*16, +16) and [128 + dt*16, +16); WG p >= 72
-// owns two v tiles.  Waves split K = 1024 four ways.
-// ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 1) void qkv_rope_kernel(QkvArgs a) {
-  constexpr int NW = 4, NT = 2, KSW = 8;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r16 = lane & 15;
-  const int p = blockIdx.x;
-  int tiles[2];
-  const bool rotated = p < 72;
-  const int head = p >> 3, dt = p & 7;
-  if (rotated) {
-    tiles[0] = head * 16 + dt;
-    tiles[1] = head * 16 + 8 + dt;
-  } else {
-    tiles[0] = 144 + 2 * (p - 72);
-    tiles[1] = tiles[0] + 1;
-  }
-  const u16* tile_ptr[NT] = {a.w + wfrag_offset(tiles[0], 0, 32), a.w + wfrag_offset(tiles[1], 0, 32)};
-  bf16x8 w[NT][KSW];
-  load_weights<NT, KSW>(w, tile_ptr, wave * KSW, lane);
-
-  __shared__ float s_rstd[64];
-  __shared__ float red[NW * 4 * NT * 64 * 4];
-  const float* scale = a.mod;
-  const float* shift = a.mod + kWidth;
-
-  for (int m0 = 0; m0 < a.M; m0 += 64) {
-    row_rstd(s_rstd, a.rowss, a.M, m0, a.eps);
-    __syncthreads();
-    f32x4 acc[4][NT];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSW; ++s) {
-      const int k = (wave * KSW + s) * 32 + g * 8;
-      bf16x8 af[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int row = m0 + mt * 16 + r16;
-        af[mt] = row < a.M ? norm_frag(a.h, row, k, s_rstd[mt * 16 + r16], scale, shift) : zero_frag();
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = mfma16x16x32(af[mt], w[t][s], acc[mt][t]);
-    }
-    store_partials<NW, NT>(red, acc, wave, lane);
-    __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 16; e += NW * 64) {
-      const int r = e >> 4, c = e & 15;
-      const int m = m0 + r;
-      if (m >= a.M) continue;
-      const float x_lo = round_bf(reduced<NW, NT>(red, r, c, 0));
-      const float x_hi = round_bf(reduced<NW, NT>(red, r, c, 1));
-      const int b = m / kHorizon, tok = m % kHorizon;
-      u16* kc = a.kcache + (size_t)b * a.s_pad * kHeadDim;
-      u16* vc = a.vcache + (size_t)b * a.s_pad * kHeadDim;
-      const int key = a.prefix_len + tok;
-      if (rotated) {
-        const int d = dt * 16 + c;
-        const u16* cs = a.cos_tab + (size_t)m * kHeadDim;
-        const u16* sn = a.sin_tab + (size_t)m * kHeadDim;
-        // (x*cos) + (rotate_half(x)*sin), rotate_half(x) = cat(-x_hi, x_lo)
-        // (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216)
-        const float o_lo = fsub(fmul(x_lo, bf2f(cs[d])), fmul(x_hi, bf2f(sn[d])));
-        const float o_hi = fadd(fmul(x_hi, bf2f(cs[d + kHalfDim])), fmul(x_lo, bf2f(sn[d + kHalfDim])));
-        if (head < kHeads) {
-          u16* qrow = a.q + (size_t)m * (kHeads * kHeadDim) + head * kHeadDim;
-          qrow[d] = f2bf(o_lo);
-          qrow[d + kHalfDim] = f2bf(o_hi);
-        } else {
-          kc[kfrag_index(key, d)] = f2bf(o_lo);
-          kc[kfrag_index(key, d + kHalfDim)] = f2bf(o_hi);
-        }
-      } else {
-        const int dv = (tiles[0] - 144) * 16 + c;
-        vc[vfrag_index(key, dv)] = f2bf(x_lo);
-        vc[vfrag_index(key, dv + 16)] = f2bf(x_hi);
-      }
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// Residual GEMM (o_proj, K = 2048 / down_proj, K = 4096): 64 workgroups, one 16-column tile
-// each, 8 waves splitting K.  Epilogue: h = bf16(h + bf16(bf16(y) * gate)) and the per-tile
-// row sums of squares that the next adaRMSNorm consumes (modeling_gemma.py:231-249, 503, 511).
-// ---------------------------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(512, 1) void residual_gemm_kernel(ResidualArgs a) {
-  constexpr int NW = 8, NT = 1, KSW = K / 32 / NW;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r16 = lane & 15;
-  const int nt = blockIdx.x;
-  const u16* tile_ptr[NT] = {a.w + wfrag_offset(nt, 0, K / 32)};
-  bf16x8 w[NT][KSW];
-  load_weights<NT, KSW>(w, tile_ptr, wave * KSW, lane);
-
-  __shared__ float red[NW * 4 * NT * 64 * 4];
-
-  for (int m0 = 0; m0 < a.M; m0 += 64) {
-    f32x4 acc[4][NT];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSW; ++s) {
-      const int k = (wave * KSW + s) * 32 + g * 8;
-      bf16x8 af[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int row = m0 + mt * 16 + r16;
-        af[mt] = row < a.M ? load_frag(a.act + (size_t)row * K + k) : zero_frag();
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt][0] = mfma16x16x32(af[mt], w[0][s], acc[mt][0]);
-    }
-    store_partials<NW, NT>(red, acc, wave, lane);
-    __syncthreads();
-    // 1024 outputs, 2 per thread; the 16 columns of a row sit in 16 consecutive threads
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int e = threadIdx.x + it * 512;
-      const int r = e >> 4, c = e & 15;
-      const int m = m0 + r;
-      const int col = nt * 16 + c;
-      float hn = 0.f;
-      if (m < a.M) {
-        const float y = round_bf(reduced<NW, NT>(red, r, c, 0));
-        const float gate = round_bf(a.mod_gate[col]);
-        const float prod = round_bf(fmul(y, gate));
-        u16* hp = a.h + (size_t)m * kWidth + col;
-        const u16 hb = f2bf(fadd(bf2f(*hp), prod));
-        *hp = hb;
-        hn = bf2f(hb);
-      }
-      float ss = hn * hn;
-      ss += __shfl_xor(ss, 1);
-      ss += __shfl_xor(ss, 2);
-      ss += __shfl_xor(ss, 4);
-      ss += __shfl_xor(ss, 8);
-      if (c == 0 && m < a.M) a.rowss[(size_t)nt * a.M + m] = ss;
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// gate_up: 256 workgroups x 4 waves; WG j owns gate tile j and up tile j (16 columns each).
-// Prologue adaRMSNorm(post_attention_layernorm); epilogue GeGLU as the fused reference kernel
-// defines it: bf16(gelu_tanh(bf16(g)) * u) (rlinf_fused_denoise.py:166-173).
-// ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float gelu_tanh(float x) {
+  // GELU tanh approximation in the fused reference kernel's op order (rlinf_fused_denoise.py:168-173)
   const float t3 = fmul(x, 0.5f);
   const float t5 = fmul(fmul(x, x), x);
   const float t8 = fadd(x, fmul(t5, 0.044715f));
@@ -457,51 +305,266 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return fmul(t3, fadd(t11, 1.0f));
 }
 
-__global__ __launch_bounds__(256, 1) void gate_up_kernel(GateUpArgs a) {
-  constexpr int NW = 4, NT = 2, KSW = 8;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// ---------------------------------------------------------------------------------------------
+// adaRMSNorm-prologue GEMMs, K = 1024: 8 waves x 4 k-steps.
+// qkv_rope: 80 workgroups; WG p < 72 owns a RoPE pair of 16-column tiles of one rotated head
+// (8 q heads + the k head), dims [dt*16, +16) and [128 + dt*16, +16); WG p >= 72 owns two v tiles.
+// gate_up: 256 workgroups; WG j owns gate tile j and up tile j.
+// ---------------------------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(kGemmThreads, 1) void norm_gemm_kernel(GemmArgs a) {
+  constexpr int NT = 2, KSW = 4, KSTEPS = kWidth / 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
-  const int nt = blockIdx.x;
-  const u16* tile_ptr[NT] = {a.wgate + wfrag_offset(nt, 0, 32), a.wup + wfrag_offset(nt, 0, 32)};
-  bf16x8 w[NT][KSW];
-  load_weights<NT, KSW>(w, tile_ptr, wave * KSW, lane);
+  const int ks0 = wave * KSW;
+  const int emt = tid >> 6, eg = (tid & 63) >> 4, ec = tid & 15;  // epilogue mapping (tid < 256)
+
+  int tile0;
+  bool rotated = false;
+  int head = 0, dt = 0;
+  const u16* tp[NT];
+  if constexpr (MODE == kModeQkv) {
+    const int p = blockIdx.x;
+    rotated = p < 72;
+    head = p >> 3;
+    dt = p & 7;
+    tile0 = rotated ? head * 16 + dt : 144 + 2 * (p - 72);
+    const int tile1 = rotated ? head * 16 + 8 + dt : tile0 + 1;
+    tp[0] = a.w + (size_t)tile0 * KSTEPS * 512;
+    tp[1] = a.w + (size_t)tile1 * KSTEPS * 512;
+  } else {
+    tile0 = blockIdx.x;
+    tp[0] = a.w + (size_t)blockIdx.x * KSTEPS * 512;
+    tp[1] = a.w2 + (size_t)blockIdx.x * KSTEPS * 512;
+  }
 
   __shared__ float s_rstd[64];
-  __shared__ float red[NW * 4 * NT * 64 * 4];
-  const float* scale = a.mod;
-  const float* shift = a.mod + kWidth;
+  __shared__ float s_mod[2 * kWidth];  // 1 + scale | shift
+  __shared__ float red[kGemmWaves * 4 * NT * 64 * 4];
+  bf16x8 w[NT][KSW];
 
   for (int m0 = 0; m0 < a.M; m0 += 64) {
-    row_rstd(s_rstd, a.rowss, a.M, m0, a.eps);
+    // ---- activation-side loads first (the norm can start as soon as they land) ...
+    u16x8 hr[4][KSW];
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) {
+      const int k = (ks0 + s) * 32 + g * 8;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = m0 + mt * 16 + r16;
+        const u16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+        hr[mt][s] = row < a.M ? *reinterpret_cast<const u16x8*>(a.h + (size_t)row * kWidth + k) : z;
+      }
+    }
+    const float4 mod4 = *reinterpret_cast<const float4*>(a.mod + tid * 4);  // scale | shift, 2048 floats
+    const int srow = tid >> 3, q8 = tid & 7;                                // row statistics: 8 threads per row
+    float4 rs0 = {0.f, 0.f, 0.f, 0.f}, rs1 = {0.f, 0.f, 0.f, 0.f};
+    if (m0 + srow < a.M) {
+      const float* rp = a.rowss + (size_t)(m0 + srow) * kRowSlots + q8 * 8;
+      rs0 = *reinterpret_cast<const float4*>(rp);
+      rs1 = *reinterpret_cast<const float4*>(rp + 4);
+    }
+    float ep_cs[4][4];  // RoPE cos/sin of this thread's 4 epilogue rows
+    if constexpr (MODE == kModeQkv) {
+      if (tid < 256 && rotated) {
+        const int d = dt * 16 + ec;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + emt * 16 + eg * 4 + i;
+          if (m < a.M) {
+            const u16* cs = a.cos_tab + (size_t)m * kHeadDim;
+            const u16* sn = a.sin_tab + (size_t)m * kHeadDim;
+            ep_cs[i][0] = bf2f(cs[d]);
+            ep_cs[i][1] = bf2f(sn[d]);
+            ep_cs[i][2] = bf2f(cs[d + kHalfDim]);
+            ep_cs[i][3] = bf2f(sn[d + kHalfDim]);
+          }
+        }
+      }
+    }
+    // ---- ... then this wave's weight fragments (once; they stay in registers across row groups)
+    if (m0 == 0) load_weights<NT, KSW>(w, tp, ks0, lane);
+
+    {
+      float v = ((rs0.x + rs0.y) + (rs0.z + rs0.w)) + ((rs1.x + rs1.y) + (rs1.z + rs1.w));
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      if (q8 == 0) s_rstd[srow] = 1.0f / sqrtf(fadd(v * (1.0f / kWidth), a.eps));
+      const bool is_scale = tid * 4 < kWidth;
+      s_mod[tid * 4 + 0] = is_scale ? fadd(1.0f, mod4.x) : mod4.x;
+      s_mod[tid * 4 + 1] = is_scale ? fadd(1.0f, mod4.y) : mod4.y;
+      s_mod[tid * 4 + 2] = is_scale ? fadd(1.0f, mod4.z) : mod4.z;
+      s_mod[tid * 4 + 3] = is_scale ? fadd(1.0f, mod4.w) : mod4.w;
+    }
     __syncthreads();
+
+    // ---- adaRMSNorm (modeling_gemma.py:82-116): A = bf16((h * rstd) * (1 + scale) + shift)
     f32x4 acc[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float rstd[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) rstd[mt] = s_rstd[mt * 16 + r16];
 #pragma unroll
     for (int s = 0; s < KSW; ++s) {
-      const int k = (wave * KSW + s) * 32 + g * 8;
-      bf16x8 af[4];
+      const int k = (ks0 + s) * 32 + g * 8;
+      const f32x4 sc0 = *reinterpret_cast<const f32x4*>(s_mod + k);
+      const f32x4 sc1 = *reinterpret_cast<const f32x4*>(s_mod + k + 4);
+      const f32x4 sh0 = *reinterpret_cast<const f32x4*>(s_mod + kWidth + k);
+      const f32x4 sh1 = *reinterpret_cast<const f32x4*>(s_mod + kWidth + k + 4);
+      const float scs[8] = {sc0[0], sc0[1], sc0[2], sc0[3], sc1[0], sc1[1], sc1[2], sc1[3]};
+      const float shs[8] = {sh0[0], sh0[1], sh0[2], sh0[3], sh1[0], sh1[1], sh1[2], sh1[3]};
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const int row = m0 + mt * 16 + r16;
-        af[mt] = row < a.M ? norm_frag(a.h, row, k, s_rstd[mt * 16 + r16], scale, shift) : zero_frag();
+        u16x8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = f2bf(fadd(fmul(fmul(bf2f(hr[mt][s][j]), rstd[mt]), scs[j]), shs[j]));
+        const bf16x8 af = as_bf16x8(o);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = mfma16x16x32(af, w[t][s], acc[mt][t]);
       }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = mfma16x16x32(af[mt], w[t][s], acc[mt][t]);
     }
-    store_partials<NW, NT>(red, acc, wave, lane);
+    store_partials<NT>(red, acc, wave, lane);
     __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 16; e += NW * 64) {
-      const int r = e >> 4, c = e & 15;
-      const int m = m0 + r;
-      if (m >= a.M) continue;
-      const float gv = round_bf(reduced<NW, NT>(red, r, c, 0));
-      const float uv = reduced<NW, NT>(red, r, c, 1);
-      a.act[(size_t)m * kMlp + nt * 16 + c] = f2bf(fmul(gelu_tanh(gv), uv));
+
+    if (tid < 256) {
+      const f32x4 v0 = reduce_waves<NT>(red, emt, tid & 63, 0);
+      const f32x4 v1 = reduce_waves<NT>(red, emt, tid & 63, 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + emt * 16 + eg * 4 + i;
+        if (m >= a.M) continue;
+        if constexpr (MODE == kModeQkv) {
+          const float x_lo = round_bf(v0[i]);
+          const float x_hi = round_bf(v1[i]);
+          const int b = m / kHorizon, tok = m % kHorizon;
+          const int key = a.prefix_len + tok;
+          if (rotated) {
+            // (x*cos) + (rotate_half(x)*sin), rotate_half(x) = cat(-x_hi, x_lo)
+            // (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216)
+            const int d = dt * 16 + ec;
+            const float o_lo = fsub(fmul(x_lo, ep_cs[i][0]), fmul(x_hi, ep_cs[i][1]));
+            const float o_hi = fadd(fmul(x_hi, ep_cs[i][2]), fmul(x_lo, ep_cs[i][3]));
+            if (head < kHeads) {
+              u16* qrow = a.q + (size_t)m * (kHeads * kHeadDim) + head * kHeadDim;
+              qrow[d] = f2bf(o_lo);
+              qrow[d + kHalfDim] = f2bf(o_hi);
+            } else {
+              u16* kc = a.kcache + (size_t)b * a.s_pad * kHeadDim;
+              kc[kfrag_index(key, d)] = f2bf(o_lo);
+              kc[kfrag_index(key, d + kHalfDim)] = f2bf(o_hi);
+            }
+          } else {
+            u16* vc = a.vcache + (size_t)b * a.s_pad * kHeadDim;
+            const int dv = (tile0 - 144) * 16 + ec;
+            vc[vfrag_index(key, dv)] = f2bf(x_lo);
+            vc[vfrag_index(key, dv + 16)] = f2bf(x_hi);
+          }
+        } else {
+          // GeGLU as the fused reference kernel defines it: bf16(gelu_tanh(bf16(g)) * u)
+          // (rlinf_fused_denoise.py:166-173)
+          a.out[(size_t)m * kMlp + tile0 * 16 + ec] = f2bf(fmul(gelu_tanh(round_bf(v0[i])), v1[i]));
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Residual GEMMs: o_proj (K = 2048, KSW = 8) and down_proj (K = 4096, KSW = 16); 64 workgroups,
+// one 16-column tile each, 8 waves splitting K.  With KSW <= 8 every A fragment is loaded up
+// front; with KSW = 16 the A fragments are streamed one 16-row m-tile at a time, the next m-tile
+// in flight while the current one is multiplied.
+// Epilogue: h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 503, 511) and the
+// tile's row sums of squares that the next adaRMSNorm reads.
+// ---------------------------------------------------------------------------------------------
+template <int KSW>
+__device__ __forceinline__ void load_a_tile(bf16x8 (&af)[KSW], const u16* act, int K, int row, int M, int ks0, int g) {
+#pragma unroll
+  for (int s = 0; s < KSW; ++s) af[s] = row < M ? load_frag(act + (size_t)row * K + (ks0 + s) * 32 + g * 8) : zero_frag();
+}
+
+template <int K, int KSW>
+__global__ __launch_bounds__(kGemmThreads, 1) void residual_gemm_kernel(GemmArgs a) {
+  constexpr int NT = 1;
+  static_assert(kGemmWaves * KSW * 32 == K, "waves must cover K");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int emt = tid >> 6, eg = (tid & 63) >> 4, ec = tid & 15;
+  const int nt = blockIdx.x;
+  const int ks0 = wave * KSW;
+  const int col = nt * 16 + ec;
+  const u16* tp[NT] = {a.w + (size_t)nt * (K / 32) * 512};
+
+  __shared__ float red[kGemmWaves * 4 * NT * 64 * 4];
+  bf16x8 w[NT][KSW];
+
+  for (int m0 = 0; m0 < a.M; m0 += 64) {
+    // epilogue operands first: the residual rows and the gate of this thread's column
+    u16 hold[4] = {0, 0, 0, 0};
+    float gate = 0.f;
+    if (tid < 256) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + emt * 16 + eg * 4 + i;
+        if (m < a.M) hold[i] = a.h_out[(size_t)m * kWidth + col];
+      }
+      gate = round_bf(a.mod[2 * kWidth + col]);
+    }
+    f32x4 acc[4][NT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (KSW <= 8) {
+      bf16x8 af[4][KSW];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) load_a_tile<KSW>(af[mt], a.act, K, m0 + mt * 16 + r16, a.M, ks0, g);
+      if (m0 == 0) load_weights<NT, KSW>(w, tp, ks0, lane);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt][0] = mfma16x16x32(af[mt][s], w[0][s], acc[mt][0]);
+    } else {
+      bf16x8 a0[KSW], a1[KSW];
+      load_a_tile<KSW>(a0, a.act, K, m0 + r16, a.M, ks0, g);
+      if (m0 == 0) load_weights<NT, KSW>(w, tp, ks0, lane);
+      load_a_tile<KSW>(a1, a.act, K, m0 + 16 + r16, a.M, ks0, g);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s) acc[0][0] = mfma16x16x32(a0[s], w[0][s], acc[0][0]);
+      load_a_tile<KSW>(a0, a.act, K, m0 + 32 + r16, a.M, ks0, g);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s) acc[1][0] = mfma16x16x32(a1[s], w[0][s], acc[1][0]);
+      load_a_tile<KSW>(a1, a.act, K, m0 + 48 + r16, a.M, ks0, g);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s) acc[2][0] = mfma16x16x32(a0[s], w[0][s], acc[2][0]);
+#pragma unroll
+      for (int s = 0; s < KSW; ++s) acc[3][0] = mfma16x16x32(a1[s], w[0][s], acc[3][0]);
+    }
+    store_partials<NT>(red, acc, wave, lane);
+    __syncthreads();
+    if (tid < 256) {
+      const f32x4 y4 = reduce_waves<NT>(red, emt, tid & 63, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + emt * 16 + eg * 4 + i;
+        float hn = 0.f;
+        if (m < a.M) {
+          const float prod = round_bf(fmul(round_bf(y4[i]), gate));
+          const u16 hb = f2bf(fadd(bf2f(hold[i]), prod));
+          a.h_out[(size_t)m * kWidth + col] = hb;
+          hn = bf2f(hb);
+        }
+        // the 16 columns of row m sit in 16 consecutive lanes
+        float ss = hn * hn;
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 8);
+        if (ec == 0 && m < a.M) a.rowss[(size_t)m * kRowSlots + nt] = ss;
+      }
     }
     __syncthreads();
   }
@@ -509,90 +572,115 @@ __global__ __launch_bounds__(256, 1) void gate_up_kernel(GateUpArgs a) {
 
 // =============================================================================================
 // attention
+//
+// One workgroup = 16 query rows (2 tokens x 8 heads sharing the single KV head) x one key split.
+// Its 4 waves take consecutive 32-key blocks of the split; each wave prefetches the next block's
+// K/V fragments while computing the current one.  S^T = K Q^T and O^T = V^T P^T keep every lane
+// on one query row (lane % 16): the online-softmax state and the P operand never leave the lane.
+// Splits are combined by the last workgroup to finish a row block (device-scope counter).
 // =============================================================================================
 
-// One workgroup = 16 query rows (2 tokens x 8 heads share the single KV head) x one key split;
-// the 4 waves split the split's key blocks (32 keys each) further and merge through LDS.
-// S^T = K Q^T and O^T = V^T P^T keep every lane on one query row (lane % 16), so the online
-// softmax statistics and the P operand never leave the lane.
+struct KvBlock {
+  bf16x8 k[16];
+  bf16x8 v[16];
+  uint32_t valid0, valid1;
+};
+
+__device__ __forceinline__ void load_kv_block(KvBlock& blk, const u16* kc, const u16* vc, const uint8_t* valid, int kb, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) blk.k[t * 8 + ds] = load_frag(kc + ((size_t)(2 * kb + t) * 8 + ds) * 512 + lane * 8);
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) blk.v[dt] = load_frag(vc + ((size_t)kb * 16 + dt) * 512 + lane * 8);
+  blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
+  blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
+}
+
+__device__ __forceinline__ void attend_block(const KvBlock& blk, const bf16x8 (&qf)[8], float& m_run, float& l_run, f32x4 (&oacc)[16]) {
+  f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) sacc[t] = mfma16x16x32(blk.k[t * 8 + ds], qf[ds], sacc[t]);
+  // scores: bf16(q.k) * 1/16 (exact in bf16); masked keys -> -inf (modeling_gemma.py:265-268)
+  float s[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = ((blk.valid0 >> (8 * i)) & 0xff) ? round_bf(sacc[0][i]) * 0.0625f : -INFINITY;
+    s[4 + i] = ((blk.valid1 >> (8 * i)) & 0xff) ? round_bf(sacc[1][i]) * 0.0625f : -INFINITY;
+  }
+  float bm = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  const float m_new = fmaxf(m_run, bm);
+  float alpha = 1.f;
+  float e[8];
+  if (m_new == -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = 0.f;
+  } else {
+    alpha = __expf(m_run - m_new);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = __expf(s[i] - m_new);
+  }
+  float esum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) esum += e[i];
+  l_run = l_run * alpha + esum;
+  m_run = m_new;
+  u16x8 pf;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pf[i] = f2bf(e[i]);
+  const bf16x8 pfrag = as_bf16x8(pf);
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) {
+    oacc[dt] *= alpha;
+    oacc[dt] = mfma16x16x32(blk.v[dt], pfrag, oacc[dt]);
+  }
+}
+
 __global__ __launch_bounds__(256, 1) void attention_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
-  const int rb = blockIdx.x;            // row block over B * 400 rows
+  const int rb = blockIdx.x;  // row block over B * 400 query rows
   const int split = blockIdx.y;
-  const int rows_per_sample = kHorizon * kQRowsPerTok;  // 400
-  const int b = (rb * 16) / rows_per_sample;
-  const int qrow = rb * 16 + r16;  // global query row (b*400 + tok*8 + head)
+  const int b = (rb * 16) / (kHorizon * kQRowsPerTok);
+  const int qrow = rb * 16 + r16;
 
   const u16* kc = a.kcache + (size_t)b * a.s_pad * kHeadDim;
   const u16* vc = a.vcache + (size_t)b * a.s_pad * kHeadDim;
   const uint8_t* valid = a.valid + (size_t)b * a.s_pad;
 
-  bf16x8 qf[8];
-#pragma unroll
-  for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(a.q + (size_t)qrow * kHeadDim + ds * 32 + g * 8);
-
   const int nkb = a.s_pad >> 5;
   const int kb_lo = split * nkb / a.nsplit, kb_hi = (split + 1) * nkb / a.nsplit;
   const int span = kb_hi - kb_lo;
   const int w_lo = kb_lo + wave * span / 4, w_hi = kb_lo + (wave + 1) * span / 4;
+  const int n = w_hi - w_lo;
+
+  bf16x8 qf[8];
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(a.q + (size_t)qrow * kHeadDim + ds * 32 + g * 8);
+  KvBlock ba, bb;
+  if (n > 0) load_kv_block(ba, kc, vc, valid, w_lo, lane);
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 oacc[16];
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt) oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int kb = w_lo; kb < w_hi; ++kb) {
-    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int ds = 0; ds < 8; ++ds)
-        sacc[t] = mfma16x16x32(load_frag(kc + ((size_t)(2 * kb + t) * 8 + ds) * 512 + lane * 8), qf[ds], sacc[t]);
-    // scores: bf16(q.k) * 1/16 (exact in bf16), masked keys -> -inf (modeling_gemma.py:265-268)
-    float s[8];
-    const uint32_t v0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
-    const uint32_t v1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s[i] = ((v0 >> (8 * i)) & 0xff) ? round_bf(sacc[0][i]) * 0.0625f : -INFINITY;
-      s[4 + i] = ((v1 >> (8 * i)) & 0xff) ? round_bf(sacc[1][i]) * 0.0625f : -INFINITY;
-    }
-    float bm = s[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float m_new = fmaxf(m_run, bm);
-    float alpha = 1.f;
-    float e[8];
-    if (m_new == -INFINITY) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = 0.f;
-    } else {
-      alpha = __expf(m_run - m_new);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = __expf(s[i] - m_new);
-    }
-    float esum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) esum += e[i];
-    l_run = l_run * alpha + esum;
-    m_run = m_new;
-    u16x8 pf;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pf[i] = f2bf(e[i]);
-    const bf16x8 pfrag = as_bf16x8(pf);
-#pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      oacc[dt] *= alpha;
-      oacc[dt] = mfma16x16x32(load_frag(vc + ((size_t)kb * 16 + dt) * 512 + lane * 8), pfrag, oacc[dt]);
-    }
+  for (int i = 0; i < n; i += 2) {
+    if (i + 1 < n) load_kv_block(bb, kc, vc, valid, w_lo + i + 1, lane);
+    attend_block(ba, qf, m_run, l_run, oacc);
+    if (i + 2 < n) load_kv_block(ba, kc, vc, valid, w_lo + i + 2, lane);
+    if (i + 1 < n) attend_block(bb, qf, m_run, l_run, oacc);
   }
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
 
-  // merge the 4 waves of this workgroup
+  // ---- merge the 4 waves of this workgroup
   __shared__ float s_m[4][16], s_l[4][16];
   __shared__ float s_o[4][16][kHeadDim + 4];
   if (g == 0) {
@@ -604,69 +692,79 @@ __global__ __launch_bounds__(256, 1) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) s_o[wave][r16][dt * 16 + g * 4 + i] = oacc[dt][i];
   __syncthreads();
-  const int rr = threadIdx.x >> 4;        // row 0..15
-  const int d0 = (threadIdx.x & 15) * 16;  // 16 dims per thread
-  float mw[4], ww[4];
+  const int rr = tid >> 4;           // row 0..15
+  const int d0 = (tid & 15) * 16;    // 16 dims per thread
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    mw[w] = s_m[w][rr];
-    M = fmaxf(M, mw[w]);
-  }
-  float L = 0.f;
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][rr]);
+  float ww[4], L = 0.f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    ww[w] = (mw[w] == -INFINITY) ? 0.f : __expf(mw[w] - M);
+    ww[w] = (s_m[w][rr] == -INFINITY) ? 0.f : __expf(s_m[w][rr] - M);
     L += s_l[w][rr] * ww[w];
   }
+  float o[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += s_o[w][rr][d0 + d] * ww[w];
+    o[d] = v;
+  }
   const int orow = rb * 16 + rr;
-  if (a.nsplit == 1) {
-    const float inv = 1.0f / L;
-    u16* out = a.out + (size_t)orow * kHeadDim + d0;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) o += s_o[w][rr][d0 + d] * ww[w];
-      out[d] = f2bf(o * inv);
-    }
-  } else {
+  if (a.nsplit > 1) {
     float* part = a.part + ((size_t)split * a.rows + orow) * kHeadDim + d0;
 #pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) o += s_o[w][rr][d0 + d] * ww[w];
-      part[d] = o;
-    }
-    if ((threadIdx.x & 15) == 0) {
+    for (int d = 0; d < 16; d += 4) *reinterpret_cast<float4*>(part + d) = float4{o[d], o[d + 1], o[d + 2], o[d + 3]};
+    if ((tid & 15) == 0) {
       a.part_m[(size_t)split * a.rows + orow] = M;
       a.part_l[(size_t)split * a.rows + orow] = L;
     }
+    return;
+  }
+  const float inv = 1.0f / L;
+  u16* out = a.out + (size_t)orow * kHeadDim + d0;
+#pragma unroll
+  for (int d = 0; d < 16; d += 4) {
+    u16x4 r4 = {f2bf(o[d] * inv), f2bf(o[d + 1] * inv), f2bf(o[d + 2] * inv), f2bf(o[d + 3] * inv)};
+    *reinterpret_cast<u16x4*>(out + d) = r4;
   }
 }
 
-// Combine split-KV partials: O = sum_c O_c e^{m_c - m} / sum_c l_c e^{m_c - m}.
+// Combine the split-KV partials in fixed split order:
+// O = sum_c O_c e^{m_c - m} / sum_c l_c e^{m_c - m}.  All loads are issued before any use.
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const int d0 = (threadIdx.x & 63) * 4;
+  float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
+  float4 oc[kMaxAttnSplits];
+#pragma unroll
+  for (int c = 0; c < kMaxAttnSplits; ++c) {
+    if (c < a.nsplit) {
+      mc[c] = a.part_m[(size_t)c * a.rows + row];
+      lc[c] = a.part_l[(size_t)c * a.rows + row];
+      oc[c] = *reinterpret_cast<const float4*>(a.part + ((size_t)c * a.rows + row) * kHeadDim + d0);
+    }
+  }
   float M = -INFINITY;
-  for (int c = 0; c < a.nsplit; ++c) M = fmaxf(M, a.part_m[(size_t)c * a.rows + row]);
-  float L = 0.f;
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < a.nsplit; ++c) {
-    const float mc = a.part_m[(size_t)c * a.rows + row];
-    const float wc = (mc == -INFINITY) ? 0.f : __expf(mc - M);
-    L += a.part_l[(size_t)c * a.rows + row] * wc;
-    const float4 p4 = *reinterpret_cast<const float4*>(a.part + ((size_t)c * a.rows + row) * kHeadDim + d0);
-    o[0] += p4.x * wc;
-    o[1] += p4.y * wc;
-    o[2] += p4.z * wc;
-    o[3] += p4.w * wc;
+#pragma unroll
+  for (int c = 0; c < kMaxAttnSplits; ++c)
+    if (c < a.nsplit) M = fmaxf(M, mc[c]);
+  float L = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMaxAttnSplits; ++c) {
+    if (c < a.nsplit) {
+      const float wc = (mc[c] == -INFINITY) ? 0.f : __expf(mc[c] - M);
+      L += lc[c] * wc;
+      o0 += oc[c].x * wc;
+      o1 += oc[c].y * wc;
+      o2 += oc[c].z * wc;
+      o3 += oc[c].w * wc;
+    }
   }
   const float inv = 1.0f / L;
-  u16x4 r4 = {f2bf(o[0] * inv), f2bf(o[1] * inv), f2bf(o[2] * inv), f2bf(o[3] * inv)};
+  u16x4 r4 = {f2bf(o0 * inv), f2bf(o1 * inv), f2bf(o2 * inv), f2bf(o3 * inv)};
   *reinterpret_cast<u16x4*>(a.out + (size_t)row * kHeadDim + d0) = r4;
 }
 
@@ -702,23 +800,23 @@ hipError_t launch_step_io(const StepIoArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t st) {
-  qkv_rope_kernel<<<80, 256, 0, st>>>(a);
+hipError_t launch_qkv_rope(const GemmArgs& a, hipStream_t st) {
+  norm_gemm_kernel<kModeQkv><<<80, 512, 0, st>>>(a);
   return hipGetLastError();
 }
 
-hipError_t launch_o_proj(const ResidualArgs& a, hipStream_t st) {
-  residual_gemm_kernel<kHeads * kHeadDim><<<kWidth / 16, 512, 0, st>>>(a);
+hipError_t launch_gate_up(const GemmArgs& a, hipStream_t st) {
+  norm_gemm_kernel<kModeGateUp><<<kMlp / 16, 512, 0, st>>>(a);
   return hipGetLastError();
 }
 
-hipError_t launch_down(const ResidualArgs& a, hipStream_t st) {
-  residual_gemm_kernel<kMlp><<<kWidth / 16, 512, 0, st>>>(a);
+hipError_t launch_o_proj(const GemmArgs& a, hipStream_t st) {
+  residual_gemm_kernel<kHeads * kHeadDim, 8><<<kWidth / 16, 512, 0, st>>>(a);
   return hipGetLastError();
 }
 
-hipError_t launch_gate_up(const GateUpArgs& a, hipStream_t st) {
-  gate_up_kernel<<<kMlp / 16, 256, 0, st>>>(a);
+hipError_t launch_down(const GemmArgs& a, hipStream_t st) {
+  residual_gemm_kernel<kMlp, 16><<<kWidth / 16, 512, 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "pi05_denoise",
     "pi05_release_graph",
     "pi05_launches_per_step",
+    "pi05_bench_kernel",
     "pi05_euler_schedule",
     "pi05_time_embedding",
     "pi05_rope_inv_freq",
@@ -65,8 +66,8 @@ class Pi05Dims(ctypes.Structure):
         ("num_steps", ctypes.c_int32),
         ("rms_eps", ctypes.c_float),
         ("rope_theta", ctypes.c_float),
-        ("time_min_period", ctypes.c_float),
-        ("time_max_period", ctypes.c_float),
+        ("time_min_period", ctypes.c_double),
+        ("time_max_period", ctypes.c_double),
     ]
 
 
@@ -102,6 +103,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_denoise": (i32, [vp, vp, vp, vp]),
         "pi05_release_graph": (i32, [vp]),
         "pi05_launches_per_step": (i32, [vp]),
+        "pi05_bench_kernel": (i32, [vp, i32, i32, i32, vp]),
         "pi05_euler_schedule": (i32, [i32, vp]),
         "pi05_time_embedding": (i32, [dims_p, ctypes.c_float, vp]),
         "pi05_rope_inv_freq": (i32, [dims_p, vp]),
@@ -276,6 +278,12 @@ class DenoiseContext:
 
     def release_graph(self) -> None:
         self._call(self.lib.pi05_release_graph(self.handle))
+
+    KERNELS = ("step_io", "qkv_rope", "attention", "o_proj", "gate_up", "down")
+
+    def bench_kernel(self, name: str, layer: int = 0, iters: int = 1, stream=None) -> None:
+        """Enqueue ``iters`` launches of one step kernel (profiling; clobbers activations)."""
+        self._call(self.lib.pi05_bench_kernel(self.handle, self.KERNELS.index(name), layer, iters, _stream_ptr(stream)))
 
     def launches_per_step(self) -> int:
         return int(self.lib.pi05_launches_per_step(self.handle))

@@ -1,0 +1,139 @@
+"""The C ABI library: it loads, exports every symbol include/pi05_denoise.h declares, and its
+host-only logic (validation, schedule, sinusoid, RoPE frequencies) agrees with the oracle.
+No GPU compute here: only entry points that never touch HIP are called."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import denoise_oracle as O
+from pi05_infer import _ext
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pi05_denoise.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_ext.LIB_PATH):
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("build_lib", os.path.join(ROOT, "pi05-infer_amd", "build_lib.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    return _ext.load_library()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pi05_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(_ext.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _ext.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (pi05_\w+)", out))
+    assert set(header_functions()) <= exported
+    assert lib.pi05_abi_version() == _ext.ABI_VERSION
+
+
+def test_default_dims_are_the_reference_geometry(lib):
+    d = _ext.default_dims()
+    assert (d.width, d.depth, d.num_heads, d.num_kv_heads, d.head_dim, d.mlp_dim) == (1024, 18, 8, 1, 256, 4096)
+    assert (d.action_dim, d.action_horizon, d.batch, d.prefix_len, d.num_steps) == (32, 50, 1, 968, 10)
+    assert d.rms_eps == np.float32(1e-6) and d.rope_theta == 10000.0
+    _ext.check_dims(d)
+
+
+@pytest.mark.parametrize(
+    "field,value,msg",
+    [
+        ("width", 2048, "width"),
+        ("num_heads", 16, "num_heads"),
+        ("num_kv_heads", 2, "num_kv_heads"),
+        ("head_dim", 128, "head_dim"),
+        ("mlp_dim", 8192, "mlp_dim"),
+        ("action_dim", 7, "action_dim"),
+        ("action_horizon", 10, "action_horizon"),
+        ("depth", 0, "depth"),
+        ("batch", 0, "batch"),
+        ("prefix_len", 0, "prefix_len"),
+        ("num_steps", 0, "num_steps"),
+        ("num_steps", 33, "num_steps"),
+        ("rms_eps", -1.0, "rms_eps"),
+    ],
+)
+def test_invalid_dims_rejected_with_message(lib, field, value, msg):
+    d = _ext.default_dims()
+    setattr(d, field, value)
+    with pytest.raises(_ext.Pi05Error) as ei:
+        _ext.check_dims(d)
+    assert ei.value.code == -1 and msg in str(ei.value)
+    assert _ext.device_bytes(d) == 0
+
+
+def test_device_bytes_covers_weights_and_cache(lib):
+    d = _ext.default_dims()
+    need = 622_854_144  # 18 layers of bf16 expert weights
+    need += 2 * 18 * 1024 * 256 * 2  # K and V cache (S padded to 1024)
+    need += 10 * 37 * 3072 * 4  # modulation table
+    got = _ext.device_bytes(d)
+    assert need <= got <= need + 64 * 2**20
+    d8 = _ext.default_dims()
+    d8.batch = 8
+    assert _ext.device_bytes(d8) > got
+
+
+def test_null_handles_and_pointers_are_invalid(lib):
+    vp = ctypes.c_void_p
+    assert lib.pi05_bind_layer(None, 0, *([None] * 11)) == -1
+    assert lib.pi05_bind_heads(None, *([None] * 10)) == -1
+    assert lib.pi05_refresh_weights(None, None) == -1
+    assert lib.pi05_prime_prefix(None, None, None, 0, 256, None, None) == -1
+    assert lib.pi05_denoise(None, None, None, None) == -1
+    assert lib.pi05_bench_kernel(None, 0, 0, 1, None) == -1
+    assert lib.pi05_release_graph(None) == -1
+    assert lib.pi05_ctx_destroy(None) == 0
+    assert lib.pi05_launches_per_step(None) == 0
+    assert lib.pi05_last_error(None)
+    assert lib.pi05_ctx_create(None, None) == -1
+    bad = _ext.default_dims()
+    bad.head_dim = 64
+    h = vp()
+    assert lib.pi05_ctx_create(ctypes.byref(bad), ctypes.byref(h)) == -1
+    assert b"head_dim" in lib.pi05_last_error(None)
+
+
+@pytest.mark.parametrize("n", list(range(1, 33)))
+def test_host_schedule_matches_oracle(lib, n):
+    assert torch.equal(_ext.euler_schedule(n), O.euler_timesteps(n))
+
+
+def test_schedule_rejects_bad_counts(lib):
+    with pytest.raises(_ext.Pi05Error):
+        _ext.euler_schedule(0)
+
+
+@pytest.mark.parametrize("t", [1.0, 0.9, 0.5, 0.1, 0.0, 0.3333333432674408])
+def test_host_time_embedding_matches_oracle(lib, t):
+    got = _ext.time_embedding(_ext.default_dims(), t)
+    ref = O.sinusoidal_time_embedding(torch.tensor([t], dtype=torch.float32), 1024, 4e-3, 4.0)[0]
+    assert torch.max((got - ref).abs()).item() <= 1.2e-7
+
+
+def test_host_rope_inv_freq_matches_oracle(lib):
+    got = _ext.rope_inv_freq(_ext.default_dims())
+    ref = O.rope_inv_freq(256, 10000.0)
+    assert torch.max((got - ref).abs() / ref).item() <= 1.2e-7

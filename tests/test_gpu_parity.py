@@ -1,0 +1,180 @@
+"""GPU parity of the gfx950 denoise engine against the CPU oracle, through the C ABI.
+
+Tolerance (the path is bf16 on the GPU, fp32 with bf16 rounding points in the oracle): for every
+per-step velocity and for the final actions, cosine similarity >= 0.9999 and max-abs error
+<= 2e-2 of the oracle's range of that tensor.  Integer work (positions, masks) is checked
+bit-exactly through its effect: ragged prefix padding must match the oracle's masked result.
+"""
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+from oracle import denoise_oracle as O
+from pi05_infer import synthetic as S
+from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+REL_MAXABS = 2e-2
+
+
+def _close(ref: torch.Tensor, got: torch.Tensor, what: str) -> None:
+    ref = ref.double().flatten().cpu()
+    got = got.double().flatten().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    cos = torch.nn.functional.cosine_similarity(ref, got, dim=0).item()
+    maxabs = (ref - got).abs().max().item()
+    rng = (ref.max() - ref.min()).item()
+    print(f"{what}: cos={cos:.7f} maxabs={maxabs:.3e} range={rng:.3f}", flush=True)
+    assert cos >= COS_MIN, f"{what}: cosine {cos} < {COS_MIN}"
+    assert maxabs <= REL_MAXABS * rng, f"{what}: max-abs {maxabs} > {REL_MAXABS} * range {rng}"
+
+
+@pytest.fixture(scope="module")
+def full_weights():
+    return S.make_weights(S.ExpertGeometry())
+
+
+def _run_case(weights, depth=18, P=968, B=1, steps=10, pad_fn=None, zero_gate=False):
+    g = replace(S.ExpertGeometry(), depth=depth)
+    w = {k: v for k, v in weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < depth}
+    if zero_gate:
+        w = S.zero_gate_weights(w, g)
+    k, v = S.make_prefix_kv(g, P, B)
+    x1 = S.make_noise(g, B)
+    pad = S.full_prefix_pad(P, B)
+    if pad_fn is not None:
+        pad_fn(pad)
+    og = O.geometry_from(g)
+    table = O.adarms_table(w, og, steps)
+    act_ref, vs_ref = O.sample_actions(w, og, k, v, pad, x1, steps, table)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    obs = Observation(k.cuda(), v.cuda(), pad.cuda())
+    act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
+    torch.cuda.synchronize()
+    return model, obs, x1, table, (act_ref, vs_ref), (act, vs)
+
+
+def _check(name, ref, got, steps):
+    (act_ref, vs_ref), (act, vs) = ref, got
+    for s in range(steps):
+        _close(vs_ref[s], vs[s], f"{name} step {s} velocity")
+    _close(act_ref, act, f"{name} actions")
+
+
+def test_c1_full_parity_and_table(full_weights):
+    print("case C1: depth 18, B=1, P=968, 10 steps", flush=True)
+    model, obs, x1, table, ref, got = _run_case(full_weights)
+    _check("C1", ref, got, 10)
+    ctx = next(iter(model._contexts.values()))
+    tab = ctx.adarms_table().cpu()
+    torch.testing.assert_close(tab, table, rtol=1e-5, atol=1e-5)
+    # graph replay is deterministic and does not drift between predicts
+    again = model.sample_actions(obs, x1.cuda())["actions"]
+    assert torch.equal(again, got[0])
+    model.close()
+
+
+def test_c2_short_prefix(full_weights):
+    print("case C2: depth 18, B=1, P=456", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, P=456)
+    _check("C2", ref, got, 10)
+    model.close()
+
+
+def test_c4_long_prefix(full_weights):
+    print("case C4: depth 18, B=1, P=3272", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, P=3272)
+    _check("C4", ref, got, 10)
+    model.close()
+
+
+def test_c3_batch8(full_weights):
+    print("case C3: depth 18, B=8, P=968 (M = 400 rows per GEMM)", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, B=8)
+    _check("C3", ref, got, 10)
+    model.close()
+
+
+def test_ragged_prefix_padding(full_weights):
+    print("case ragged: depth 4, B=3, P=300, padded tails", flush=True)
+
+    def pad_fn(pad):
+        pad[0, 280:] = False
+        pad[1, 100:] = False
+        pad[2, 5:17] = False
+
+    model, _, _, _, ref, got = _run_case(full_weights, depth=4, P=300, B=3, steps=3, pad_fn=pad_fn)
+    _check("ragged", ref, got, 3)
+    model.close()
+
+
+def test_tiny_prefix_and_odd_steps(full_weights):
+    print("case tiny: depth 2, B=1, P=1, 7 steps", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, depth=2, P=1, steps=7)
+    _check("tiny", ref, got, 7)
+    model.close()
+
+
+def test_zero_gates_identity_layers(full_weights):
+    print("case zero-gate: depth 3, P=64", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, depth=3, P=64, steps=2, zero_gate=True)
+    _check("zero-gate", ref, got, 2)
+    model.close()
+
+
+def test_weight_refresh_in_place(full_weights):
+    print("case refresh: depth 2, P=128, weights updated in place", flush=True)
+    g = replace(S.ExpertGeometry(), depth=2)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 2}
+    k, v = S.make_prefix_kv(g, 128)
+    x1 = S.make_noise(g)
+    pad = S.full_prefix_pad(128)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=3), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    obs = Observation(k.cuda(), v.cuda(), pad.cuda())
+    first = model.sample_actions(obs, x1.cuda())["actions"].clone()
+    # RL-style weight sync: scale one layer's down_proj and the time MLP in place
+    name = S.layer_param_names(1)["wdown"]
+    model.params[name].mul_(1.5)
+    model.params["time_mlp_out.weight"].mul_(0.5)
+    model.invalidate_weight_derived_caches()
+    second = model.sample_actions(obs, x1.cuda())["actions"]
+    w2 = dict(w)
+    w2[name] = (w[name].float() * 1.5).to(torch.bfloat16)
+    w2["time_mlp_out.weight"] = w["time_mlp_out.weight"] * 0.5
+    og = O.geometry_from(g)
+    ref, _ = O.sample_actions(w2, og, k, v, pad, x1, 3)
+    assert not torch.equal(first, second)
+    _close(ref, second, "refresh actions")
+    model.close()
+
+
+def test_bad_prefix_shapes_rejected(full_weights):
+    from pi05_infer import _ext
+
+    g = replace(S.ExpertGeometry(), depth=2)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 2}
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=2), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    k, v = S.make_prefix_kv(g, 32)
+    pad = S.full_prefix_pad(32).cuda()
+    ctx = model._context(1, 32, 2)
+    with pytest.raises(ValueError):
+        ctx.prime_prefix([k[:, i : i + 1, :16].cuda() for i in range(2)], [v[:, i : i + 1].cuda() for i in range(2)], pad)
+    with pytest.raises(ValueError):
+        ctx.prime_prefix([k[:, i : i + 1].cuda() for i in range(1)], [v[:, i : i + 1].cuda() for i in range(1)], pad)
+    with pytest.raises(ValueError):
+        ctx.denoise(torch.zeros(1, 50, 16, device="cuda"))
+    bad = _ext.make_dims(g, 1, 32, 2)
+    bad.head_dim = 128
+    with pytest.raises(_ext.Pi05Error):
+        _ext.check_dims(bad)
+    model.close()

@@ -1,0 +1,128 @@
+"""Host-side logic that runs without a GPU: the builder, the engine's Python surface, the dtype
+policy and the synthetic-input recipe."""
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+from pi05_infer import synthetic as S
+from pi05_infer.builder import build_model, get_model
+from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+
+SMALL = replace(S.ExpertGeometry(), width=64, depth=2, head_dim=16, mlp_dim=128)
+
+
+def test_build_model_random_init_and_dtype_policy():
+    m = build_model("random:0", "pi05_libero", geometry=SMALL, num_steps=4)
+    assert m.config.num_steps == 4 and m.config.config_name == "pi05_libero"
+    for name, t in m.state_dict().items():
+        is_expert_linear = any(k in name for k in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"))
+        assert t.dtype == (torch.bfloat16 if is_expert_linear else torch.float32), name
+    assert len(m.state_dict()) == len(S.parameter_specs(SMALL))
+
+
+@pytest.mark.parametrize(
+    "args,exc",
+    [
+        (("random", "pi0_libero"), NotImplementedError),
+        (("random", "no_such_config"), ValueError),
+    ],
+)
+def test_build_model_rejects_unsupported_configs(args, exc):
+    with pytest.raises(exc):
+        build_model(*args, geometry=SMALL)
+
+
+def test_build_model_rejects_unknown_overrides():
+    with pytest.raises(TypeError):
+        build_model("random", "pi05_libero", geometry=SMALL, no_such_field=1)
+
+
+def test_get_model_shim():
+    class Cfg:
+        model_path = "random:3"
+        openpi = {"config_name": "pi05_turtle", "num_steps": 5}
+        openpi_data = None
+
+    m = get_model(Cfg())
+    assert m.config.config_name == "pi05_turtle" and m.config.num_steps == 5
+
+
+def test_checkpoint_roundtrip_safetensors(tmp_path):
+    import safetensors.torch
+
+    w = S.make_weights(SMALL, seed=5)
+    safetensors.torch.save_file({k: v.contiguous() for k, v in w.items()}, str(tmp_path / "model.safetensors"))
+    m = build_model(str(tmp_path), "pi05_libero", geometry=SMALL)
+    for k, v in w.items():
+        assert torch.equal(m.state_dict()[k], v)
+
+
+def test_checkpoint_full_weights_pt(tmp_path):
+    w = S.make_weights(SMALL, seed=6)
+    d = tmp_path / "model_state_dict"
+    d.mkdir()
+    torch.save(w, str(d / "full_weights.pt"))
+    m = build_model(str(tmp_path), "pi05_libero", geometry=SMALL)
+    assert torch.equal(m.state_dict()["action_in_proj.weight"], w["action_in_proj.weight"])
+
+
+def test_load_state_dict_checks_shapes_and_reports_missing():
+    m = OpenPi0Inference(OpenPi0InferConfig(), SMALL)
+    w = S.make_weights(SMALL)
+    bad = dict(w)
+    bad["action_in_proj.weight"] = torch.zeros(3, 3)
+    with pytest.raises(ValueError):
+        m.load_state_dict(bad)
+    part = {k: v for k, v in w.items() if "layers.1." not in k}
+    missing, unexpected = m.load_state_dict({**part, "extra.tensor": torch.zeros(1)})
+    assert missing and all("layers.1." in n for n in missing) and unexpected == ["extra.tensor"]
+    with pytest.raises(KeyError):
+        m.load_state_dict(part, strict=True)
+
+
+def test_engine_requires_gpu_and_pi05():
+    with pytest.raises(NotImplementedError):
+        OpenPi0Inference(OpenPi0InferConfig(pi05=False), SMALL)
+    m = build_model("random", "pi05_libero", geometry=SMALL)
+    k, v = S.make_prefix_kv(SMALL, 8)
+    obs = Observation(k, v, S.full_prefix_pad(8))
+    with pytest.raises(RuntimeError, match="gfx950"):
+        m.sample_actions(obs, S.make_noise(SMALL))
+
+
+def test_observation_from_dynamic_cache_dict():
+    k, v = S.make_prefix_kv(SMALL, 8)
+    kv = [(k[:, i : i + 1], v[:, i : i + 1]) for i in range(SMALL.depth)]
+    obs = Observation.from_dict({"past_key_values": kv, "prefix_pad_masks": S.full_prefix_pad(8)})
+    assert len(obs.prefix_k) == SMALL.depth and torch.equal(obs.prefix_v[1], v[:, 1:2])
+
+
+def test_compat_shims():
+    m = build_model("random", "pi05_libero", geometry=SMALL)
+    assert not m.is_cuda_graph_enabled()
+    m.capture_cuda_graph(train_batch_size=1, eval_batch_size=1)
+    assert m.is_cuda_graph_enabled()
+    m.release_cuda_graph()
+    assert not m.is_cuda_graph_enabled()
+    m.enable_torch_compile("max-autotune")
+    assert m.torch_compile_enabled
+    out = m.output_transform({"actions": torch.zeros(2, 50, 32)})
+    assert out["actions"].shape == (2, m.config.action_chunk, 32)
+
+
+def test_synthetic_recipe_is_deterministic_and_depth_independent():
+    a = S.make_weights(SMALL, seed=0)
+    b = S.make_weights(replace(SMALL, depth=1), seed=0)
+    n0 = S.layer_param_names(0)["wq"]
+    assert torch.equal(a[n0], b[n0])
+    assert torch.equal(a["action_in_proj.weight"], b["action_in_proj.weight"])
+    c = S.make_weights(SMALL, seed=1)
+    assert not torch.equal(a[n0], c[n0])
+    x = S.make_noise(SMALL, batch=3)
+    assert torch.equal(x[1], S.make_noise(SMALL, batch=1, seed=3)[0])
+    k1, _ = S.make_prefix_kv(SMALL, 16, batch=2)
+    assert k1.dtype == torch.bfloat16 and k1.shape == (2, SMALL.depth, 16, SMALL.head_dim)
+    std = a[n0].float().std().item()
+    assert 0.018 < std < 0.022
