@@ -2,8 +2,8 @@
  * pi05_denoise.h -- C ABI of the MI355X (gfx950) pi0.5 action-expert denoise engine.
  *
  * One context (`pi05_ctx`) owns everything one shape signature needs: packed bf16 expert weights,
- * the adaRMS modulation table, the re-laid-out static KV cache, activation buffers and the hipGraph
- * that replays the whole num_steps Euler loop.  The signature is (batch, prefix_len, num_steps);
+ * the adaRMS modulation table, the re-laid-out static KV cache and the activation buffers of the
+ * whole num_steps Euler loop.  The signature is (batch, prefix_len, num_steps);
  * a different signature needs a different context (the reference captures its graph per
  * signature as well: engine.py:884-906).
  *
@@ -134,9 +134,11 @@ int pi05_prime_prefix(pi05_ctx* ctx, const void* const* k_layers, const void* co
                       int64_t kv_batch_stride, int64_t kv_row_stride, const uint8_t* prefix_pad,
                       void* stream);
 
-/* Run the full num_steps Euler denoise loop (captured once as a hipGraph and replayed):
- * x_inout [B, A, a] fp32 holds the initial noise x_1 on entry and the actions x_0 on exit.
- * v_trace (nullable) [num_steps, B, A, a] fp32 receives each step's velocity.
+/* Run the full num_steps Euler denoise loop (one cooperative kernel, or a hipGraph replay in the
+ * graph schedule): x_inout [B, A, a] fp32 holds the initial noise x_1 on entry and the actions
+ * x_0 on exit.  v_trace (nullable) [num_steps, B, A, a] fp32 receives each step's velocity.
+ * The persistent schedule returns after the kernel has finished (it synchronises `stream` to
+ * report a kernel-side timeout as PI05_E_HIP); the graph schedule only enqueues.
  * Replaces sample_actions' denoise loop (engine.py:389-405) with sample_mean_var_val /
  * get_velocity / the expert forward (engine.py:629-768, modeling_gemma.py:662-794). */
 int pi05_denoise(pi05_ctx* ctx, float* x_inout, float* v_trace, void* stream);
@@ -145,15 +147,37 @@ int pi05_denoise(pi05_ctx* ctx, float* x_inout, float* v_trace, void* stream);
  * release_cuda_graph (_vendored/base_policy.py:96-102). */
 int pi05_release_graph(pi05_ctx* ctx);
 
-/* Number of kernel launches in one denoise step (for profiling). */
+/* Execution schedules of pi05_denoise.
+ *  PI05_SCHEDULE_PERSISTENT (default where the device supports cooperative launch): the whole
+ *    Euler loop is ONE cooperative kernel, one workgroup per compute unit, whose phases hand
+ *    activations to each other through device memory and per-phase flags.
+ *  PI05_SCHEDULE_GRAPH: one hipGraph of 1 + depth * 5..6 kernels per Euler step.
+ * Both compute the same function with the same rounding points.  The reference runs its loop
+ * eagerly or replays one captured flow_ode step per Euler step as a CUDA graph
+ * (engine.py:831-860, 908-960); PI05_SCHEDULE_GRAPH is the counterpart of that graph, the
+ * persistent kernel has no counterpart in the reference. */
+#define PI05_SCHEDULE_PERSISTENT 0
+#define PI05_SCHEDULE_GRAPH 1
+
+/* Switch a context's schedule.  Frees the previous schedule's activation buffers, so the prefix
+ * must be primed again (pi05_prime_prefix) before the next pi05_denoise; weights stay bound and
+ * packed.  Synchronises the device.  No counterpart in the reference (see above). */
+int pi05_set_schedule(pi05_ctx* ctx, int schedule);
+
+/* Current schedule of `ctx` (PI05_SCHEDULE_*), or PI05_E_INVALID for NULL. */
+int pi05_get_schedule(const pi05_ctx* ctx);
+
+/* Number of kernel launches in one denoise step (for profiling): 1 + depth * 5..6 in the graph
+ * schedule, 0 in the persistent schedule (one launch per pi05_denoise). */
 int pi05_launches_per_step(const pi05_ctx* ctx);
 
 /* Profiling hook: enqueue `iters` back-to-back launches of one kernel of the denoise step with the
  * arguments the graph uses for Euler step 0 and decoder layer `layer`, on `stream`.  kernel_id:
  * 0 step boundary (final norm + action_out_proj + Euler + action_in_proj), 1 qkv_rope,
- * 2 attention, 3 o_proj, 4 gate_up, 5 down_proj.  It overwrites the context's activations, so
- * call pi05_denoise again afterwards for a meaningful result.  No counterpart in the reference
- * (its tools/ time kernels from nsys traces); it lets a benchmark time one kernel with events. */
+ * 2 attention, 3 o_proj, 4 gate_up, 5 down_proj.  Graph schedule only (PI05_E_STATE otherwise).
+ * It overwrites the context's activations, so call pi05_denoise again afterwards for a
+ * meaningful result.  No counterpart in the reference (its tools/ time kernels from nsys
+ * traces); it lets a benchmark time one kernel with events. */
 int pi05_bench_kernel(pi05_ctx* ctx, int kernel_id, int layer, int iters, void* stream);
 
 /* ---- host-only helpers (no GPU needed; what the context computes on the host) ---- */

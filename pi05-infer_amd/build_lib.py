@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
-SOURCES = ["pi05_kernels.hip", "pi05_engine.hip"]
+SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

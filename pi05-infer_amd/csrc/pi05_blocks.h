@@ -1,0 +1,118 @@
+// Device building blocks shared by the denoise kernels: MFMA weight-fragment streaming, the
+// cross-wave reduction, GeGLU, and one 32-key block of the MQA online-softmax attention.
+#pragma once
+
+#include "pi05_device.h"
+
+namespace pi05 {
+
+enum GemmMode { kModeQkv = 0, kModeGateUp = 1 };
+
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = kGemmWaves * 64;
+
+template <int NT, int KSW>
+__device__ __forceinline__ void load_weights(bf16x8 (&w)[NT][KSW], const u16* const (&tile)[NT], int ks0, int lane) {
+#pragma unroll
+  for (int s = 0; s < KSW; ++s)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u16x8* p = reinterpret_cast<const u16x8*>(tile[t] + (size_t)(ks0 + s) * 512 + lane * 8);
+      w[t][s] = as_bf16x8(__builtin_nontemporal_load(p));
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void store_partials(float* red, const f32x4 (&acc)[4][NT], int wave, int lane) {
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      *reinterpret_cast<f32x4*>(red + ((((size_t)wave * 4 + mt) * NT + t) * 64 + lane) * 4) = acc[mt][t];
+}
+
+// Sum over the 8 waves, in wave order, of the D fragment (m-tile mt, lane) of tile t.
+template <int NT>
+__device__ __forceinline__ f32x4 reduce_waves(const float* red, int mt, int lane, int t) {
+  f32x4 v = *reinterpret_cast<const f32x4*>(red + (((size_t)mt * NT + t) * 64 + lane) * 4);
+#pragma unroll
+  for (int w = 1; w < kGemmWaves; ++w) v += *reinterpret_cast<const f32x4*>(red + ((((size_t)w * 4 + mt) * NT + t) * 64 + lane) * 4);
+  return v;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // GELU tanh approximation in the fused reference kernel's op order (rlinf_fused_denoise.py:168-173)
+  const float t3 = fmul(x, 0.5f);
+  const float t5 = fmul(fmul(x, x), x);
+  const float t8 = fadd(x, fmul(t5, 0.044715f));
+  const float t11 = tanhf(fmul(t8, 0.7978845608028654f));
+  return fmul(t3, fadd(t11, 1.0f));
+}
+
+// One 32-key block of K/V fragments (prefetched as a unit) and its key-valid bytes.
+struct KvBlock {
+  bf16x8 k[16];
+  bf16x8 v[16];
+  uint32_t valid0, valid1;
+};
+
+// kc / vc: fragment-major K / V of the block's key range, kb: block index within it;
+// valid: the 32 key-valid bytes of this block.
+__device__ __forceinline__ void load_kv_block(KvBlock& blk, const u16* kc, const u16* vc, const uint8_t* valid, int kb, int lane) {
+  const int g = lane >> 4;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) blk.k[t * 8 + ds] = load_frag(kc + ((size_t)(2 * kb + t) * 8 + ds) * 512 + lane * 8);
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) blk.v[dt] = load_frag(vc + ((size_t)kb * 16 + dt) * 512 + lane * 8);
+  blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + g * 4);
+  blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + 16 + g * 4);
+}
+
+__device__ __forceinline__ void attend_block(const KvBlock& blk, const bf16x8 (&qf)[8], float& m_run, float& l_run, f32x4 (&oacc)[16]) {
+  f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) sacc[t] = mfma16x16x32(blk.k[t * 8 + ds], qf[ds], sacc[t]);
+  // scores: bf16(q.k) * 1/16 (exact in bf16); masked keys -> -inf (modeling_gemma.py:265-268)
+  float s[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = ((blk.valid0 >> (8 * i)) & 0xff) ? round_bf(sacc[0][i]) * 0.0625f : -INFINITY;
+    s[4 + i] = ((blk.valid1 >> (8 * i)) & 0xff) ? round_bf(sacc[1][i]) * 0.0625f : -INFINITY;
+  }
+  float bm = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  const float m_new = fmaxf(m_run, bm);
+  float alpha = 1.f;
+  float e[8];
+  if (m_new == -INFINITY) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = 0.f;
+  } else {
+    alpha = __expf(m_run - m_new);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = __expf(s[i] - m_new);
+  }
+  float esum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) esum += e[i];
+  l_run = l_run * alpha + esum;
+  m_run = m_new;
+  u16x8 pf;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) pf[i] = f2bf(e[i]);
+  const bf16x8 pfrag = as_bf16x8(pf);
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) {
+    oacc[dt] *= alpha;
+    oacc[dt] = mfma16x16x32(blk.v[dt], pfrag, oacc[dt]);
+  }
+}
+
+}  // namespace pi05

@@ -55,45 +55,61 @@ struct HeadBind {
   bool set = false;
 };
 
-// Device buffer plan of one signature (sizes in bytes).
+// Device buffer plan of one signature (sizes in bytes).  "Common" buffers exist in both
+// schedules; the graph schedule keeps one activation set that every kernel overwrites, the
+// persistent schedule slices its activations per (Euler step, layer) so that no buffer is read
+// before it is written within one launch.
 struct Plan {
   int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1, mgroups = 1;
-  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, kv = 0, valid = 0, rope = 0, pos = 0;
-  size_t h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0, ptrs = 0, invf = 0;
-  size_t total() const {
-    return wpack + table + temb + 2 * cond + heads + 2 * kv + valid + 2 * rope + pos + h + rowss + q + o + act + part +
-           2 * partml + x + trace + ptrs + invf;
+  // common
+  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, rope = 0, pos = 0, ptrs = 0, invf = 0;
+  // graph schedule
+  size_t kv = 0, valid = 0, h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0;
+  // persistent schedule
+  int s_pre = 0, nsplit_p = 1, nrb = 0, mp = 0, flag_stride = 0;
+  size_t p_kv = 0, p_valid = 0, p_h = 0, p_rowss = 0, p_hmid = 0, p_rowss_mid = 0, p_q = 0, p_suf = 0, p_act = 0;
+  size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_ctr = 0, p_euler = 0;
+  size_t common() const { return wpack + table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf; }
+  size_t graph_bytes() const { return 2 * kv + valid + h + rowss + q + o + act + part + 2 * partml + x + trace; }
+  size_t persistent_bytes() const {
+    return 2 * p_kv + p_valid + p_h + p_rowss + p_hmid + p_rowss_mid + 2 * p_q + 2 * p_suf + p_act + p_apart + 2 * p_apartml +
+           p_dpart + p_x + p_flags + p_ctr + p_euler + 256;
   }
 };
 
-// Split-KV factor: one 32-key block per wave (4 per workgroup) up to kMaxAttnSplits splits;
-// longer prefixes give each wave several blocks instead.
+// Split-KV factor of the graph schedule: one 32-key block per wave (4 per workgroup), at most 8
+// splits; longer prefixes give each wave several blocks instead.
 int choose_nsplit(int s_pad) {
   const int nkb = s_pad / 32;
   int ns = (nkb + 3) / 4;
   if (ns < 1) ns = 1;
-  if (ns > kMaxAttnSplits) ns = kMaxAttnSplits;
+  if (ns > 8) ns = 8;
   return ns;
 }
 
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 Plan make_plan(const pi05_dims& d) {
   Plan p;
+  const size_t L = d.depth, T = d.num_steps;
   p.M = d.batch * kHorizon;
   p.S = d.prefix_len + kHorizon;
   p.s_pad = (p.S + 31) / 32 * 32;
   p.n_norms = 2 * d.depth + 1;
   p.rows = p.M * kHeads;
   p.nsplit = choose_nsplit(p.s_pad);
-  p.wpack = (size_t)d.depth * kLayerElems * 2;
-  p.table = (size_t)d.num_steps * p.n_norms * kModW * 4;
-  p.temb = (size_t)d.num_steps * kWidth * 4;
-  p.cond = (size_t)d.num_steps * kWidth * 4;
+  p.wpack = L * kLayerElems * 2;
+  p.table = T * p.n_norms * kModW * 4;
+  p.temb = T * kWidth * 4;
+  p.cond = T * kWidth * 4;
   p.heads = ((size_t)kWidth * kActDim * 2 + kWidth + kActDim) * 4;
-  p.kv = (size_t)d.depth * d.batch * p.s_pad * kHeadDim * 2;
-  p.valid = (size_t)d.batch * p.s_pad;
   p.rope = (size_t)p.M * kHeadDim * 2;
   p.pos = (size_t)p.M * 4;
+  p.ptrs = 2 * L * sizeof(void*);
+  p.invf = (size_t)kHalfDim * 4;
+
+  p.kv = L * d.batch * p.s_pad * kHeadDim * 2;
+  p.valid = (size_t)d.batch * p.s_pad;
   p.h = (size_t)p.M * kWidth * 2;
   p.rowss = (size_t)kRowSlots * p.M * 4;
   p.q = (size_t)p.M * kHeads * kHeadDim * 2;
@@ -103,9 +119,33 @@ Plan make_plan(const pi05_dims& d) {
   p.partml = p.nsplit > 1 ? (size_t)p.nsplit * p.rows * 4 : 0;
   p.mgroups = (p.M + 63) / 64;
   p.x = (size_t)p.M * kActDim * 4;
-  p.trace = (size_t)d.num_steps * p.M * kActDim * 4;
-  p.ptrs = (size_t)2 * d.depth * sizeof(void*);
-  p.invf = (size_t)kHalfDim * 4;
+  p.trace = T * p.M * kActDim * 4;
+
+  // persistent: prefix keys padded to a 32-key boundary, then one 64-key block of action keys;
+  // split count such that every wave normally owns one 32-key block
+  p.s_pre = (d.prefix_len + 31) / 32 * 32;
+  const int nkb = p.s_pre / 32 + 2;
+  p.nsplit_p = (nkb + 3) / 4;
+  if (p.nsplit_p > kMaxAttnSplits) p.nsplit_p = kMaxAttnSplits;
+  p.nrb = p.rows / 16;
+  p.mp = (p.M + 63) / 64 * 64;
+  p.flag_stride = (int)round_up(p.M > 256 ? p.M : 256, 64);
+  p.p_kv = L * d.batch * p.s_pre * kHeadDim * 2;
+  p.p_valid = round_up((size_t)d.batch * (p.s_pre + 64), 256);
+  p.p_h = T * (L + 1) * p.M * kWidth * 2;
+  p.p_rowss = T * (L + 1) * p.M * kRowSlots * 4;
+  p.p_hmid = T * L * p.M * kWidth * 2;
+  p.p_rowss_mid = T * L * p.M * kRowSlots * 4;
+  p.p_q = T * L * p.M * kHeads * kHeadDim * 2;
+  p.p_suf = T * L * d.batch * 64 * kHeadDim * 2;
+  p.p_act = T * L * p.M * kMlp * 2;
+  p.p_apart = (size_t)p.nsplit_p * p.rows * kHeadDim * 4;
+  p.p_apartml = round_up((size_t)p.nsplit_p * p.rows * 4, 256);
+  p.p_dpart = (size_t)4 * (kWidth / 16) * p.mp * 16 * 4;
+  p.p_x = round_up(T * p.M * kActDim * 4, 256);
+  p.p_flags = (T + 1) * (L + 1) * 6 * p.flag_stride * 4;
+  p.p_ctr = round_up(T * L * (p.nrb + kWidth / 16) * 4, 256);
+  p.p_euler = round_up(T * 4 * 4, 256);
   return p;
 }
 
@@ -194,23 +234,30 @@ struct pi05_ctx {
   pi05_dims d{};
   Plan plan;
   int device = -1;
+  int schedule = PI05_SCHEDULE_PERSISTENT;
+  int grid = 0;  // persistent schedule: one workgroup per compute unit
   std::vector<LayerBind> layers;
   HeadBind heads;
   std::vector<float> ts;
   std::vector<const void*> kv_host_ptrs;
 
+  // common
   u16* wpack = nullptr;
   float* table = nullptr;
   float* temb = nullptr;
   float* cond1 = nullptr;
   float* cond = nullptr;
   float* heads_buf = nullptr;  // in_w [W,a] | out_w [a,W] | in_b [W] | out_b [a]
-  u16* kcache = nullptr;
-  u16* vcache = nullptr;
-  uint8_t* valid = nullptr;
   u16* cos_tab = nullptr;
   u16* sin_tab = nullptr;
   int32_t* positions = nullptr;
+  const void** kv_ptrs = nullptr;
+  float* inv_freq = nullptr;
+
+  // graph schedule
+  u16* kcache = nullptr;
+  u16* vcache = nullptr;
+  uint8_t* valid = nullptr;
   u16* h = nullptr;
   float* rowss = nullptr;
   u16* q = nullptr;
@@ -221,11 +268,15 @@ struct pi05_ctx {
   float* part_l = nullptr;
   float* x = nullptr;
   float* trace = nullptr;
-  const void** kv_ptrs = nullptr;
-  float* inv_freq = nullptr;
-
   hipStream_t cap = nullptr;
   hipGraphExec_t exec[2] = {nullptr, nullptr};
+
+  // persistent schedule
+  char* pbase = nullptr;  // one allocation, carved by carve_persistent()
+  MegaArgs mega{};
+  unsigned epoch = 0;
+  unsigned* host_err = nullptr;  // pinned host word the kernel sets on a timed-out wait
+
   bool weights_ready = false;
   bool primed = false;
   std::string err;
@@ -257,17 +308,33 @@ float* heads_out_w(pi05_ctx* c) { return c->heads_buf + (size_t)kWidth * kActDim
 float* heads_in_b(pi05_ctx* c) { return c->heads_buf + (size_t)kWidth * kActDim * 2; }
 float* heads_out_b(pi05_ctx* c) { return heads_in_b(c) + kWidth; }
 
-void free_all(pi05_ctx* c) {
+void free_schedule(pi05_ctx* c) {
   for (auto& e : c->exec)
     if (e) {
       (void)hipGraphExecDestroy(e);
       e = nullptr;
     }
-  void* bufs[] = {c->wpack, c->table, c->temb, c->cond1, c->cond, c->heads_buf, c->kcache, c->vcache, c->valid,
-                  c->cos_tab, c->sin_tab, c->positions, c->h, c->rowss, c->q, c->o, c->act, c->part, c->part_m,
-                  c->part_l, c->x, c->trace, (void*)c->kv_ptrs, c->inv_freq};
+  void** bufs[] = {(void**)&c->kcache, (void**)&c->vcache, (void**)&c->valid, (void**)&c->h, (void**)&c->rowss,
+                   (void**)&c->q, (void**)&c->o, (void**)&c->act, (void**)&c->part, (void**)&c->part_m,
+                   (void**)&c->part_l, (void**)&c->x, (void**)&c->trace, (void**)&c->pbase};
+  for (void** p : bufs)
+    if (*p) {
+      (void)hipFree(*p);
+      *p = nullptr;
+    }
+  c->mega = MegaArgs{};
+  c->epoch = 0;
+  c->primed = false;
+}
+
+void free_all(pi05_ctx* c) {
+  free_schedule(c);
+  void* bufs[] = {c->wpack, c->table, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
+                  c->positions, (void*)c->kv_ptrs, c->inv_freq};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
+  if (c->host_err) (void)hipHostFree(c->host_err);
+  c->host_err = nullptr;
   if (c->cap) (void)hipStreamDestroy(c->cap);
   c->cap = nullptr;
 }
@@ -283,6 +350,114 @@ hipError_t dalloc(T** p, size_t bytes) {
   if (e != hipSuccess) return e;
   e = hipMemset(v, 0, bytes);
   *p = reinterpret_cast<T*>(v);
+  return e;
+}
+
+// Slice the persistent schedule's single allocation (every slice 256-byte aligned) and fill the
+// launch-invariant part of the kernel arguments.
+void carve_persistent(pi05_ctx* c) {
+  const Plan& p = c->plan;
+  const pi05_dims& d = c->d;
+  char* cur = c->pbase;
+  auto take = [&cur](size_t bytes) {
+    char* r = cur;
+    cur += round_up(bytes, 256);
+    return r;
+  };
+  MegaArgs& a = c->mega;
+  a = MegaArgs{};
+  a.err = reinterpret_cast<unsigned*>(take(256));
+  a.flags = reinterpret_cast<unsigned*>(take(p.p_flags));
+  a.counters = reinterpret_cast<unsigned*>(take(p.p_ctr));
+  a.ctr_down_off = (size_t)d.num_steps * d.depth * p.nrb;
+  a.flag_stride = p.flag_stride;
+  a.depth = d.depth;
+  a.steps = d.num_steps;
+  a.M = p.M;
+  a.batch = d.batch;
+  a.mp = p.mp;
+  a.nsplit = p.nsplit_p;
+  a.s_pre = p.s_pre;
+  a.eps = d.rms_eps;
+  a.table = c->table;
+  a.euler = reinterpret_cast<float*>(take(p.p_euler));
+  a.in_w = heads_in_w(c);
+  a.out_w = heads_out_w(c);
+  a.in_b = heads_in_b(c);
+  a.out_b = heads_out_b(c);
+  a.wpack = c->wpack;
+  a.cos_tab = c->cos_tab;
+  a.sin_tab = c->sin_tab;
+  a.kpre = reinterpret_cast<u16*>(take(p.p_kv));
+  a.vpre = reinterpret_cast<u16*>(take(p.p_kv));
+  a.valid = reinterpret_cast<uint8_t*>(take(p.p_valid));
+  a.h = reinterpret_cast<u16*>(take(p.p_h));
+  a.rowss = reinterpret_cast<float*>(take(p.p_rowss));
+  a.hmid = reinterpret_cast<u16*>(take(p.p_hmid));
+  a.rowss_mid = reinterpret_cast<float*>(take(p.p_rowss_mid));
+  a.q = reinterpret_cast<u16*>(take(p.p_q));
+  a.o = reinterpret_cast<u16*>(take(p.p_q));
+  a.ksuf = reinterpret_cast<u16*>(take(p.p_suf));
+  a.vsuf = reinterpret_cast<u16*>(take(p.p_suf));
+  a.act = reinterpret_cast<u16*>(take(p.p_act));
+  a.apart = reinterpret_cast<float*>(take(p.p_apart));
+  a.apart_m = reinterpret_cast<float*>(take(p.p_apartml));
+  a.apart_l = reinterpret_cast<float*>(take(p.p_apartml));
+  a.dpart = reinterpret_cast<float*>(take(p.p_dpart));
+  a.x = reinterpret_cast<float*>(take(p.p_x));
+}
+
+// Allocate the buffers of c->schedule (the previous schedule's buffers must be freed).
+hipError_t alloc_schedule(pi05_ctx* c) {
+  const Plan& p = c->plan;
+  hipError_t ae = hipSuccess;
+#define ALLOC(field, bytes) \
+  if (ae == hipSuccess) ae = dalloc(&c->field, bytes)
+  if (c->schedule == PI05_SCHEDULE_GRAPH) {
+    ALLOC(kcache, p.kv);
+    ALLOC(vcache, p.kv);
+    ALLOC(valid, p.valid);
+    ALLOC(h, p.h);
+    ALLOC(rowss, p.rowss);
+    ALLOC(q, p.q);
+    ALLOC(o, p.o);
+    ALLOC(act, p.act);
+    ALLOC(part, p.part);
+    ALLOC(part_m, p.partml);
+    ALLOC(part_l, p.partml);
+    ALLOC(x, p.x);
+    ALLOC(trace, p.trace);
+  } else {
+    // zero-filled: flags and counters must start at 0 (epoch 0 never matches a launch)
+    ALLOC(pbase, p.persistent_bytes() + 64 * 256);
+    if (ae == hipSuccess) carve_persistent(c);
+    if (ae == hipSuccess) {
+      std::vector<float> eu((size_t)c->d.num_steps * 4);
+      for (int s = 0; s < c->d.num_steps; ++s) {
+        // flow_ode mean coefficients of step s (engine.py:664-675)
+        const float t = c->ts[s];
+        const float delta = c->ts[s] - c->ts[s + 1];
+        const float x1w = t - delta;
+        eu[4 * s + 0] = t;
+        eu[4 * s + 1] = 1.0f - t;
+        eu[4 * s + 2] = 1.0f - x1w;
+        eu[4 * s + 3] = x1w;
+      }
+      ae = hipMemcpy(const_cast<float*>(c->mega.euler), eu.data(), eu.size() * 4, hipMemcpyHostToDevice);
+    }
+  }
+#undef ALLOC
+  return ae;
+}
+
+// After a launch whose waits timed out: bring flags, counters and the error word back to zero.
+hipError_t reset_persistent(pi05_ctx* c, hipStream_t st) {
+  const Plan& p = c->plan;
+  hipError_t e = hipMemsetAsync(c->mega.flags, 0, p.p_flags, st);
+  if (e == hipSuccess) e = hipMemsetAsync(c->mega.counters, 0, p.p_ctr, st);
+  if (e == hipSuccess) e = hipMemsetAsync(c->mega.err, 0, 256, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  c->epoch = 0;
   return e;
 }
 
@@ -470,7 +645,8 @@ int pi05_check_dims(const pi05_dims* dims) {
 size_t pi05_ctx_device_bytes(const pi05_dims* dims) {
   std::string msg;
   if (!check_dims_msg(dims, &msg)) return 0;
-  return make_plan(*dims).total();
+  const Plan p = make_plan(*dims);
+  return p.common() + p.persistent_bytes();
 }
 
 const char* pi05_last_error(const pi05_ctx* ctx) { return ctx ? ctx->err.c_str() : g_last_error.c_str(); }
@@ -515,25 +691,24 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   ALLOC(cond1, p.cond);
   ALLOC(cond, p.cond);
   ALLOC(heads_buf, p.heads);
-  ALLOC(kcache, p.kv);
-  ALLOC(vcache, p.kv);
-  ALLOC(valid, p.valid);
   ALLOC(cos_tab, p.rope);
   ALLOC(sin_tab, p.rope);
   ALLOC(positions, p.pos);
-  ALLOC(h, p.h);
-  ALLOC(rowss, p.rowss);
-  ALLOC(q, p.q);
-  ALLOC(o, p.o);
-  ALLOC(act, p.act);
-  ALLOC(part, p.part);
-  ALLOC(part_m, p.partml);
-  ALLOC(part_l, p.partml);
-  ALLOC(x, p.x);
-  ALLOC(trace, p.trace);
   ALLOC(kv_ptrs, p.ptrs);
   ALLOC(inv_freq, p.invf);
 #undef ALLOC
+  if (ae == hipSuccess) {
+    ae = hipHostMalloc(reinterpret_cast<void**>(&c->host_err), sizeof(unsigned), hipHostMallocMapped);
+    if (ae == hipSuccess) *c->host_err = 0;
+  }
+  // the persistent schedule needs every workgroup of the grid resident at once
+  int coop = 0, per_cu = 0;
+  if (ae == hipSuccess) ae = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+  if (ae == hipSuccess)
+    ae = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0);
+  c->grid = prop.multiProcessorCount;
+  c->schedule = (coop && per_cu >= 1) ? PI05_SCHEDULE_PERSISTENT : PI05_SCHEDULE_GRAPH;
+  if (ae == hipSuccess) ae = alloc_schedule(c);
   if (ae == hipSuccess) ae = hipStreamCreateWithFlags(&c->cap, hipStreamNonBlocking);
   if (ae == hipSuccess) {
     std::vector<float> invf(kHalfDim);
@@ -708,30 +883,65 @@ int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* cons
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // the pointer table is tiny; a synchronous copy keeps the host vector's lifetime trivial
   HIPCHK(c, hipMemcpy(c->kv_ptrs, c->kv_host_ptrs.data(), c->plan.ptrs, hipMemcpyHostToDevice));
+  const bool persistent = c->schedule == PI05_SCHEDULE_PERSISTENT;
+  // graph schedule: one cache of s_pad keys, action keys at [P, P + A);
+  // persistent: prefix keys padded to s_pre, action keys in a separate per-step block
+  const int kv_keys = persistent ? c->plan.s_pre : c->plan.s_pad;
   PrimeKvArgs ka{};
   ka.k_ptrs = c->kv_ptrs;
   ka.v_ptrs = c->kv_ptrs + d.depth;
   ka.batch_stride = kv_batch_stride;
   ka.row_stride = kv_row_stride;
-  ka.kcache = c->kcache;
-  ka.vcache = c->vcache;
+  ka.kcache = persistent ? const_cast<u16*>(c->mega.kpre) : c->kcache;
+  ka.vcache = persistent ? const_cast<u16*>(c->mega.vpre) : c->vcache;
   ka.batch = d.batch;
   ka.prefix_len = d.prefix_len;
-  ka.s_pad = c->plan.s_pad;
+  ka.s_pad = kv_keys;
+  ka.suffix_base = persistent ? kv_keys : d.prefix_len;
   HIPCHK(c, launch_prime_kv(ka, d.depth, st));
   PrimeTablesArgs ta{};
   ta.prefix_pad = prefix_pad;
   ta.inv_freq = c->inv_freq;
   ta.positions = c->positions;
-  ta.valid = c->valid;
+  ta.valid = persistent ? const_cast<uint8_t*>(c->mega.valid) : c->valid;
   ta.cos_tab = c->cos_tab;
   ta.sin_tab = c->sin_tab;
   ta.prefix_len = d.prefix_len;
-  ta.s_pad = c->plan.s_pad;
+  ta.s_pad = persistent ? kv_keys + 64 : kv_keys;
+  ta.suffix_base = persistent ? kv_keys : d.prefix_len;
   HIPCHK(c, launch_prime_tables(ta, d.batch, st));
   c->primed = true;
   return PI05_OK;
 }
+
+namespace {
+
+int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t st) {
+  if (c->epoch >= (1u << 26)) {
+    // keep epoch * nsplit far from wrapping: restart the count from zeroed flags/counters
+    HIPCHK(c, reset_persistent(c, st));
+  }
+  MegaArgs a = c->mega;
+  a.epoch = ++c->epoch;
+  a.x_io = x_inout;
+  a.trace = v_trace;
+  unsigned* host_err_dev = nullptr;
+  HIPCHK(c, hipHostGetDevicePointer(reinterpret_cast<void**>(&host_err_dev), c->host_err, 0));
+  a.host_err = host_err_dev;
+  *c->host_err = 0;
+  HIPCHK(c, launch_denoise_loop(a, c->grid, st));
+  // a timed-out wait inside the kernel is only visible after it ends
+  HIPCHK(c, hipStreamSynchronize(st));
+  if (__atomic_load_n(c->host_err, __ATOMIC_ACQUIRE) != 0) {
+    const hipError_t e = reset_persistent(c, st);
+    *c->host_err = 0;
+    return c->fail(PI05_E_HIP, "denoise kernel: a workgroup timed out waiting for its inputs (state reset%s)",
+                   e == hipSuccess ? "" : ", reset failed");
+  }
+  return PI05_OK;
+}
+
+}  // namespace
 
 int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
   if (!c) {
@@ -742,6 +952,7 @@ int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
   if (!c->weights_ready) return c->fail(PI05_E_STATE, "weights not bound/refreshed (call pi05_refresh_weights)");
   if (!c->primed) return c->fail(PI05_E_STATE, "prefix not primed (call pi05_prime_prefix)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (c->schedule == PI05_SCHEDULE_PERSISTENT) return denoise_persistent(c, x_inout, v_trace, st);
   const bool with_trace = v_trace != nullptr;
   int rc = ensure_graph(c, with_trace);
   if (rc != PI05_OK) return rc;
@@ -751,6 +962,33 @@ int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
   if (with_trace) HIPCHK(c, hipMemcpyAsync(v_trace, c->trace, c->plan.trace, hipMemcpyDeviceToDevice, st));
   return PI05_OK;
 }
+
+int pi05_set_schedule(pi05_ctx* c, int schedule) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (schedule != PI05_SCHEDULE_PERSISTENT && schedule != PI05_SCHEDULE_GRAPH)
+    return c->fail(PI05_E_INVALID, "schedule %d is not PI05_SCHEDULE_PERSISTENT or PI05_SCHEDULE_GRAPH", schedule);
+  if (schedule == c->schedule) return PI05_OK;
+  if (schedule == PI05_SCHEDULE_PERSISTENT) {
+    int coop = 0, per_cu = 0;
+    HIPCHK(c, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device));
+    HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0));
+    if (!coop || per_cu < 1) return c->fail(PI05_E_NODEVICE, "device cannot run the persistent schedule (cooperative launch)");
+  }
+  HIPCHK(c, hipDeviceSynchronize());
+  free_schedule(c);
+  c->schedule = schedule;
+  const hipError_t e = alloc_schedule(c);
+  if (e != hipSuccess) {
+    free_schedule(c);
+    return c->fail(e == hipErrorOutOfMemory ? PI05_E_NOMEM : PI05_E_HIP, "schedule buffers: %s", hipGetErrorString(e));
+  }
+  return PI05_OK;
+}
+
+int pi05_get_schedule(const pi05_ctx* c) { return c ? c->schedule : PI05_E_INVALID; }
 
 int pi05_release_graph(pi05_ctx* c) {
   if (!c) {
@@ -767,6 +1005,7 @@ int pi05_release_graph(pi05_ctx* c) {
 
 int pi05_launches_per_step(const pi05_ctx* c) {
   if (!c) return 0;
+  if (c->schedule == PI05_SCHEDULE_PERSISTENT) return 0;
   return 1 + c->d.depth * (c->plan.nsplit > 1 ? 6 : 5);
 }
 
@@ -779,6 +1018,7 @@ int pi05_bench_kernel(pi05_ctx* c, int kernel_id, int layer, int iters, void* st
   if (layer < 0 || layer >= c->d.depth) return c->fail(PI05_E_INVALID, "layer %d out of range", layer);
   if (iters < 1 || iters > 100000) return c->fail(PI05_E_INVALID, "iters %d out of range [1, 100000]", iters);
   if (!c->weights_ready || !c->primed) return c->fail(PI05_E_STATE, "weights and prefix must be ready");
+  if (c->schedule != PI05_SCHEDULE_GRAPH) return c->fail(PI05_E_STATE, "per-kernel timing needs the graph schedule");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   for (int i = 0; i < iters; ++i) {
     const int rc = kernel_id == kKStepIo ? enqueue_step_io(c, st, 1, false) : enqueue_layer(c, st, 0, layer, 1u << kernel_id);

@@ -18,6 +18,7 @@ struct PrimeKvArgs {
   u16* kcache;           // [depth][B] fragment-major blocks of s_pad * D
   u16* vcache;
   int batch, prefix_len, s_pad;
+  int suffix_base;  // keys [suffix_base, suffix_base + A) belong to the action tokens: left untouched
 };
 
 struct PrimeTablesArgs {
@@ -27,7 +28,8 @@ struct PrimeTablesArgs {
   uint8_t* valid;             // [B, s_pad]
   u16* cos_tab;               // [B, A, D] bf16
   u16* sin_tab;
-  int prefix_len, s_pad;
+  int prefix_len, s_pad;  // s_pad: keys per batch row of the valid mask
+  int suffix_base;        // first key of the action tokens in the mask
 };
 
 struct GemvArgs {
@@ -71,7 +73,7 @@ struct GemmArgs {
   int M, prefix_len, s_pad;
 };
 
-constexpr int kMaxAttnSplits = 8;
+constexpr int kMaxAttnSplits = 16;
 
 struct AttnArgs {
   const u16* q;        // [rows, D] (rows = M * H)
@@ -84,6 +86,53 @@ struct AttnArgs {
   float* part_l;
   int rows, s_pad, nsplit;
 };
+
+// The whole Euler loop as one cooperative kernel.  Per-launch buffers are sliced per Euler step
+// s and layer l ("slw" = s * depth + l); h and rowss slices are per (s, l') with l' in [0, depth]
+// (l' = depth is the output of the last layer).
+struct MegaArgs {
+  unsigned epoch;      // this launch's flag value (1, 2, ...); flags/counters start at 0
+  unsigned* err;       // set to 1 by a workgroup whose wait timed out
+  unsigned* flags;     // [(steps+1)][depth+1][6 phases][flag_stride]
+  unsigned* counters;  // attention [steps*depth][nrb] then down [steps*depth][64]
+  size_t ctr_down_off;
+  int flag_stride;
+  int depth, steps, M, batch, mp, nsplit, s_pre;
+  float eps;
+  const float* table;   // [steps][2*depth+1][3W] adaRMS modulation rows
+  const float* euler;   // [steps][4]: t, 1 - t, x0 weight, x1 weight
+  const float* out_w;   // [a, W]
+  const float* out_b;   // [a]
+  const float* in_w;    // [W, a]
+  const float* in_b;    // [W]
+  const u16* wpack;     // [depth] packed layer weights
+  const u16* cos_tab;   // [M, D]
+  const u16* sin_tab;
+  const u16* kpre;      // [depth][B] fragment-major prefix K of s_pre keys
+  const u16* vpre;
+  const uint8_t* valid; // [B][s_pre + 64]
+  u16* h;               // [steps][depth+1][M, W]
+  float* rowss;         // [steps][depth+1][M][64]
+  u16* hmid;            // [steps][depth][M, W] residual stream after attention
+  float* rowss_mid;     // [steps][depth][M][64]
+  u16* q;               // [steps][depth][M, H*D]
+  u16* ksuf;            // [steps][depth][B] fragment-major K of the 64-key action block
+  u16* vsuf;
+  u16* o;               // [steps][depth][M, H*D]
+  u16* act;             // [steps][depth][M, I]
+  float* apart;         // [nsplit][M*H][D] attention split partials (reused per layer)
+  float* apart_m;       // [nsplit][M*H]
+  float* apart_l;
+  float* dpart;         // [4][64][mp][16] down_proj K-split partials (reused per layer)
+  float* x;             // [steps][M, a] actions after step s (slot 0 unused)
+  float* x_io;          // [M, a] caller's buffer: noise on entry, actions on exit
+  float* trace;         // [steps][M, a] caller's velocity buffer (nullable)
+  unsigned* host_err;   // pinned host word, set with err (device-visible mapping)
+};
+
+hipError_t launch_denoise_loop(const MegaArgs& a, int grid, hipStream_t st);
+int denoise_loop_threads();
+const void* denoise_loop_kernel_ptr();
 
 hipError_t launch_pack_weight(const void* src, u16* dst, int N, int K, hipStream_t st);
 hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 ABI_VERSION = 1
 
 PI05_OK = 0
+SCHEDULES = {"persistent": 0, "graph": 1}
 ERROR_NAMES = {-1: "PI05_E_INVALID", -2: "PI05_E_STATE", -3: "PI05_E_HIP", -4: "PI05_E_NOMEM", -5: "PI05_E_NODEVICE"}
 
 # every exported symbol of include/pi05_denoise.h
@@ -35,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "pi05_prime_prefix",
     "pi05_denoise",
     "pi05_release_graph",
+    "pi05_set_schedule",
+    "pi05_get_schedule",
     "pi05_launches_per_step",
     "pi05_bench_kernel",
     "pi05_euler_schedule",
@@ -102,6 +105,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_prime_prefix": (i32, [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp, vp]),
         "pi05_denoise": (i32, [vp, vp, vp, vp]),
         "pi05_release_graph": (i32, [vp]),
+        "pi05_set_schedule": (i32, [vp, i32]),
+        "pi05_get_schedule": (i32, [vp]),
         "pi05_launches_per_step": (i32, [vp]),
         "pi05_bench_kernel": (i32, [vp, i32, i32, i32, vp]),
         "pi05_euler_schedule": (i32, [i32, vp]),
@@ -278,6 +283,18 @@ class DenoiseContext:
 
     def release_graph(self) -> None:
         self._call(self.lib.pi05_release_graph(self.handle))
+
+    @property
+    def schedule(self) -> str:
+        """``"persistent"`` (one cooperative kernel per denoise) or ``"graph"`` (hipGraph of kernels)."""
+        code = int(self.lib.pi05_get_schedule(self.handle))
+        return {v: k for k, v in SCHEDULES.items()}[code]
+
+    def set_schedule(self, name: str) -> None:
+        """Switch schedule; the prefix must be primed again afterwards."""
+        if name not in SCHEDULES:
+            raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}, got {name!r}")
+        self._call(self.lib.pi05_set_schedule(self.handle, SCHEDULES[name]))
 
     KERNELS = ("step_io", "qkv_rope", "attention", "o_proj", "gate_up", "down")
 

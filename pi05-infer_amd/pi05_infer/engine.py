@@ -100,6 +100,7 @@ class OpenPi0Inference:
         self.torch_compile_enabled = False
         self._torch_compile_mode = None
         self.training = False
+        self.schedule: Optional[str] = None  # None: the library's default for the device
 
     # ------------------------------------------------------------------ parameters
     def expected_parameters(self) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
@@ -186,6 +187,8 @@ class OpenPi0Inference:
             if missing:
                 raise RuntimeError(f"weights not loaded: {missing[:3]} ...")
             ctx = _ext.DenoiseContext(self.geometry, batch, prefix_len, num_steps, self.device)
+            if self.schedule is not None:
+                ctx.set_schedule(self.schedule)
             self._bind(ctx)
             ctx.refresh_weights()
             self._contexts[key] = ctx
@@ -230,9 +233,21 @@ class OpenPi0Inference:
         ctx.denoise(x, tr)
         return x, tr
 
+    def set_schedule(self, name: Optional[str]) -> None:
+        """Execution schedule of the denoise loop: ``"persistent"`` (the whole loop is one
+        cooperative kernel) or ``"graph"`` (one hipGraph of per-layer kernels); None restores the
+        library default.  Applies to existing contexts too (each predict primes its prefix)."""
+        if name is not None and name not in _ext.SCHEDULES:
+            raise ValueError(f"schedule must be one of {sorted(_ext.SCHEDULES)} or None, got {name!r}")
+        self.schedule = name
+        if name is not None:
+            for c in self._contexts.values():
+                c.set_schedule(name)
+
     def capture_cuda_graph(self, train_batch_size: int, eval_batch_size: int):
-        """The engine always replays its whole Euler loop as one hipGraph, captured lazily per
-        (B, P, num_steps) signature; this only records that graph use was requested."""
+        """The engine always runs its whole Euler loop as one launch (a persistent kernel, or a
+        hipGraph captured lazily per (B, P, num_steps) signature in the graph schedule); this
+        only records that graph use was requested."""
         self.cuda_graph_manager = {"eval_batch_size": eval_batch_size}
 
     def is_cuda_graph_enabled(self) -> bool:

@@ -87,8 +87,11 @@ def test_invalid_dims_rejected_with_message(lib, field, value, msg):
 def test_device_bytes_covers_weights_and_cache(lib):
     d = _ext.default_dims()
     need = 622_854_144  # 18 layers of bf16 expert weights
-    need += 2 * 18 * 1024 * 256 * 2  # K and V cache (S padded to 1024)
+    need += 2 * 18 * 992 * 256 * 2  # prefix K and V cache (P padded to 992)
     need += 10 * 37 * 3072 * 4  # modulation table
+    # per-(step, layer) activation slices of the persistent schedule: GeGLU output, q and o,
+    # residual stream before and after attention
+    need += 10 * 18 * 50 * (4096 + 2 * 2048 + 1024) * 2 + 10 * 19 * 50 * 1024 * 2
     got = _ext.device_bytes(d)
     assert need <= got <= need + 64 * 2**20
     d8 = _ext.default_dims()

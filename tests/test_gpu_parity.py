@@ -38,7 +38,11 @@ def full_weights():
     return S.make_weights(S.ExpertGeometry())
 
 
-def _run_case(weights, depth=18, P=968, B=1, steps=10, pad_fn=None, zero_gate=False):
+SCHEDULES = ("persistent", "graph")
+
+
+def _run_case(weights, depth=18, P=968, B=1, steps=10, pad_fn=None, zero_gate=False, schedules=SCHEDULES):
+    """Oracle once, then the engine under each schedule; returns results per schedule."""
     g = replace(S.ExpertGeometry(), depth=depth)
     w = {k: v for k, v in weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < depth}
     if zero_gate:
@@ -55,16 +59,22 @@ def _run_case(weights, depth=18, P=968, B=1, steps=10, pad_fn=None, zero_gate=Fa
     model.load_state_dict(w)
     model.to("cuda")
     obs = Observation(k.cuda(), v.cuda(), pad.cuda())
-    act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
-    torch.cuda.synchronize()
-    return model, obs, x1, table, (act_ref, vs_ref), (act, vs)
+    got = {}
+    for sched in schedules:
+        print(f"  schedule {sched}", flush=True)
+        model.set_schedule(sched)
+        act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
+        torch.cuda.synchronize()
+        got[sched] = (act, vs)
+    return model, obs, x1, table, (act_ref, vs_ref), got
 
 
 def _check(name, ref, got, steps):
-    (act_ref, vs_ref), (act, vs) = ref, got
-    for s in range(steps):
-        _close(vs_ref[s], vs[s], f"{name} step {s} velocity")
-    _close(act_ref, act, f"{name} actions")
+    act_ref, vs_ref = ref
+    for sched, (act, vs) in got.items():
+        for s in range(steps):
+            _close(vs_ref[s], vs[s], f"{name} [{sched}] step {s} velocity")
+        _close(act_ref, act, f"{name} [{sched}] actions")
 
 
 def test_c1_full_parity_and_table(full_weights):
@@ -74,9 +84,16 @@ def test_c1_full_parity_and_table(full_weights):
     ctx = next(iter(model._contexts.values()))
     tab = ctx.adarms_table().cpu()
     torch.testing.assert_close(tab, table, rtol=1e-5, atol=1e-5)
-    # graph replay is deterministic and does not drift between predicts
-    again = model.sample_actions(obs, x1.cuda())["actions"]
-    assert torch.equal(again, got[0])
+    # every schedule is deterministic and does not drift between predicts; a predict with other
+    # noise in between must not leave anything behind that a later predict reads
+    for sched in SCHEDULES:
+        model.set_schedule(sched)
+        first = model.sample_actions(obs, x1.cuda())["actions"].clone()
+        assert torch.equal(first, got[sched][0]), sched
+        other = model.sample_actions(obs, (x1 * -0.5).cuda())["actions"].clone()
+        assert not torch.equal(other, first)
+        again = model.sample_actions(obs, x1.cuda())["actions"]
+        assert torch.equal(again, first), sched
     model.close()
 
 
@@ -145,14 +162,16 @@ def test_weight_refresh_in_place(full_weights):
     model.params[name].mul_(1.5)
     model.params["time_mlp_out.weight"].mul_(0.5)
     model.invalidate_weight_derived_caches()
-    second = model.sample_actions(obs, x1.cuda())["actions"]
     w2 = dict(w)
     w2[name] = (w[name].float() * 1.5).to(torch.bfloat16)
     w2["time_mlp_out.weight"] = w["time_mlp_out.weight"] * 0.5
     og = O.geometry_from(g)
     ref, _ = O.sample_actions(w2, og, k, v, pad, x1, 3)
-    assert not torch.equal(first, second)
-    _close(ref, second, "refresh actions")
+    for sched in SCHEDULES:
+        model.set_schedule(sched)
+        second = model.sample_actions(obs, x1.cuda())["actions"]
+        assert not torch.equal(first, second)
+        _close(ref, second, f"refresh actions [{sched}]")
     model.close()
 
 
@@ -177,4 +196,26 @@ def test_bad_prefix_shapes_rejected(full_weights):
     bad.head_dim = 128
     with pytest.raises(_ext.Pi05Error):
         _ext.check_dims(bad)
+    with pytest.raises(_ext.Pi05Error):
+        ctx._call(ctx.lib.pi05_set_schedule(ctx.handle, 7))
+    # switching schedule drops the primed prefix: denoise must refuse until primed again
+    other = "graph" if ctx.schedule == "persistent" else "persistent"
+    ctx.set_schedule(other)
+    assert ctx.schedule == other
+    with pytest.raises(_ext.Pi05Error, match="PI05_E_STATE"):
+        ctx.denoise(torch.zeros(1, 50, 32, device="cuda"))
+    model.close()
+
+
+def test_persistent_is_default_and_single_launch(full_weights):
+    g = replace(S.ExpertGeometry(), depth=2)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 2}
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=2), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    ctx = model._context(1, 32, 2)
+    assert ctx.schedule == "persistent"
+    assert ctx.launches_per_step() == 0
+    ctx.set_schedule("graph")
+    assert ctx.launches_per_step() in (1 + 2 * 5, 1 + 2 * 6)
     model.close()
