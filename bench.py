@@ -1,12 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark of the pi0.5 action-expert denoise loop on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4]
+                    [--schedule persistent|graph] [--no-cpu-baseline]
 
 One bench "step" is one predict's denoise: the 10-step flow-matching Euler loop of the 18-layer
-expert over a static prefix KV cache (one hipGraph replay), with weights, KV and noise already
-resident in HBM.  Random-init weights (seed 0), N(0,1) bf16 prefix KV (seed 1), N(0,1) noise
-(seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
+expert over a static prefix KV cache, with weights, KV and noise already resident in HBM.  In the
+default (persistent) schedule that is ONE launch of the cooperative denoise kernel; in the graph
+schedule one hipGraph replay.  Random-init weights (seed 0), N(0,1) bf16 prefix KV (seed 1),
+N(0,1) noise (seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -45,13 +47,6 @@ def algorithmic_bytes_per_predict(depth: int, batch: int, prefix_len: int, steps
     return steps * (weights + kv + mod + heads + x)
 
 
-def gate_up_bytes(batch: int) -> int:
-    """Algorithmic bytes of one gate_up launch: gate + up bf16 weights, the residual rows it
-    normalises, its modulation scale/shift and the GeGLU output."""
-    M = 50 * batch
-    return 2 * 4096 * 1024 * 2 + M * 1024 * 2 + 2 * 1024 * 4 + M * 4096 * 2
-
-
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -82,8 +77,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
+    ap.add_argument("--schedule", default=None, choices=["persistent", "graph"],
+                    help="execution schedule (default: the library's choice, persistent on MI355X)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-predicts", type=int, default=3, help="predicts in the CPU-baseline sample")
+    ap.add_argument("--cpu-predicts", type=int, default=8, help="predicts in the CPU-baseline sample")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs the denoise loop on one GPU; runs with --gpus > 1 are not "
@@ -105,36 +102,33 @@ def main() -> int:
     k, v = S.make_prefix_kv(g, P, B)
     x1 = S.make_noise(g, B).cuda()
     obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(P, B).cuda())
-    model.sample_actions(obs, x1)  # builds the context, primes the prefix, captures the graph
+    if args.schedule is not None:
+        model.set_schedule(args.schedule)
+    model.sample_actions(obs, x1)  # builds the context, primes the prefix (and captures the graph)
     ctx = model._context(B, P, steps)
+    schedule = ctx.schedule
     stream = torch.cuda.current_stream()
     xs = [x1.clone() for _ in range(args.warmup + args.steps)]
 
     for i in range(args.warmup):
-        ctx.denoise(xs[i])
+        ctx.denoise(xs[i], stream=stream)
     torch.cuda.synchronize()
+    # timed region: K predicts back to back on `stream`, the stream every launch goes to
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     e0.record(stream)
     for i in range(args.steps):
-        ctx.denoise(xs[args.warmup + i])
+        ctx.denoise(xs[args.warmup + i], stream=stream)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_predict = e0.elapsed_time(e1) / args.steps
 
-    # dominant kernel (gate_up, the largest weight stream), timed with events on its stream
-    kiters = 200
-    ctx.bench_kernel("gate_up", 0, 10)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    ctx.bench_kernel("gate_up", 0, kiters)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    gu_us = e0.elapsed_time(e1) * 1e3 / kiters
-    gu_bytes = gate_up_bytes(B)
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-
+    # dominant kernel: in the persistent schedule the whole predict is one launch of
+    # denoise_loop_kernel, so its average launch duration is the timed region / K (each predict's
+    # host-side completion check adds a few microseconds, so this slightly overstates it)
     pred_bytes = algorithmic_bytes_per_predict(g.depth, B, P, steps)
-    pred_gbs = pred_bytes / (ms_per_predict * 1e-3) / 1e9
+    launch_us = ms_per_predict * 1e3
+    pred_gbs = pred_bytes / (launch_us * 1e-6) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -160,7 +154,7 @@ def main() -> int:
                       f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}",
         }
 
-    traffic = read_traffic("gate_up_c1_traffic.txt") if args.config == "c1" else None
+    traffic = read_traffic(f"denoise_loop_{args.config}_traffic.txt") if schedule == "persistent" else None
     out = {
         "metric": METRIC,
         "value": round(ms_per_predict, 4),
@@ -179,29 +173,27 @@ def main() -> int:
             "batch": B,
             "prefix_len": P,
             "num_steps": steps,
+            "schedule": schedule,
             "launches_per_step": ctx.launches_per_step(),
         },
         "roofline": {
-            "kernel": "gate_up (adaRMSNorm + gate|up GEMM + GeGLU)",
+            "kernel": "denoise_loop_kernel (whole predict, one launch)" if schedule == "persistent"
+                      else "whole predict (one hipGraph replay)",
             "bound": "hbm",
-            "achieved": round(gu_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "avg_launch_us": round(gu_us, 3),
-            "algorithmic_bytes_per_launch": gu_bytes,
-        },
-        "predict_roofline": {
             "achieved": round(pred_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(pred_gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_predict": pred_bytes,
+            "traffic": traffic,
+            "avg_launch_us": round(launch_us, 2),
+            "algorithmic_bytes_per_launch": pred_bytes,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+    # release the context (device memory, pinned error word) before interpreter teardown
+    model.close()
+    torch.cuda.synchronize()
     return 0
 
 

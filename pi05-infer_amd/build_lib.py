@@ -1,4 +1,5 @@
-"""Build libpi05_denoise.so for gfx950 with hipcc (in-tree, next to the Python package).
+"""Build libpi05_denoise.so for gfx950 with hipcc (in-tree, next to the Python package), and the
+C-ABI benchmark driver ``denoise_bench`` linked against it.
 
     python pi05-infer_amd/build_lib.py [--verbose]
 """
@@ -15,6 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
 SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip"]
+BENCH_SRC = "denoise_bench.hip"
+BENCH_OUT = os.path.join(HERE, "pi05_infer", "denoise_bench")
 
 HIPCC_FLAGS = [
     "-O3",
@@ -33,8 +36,7 @@ def hipcc() -> str:
     return path if os.path.exists(path) else "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], "-o", OUT + ".tmp"]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -44,7 +46,16 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs))
+
+
+def build(verbose: bool = False) -> str:
+    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], "-o", OUT + ".tmp"],
+         verbose)
     os.replace(OUT + ".tmp", OUT)
+    bench_flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    _run([hipcc(), *bench_flags, f"-I{INCLUDE}", os.path.join(CSRC, BENCH_SRC), f"-L{os.path.dirname(OUT)}", "-lpi05_denoise",
+          "-Wl,-rpath,$ORIGIN", "-o", BENCH_OUT + ".tmp"], verbose)
+    os.replace(BENCH_OUT + ".tmp", BENCH_OUT)
     return OUT
 
 
