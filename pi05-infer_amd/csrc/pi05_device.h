@@ -69,6 +69,18 @@ __host__ __device__ constexpr size_t wfrag_offset(int nt, int ks, int ksteps) {
   return ((size_t)nt * ksteps + ks) * 512;  // in bf16 elements
 }
 
+// Activation X[R][K] (row-major meaning) stored as MFMA A-operand fragments: fragment
+// (m-tile mt, k-step ks) holds X[mt*16 + l%16][ks*32 + (l/16)*8 + j] for lane l, j < 8,
+// fragments m-tile major.  afrag_offset gives the element offset of fragment (mt, ks) for
+// K = 32 * ksteps; afrag_index the element (m, k).  Eight consecutive k of one row are 16
+// contiguous bytes; one fragment is 1 KiB.
+__host__ __device__ constexpr size_t afrag_offset(int mt, int ks, int ksteps) {
+  return ((size_t)mt * ksteps + ks) * 512;
+}
+__host__ __device__ constexpr size_t afrag_index(int m, int k, int ksteps) {
+  return afrag_offset(m >> 4, k >> 5, ksteps) + (size_t)((((k & 31) >> 3) << 4) + (m & 15)) * 8 + (k & 7);
+}
+
 // Per-layer packed weight block (bf16 elements): q|k|v rows as 160 tiles over K=1024, then o_proj
 // (64 tiles over K=2048), gate (256 tiles over 1024), up (256 tiles over 1024), down (64 tiles over 4096).
 constexpr size_t kQkvElems = (size_t)kQkvCols * kWidth;

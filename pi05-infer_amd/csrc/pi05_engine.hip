@@ -66,10 +66,10 @@ struct Plan {
   // graph schedule
   size_t kv = 0, valid = 0, h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0;
   // persistent schedule
-  int s_pre = 0, nsplit_p = 1, nrb = 0, mp = 0, flag_stride = 0;
+  int s_pre = 0, nsplit_p = 1, nbp = 0, R = 0, max_items = 0;
   size_t p_kv = 0, p_valid = 0, p_h = 0, p_rowss = 0, p_hmid = 0, p_rowss_mid = 0, p_q = 0, p_suf = 0, p_act = 0;
   size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_ctr = 0, p_euler = 0;
-  size_t common() const { return wpack + table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf; }
+  size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf; }
   size_t graph_bytes() const { return 2 * kv + valid + h + rowss + q + o + act + part + 2 * partml + x + trace; }
   size_t persistent_bytes() const {
     return 2 * p_kv + p_valid + p_h + p_rowss + p_hmid + p_rowss_mid + 2 * p_q + 2 * p_suf + p_act + p_apart + 2 * p_apartml +
@@ -122,29 +122,31 @@ Plan make_plan(const pi05_dims& d) {
   p.trace = T * p.M * kActDim * 4;
 
   // persistent: prefix keys padded to a 32-key boundary, then one 64-key block of action keys;
-  // split count such that every wave normally owns one 32-key block
+  // split count such that every wave normally owns one 32-key block.  Activation rows are padded
+  // to 64 per sample (R rows), attention works on nbp two-token row blocks.
   p.s_pre = (d.prefix_len + 31) / 32 * 32;
   const int nkb = p.s_pre / 32 + 2;
   p.nsplit_p = (nkb + 3) / 4;
   if (p.nsplit_p > kMaxAttnSplits) p.nsplit_p = kMaxAttnSplits;
-  p.nrb = p.rows / 16;
-  p.mp = (p.M + 63) / 64 * 64;
-  p.flag_stride = (int)round_up(p.M > 256 ? p.M : 256, 64);
+  p.R = 64 * d.batch;
+  p.nbp = d.batch * (kHorizon / 2);
+  const size_t R = p.R;
+  p.max_items = p.M > 256 ? p.M : 256;
   p.p_kv = L * d.batch * p.s_pre * kHeadDim * 2;
   p.p_valid = round_up((size_t)d.batch * (p.s_pre + 64), 256);
-  p.p_h = T * (L + 1) * p.M * kWidth * 2;
-  p.p_rowss = T * (L + 1) * p.M * kRowSlots * 4;
-  p.p_hmid = T * L * p.M * kWidth * 2;
-  p.p_rowss_mid = T * L * p.M * kRowSlots * 4;
-  p.p_q = T * L * p.M * kHeads * kHeadDim * 2;
+  p.p_h = T * (L + 1) * R * kWidth * 2;
+  p.p_rowss = T * (L + 1) * R * kRowSlots * 4;
+  p.p_hmid = T * L * R * kWidth * 2;
+  p.p_rowss_mid = T * L * R * kRowSlots * 4;
+  p.p_q = T * L * R * kHeads * kHeadDim * 2;
   p.p_suf = T * L * d.batch * 64 * kHeadDim * 2;
-  p.p_act = T * L * p.M * kMlp * 2;
-  p.p_apart = (size_t)p.nsplit_p * p.rows * kHeadDim * 4;
-  p.p_apartml = round_up((size_t)p.nsplit_p * p.rows * 4, 256);
-  p.p_dpart = (size_t)4 * (kWidth / 16) * p.mp * 16 * 4;
+  p.p_act = T * L * R * kMlp * 2;
+  p.p_apart = T * L * p.nsplit_p * p.nbp * 16 * kHeadDim * 4;
+  p.p_apartml = round_up(T * L * p.nsplit_p * p.nbp * 16 * 4, 256);
+  p.p_dpart = T * L * 2 * 4 * (kWidth / 16) * R * 16 * 4;
   p.p_x = round_up(T * p.M * kActDim * 4, 256);
-  p.p_flags = (T + 1) * (L + 1) * 6 * p.flag_stride * 4;
-  p.p_ctr = round_up(T * L * (p.nrb + kWidth / 16) * 4, 256);
+  p.p_flags = (T + 1) * (L + 1) * 6 * 8 * 128;  // 8 replicas of each phase counter, 128 B apart
+  p.p_ctr = round_up(T * L * (p.nbp + 2 * (kWidth / 16)) * 4, 256);
   p.p_euler = round_up(T * 4 * 4, 256);
   return p;
 }
@@ -244,6 +246,7 @@ struct pi05_ctx {
   // common
   u16* wpack = nullptr;
   float* table = nullptr;
+  float* table_s1 = nullptr;  // table with 1 + scale (persistent kernel's adaRMSNorm operand)
   float* temb = nullptr;
   float* cond1 = nullptr;
   float* cond = nullptr;
@@ -329,7 +332,7 @@ void free_schedule(pi05_ctx* c) {
 
 void free_all(pi05_ctx* c) {
   free_schedule(c);
-  void* bufs[] = {c->wpack, c->table, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
+  void* bufs[] = {c->wpack, c->table, c->table_s1, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
                   c->positions, (void*)c->kv_ptrs, c->inv_freq};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
@@ -369,17 +372,18 @@ void carve_persistent(pi05_ctx* c) {
   a.err = reinterpret_cast<unsigned*>(take(256));
   a.flags = reinterpret_cast<unsigned*>(take(p.p_flags));
   a.counters = reinterpret_cast<unsigned*>(take(p.p_ctr));
-  a.ctr_down_off = (size_t)d.num_steps * d.depth * p.nrb;
-  a.flag_stride = p.flag_stride;
+  a.ctr_o_off = (size_t)d.num_steps * d.depth * p.nbp;
+  a.ctr_down_off = a.ctr_o_off + (size_t)d.num_steps * d.depth * (kWidth / 16);
   a.depth = d.depth;
   a.steps = d.num_steps;
-  a.M = p.M;
   a.batch = d.batch;
-  a.mp = p.mp;
+  a.R = p.R;
+  a.nbp = p.nbp;
   a.nsplit = p.nsplit_p;
   a.s_pre = p.s_pre;
   a.eps = d.rms_eps;
   a.table = c->table;
+  a.table_s1 = c->table_s1;
   a.euler = reinterpret_cast<float*>(take(p.p_euler));
   a.in_w = heads_in_w(c);
   a.out_w = heads_out_w(c);
@@ -687,6 +691,7 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   if (ae == hipSuccess) ae = dalloc(&c->field, bytes)
   ALLOC(wpack, p.wpack);
   ALLOC(table, p.table);
+  ALLOC(table_s1, p.table);
   ALLOC(temb, p.temb);
   ALLOC(cond1, p.cond);
   ALLOC(cond, p.cond);
@@ -706,8 +711,9 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   if (ae == hipSuccess) ae = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
   if (ae == hipSuccess)
     ae = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0);
+  // one workgroup per CU; the weight phases have 256 items, one per workgroup
   c->grid = prop.multiProcessorCount;
-  c->schedule = (coop && per_cu >= 1) ? PI05_SCHEDULE_PERSISTENT : PI05_SCHEDULE_GRAPH;
+  c->schedule = (coop && per_cu >= 1 && c->grid >= 256) ? PI05_SCHEDULE_PERSISTENT : PI05_SCHEDULE_GRAPH;
   if (ae == hipSuccess) ae = alloc_schedule(c);
   if (ae == hipSuccess) ae = hipStreamCreateWithFlags(&c->cap, hipStreamNonBlocking);
   if (ae == hipSuccess) {
@@ -847,6 +853,7 @@ int pi05_refresh_weights(pi05_ctx* c, void* stream) {
     GemvArgs gd{w, b, c->cond, c->table, kModW, kWidth, S, p.n_norms * kModW, n * kModW, 0};
     HIPCHK(c, launch_gemv_rows(gd, st));
   }
+  HIPCHK(c, launch_scale_plus_one(c->table, c->table_s1, S * p.n_norms, st));
   c->weights_ready = true;
   return PI05_OK;
 }
@@ -917,8 +924,8 @@ int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* cons
 namespace {
 
 int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t st) {
-  if (c->epoch >= (1u << 26)) {
-    // keep epoch * nsplit far from wrapping: restart the count from zeroed flags/counters
+  if (c->epoch >= (1u << 31) / (unsigned)c->plan.max_items) {
+    // keep epoch * items below 2^31: restart the count from zeroed counters
     HIPCHK(c, reset_persistent(c, st));
   }
   MegaArgs a = c->mega;
@@ -975,7 +982,8 @@ int pi05_set_schedule(pi05_ctx* c, int schedule) {
     int coop = 0, per_cu = 0;
     HIPCHK(c, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device));
     HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0));
-    if (!coop || per_cu < 1) return c->fail(PI05_E_NODEVICE, "device cannot run the persistent schedule (cooperative launch)");
+    if (!coop || per_cu < 1 || c->grid < 256)
+      return c->fail(PI05_E_NODEVICE, "device cannot run the persistent schedule (cooperative launch of 256 workgroups)");
   }
   HIPCHK(c, hipDeviceSynchronize());
   free_schedule(c);

@@ -87,46 +87,50 @@ struct AttnArgs {
   int rows, s_pad, nsplit;
 };
 
-// The whole Euler loop as one cooperative kernel.  Per-launch buffers are sliced per Euler step
-// s and layer l ("slw" = s * depth + l); h and rowss slices are per (s, l') with l' in [0, depth]
-// (l' = depth is the output of the last layer).
+// The whole Euler loop as one cooperative kernel.  Activations live in per-(Euler step s,
+// layer l) slices ("slw" = s * depth + l; h / rowss slices are per (s, l') with l' in
+// [0, depth], l' = depth being the last layer's output) that are written once per launch.
+// Rows are padded per sample: row r = b * 64 + t for action token t < 50 (rows t >= 50 stay
+// zero), R = 64 * B rows.  Activation matrices are stored as MFMA A-operand fragments
+// (pi05_device.h: afrag_offset), so one wave-wide 16-byte load reads 1 KiB of contiguous memory.
 struct MegaArgs {
   unsigned epoch;      // this launch's flag value (1, 2, ...); flags/counters start at 0
   unsigned* err;       // set to 1 by a workgroup whose wait timed out
-  unsigned* flags;     // [(steps+1)][depth+1][6 phases][flag_stride]
-  unsigned* counters;  // attention [steps*depth][nrb] then down [steps*depth][64]
-  size_t ctr_down_off;
-  int flag_stride;
-  int depth, steps, M, batch, mp, nsplit, s_pre;
+  unsigned* flags;     // phase completion counters [(steps+1)][depth+1][6 phases], 128 B apart
+  unsigned* counters;  // [steps*depth][nbp] attention, then [steps*depth][64] o_proj, then down
+  size_t ctr_o_off, ctr_down_off;
+  int depth, steps, batch, R, nbp, nsplit, s_pre;
   float eps;
-  const float* table;   // [steps][2*depth+1][3W] adaRMS modulation rows
+  const float* table;   // [steps][2*depth+1][3W] adaRMS modulation rows: scale | shift | gate
+  const float* table_s1;  // the same rows with 1 + scale in place of scale
   const float* euler;   // [steps][4]: t, 1 - t, x0 weight, x1 weight
   const float* out_w;   // [a, W]
   const float* out_b;   // [a]
   const float* in_w;    // [W, a]
   const float* in_b;    // [W]
   const u16* wpack;     // [depth] packed layer weights
-  const u16* cos_tab;   // [M, D]
+  const u16* cos_tab;   // [B*50, D] bf16 RoPE tables (compact rows b*50 + t)
   const u16* sin_tab;
   const u16* kpre;      // [depth][B] fragment-major prefix K of s_pre keys
   const u16* vpre;
   const uint8_t* valid; // [B][s_pre + 64]
-  u16* h;               // [steps][depth+1][M, W]
-  float* rowss;         // [steps][depth+1][M][64]
-  u16* hmid;            // [steps][depth][M, W] residual stream after attention
-  float* rowss_mid;     // [steps][depth][M][64]
-  u16* q;               // [steps][depth][M, H*D]
+  u16* h;               // [steps][depth+1] A fragments of [R, W]
+  float* rowss;         // [steps][depth+1] per-16-column partial sums of squares of the rows:
+                        // slot l' = 0 row-major [R][64], slots l' > 0 tile-major [64][R]
+  u16* hmid;            // [steps][depth] residual stream after attention, A fragments [R, W]
+  float* rowss_mid;     // [steps][depth] tile-major [64][R]
+  u16* q;               // [steps][depth] fragments of [R*8 query rows (r*8 + head), D]
   u16* ksuf;            // [steps][depth][B] fragment-major K of the 64-key action block
   u16* vsuf;
-  u16* o;               // [steps][depth][M, H*D]
-  u16* act;             // [steps][depth][M, I]
-  float* apart;         // [nsplit][M*H][D] attention split partials (reused per layer)
-  float* apart_m;       // [nsplit][M*H]
+  u16* o;               // [steps][depth] A fragments of [R, H*D]
+  u16* act;             // [steps][depth] A fragments of [R, I]
+  float* apart;         // [steps][depth][nsplit][nbp*16][D] attention split partials
+  float* apart_m;       // [steps][depth][nsplit][nbp*16]
   float* apart_l;
-  float* dpart;         // [4][64][mp][16] down_proj K-split partials (reused per layer)
-  float* x;             // [steps][M, a] actions after step s (slot 0 unused)
-  float* x_io;          // [M, a] caller's buffer: noise on entry, actions on exit
-  float* trace;         // [steps][M, a] caller's velocity buffer (nullable)
+  float* dpart;         // [steps][depth][o_proj | down][4][64][R][16] K-quarter partials
+  float* x;             // [steps][B*50, a] actions after step s (slot 0 unused)
+  float* x_io;          // [B*50, a] caller's buffer: noise on entry, actions on exit
+  float* trace;         // [steps][B*50, a] caller's velocity buffer (nullable)
   unsigned* host_err;   // pinned host word, set with err (device-visible mapping)
 };
 
@@ -138,6 +142,8 @@ hipError_t launch_pack_weight(const void* src, u16* dst, int N, int K, hipStream
 hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);
 hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t st);
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st);
+// out[r] = in[r] with 1 + scale in place of scale, for rows of [3W] modulation (scale | shift | gate)
+hipError_t launch_scale_plus_one(const float* in, float* out, int rows, hipStream_t st);
 hipError_t launch_step_io(const StepIoArgs& a, hipStream_t st);
 hipError_t launch_qkv_rope(const GemmArgs& a, hipStream_t st);
 hipError_t launch_gate_up(const GemmArgs& a, hipStream_t st);

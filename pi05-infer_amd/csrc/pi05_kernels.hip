@@ -139,6 +139,12 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(GemvArgs a) {
   }
 }
 
+__global__ void scale_plus_one_kernel(const float* __restrict__ in, float* __restrict__ out, int rows) {
+  const size_t n = (size_t)rows * kModW;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = (i % kModW) < (size_t)kWidth ? fadd(1.0f, in[i]) : in[i];
+}
+
 // =============================================================================================
 // step boundary: final norm + action_out_proj + Euler (previous step), action_in_proj (this step)
 // One workgroup per token row; every global load is issued before the first dependent use.
@@ -688,6 +694,11 @@ hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t 
 
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st) {
   gemv_rows_kernel<<<(a.rows + 3) / 4, 256, 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale_plus_one(const float* in, float* out, int rows, hipStream_t st) {
+  scale_plus_one_kernel<<<256, 256, 0, st>>>(in, out, rows);
   return hipGetLastError();
 }
 
