@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -62,17 +63,17 @@ struct HeadBind {
 struct Plan {
   int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1, mgroups = 1;
   // common
-  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, rope = 0, pos = 0, ptrs = 0, invf = 0;
+  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, rope = 0, pos = 0, ptrs = 0, invf = 0, bias = 0;
   // graph schedule
   size_t kv = 0, valid = 0, h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0;
   // persistent schedule
-  int s_pre = 0, nsplit_p = 1, nbp = 0, R = 0, max_items = 0;
-  size_t p_kv = 0, p_valid = 0, p_h = 0, p_rowss = 0, p_hmid = 0, p_rowss_mid = 0, p_q = 0, p_suf = 0, p_act = 0;
+  int s_pre = 0, nsplit_p = 1, nsplit_pad = 4, nbp = 0, nbp_pad = 4, R = 0, fstride = 256, max_items = 0;
+  size_t p_kv = 0, p_valid = 0, p_h = 0, p_g = 0, p_ss = 0, p_hmid = 0, p_ssmid = 0, p_q = 0, p_suf = 0, p_act = 0;
   size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_ctr = 0, p_euler = 0;
-  size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf; }
+  size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf + bias; }
   size_t graph_bytes() const { return 2 * kv + valid + h + rowss + q + o + act + part + 2 * partml + x + trace; }
   size_t persistent_bytes() const {
-    return 2 * p_kv + p_valid + p_h + p_rowss + p_hmid + p_rowss_mid + 2 * p_q + 2 * p_suf + p_act + p_apart + 2 * p_apartml +
+    return 2 * p_kv + p_valid + p_h + p_g + p_ss + p_hmid + p_g + p_ssmid + 2 * p_q + 2 * p_suf + p_act + p_apart + p_apartml +
            p_dpart + p_x + p_flags + p_ctr + p_euler + 256;
   }
 };
@@ -107,6 +108,7 @@ Plan make_plan(const pi05_dims& d) {
   p.pos = (size_t)p.M * 4;
   p.ptrs = 2 * L * sizeof(void*);
   p.invf = (size_t)kHalfDim * 4;
+  p.bias = T * L * kBiasCols * 4;
 
   p.kv = L * d.batch * p.s_pad * kHeadDim * 2;
   p.valid = (size_t)d.batch * p.s_pad;
@@ -128,25 +130,37 @@ Plan make_plan(const pi05_dims& d) {
   const int nkb = p.s_pre / 32 + 2;
   p.nsplit_p = (nkb + 3) / 4;
   if (p.nsplit_p > kMaxAttnSplits) p.nsplit_p = kMaxAttnSplits;
+  p.nsplit_pad = (p.nsplit_p + 3) / 4 * 4;
   p.R = 64 * d.batch;
   p.nbp = d.batch * (kHorizon / 2);
+  p.nbp_pad = (p.nbp + 3) / 4 * 4;
   const size_t R = p.R;
   p.max_items = p.M > 256 ? p.M : 256;
+  // flag words per phase instance: the largest item count of any phase (io rows, attention split
+  // and merge flags, 256 GEMM items), 16-byte aligned sub-ranges
+  size_t fw = 256;
+  fw = std::max(fw, (size_t)p.M);
+  fw = std::max(fw, (size_t)p.nbp * p.nsplit_pad);
+  fw = std::max(fw, (size_t)4 * p.nbp_pad);
+  p.fstride = (int)round_up(fw, 256);
   p.p_kv = L * d.batch * p.s_pre * kHeadDim * 2;
   p.p_valid = round_up((size_t)d.batch * (p.s_pre + 64), 256);
   p.p_h = T * (L + 1) * R * kWidth * 2;
-  p.p_rowss = T * (L + 1) * R * kRowSlots * 4;
+  p.p_g = T * L * R * kWidth * 2;
+  p.p_ss = T * (L + 1) * R * kRowSlots * 4;
   p.p_hmid = T * L * R * kWidth * 2;
-  p.p_rowss_mid = T * L * R * kRowSlots * 4;
+  p.p_ssmid = T * L * R * kRowSlots * 4;
   p.p_q = T * L * R * kHeads * kHeadDim * 2;
   p.p_suf = T * L * d.batch * 64 * kHeadDim * 2;
   p.p_act = T * L * R * kMlp * 2;
   p.p_apart = T * L * p.nsplit_p * p.nbp * 16 * kHeadDim * 4;
-  p.p_apartml = round_up(T * L * p.nsplit_p * p.nbp * 16 * 4, 256);
+  p.p_apartml = round_up(T * L * p.nsplit_p * p.nbp * 32 * 4, 256);
   p.p_dpart = T * L * 2 * 4 * (kWidth / 16) * R * 16 * 4;
   p.p_x = round_up(T * p.M * kActDim * 4, 256);
-  p.p_flags = (T + 1) * (L + 1) * 6 * 8 * 128;  // 8 replicas of each phase counter, 128 B apart
-  p.p_ctr = round_up(T * L * (p.nbp + 2 * (kWidth / 16)) * 4, 256);
+  // 7 phases per (step, layer), 8 replicas each; 1 KiB of slack for the 16-byte flag loads past
+  // a range's end
+  p.p_flags = (T + 1) * (L + 1) * 7 * 8 * (size_t)p.fstride * 4 + 1024;
+  p.p_ctr = round_up(T * L * 2 * (kWidth / 16) * 4, 256);
   p.p_euler = round_up(T * 4 * 4, 256);
   return p;
 }
@@ -247,6 +261,7 @@ struct pi05_ctx {
   u16* wpack = nullptr;
   float* table = nullptr;
   float* table_s1 = nullptr;  // table with 1 + scale (persistent kernel's adaRMSNorm operand)
+  float* bias = nullptr;      // shift . W^T per (step, layer) (persistent kernel's adaRMSNorm fold)
   float* temb = nullptr;
   float* cond1 = nullptr;
   float* cond = nullptr;
@@ -332,7 +347,7 @@ void free_schedule(pi05_ctx* c) {
 
 void free_all(pi05_ctx* c) {
   free_schedule(c);
-  void* bufs[] = {c->wpack, c->table, c->table_s1, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
+  void* bufs[] = {c->wpack, c->table, c->table_s1, c->bias, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
                   c->positions, (void*)c->kv_ptrs, c->inv_freq};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
@@ -372,18 +387,21 @@ void carve_persistent(pi05_ctx* c) {
   a.err = reinterpret_cast<unsigned*>(take(256));
   a.flags = reinterpret_cast<unsigned*>(take(p.p_flags));
   a.counters = reinterpret_cast<unsigned*>(take(p.p_ctr));
-  a.ctr_o_off = (size_t)d.num_steps * d.depth * p.nbp;
-  a.ctr_down_off = a.ctr_o_off + (size_t)d.num_steps * d.depth * (kWidth / 16);
+  a.ctr_down_off = (size_t)d.num_steps * d.depth * (kWidth / 16);
+  a.fstride = p.fstride;
   a.depth = d.depth;
   a.steps = d.num_steps;
   a.batch = d.batch;
   a.R = p.R;
   a.nbp = p.nbp;
+  a.nbp_pad = p.nbp_pad;
   a.nsplit = p.nsplit_p;
+  a.nsplit_pad = p.nsplit_pad;
   a.s_pre = p.s_pre;
   a.eps = d.rms_eps;
   a.table = c->table;
   a.table_s1 = c->table_s1;
+  a.bias = c->bias;
   a.euler = reinterpret_cast<float*>(take(p.p_euler));
   a.in_w = heads_in_w(c);
   a.out_w = heads_out_w(c);
@@ -396,17 +414,18 @@ void carve_persistent(pi05_ctx* c) {
   a.vpre = reinterpret_cast<u16*>(take(p.p_kv));
   a.valid = reinterpret_cast<uint8_t*>(take(p.p_valid));
   a.h = reinterpret_cast<u16*>(take(p.p_h));
-  a.rowss = reinterpret_cast<float*>(take(p.p_rowss));
+  a.g = reinterpret_cast<u16*>(take(p.p_g));
+  a.ss = reinterpret_cast<float*>(take(p.p_ss));
   a.hmid = reinterpret_cast<u16*>(take(p.p_hmid));
-  a.rowss_mid = reinterpret_cast<float*>(take(p.p_rowss_mid));
+  a.gmid = reinterpret_cast<u16*>(take(p.p_g));
+  a.ssmid = reinterpret_cast<float*>(take(p.p_ssmid));
   a.q = reinterpret_cast<u16*>(take(p.p_q));
   a.o = reinterpret_cast<u16*>(take(p.p_q));
   a.ksuf = reinterpret_cast<u16*>(take(p.p_suf));
   a.vsuf = reinterpret_cast<u16*>(take(p.p_suf));
   a.act = reinterpret_cast<u16*>(take(p.p_act));
   a.apart = reinterpret_cast<float*>(take(p.p_apart));
-  a.apart_m = reinterpret_cast<float*>(take(p.p_apartml));
-  a.apart_l = reinterpret_cast<float*>(take(p.p_apartml));
+  a.apart_ml = reinterpret_cast<float*>(take(p.p_apartml));
   a.dpart = reinterpret_cast<float*>(take(p.p_dpart));
   a.x = reinterpret_cast<float*>(take(p.p_x));
 }
@@ -692,6 +711,7 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   ALLOC(wpack, p.wpack);
   ALLOC(table, p.table);
   ALLOC(table_s1, p.table);
+  ALLOC(bias, p.bias);
   ALLOC(temb, p.temb);
   ALLOC(cond1, p.cond);
   ALLOC(cond, p.cond);
@@ -854,6 +874,8 @@ int pi05_refresh_weights(pi05_ctx* c, void* stream) {
     HIPCHK(c, launch_gemv_rows(gd, st));
   }
   HIPCHK(c, launch_scale_plus_one(c->table, c->table_s1, S * p.n_norms, st));
+  ShiftBiasArgs sb{c->wpack, c->table, c->bias, c->d.depth, S};
+  HIPCHK(c, launch_shift_bias(sb, st));
   c->weights_ready = true;
   return PI05_OK;
 }

@@ -88,52 +88,71 @@ struct AttnArgs {
 };
 
 // The whole Euler loop as one cooperative kernel.  Activations live in per-(Euler step s,
-// layer l) slices ("slw" = s * depth + l; h / rowss slices are per (s, l') with l' in
-// [0, depth], l' = depth being the last layer's output) that are written once per launch.
-// Rows are padded per sample: row r = b * 64 + t for action token t < 50 (rows t >= 50 stay
-// zero), R = 64 * B rows.  Activation matrices are stored as MFMA A-operand fragments
-// (pi05_device.h: afrag_offset), so one wave-wide 16-byte load reads 1 KiB of contiguous memory.
+// layer l) slices ("slw" = s * depth + l; h / ss slices are per (s, l') with l' in [0, depth],
+// l' = depth being the last layer's output) that are written once per launch.  Rows are padded
+// per sample: row r = b * 64 + t for action token t < 50 (rows t >= 50 stay zero), R = 64 * B
+// rows.  Activation matrices are stored as MFMA A-operand fragments (pi05_device.h:
+// afrag_offset), so one wave-wide 16-byte load reads 1 KiB of contiguous memory.
+//
+// adaRMSNorm is folded into the GEMM that consumes it: next to each residual-stream slice h the
+// producer writes g = bf16(h * (1 + scale)) and per-16-column partial sums of squares ss of the
+// rows; the consumer computes y = rstd * (g . W^T) + shift . W^T, with shift . W^T precomputed
+// per (step, layer) in `bias`.
+constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gate, then 4096 up
+
 struct MegaArgs {
   unsigned epoch;      // this launch's flag value (1, 2, ...); flags/counters start at 0
   unsigned* err;       // set to 1 by a workgroup whose wait timed out
-  unsigned* flags;     // phase completion counters [(steps+1)][depth+1][6 phases], 128 B apart
-  unsigned* counters;  // [steps*depth][nbp] attention, then [steps*depth][64] o_proj, then down
-  size_t ctr_o_off, ctr_down_off;
-  int depth, steps, batch, R, nbp, nsplit, s_pre;
+  unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][fstride]
+  unsigned* counters;  // K-quarter election counters [steps*depth][64] o_proj, then down
+  size_t ctr_down_off;
+  int fstride;         // flag words per phase instance (multiple of 256)
+  int depth, steps, batch, R, nbp, nsplit, nsplit_pad, nbp_pad, s_pre;
   float eps;
-  const float* table;   // [steps][2*depth+1][3W] adaRMS modulation rows: scale | shift | gate
+  const float* table;     // [steps][2*depth+1][3W] adaRMS modulation rows: scale | shift | gate
   const float* table_s1;  // the same rows with 1 + scale in place of scale
-  const float* euler;   // [steps][4]: t, 1 - t, x0 weight, x1 weight
-  const float* out_w;   // [a, W]
-  const float* out_b;   // [a]
-  const float* in_w;    // [W, a]
-  const float* in_b;    // [W]
-  const u16* wpack;     // [depth] packed layer weights
-  const u16* cos_tab;   // [B*50, D] bf16 RoPE tables (compact rows b*50 + t)
+  const float* bias;      // [steps][depth][kBiasCols] shift . W^T of the norm each GEMM consumes
+  const float* euler;     // [steps][4]: t, 1 - t, x0 weight, x1 weight
+  const float* out_w;     // [a, W]
+  const float* out_b;     // [a]
+  const float* in_w;      // [W, a]
+  const float* in_b;      // [W]
+  const u16* wpack;       // [depth] packed layer weights
+  const u16* cos_tab;     // [B*50, D] bf16 RoPE tables (compact rows b*50 + t)
   const u16* sin_tab;
-  const u16* kpre;      // [depth][B] fragment-major prefix K of s_pre keys
+  const u16* kpre;        // [depth][B] fragment-major prefix K of s_pre keys
   const u16* vpre;
-  const uint8_t* valid; // [B][s_pre + 64]
-  u16* h;               // [steps][depth+1] A fragments of [R, W]
-  float* rowss;         // [steps][depth+1] per-16-column partial sums of squares of the rows:
-                        // slot l' = 0 row-major [R][64], slots l' > 0 tile-major [64][R]
-  u16* hmid;            // [steps][depth] residual stream after attention, A fragments [R, W]
-  float* rowss_mid;     // [steps][depth] tile-major [64][R]
-  u16* q;               // [steps][depth] fragments of [R*8 query rows (r*8 + head), D]
-  u16* ksuf;            // [steps][depth][B] fragment-major K of the 64-key action block
+  const uint8_t* valid;   // [B][s_pre + 64]
+  u16* h;                 // [steps][depth+1] A fragments of [R, W]: residual stream into layer l'
+  u16* g;                 // [steps][depth] A fragments of [R, W]: bf16(h * (1 + scale)) of norm 2l
+  float* ss;              // [steps][depth+1] tile-major [64][R] partial sums of squares of h rows
+  u16* hmid;              // [steps][depth] residual stream after attention, A fragments [R, W]
+  u16* gmid;              // [steps][depth] bf16(hmid * (1 + scale)) of norm 2l+1
+  float* ssmid;           // [steps][depth] tile-major [64][R]
+  u16* q;                 // [steps][depth] fragments of [R*8 query rows (r*8 + head), D]
+  u16* ksuf;              // [steps][depth][B] fragment-major K of the 64-key action block
   u16* vsuf;
-  u16* o;               // [steps][depth] A fragments of [R, H*D]
-  u16* act;             // [steps][depth] A fragments of [R, I]
-  float* apart;         // [steps][depth][nsplit][nbp*16][D] attention split partials
-  float* apart_m;       // [steps][depth][nsplit][nbp*16]
-  float* apart_l;
-  float* dpart;         // [steps][depth][o_proj | down][4][64][R][16] K-quarter partials
-  float* x;             // [steps][B*50, a] actions after step s (slot 0 unused)
-  float* x_io;          // [B*50, a] caller's buffer: noise on entry, actions on exit
-  float* trace;         // [steps][B*50, a] caller's velocity buffer (nullable)
-  unsigned* host_err;   // pinned host word, set with err (device-visible mapping)
+  u16* o;                 // [steps][depth] A fragments of [R, H*D]
+  u16* act;               // [steps][depth] A fragments of [R, I]
+  float* apart;           // [steps][depth][nsplit][nbp][16][D] attention split partials
+  float* apart_ml;        // [steps][depth][nsplit][nbp][2][16] running max | sum of the splits
+  float* dpart;           // [steps][depth][o_proj | down][4][64][R][16] K-quarter partials
+  float* x;               // [steps][B*50, a] actions after step s (slot 0 unused)
+  float* x_io;            // [B*50, a] caller's buffer: noise on entry, actions on exit
+  float* trace;           // [steps][B*50, a] caller's velocity buffer (nullable)
+  unsigned* host_err;     // pinned host word, set with err (device-visible mapping)
 };
 
+// bias[s][l][j] = sum_k shift_{s, norm(j)}[k] * W_l[j][k] from the packed weights, for the fused
+// q|k|v columns (norm 2l) and the gate and up columns (norm 2l+1).
+struct ShiftBiasArgs {
+  const u16* wpack;    // [depth] packed layer weights
+  const float* table;  // [steps][2*depth+1][3W]
+  float* bias;         // [steps][depth][kBiasCols]
+  int depth, steps;
+};
+
+hipError_t launch_shift_bias(const ShiftBiasArgs& a, hipStream_t st);
 hipError_t launch_denoise_loop(const MegaArgs& a, int grid, hipStream_t st);
 int denoise_loop_threads();
 const void* denoise_loop_kernel_ptr();

@@ -90,8 +90,11 @@ def test_device_bytes_covers_weights_and_cache(lib):
     need += 2 * 18 * 992 * 256 * 2  # prefix K and V cache (P padded to 992)
     need += 10 * 37 * 3072 * 4  # modulation table
     # per-(step, layer) activation slices of the persistent schedule (rows padded to 64 per
-    # sample): GeGLU output, q and o, residual stream before and after attention
-    need += 10 * 18 * 64 * (4096 + 2 * 2048 + 1024) * 2 + 10 * 19 * 64 * 1024 * 2
+    # sample): GeGLU output, q and o, residual stream before and after attention, and the two
+    # modulated copies g = bf16(h * (1 + scale)) that the folded adaRMSNorm GEMMs consume
+    need += 10 * 18 * 64 * (4096 + 2 * 2048 + 3 * 1024) * 2 + 10 * 19 * 64 * 1024 * 2
+    # shift . W^T per (step, layer): 2560 q|k|v + 2 x 4096 gate|up columns, fp32
+    need += 10 * 18 * (2560 + 2 * 4096) * 4
     # per-(step, layer) split partials: attention (9 key splits x 25 row blocks x 16 rows x 256
     # fp32) and the o_proj / down_proj K quarters (2 x 4 x 64 tiles x 64 rows x 16 fp32)
     need += 10 * 18 * (9 * 25 * 16 * 256 + 2 * 4 * 64 * 64 * 16) * 4
