@@ -166,23 +166,30 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
   f += (size_t)(blockIdx.x % kFlagCopies) * a.fstride;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
+    const unsigned ep = a.epoch;
     int ok = 1;
+    // two coherent (sc1) 16-byte polls in flight: a completion is seen one load latency after it
+    // lands, not up to two
+    const brsrc rf = make_rsrc(f, (size_t)a.fstride * 4);
     for (int base = 0; base < n && ok; base += 256) {
       const int i0 = base + lane * 4;
-      for (int spins = 0;; ++spins) {
-        bool done = true;
-        if (i0 < n) {
-          const u32x4 v = ld_flags4(f + i0);
-          done = v[0] == a.epoch && (i0 + 1 >= n || v[1] == a.epoch) && (i0 + 2 >= n || v[2] == a.epoch) &&
-                 (i0 + 3 >= n || v[3] == a.epoch);
-        }
-        if (__all(done)) break;
-        if (spins > kSpinLimit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) != 0)) {
+      const int off = i0 < n ? i0 * 4 : kOob;
+      auto done = [&](u32x4 v) {
+        return i0 >= n || (v[0] == ep && (i0 + 1 >= n || v[1] == ep) && (i0 + 2 >= n || v[2] == ep) && (i0 + 3 >= n || v[3] == ep));
+      };
+      u32x4 va = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
+      for (int spins = 0;; spins += 2) {
+        __builtin_amdgcn_s_sleep(1);
+        u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
+        if (__all(done(va))) break;
+        __builtin_amdgcn_s_sleep(1);
+        va = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
+        if (__all(done(vb))) break;
+        if (spins > kSpinLimit || ((spins & 63) == 62 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) != 0)) {
           if (lane == 0) record_error(a);
           ok = 0;
           break;
         }
-        __builtin_amdgcn_s_sleep(1);
       }
     }
     if (lane == 0) *s_flag = ok;
@@ -310,9 +317,9 @@ __device__ __forceinline__ void store_wave_partials(float* red, const f32x4 (&ac
 }
 
 // Sum the compute waves' D fragments (red[wave][mt][t][lane], f32x4) in wave order and scatter
-// them row-major into the LDS tile T[64][TS] (column t*16 + n), which may alias red.  Every
-// thread of the workgroup calls it (it holds a barrier); thread tid < 256 owns m-tile tid/64,
-// lane tid%64 of every tile t (the copy wave takes m-tile 3: LDS work only).
+// them row-major into the LDS tile T[64][TS] (column t*16 + n), which must not alias red.  Thread
+// tid < 256 owns m-tile tid/64, lane tid%64 of every tile t (the copy wave takes m-tile 3: LDS
+// work only).
 template <int NT, int TS>
 __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
   const int tid = threadIdx.x;
@@ -324,7 +331,6 @@ __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
 #pragma unroll
     for (int w = 1; w < kCompWaves; ++w) v[t] += *reinterpret_cast<const f32x4*>(red + (((size_t)(w * 4 + mt) * NT + t) * 64 + ln) * 4);
   }
-  __syncthreads();
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -378,24 +384,33 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
   bool waited = false;
   for (int c = blockIdx.x; c < NC; c += gridDim.x) {
     const int b = c / kHorizon, t = c % kHorizon, r = b * kRowsPerSample + t;
-    // ---- loads that do not depend on the previous phase
+    // ---- loads that do not depend on the previous phase (waves 1 and 2 only: wave 0 polls, so
+    // it issues nothing ahead of its polls and loads its share after the wait)
     float4 wo[kOutRun / 4];
     float4 sc[2] = {}, sh[2] = {};
-    if (has_prev && comp) {
+    auto load_wo = [&]() {
 #pragma unroll
       for (int q = 0; q < kOutRun / 4; ++q)
         if (q < nq) wo[q] = *reinterpret_cast<const float4*>(a.out_w + (size_t)j * kWidth + k0 + q * 4);
-      if (tid < 128) {
-        const float* fmod = a.table + ((size_t)(s - 1) * NN + (NN - 1)) * kModW;
-        sc[0] = *reinterpret_cast<const float4*>(fmod + kc);
-        sc[1] = *reinterpret_cast<const float4*>(fmod + kc + 4);
-        sh[0] = *reinterpret_cast<const float4*>(fmod + kWidth + kc);
-        sh[1] = *reinterpret_cast<const float4*>(fmod + kWidth + kc + 4);
-      }
+    };
+    auto load_mod = [&]() {  // final norm: 1 + scale and shift of this thread's 8 columns
+      const float* fmod = a.table + ((size_t)(s - 1) * NN + (NN - 1)) * kModW;
+      sc[0] = *reinterpret_cast<const float4*>(fmod + kc);
+      sc[1] = *reinterpret_cast<const float4*>(fmod + kc + 4);
+      sh[0] = *reinterpret_cast<const float4*>(fmod + kWidth + kc);
+      sh[1] = *reinterpret_cast<const float4*>(fmod + kWidth + kc + 4);
+    };
+    if (has_prev && comp && tid >= 64) {
+      load_wo();
+      if (tid < 128) load_mod();
     }
     if (has_prev && !waited) {
       if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), kTiles, s_flag)) return false;
       waited = true;
+    }
+    if (has_prev && tid < 64) {
+      load_wo();
+      load_mod();
     }
     if (has_prev) {
       const size_t sl = (size_t)(s - 1) * (L + 1) + L;
@@ -554,14 +569,8 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   float* s_rstd = smem + kLdsWork;  // [64]
   float* s_bias = s_rstd + 64;      // [32] shift . W^T of the item's two tiles
   float* s_rs = s_bias + 32;        // [3][64] row sums of squares over tiles 22w .. 22w+21
-  float* red = s_rs + 192;          // [3 waves][4 m-tiles][NT][64 lanes][4]; then T
-  float* T = red;                   // [64][TS]
-  // the item's shift . W^T columns (static within the launch)
-  if (tid < 32) {
-    const int col = MODE == kModeQkv ? (tid < 16 ? tile0 * 16 + tid : (rotated ? tile0 + 8 : tile0 + 1) * 16 + tid - 16)
-                                     : (tid < 16 ? kQkvCols + tile0 * 16 + tid : kQkvCols + kMlp + tile0 * 16 + tid - 16);
-    s_bias[tid] = bias[col];
-  }
+  float* red = s_rs + 192;          // [3 waves][4 m-tiles][NT][64 lanes][4]
+  float* T = red + kCompWaves * 4 * NT * 256;  // [64][TS]
   PHASE_TS(s, l, PH, 1);
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
@@ -569,6 +578,12 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     if (!wait_flags(a, dep, ndep, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
+  // the item's shift . W^T columns (static within the launch; loaded here, not ahead of the polls)
+  if (tid < 32) {
+    const int col = MODE == kModeQkv ? (tid < 16 ? tile0 * 16 + tid : (rotated ? tile0 + 8 : tile0 + 1) * 16 + tid - 16)
+                                     : (tid < 16 ? kQkvCols + tile0 * 16 + tid : kQkvCols + kMlp + tile0 * 16 + tid - 16);
+    s_bias[tid] = bias[col];
+  }
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
   for (int b = 0; b < a.batch; ++b) {
     const int m0 = b * kRowsPerSample;
@@ -771,14 +786,10 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   unsigned* fmerge = flag_base(a, s, l, kPhMerge);
   // copy wave, workgroups without a qkv item: B5 gate_up(l) tile 0 -> A (lower half)
   if (blockIdx.x >= kQkvItems) copy_norm_w<kModeGateUp>(a, l, 0, smem);
-  constexpr int QSTR = 68;                             // one quarter of the head dim (+4) per row
   u16* s_q = reinterpret_cast<u16*>(smem + kLdsWork);  // [8 fragments][512] bf16 (2048 floats)
-  float* s_o = smem + kLdsWork;                        // [3 waves][16][QSTR] after the compute (aliases s_q)
-  float* s_f = s_o + kCompWaves * 16 * QSTR;           // [16][FSTR] merged partial
-  constexpr int FSTR = kHeadDim + 4;
-  float* s_m = s_f + 16 * FSTR;                        // [3][16] running max per wave
+  float* s_o = smem + kLdsWork;                        // [waves 1, 2][16 d-tiles][64 lanes][4] after the compute
+  float* s_m = s_o + 2 * 16 * 256;                     // [3][16] running max per wave
   float* s_l = s_m + 48;                               // [3][16] running sum per wave
-  float* s_w = s_l + 48;                               // [3][16] merge weights, then [16] max | [16] sum
   const u16* stg = reinterpret_cast<const u16*>(smem + kLdsStage);
   PHASE_TS(s, l, kPhSplit, 0);
   bool waited = false;
@@ -805,36 +816,38 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       lds_burst(smem + kLdsStage, kpre + (size_t)(2 * kbs) * 8 * 512, 16);
       lds_copy(smem + kLdsStage + 4096, vpre + (size_t)kbs * 16 * 512, 16);
     }
+    // waves 1 and 2 load their first block before the wait if it is from the static prefix; wave 0
+    // polls, so it issues nothing ahead of its polls
     KvBlock blk;
-    if (comp && kb0 < kb_hi && kb0 < nkb_pre) load(blk, kb0);
-    uint32_t sv0 = 0, sv1 = 0;  // key-valid bytes of the staged block (wave 0)
-    if (staged && wave == 0) {
-      sv0 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + g * 4);
-      sv1 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + 16 + g * 4);
-    }
+    if (comp && wave != 0 && kb0 < kb_hi && kb0 < nkb_pre) load(blk, kb0);
     PHASE_TS(s, l, kPhSplit, 1);
     if (!waited) {
       if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
       waited = true;
     }
     PHASE_TS(s, l, kPhSplit, 2);
-    // the row block's query fragments -> LDS (direct-to-LDS, compute waves), then the first
-    // block if it is an action-key block; the copy wave's staged block lands too
+    // the row block's query fragments -> LDS (direct-to-LDS, compute waves), then the blocks not
+    // yet loaded; the copy wave's staged block lands too
     const u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
+    uint32_t sv0 = 0, sv1 = 0;  // key-valid bytes of the staged block (wave 0)
     if (comp) {
       const int wu = __builtin_amdgcn_readfirstlane(wave);  // LDS addresses of direct-to-LDS loads are wave-uniform
       for (int f = wu; f < 8; f += kCompWaves)
         __builtin_amdgcn_global_load_lds(const_cast<u16*>(qs + afrag_offset(rbq, f, kHeadDim / 32)) + lane * 8, s_q + (size_t)f * 512, 16,
                                          0, 0);
-      if (kb0 < kb_hi && kb0 >= nkb_pre) load(blk, kb0);
+      if (kb0 < kb_hi && (wave == 0 || kb0 >= nkb_pre)) load(blk, kb0);
+      if (staged && wave == 0) {
+        sv0 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + g * 4);
+        sv1 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + 16 + g * 4);
+      }
     }
     wait_vmcnt<0>();
     __syncthreads();
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 oacc[16];
-    if (comp) {
 #pragma unroll
-      for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (comp) {
       for (int kb = kb0; kb < kb_hi; kb += kCompWaves) {
         if (kb != kb0) {
           if (kb == kbs && staged) {
@@ -855,62 +868,54 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       l_run += __shfl_xor(l_run, 32);
     }
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 4);
-    // ---- merge the 3 waves, one quarter of the head dim at a time: each wave puts its O rows of
-    // the quarter in LDS, then every thread combines one float4 of the quarter into s_f
+    // ---- merge the 3 waves: waves 1 and 2 put their O fragments and (max, sum) per row in LDS;
+    // wave 0 combines them with its own and stores the split's partial: fp32 [16 rows][D], row
+    // r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
     __syncthreads();  // s_q and the staged block are dead; s_o aliases s_q
     if (comp && g == 0) {
       s_m[wave * 16 + r16] = m_run;
       s_l[wave * 16 + r16] = l_run;
     }
+    if (wave == 1 || wave == 2) {
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(s_o + (((size_t)(wave - 1) * 16 + dt) * 64 + lane) * 4) = oacc[dt];
+    }
     __syncthreads();
-    if (tid < 16) {
-      float Mx = -INFINITY, Lx = 0.f;
+    if (tid < 64) {
+      float mw[3], Mx = -INFINITY, Lx = 0.f, ww[3];
 #pragma unroll
-      for (int v = 0; v < kCompWaves; ++v) Mx = fmaxf(Mx, s_m[v * 16 + tid]);
-#pragma unroll
-      for (int v = 0; v < kCompWaves; ++v) {
-        const float w = (s_m[v * 16 + tid] == -INFINITY) ? 0.f : __expf(s_m[v * 16 + tid] - Mx);
-        s_w[v * 16 + tid] = w;
-        Lx += s_l[v * 16 + tid] * w;
+      for (int v = 0; v < 3; ++v) {
+        mw[v] = s_m[v * 16 + r16];
+        Mx = fmaxf(Mx, mw[v]);
       }
-      s_w[kCompWaves * 16 + tid] = Mx;  // the split's running max and sum per row
-      s_w[kCompWaves * 16 + 16 + tid] = Lx;
-    }
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      // oacc[dt] holds O[row r16][dt*16 + g*4 + i]; quarter qq = d-tiles 4qq..4qq+3
-      if (comp) {
+      for (int v = 0; v < 3; ++v) {
+        ww[v] = (mw[v] == -INFINITY) ? 0.f : __expf(mw[v] - Mx);
+        Lx += s_l[v * 16 + r16] * ww[v];
+      }
+      float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim + (size_t)r16 * kHeadDim + g * 4;
 #pragma unroll
-        for (int d4 = 0; d4 < 4; ++d4) *reinterpret_cast<f32x4*>(s_o + (wave * 16 + r16) * QSTR + d4 * 16 + g * 4) = oacc[qq * 4 + d4];
+      for (int dt = 0; dt < 16; ++dt) {
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(s_o + ((size_t)dt * 64 + lane) * 4);
+        const f32x4 o2 = *reinterpret_cast<const f32x4*>(s_o + ((size_t)(16 + dt) * 64 + lane) * 4);
+        const f32x4 o = oacc[dt] * ww[0] + o1 * ww[1] + o2 * ww[2];
+        st_f32x4(part + dt * 16, float4{o[0], o[1], o[2], o[3]});
       }
-      __syncthreads();
-      // 16 rows x 16 float4 of the quarter: one per thread (the copy wave helps: LDS only)
-      {
-        const int row = tid >> 4, c4 = tid & 15;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < kCompWaves; ++w) v += *reinterpret_cast<const f32x4*>(s_o + (w * 16 + row) * QSTR + c4 * 4) * s_w[w * 16 + row];
-        *reinterpret_cast<f32x4*>(s_f + row * FSTR + qq * 64 + c4 * 4) = v;
+      if (g == 0) {
+        st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + r16, Mx);
+        st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + 16 + r16, Lx);
       }
-      __syncthreads();
-    }
-    if (comp) {
-      float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim;
-      for (int e4 = tid; e4 < 16 * kHeadDim / 4; e4 += kCompThreads) {
-        const int e = e4 * 4, row = e >> 8, col = e & 255;
-        st_f32x4(part + e, *reinterpret_cast<const float4*>(s_f + row * FSTR + col));
-      }
-      if (tid < 32) st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + tid, s_w[kCompWaves * 16 + tid]);
     }
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 5);
     publish(a, fsplit + bp * a.nsplit_pad + split, a.epoch);
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
     __syncthreads();  // the LDS tiles are reused by the next item
   }
-  copy_norm_w<kModeGateUp>(a, l, 1, smem);  // B6 gate_up(l) tile 1 -> A upper half
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
-  // on work of its own.
+  // on work of its own.  All four waves merge (the copy wave has nothing in flight by now): thread
+  // t owns row t/64 of the head pair (r16 = 2hp + (j&1) + 8*(j>>1)) and dims (t%64)*4 .. +3, and
+  // loads every split's (max, sum, O) at once.
   bool first_merge = true;
   u16* s_ob = reinterpret_cast<u16*>(smem + kLdsWork);  // [4 rows][D] bf16
   for (int role = blockIdx.x; role < kKSplit * nbp; role += gridDim.x) {
@@ -919,47 +924,37 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     if (first_merge) PHASE_TS(s, l, kPhMerge, 1);
     if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
     if (first_merge) PHASE_TS(s, l, kPhMerge, 2);
-    // element e: row j = e/64 of the head pair (r16 = 2hp + (j&1) + 8*(j>>1)), dims (e%64)*4..+3
-    if (comp) {
-      for (int e = tid; e < 256; e += kCompThreads) {
-        const int jr = e >> 6, rr = 2 * hp + (jr & 1) + 8 * (jr >> 1);
-        const int d0 = (e & 63) * 4;
-        float Mb = -INFINITY, Lb = 0.f;
-        f32x4 ob = {0.f, 0.f, 0.f, 0.f};
-        for (int c0 = 0; c0 < nsplit; c0 += 8) {
-          float mc[8], lc[8];
-          f32x4 oc[8];
+    {
+      const int jr = tid >> 6, rr = 2 * hp + (jr & 1) + 8 * (jr >> 1);
+      const int d0 = (tid & 63) * 4;
+      const brsrc rml = make_rsrc(apart_ml, (size_t)nsplit * nbp * 32 * 4);
+      const brsrc rpo = make_rsrc(apart, (size_t)nsplit * nbp * 16 * kHeadDim * 4);
+      float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
+      f32x4 oc[kMaxAttnSplits];
 #pragma unroll
-          for (int cc = 0; cc < 8; ++cc) {
-            const int c = c0 + cc;
-            mc[cc] = -INFINITY;
-            lc[cc] = 0.f;
-            oc[cc] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (c < nsplit) {
-              const float* ml = apart_ml + ((size_t)c * nbp + bp) * 32;
-              mc[cc] = ml[rr];
-              lc[cc] = ml[16 + rr];
-              oc[cc] = *reinterpret_cast<const f32x4*>(apart + (((size_t)c * nbp + bp) * 16 + rr) * kHeadDim + d0);
-            }
-          }
-          float Mn = Mb;
-#pragma unroll
-          for (int cc = 0; cc < 8; ++cc) Mn = fmaxf(Mn, mc[cc]);
-          const float rescale = (Mb == -INFINITY) ? 0.f : __expf(Mb - Mn);
-          Lb *= rescale;
-          ob *= rescale;
-#pragma unroll
-          for (int cc = 0; cc < 8; ++cc) {
-            const float wc = (mc[cc] == -INFINITY) ? 0.f : __expf(mc[cc] - Mn);
-            Lb += lc[cc] * wc;
-            ob += oc[cc] * wc;
-          }
-          Mb = Mn;
-        }
-        const float inv = 1.0f / Lb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_ob[jr * kHeadDim + d0 + i] = f2bf(ob[i] * inv);
+      for (int c = 0; c < kMaxAttnSplits; ++c) {
+        const bool ok = c < nsplit;
+        const int mo = (c * nbp + bp) * 32 + rr;
+        buf_f32(mc[c], rml, ok ? mo * 4 : kOob);
+        buf_f32(lc[c], rml, ok ? (mo + 16) * 4 : kOob);
+        oc[c] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rpo, ok ? (int)((((size_t)(c * nbp + bp) * 16 + rr) * kHeadDim + d0) * 4) : kOob, 0, 0));
       }
+      sched_fence();
+      float Mb = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < kMaxAttnSplits; ++c) Mb = fmaxf(Mb, c < nsplit ? mc[c] : -INFINITY);
+      float Lb = 0.f;
+      f32x4 ob = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kMaxAttnSplits; ++c) {
+        const float wc = (c >= nsplit || mc[c] == -INFINITY) ? 0.f : __expf(mc[c] - Mb);
+        Lb += lc[c] * wc;
+        ob += oc[c] * wc;
+      }
+      const float inv = 1.0f / Lb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_ob[jr * kHeadDim + d0 + i] = f2bf(ob[i] * inv);
     }
     __syncthreads();
     if (tid < 128) {
@@ -978,6 +973,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     first_merge = false;
     __syncthreads();  // s_ob is reused by the next role
   }
+  copy_norm_w<kModeGateUp>(a, l, 1, smem);  // B6 gate_up(l) tile 1 -> A upper half
   return true;
 }
 
@@ -1011,7 +1007,14 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   const int col = nt * 16;
   float4 g4[4] = {}, s14[4] = {};
   const bool next_g = !kDown || l + 1 < L;  // the last layer's output feeds the final norm only
+  PHASE_TS(s, l, PH, 1);
+  {
+    const unsigned* dep = kDown ? flag_base(a, s, l, kPhGu) + ksp * 64 : flag_base(a, s, l, kPhMerge) + ksp * a.nbp_pad;
+    if (!wait_flags(a, dep, kDown ? 64 : a.nbp, s_flag)) return false;
+  }
+  PHASE_TS(s, l, PH, 2);
   if (tid < 64) {
+    // the finisher's gate and 1 + scale (loaded after the polls, used much later)
     const float* gmod = a.table + ((size_t)s * NN + 2 * l + (kDown ? 1 : 0)) * kModW + 2 * kWidth + col;
     const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + (kDown ? 2 : 1)) * kModW + col;
 #pragma unroll
@@ -1020,12 +1023,6 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
       if (next_g) s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
     }
   }
-  PHASE_TS(s, l, PH, 1);
-  {
-    const unsigned* dep = kDown ? flag_base(a, s, l, kPhGu) + ksp * 64 : flag_base(a, s, l, kPhMerge) + ksp * a.nbp_pad;
-    if (!wait_flags(a, dep, kDown ? 64 : a.nbp, s_flag)) return false;
-  }
-  PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + (kDown ? kLdsB : kLdsC));  // this item's K-quarter fragments
   const u16* act = kDown ? a.act + slw * (size_t)R * kMlp : a.o + slw * (size_t)R * (kHeads * kHeadDim);
   // this phase's K-quarter partials [quarter][tile][row][16] (written once per launch)
@@ -1147,9 +1144,9 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
 // =============================================================================================
 // the kernel
 // =============================================================================================
-static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 <= kWorkFloats && 64 * 33 <= kCompWaves * 4 * 2 * 256, "norm GEMM working area");
+static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
 static_assert(kCompWaves * 4 * 256 + 64 * 17 <= kWorkFloats, "residual working area");
-static_assert(kCompWaves * 16 * 68 + 16 * (kHeadDim + 4) + 3 * 48 + 32 <= kWorkFloats && 2048 <= kCompWaves * 16 * 68, "attention working area");
+static_assert(2 * 16 * 256 + 2 * 48 <= kWorkFloats && 2048 <= 2 * 16 * 256, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
 
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
