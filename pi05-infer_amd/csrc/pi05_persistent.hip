@@ -36,15 +36,25 @@ namespace pi05 {
 // records s_memrealtime (100 MHz) at fixed points of every phase of Euler step 1, layers 0..3,
 // into pi05_phase_ts[workgroup][layer*7 + phase][event].  Compiled out otherwise.
 #ifdef PI05_PHASE_TIMESTAMPS
-__device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 10];
+constexpr int kCompThreadsTs = 192;
+__device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 16];
 #define PHASE_TS(s, l, ph, ev)                                                                  \
   do {                                                                                          \
     if ((s) == 1 && (l) < 4 && threadIdx.x == 0 && blockIdx.x < 256)                           \
-      pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 10 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
+      pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+// the same, recorded by the copy wave's first lane
+#define PHASE_TS_CW(s, l, ph, ev)                                                               \
+  do {                                                                                          \
+    if ((s) == 1 && (l) < 4 && threadIdx.x == kCompThreadsTs && blockIdx.x < 256)              \
+      pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 #else
 #define PHASE_TS(s, l, ph, ev) \
   do {                         \
+  } while (0)
+#define PHASE_TS_CW(s, l, ph, ev) \
+  do {                            \
   } while (0)
 #endif
 
@@ -625,11 +635,13 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     if (b == 0) PHASE_TS(s, l, PH, 4);
     __syncthreads();  // every wave is done with region A; the row sums are in LDS
     if (b == 0) PHASE_TS(s, l, PH, 3);
+    if (b == 0) PHASE_TS_CW(s, l, PH, 8);
     if (MODE == kModeQkv && b == a.batch - 1) copy_norm_w<kModeGateUp>(a, l, 0, smem);  // B5 gate_up(l) tile 0 -> A
     if constexpr (MODE == kModeGateUp) {
       int ln;
       if (b == a.batch - 1 && next_layer(a, s, l, &ln)) copy_norm_w<kModeQkv>(a, ln, 0, smem);  // B2 next qkv tile 0 -> A
     }
+    if (b == 0) PHASE_TS_CW(s, l, PH, 9);
     if (comp) store_wave_partials<NT>(red, acc, wave, lane);
     if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
     __syncthreads();
@@ -810,12 +822,14 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     const int kb0 = kb_lo + wave;
     const int kbs = kb_lo + kCompWaves;  // wave 0's second block, staged in LDS if from the prefix
     const bool staged = kbs < kb_hi && kbs < nkb_pre;
+    if (item == (int)blockIdx.x) PHASE_TS_CW(s, l, kPhSplit, 10);
     if (staged) {
       // copy wave: K fragments of key tiles 2kbs, 2kbs+1 and V fragments of block kbs are two
       // contiguous runs of 16
       lds_burst(smem + kLdsStage, kpre + (size_t)(2 * kbs) * 8 * 512, 16);
       lds_copy(smem + kLdsStage + 4096, vpre + (size_t)kbs * 16 * 512, 16);
     }
+    if (item == (int)blockIdx.x) PHASE_TS_CW(s, l, kPhSplit, 11);
     // waves 1 and 2 load their first block before the wait if it is from the static prefix; wave 0
     // polls, so it issues nothing ahead of its polls
     KvBlock blk;
@@ -973,7 +987,9 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     first_merge = false;
     __syncthreads();  // s_ob is reused by the next role
   }
+  PHASE_TS_CW(s, l, kPhMerge, 10);
   copy_norm_w<kModeGateUp>(a, l, 1, smem);  // B6 gate_up(l) tile 1 -> A upper half
+  PHASE_TS_CW(s, l, kPhMerge, 11);
   return true;
 }
 
@@ -992,10 +1008,12 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = blockIdx.x;
   PHASE_TS(s, l, PH, 0);
+  PHASE_TS_CW(s, l, PH, 10);
   if constexpr (kDown) {
     int ln;
     if (next_layer(a, s, l, &ln)) copy_norm_w<kModeQkv>(a, ln, 1, smem);  // B3 next qkv tile 1 -> A
   }
+  PHASE_TS_CW(s, l, PH, 11);
   if (item >= kTiles * kKSplit) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const bool comp = tid < kCompThreads;
