@@ -36,32 +36,30 @@ namespace pi05 {
 // records s_memrealtime (100 MHz) at fixed points of every phase of Euler step 1, layers 0..3,
 // into pi05_phase_ts[workgroup][layer*7 + phase][event].  Compiled out otherwise.
 #ifdef PI05_PHASE_TIMESTAMPS
-constexpr int kCompThreadsTs = 192;
 __device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 16];
 #define PHASE_TS(s, l, ph, ev)                                                                  \
   do {                                                                                          \
     if ((s) == 1 && (l) < 4 && threadIdx.x == 0 && blockIdx.x < 256)                           \
       pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
-// the same, recorded by the copy wave's first lane
-#define PHASE_TS_CW(s, l, ph, ev)                                                               \
+// the same, recorded by the first lane of wave w
+#define PHASE_TS_W(w, s, l, ph, ev)                                                             \
   do {                                                                                          \
-    if ((s) == 1 && (l) < 4 && threadIdx.x == kCompThreadsTs && blockIdx.x < 256)              \
+    if ((s) == 1 && (l) < 4 && threadIdx.x == 64 * (w) && blockIdx.x < 256)                    \
       pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 #else
 #define PHASE_TS(s, l, ph, ev) \
   do {                         \
   } while (0)
-#define PHASE_TS_CW(s, l, ph, ev) \
-  do {                            \
+#define PHASE_TS_W(w, s, l, ph, ev) \
+  do {                              \
   } while (0)
 #endif
 
 constexpr int kCompWaves = 3;
 constexpr int kCompThreads = kCompWaves * 64;
 constexpr int kThreads = kCompThreads + 64;  // + the copy wave
-constexpr int kBurst = 32;                   // fragments per copy burst
 constexpr int kSpinLimit = 1 << 20;          // polls (each >= ~1 us): a legitimate wait spans a few phases
 constexpr int kRowsPerSample = 64;           // padded rows per sample (50 action tokens)
 
@@ -70,19 +68,35 @@ __device__ __forceinline__ void st_u32(void* p, uint32_t v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-// One 16-byte write-through vector store (whole 16-byte chunks, so lines are assembled from full
-// chunks).  Completion is tracked by vmcnt like any vector store; publish() waits for it.  A
-// vector store of more than 8 bytes reads its data VGPRs after issue, so the next instruction
-// must not be a VALU write to them: the compiler cannot see into the asm, hence the wait states.
-__device__ __forceinline__ void st_wt16(void* p, u32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
+// Buffer resources: a load at a byte offset past the resource's size returns zeros without
+// touching memory (the hardware range check).  Masking lanes (padded rows) and surplus k-steps
+// this way keeps the load sequences free of branches, so the compiler can count the loads in
+// flight and let each MFMA wait only for its own operands.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+constexpr int kOob = 0x7fffff00;  // an offset past every resource
+__device__ __forceinline__ brsrc make_rsrc(const void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ void st_bf16x8(u16* p, const u16 (&v)[8]) {
-  st_wt16(p, u32x4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
-                   (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)});
+// A pointer every lane holds the same value of, moved to scalar registers.
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
 }
-__device__ __forceinline__ void st_f32x4(float* p, float4 v) {
-  st_wt16(p, u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)});
+// One 16-byte write-through (sc1) store at `off` bytes past `base` (the same in every lane):
+// whole 16-byte chunks, so lines are assembled from full chunks.  A buffer store the compiler
+// sees, so it schedules the loads feeding it freely; completion is tracked by vmcnt like any
+// vector store, and publish() waits for it.
+__device__ __forceinline__ void st_wt16(const void* base, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(uniform_ptr(base), 0x7fffffff), off, 0, 16);
+}
+__device__ __forceinline__ void st_bf16x8(u16* base, size_t idx, const u16 (&v)[8]) {
+  st_wt16(base, (uint32_t)(idx * 2), u32x4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                                            (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)});
+}
+__device__ __forceinline__ void st_f32x4(float* base, size_t idx, float4 v) {
+  st_wt16(base, (uint32_t)(idx * 4), u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)});
 }
 __device__ __forceinline__ void st_f32(float* p, float v) { st_u32(p, __float_as_uint(v)); }
 __device__ __forceinline__ uint32_t ld_u32(const void* p) {
@@ -112,15 +126,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ bool copy_wave() { return threadIdx.x >= kCompThreads; }
 
-// Buffer resources: a load at a byte offset past the resource's size returns zeros without
-// touching memory (the hardware range check).  Masking lanes (padded rows) and surplus k-steps
-// this way keeps the load sequences free of branches, so the compiler can count the loads in
-// flight and let each MFMA wait only for its own operands.
-typedef __amdgpu_buffer_rsrc_t brsrc;
-constexpr int kOob = 0x7fffff00;  // an offset past every resource
-__device__ __forceinline__ brsrc make_rsrc(const void* base, size_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
+// s_waitcnt vmcnt(0) that is also a compiler barrier for memory operations: every store issued
+// before it in program order stays before it, so its completion is what the wait observes.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Operand blocks are loaded with the compiler's own buffer loads (so it counts them) and fenced
 // with a scheduling barrier after the last one: the scheduler may not sink a load next to its
 // use, so a whole block is in flight at once and each MFMA waits only for its own fragments.
@@ -213,7 +222,7 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
 // The compute waves' stores for this item are complete -> wave 0 sets the item's flag in every
 // replica.  Every thread of the workgroup calls it (it holds a barrier).
 __device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsigned epoch) {
-  if (!copy_wave()) wait_vmcnt<0>();
+  if (!copy_wave()) wait_stores();
   __syncthreads();
   if (threadIdx.x < kFlagCopies) st_u32(flag + (size_t)threadIdx.x * a.fstride, epoch);
 }
@@ -221,7 +230,7 @@ __device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsig
 // Last-arrival election on a device-scope counter that every launch advances by `n` per slot;
 // the compute waves' stores are complete before the workgroup counts itself in.
 __device__ bool last_arrival(const MegaArgs& a, unsigned* ctr, unsigned n, int* s_flag) {
-  if (!copy_wave()) wait_vmcnt<0>();
+  if (!copy_wave()) wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -235,19 +244,21 @@ __device__ bool last_arrival(const MegaArgs& a, unsigned* ctr, unsigned n, int* 
 
 // ---- LDS map (floats) -------------------------------------------------------------------------
 //   A: qkv or gate_up weight fragments of this workgroup's item: two 32-fragment tiles (64 KiB);
-//      during attention its upper half stages one 32-key KV block
+//      during attention its upper half holds the O fragments of waves 1 and 2
 //   B: down_proj weight fragments (32 KiB)
 //   C: o_proj weight fragments (16 KiB)
 //   then the working area of the current phase.
-// Copy schedule (copy wave, per layer l; B1..B6 are bursts of at most 32 fragments):
-//   gate_up(l-1) start : wait for all copies (gate_up(l-1) weights), B1 o_proj(l) -> C
-//   gate_up(l-1) MFMA  : B2 qkv(l) tile 0 -> A                     (workgroups with a qkv item)
-//   down(l-1) start    : B3 qkv(l) tile 1 -> A                     (workgroups with a qkv item)
-//   qkv(l) start       : wait for all copies (qkv(l), o_proj(l) weights), B4 down(l) -> B
-//   qkv(l) MFMA        : B5 gate_up(l) tile 0 -> A  (workgroups without a qkv item: attention start)
-//   attention(l)       : per split item, the KV block wave 0 attends second -> A upper half
-//   attention(l) end   : B6 gate_up(l) tile 1 -> A upper half
-// Before each burst the copy wave waits until at most 31 of its copies are in flight.
+// Copy schedule (copy wave, per layer l).  A 63-copy burst takes about 1.3 us to issue and its
+// fragments land 2-3 us later, so every burst is issued just before a flag wait (the copy wave
+// reaches the wait's barrier while the producers are still working) and never between two
+// compute barriers, where it would hold up the compute waves:
+//   qkv(l) wait      : all copies landed (qkv(l), o_proj(l) weights); down(l) -> B (32)
+//   attention(l) wait: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's own
+//                      KV block loads
+//   o_proj(l) wait   : gate_up(l) tile 0 fragments 16..31 (16) and tile 1 (32) -> A
+//   gate_up(l) wait  : all copies landed (gate_up(l) weights); o_proj(l+1) -> C (16)
+//   down(l) wait     : qkv(l+1) tile 0 (32) and tile 1 fragments 0..30 (31) -> A
+// so at most 63 copies are ever in flight and a burst never waits for the one before it.
 constexpr int kLdsA = 0;
 constexpr int kLdsB = kLdsA + 16384;
 constexpr int kLdsC = kLdsB + 8192;
@@ -255,43 +266,48 @@ constexpr int kLdsWork = kLdsC + 4096;
 constexpr int kWorkFloats = 8736;
 constexpr int kLdsFloats = kLdsWork + kWorkFloats;
 static_assert(kLdsFloats * 4 <= 160 * 1024, "LDS budget of a gfx950 workgroup");
-constexpr int kLdsStage = kLdsA + 8192;  // upper half of A: one staged KV block (32 KiB) during attention
+constexpr int kLdsA1 = kLdsA + 8192;  // upper half of A (tile 1); during attention: wave O slots
 
-// Direct-to-LDS copy of a run of nfrag contiguous 1 KiB fragments by the copy wave: fragment f of
-// src lands at dst + f KiB.  Not unrolled, so the addresses are formed as the loop goes rather
-// than all held in registers.
-__device__ __forceinline__ void lds_copy(float* dst, const u16* src, int nfrag) {
+// A burst of N contiguous 1 KiB fragments (N <= 63, a compile-time count) from src to LDS dst by
+// the copy wave: first make room (at most 63 - N copies in flight), then N buffer loads straight
+// into LDS (fragment f of src lands at dst + f KiB).  One VGPR holds the lane offset and the
+// fragment offset is a scalar, and the sequence is unrolled, so the compiler counts the copies
+// exactly and waits for later loads of this wave precisely.
+template <int N>
+__device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
+  static_assert(N > 0 && N <= 63, "vmcnt range");
   if (!copy_wave()) return;
-  const u16* p = src + (threadIdx.x & 63) * 8;
+  wait_vmcnt<63 - N>();
+  const brsrc r = make_rsrc(src, (size_t)N * 1024);
+  const unsigned vo = (threadIdx.x & 63) * 16;
   u16* d = reinterpret_cast<u16*>(dst);
-#pragma unroll 1
-  for (int f = 0; f < nfrag; ++f) __builtin_amdgcn_global_load_lds(const_cast<u16*>(p) + (size_t)f * 512, d + (size_t)f * 512, 16, 0, 0);
-}
-// A burst (nfrag <= kBurst): first make room (at most 31 copies in flight), then copy.
-__device__ __forceinline__ void lds_burst(float* dst, const u16* src, int nfrag) {
-  if (!copy_wave()) return;
-  wait_vmcnt<kBurst - 1>();
-  lds_copy(dst, src, nfrag);
+#pragma unroll
+  for (int f = 0; f < N; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, vo, f * 1024, 0, 0);
 }
 
-// Tile `which` (0 or 1) of the qkv (MODE = kModeQkv) or gate_up weights of item blockIdx.x -> A.
+// Fragments [F0, F0 + N) of tile `which` (0 or 1) of the qkv (MODE = kModeQkv) or gate_up
+// weights of item blockIdx.x -> region A.  A qkv item's tile 1 is copied without its last
+// fragment (k-step 31), which the wave owning that k-step loads into registers: both qkv tiles
+// then fit one 63-copy burst.
 template <int MODE>
-__device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
+__device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
   const int p = blockIdx.x;
-  if (p >= (MODE == kModeQkv ? kQkvItems : kGuItems)) return;
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
-  const u16* t;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
     const int head = p >> 3, dt = p & 7;
     const int tile0 = rotated ? head * 16 + dt : 144 + 2 * (p - 72);
     const int tile = which == 0 ? tile0 : (rotated ? tile0 + 8 : tile0 + 1);
-    t = wl + kOffQkv + (size_t)tile * KSTEPS * 512;
+    return wl + kOffQkv + (size_t)tile * KSTEPS * 512;
   } else {
-    t = wl + (which == 0 ? kOffGate : kOffUp) + (size_t)p * KSTEPS * 512;
+    return wl + (which == 0 ? kOffGate : kOffUp) + (size_t)p * KSTEPS * 512;
   }
-  lds_burst(smem + kLdsA + which * KSTEPS * 256, t, KSTEPS);
+}
+template <int MODE, int F0, int N>
+__device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
+  if (!copy_wave() || blockIdx.x >= (MODE == kModeQkv ? kQkvItems : kGuItems)) return;
+  lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE>(a, l, which) + F0 * 512);
 }
 
 // o_proj (KSTEPS = 64, region C) or down_proj (KSTEPS = 128, region B) weights of item
@@ -300,12 +316,11 @@ template <int KSTEPS>
 __device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
   constexpr bool kDown = KSTEPS == kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit;
-  static_assert(KQ <= kBurst, "one burst per K quarter");
   const int item = blockIdx.x;
-  if (item >= kTiles * kKSplit) return;
+  if (!copy_wave() || item >= kTiles * kKSplit) return;
   const int nt = item % kTiles, ksp = item / kTiles;
   const u16* tile = a.wpack + (size_t)l * kLayerElems + (kDown ? kOffDown : kOffO) + (size_t)nt * KSTEPS * 512 + (size_t)ksp * KQ * 512;
-  lds_burst(smem + (kDown ? kLdsB : kLdsC), tile, KQ);
+  lds_burst<KQ>(smem + (kDown ? kLdsB : kLdsC), tile);
 }
 
 // The layer after (s, l): (s, l + 1), or (s + 1, 0) after the last layer; false past the loop.
@@ -334,17 +349,20 @@ template <int NT, int TS>
 __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
   const int tid = threadIdx.x;
   const int mt = tid >> 6, ln = tid & 63;
-  f32x4 v[NT];
+  f32x4 r[kCompWaves][NT];
+#pragma unroll
+  for (int w = 0; w < kCompWaves; ++w)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) r[w][t] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * 4 + mt) * NT + t) * 64 + ln) * 4);
+  sched_fence();  // every read in flight before the first sum
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    v[t] = *reinterpret_cast<const f32x4*>(red + (((size_t)(0 * 4 + mt) * NT + t) * 64 + ln) * 4);
+    f32x4 v = r[0][t];
 #pragma unroll
-    for (int w = 1; w < kCompWaves; ++w) v[t] += *reinterpret_cast<const f32x4*>(red + (((size_t)(w * 4 + mt) * NT + t) * 64 + ln) * 4);
+    for (int w = 1; w < kCompWaves; ++w) v += r[w][t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) T[(mt * 16 + (ln >> 4) * 4 + i) * TS + t * 16 + (ln & 15)] = v[i];
   }
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) T[(mt * 16 + (ln >> 4) * 4 + i) * TS + t * 16 + (ln & 15)] = v[t][i];
 }
 
 // Row sums of squares, tiles [t0, t0 + 32), of the 64 rows of sample b (lane = row) from the
@@ -515,8 +533,8 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
           const float hf = bf2f(hv8[q]);
           ss += hf * hf;
         }
-        st_bf16x8(a.h + sl * R * kWidth + afrag_index(r, k, kWidth / 32), hv8);
-        st_bf16x8(a.g + slg * R * kWidth + afrag_index(r, k, kWidth / 32), gv8);
+        st_bf16x8(a.h + sl * R * kWidth, afrag_index(r, k, kWidth / 32), hv8);
+        st_bf16x8(a.g + slg * R * kWidth, afrag_index(r, k, kWidth / 32), gv8);
         ss += __shfl_xor(ss, 1);  // the tile's other 8 columns
         if ((tid & 1) == 0) st_f32(a.ss + (sl * kTiles + (tid >> 1)) * R + r, ss);
       }
@@ -581,6 +599,24 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   float* s_rs = s_bias + 32;        // [3][64] row sums of squares over tiles 22w .. 22w+21
   float* red = s_rs + 192;          // [3 waves][4 m-tiles][NT][64 lanes][4]
   float* T = red + kCompWaves * 4 * NT * 256;  // [64][TS]
+  // static operands, loaded ahead of the polls by waves 1 and 2 (wave 0 polls, so it issues
+  // nothing before them): wave 2's qkv tile-1 fragment of k-step 31 (not in LDS), and the RoPE
+  // cos/sin chunks of the first sample for the epilogue threads 64..163 (row, half)
+  bf16x8 w31 = {};
+  u16x8 rcs[4] = {};
+  const int et = tid - 64;  // RoPE epilogue thread: row et/2, half et%2
+  const bool rope_thread = MODE == kModeQkv && rotated && et >= 0 && et < 2 * kHorizon;
+  auto load_rope = [&](int b) {
+    const size_t cr = (size_t)(b * kHorizon + (et >> 1)) * kHeadDim + dt * 16 + (et & 1) * 8;
+    rcs[0] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr);
+    rcs[1] = *reinterpret_cast<const u16x8*>(a.sin_tab + cr);
+    rcs[2] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr + kHalfDim);
+    rcs[3] = *reinterpret_cast<const u16x8*>(a.sin_tab + cr + kHalfDim);
+  };
+  if constexpr (MODE == kModeQkv) {
+    if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(norm_w_tile<kModeQkv>(a, l, 1) + 31 * 512 + lane * 8));
+    if (rope_thread) load_rope(0);
+  }
   PHASE_TS(s, l, PH, 1);
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
@@ -626,22 +662,17 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // zero A for wave 2's surplus step: any finite weights (k-step 31's)
+      // zero A for wave 2's surplus step: any finite weights (k-step 31's); qkv tile 1's k-step 31
+      // fragment is wave 2's register copy
       mfma_steps<KSW, NT, 0>(acc, hr, [&](int t, int s2) {
         const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
+        if (MODE == kModeQkv && t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
         return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
       });
     }
     if (b == 0) PHASE_TS(s, l, PH, 4);
     __syncthreads();  // every wave is done with region A; the row sums are in LDS
     if (b == 0) PHASE_TS(s, l, PH, 3);
-    if (b == 0) PHASE_TS_CW(s, l, PH, 8);
-    if (MODE == kModeQkv && b == a.batch - 1) copy_norm_w<kModeGateUp>(a, l, 0, smem);  // B5 gate_up(l) tile 0 -> A
-    if constexpr (MODE == kModeGateUp) {
-      int ln;
-      if (b == a.batch - 1 && next_layer(a, s, l, &ln)) copy_norm_w<kModeQkv>(a, ln, 0, smem);  // B2 next qkv tile 0 -> A
-    }
-    if (b == 0) PHASE_TS_CW(s, l, PH, 9);
     if (comp) store_wave_partials<NT>(red, acc, wave, lane);
     if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
     __syncthreads();
@@ -653,20 +684,25 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
         // (x*cos) + (rotate_half(x)*sin), rotate_half(x) = cat(-x_hi, x_lo), from the bf16
         // GEMM values (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216); chunk
         // (row, half): 8 dims d and their partners d + 128
-        if (tid < 2 * kHorizon) {
-          const int row = tid >> 1, half = tid & 1;
-          const size_t cr = (size_t)(b * kHorizon + row) * kHeadDim + dt * 16 + half * 8;
-          const u16x8 cs_lo = *reinterpret_cast<const u16x8*>(a.cos_tab + cr);
-          const u16x8 sn_lo = *reinterpret_cast<const u16x8*>(a.sin_tab + cr);
-          const u16x8 cs_hi = *reinterpret_cast<const u16x8*>(a.cos_tab + cr + kHalfDim);
-          const u16x8 sn_hi = *reinterpret_cast<const u16x8*>(a.sin_tab + cr + kHalfDim);
+        if (rope_thread) {
+          const int row = et >> 1, half = et & 1;
+          if (b > 0) load_rope(b);
+          const u16x8 cs_lo = rcs[0], sn_lo = rcs[1], cs_hi = rcs[2], sn_hi = rcs[3];
           const float rstd = s_rstd[row];
+          float tl[8], th[8], bl[8], bh[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            tl[q] = T[row * TS + half * 8 + q];
+            th[q] = T[row * TS + 16 + half * 8 + q];
+            bl[q] = s_bias[half * 8 + q];
+            bh[q] = s_bias[16 + half * 8 + q];
+          }
+          sched_fence();
           u16 olo[8], ohi[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
-            const int cl = half * 8 + q;
-            const float x_lo = round_bf(__builtin_fmaf(rstd, T[row * TS + cl], s_bias[cl]));
-            const float x_hi = round_bf(__builtin_fmaf(rstd, T[row * TS + 16 + cl], s_bias[16 + cl]));
+            const float x_lo = round_bf(__builtin_fmaf(rstd, tl[q], bl[q]));
+            const float x_hi = round_bf(__builtin_fmaf(rstd, th[q], bh[q]));
             olo[q] = f2bf(fsub(fmul(x_lo, bf2f(cs_lo[q])), fmul(x_hi, bf2f(sn_lo[q]))));
             ohi[q] = f2bf(fadd(fmul(x_hi, bf2f(cs_hi[q])), fmul(x_lo, bf2f(sn_hi[q]))));
           }
@@ -674,12 +710,12 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
           if (head < kHeads) {
             u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
             const int qrow = (m0 + row) * kQRowsPerTok + head;
-            st_bf16x8(qs + afrag_index(qrow, d, kHeadDim / 32), olo);
-            st_bf16x8(qs + afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
+            st_bf16x8(qs, afrag_index(qrow, d, kHeadDim / 32), olo);
+            st_bf16x8(qs, afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
           } else {
             u16* kc = a.ksuf + (slw * a.batch + b) * 64 * kHeadDim;
-            st_bf16x8(kc + kfrag_index(row, d), olo);
-            st_bf16x8(kc + kfrag_index(row, d + kHalfDim), ohi);
+            st_bf16x8(kc, kfrag_index(row, d), olo);
+            st_bf16x8(kc, kfrag_index(row, d + kHalfDim), ohi);
           }
         }
       } else if (comp) {
@@ -694,7 +730,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
           }
           const int dv = (tile0 - 144) * 16 + dcol;
           u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
-          st_bf16x8(vc + ((size_t)kb * 16 + (dv >> 4)) * 512 + (size_t)(gg * 16 + (dv & 15)) * 8, v8);
+          st_bf16x8(vc, ((size_t)kb * 16 + (dv >> 4)) * 512 + (size_t)(gg * 16 + (dv & 15)) * 8, v8);
         }
       }
     } else {
@@ -703,15 +739,23 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
       if (tid < 2 * kHorizon) {
         const int row = tid >> 1, half = tid & 1;
         const float rstd = s_rstd[row];
+        float tg[8], tu[8], bg[8], bu[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          tg[q] = T[row * TS + half * 8 + q];
+          tu[q] = T[row * TS + 16 + half * 8 + q];
+          bg[q] = s_bias[half * 8 + q];
+          bu[q] = s_bias[16 + half * 8 + q];
+        }
+        sched_fence();
         u16 o8[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const int cl = half * 8 + q;
-          const float gt = round_bf(__builtin_fmaf(rstd, T[row * TS + cl], s_bias[cl]));
-          const float up = __builtin_fmaf(rstd, T[row * TS + 16 + cl], s_bias[16 + cl]);
+          const float gt = round_bf(__builtin_fmaf(rstd, tg[q], bg[q]));
+          const float up = __builtin_fmaf(rstd, tu[q], bu[q]);
           o8[q] = f2bf(fmul(gelu_tanh(gt), up));
         }
-        st_bf16x8(a.act + slw * (size_t)R * kMlp + afrag_index(m0 + row, tile0 * 16 + half * 8, kMlp / 32), o8);
+        st_bf16x8(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + row, tile0 * 16 + half * 8, kMlp / 32), o8);
       }
     }
     __syncthreads();  // T and s_rstd are reused by the next sample
@@ -796,15 +840,14 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   float* apart_ml = a.apart_ml + slw * (size_t)nsplit * nbp * 32;
   unsigned* fsplit = flag_base(a, s, l, kPhSplit);
   unsigned* fmerge = flag_base(a, s, l, kPhMerge);
-  // copy wave, workgroups without a qkv item: B5 gate_up(l) tile 0 -> A (lower half)
-  if (blockIdx.x >= kQkvItems) copy_norm_w<kModeGateUp>(a, l, 0, smem);
   u16* s_q = reinterpret_cast<u16*>(smem + kLdsWork);  // [8 fragments][512] bf16 (2048 floats)
-  float* s_o = smem + kLdsWork;                        // [waves 1, 2][16 d-tiles][64 lanes][4] after the compute
-  float* s_m = s_o + 2 * 16 * 256;                     // [3][16] running max per wave
-  float* s_l = s_m + 48;                               // [3][16] running sum per wave
-  const u16* stg = reinterpret_cast<const u16*>(smem + kLdsStage);
+  // O fragments of waves 1..3 ([16 d-tiles][64 lanes][4] each): waves 1, 2 in the upper half of
+  // A, wave 3 behind s_q; then the running max and sum of every wave
+  auto o_slot = [&](int w) { return w < 3 ? smem + kLdsA1 + (w - 1) * 4096 : smem + kLdsWork + 2048; };
+  float* s_m = smem + kLdsWork + 2048 + 4096;  // [4][16]
+  float* s_l = s_m + 64;                       // [4][16]
   PHASE_TS(s, l, kPhSplit, 0);
-  bool waited = false;
+  bool waited = false, burst = false;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int bp = item % nbp, split = item / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
@@ -819,21 +862,21 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       if (kb >= nkb_pre) load_kv_block(blk, ksf, vsf, valid + kb * 32, kb - nkb_pre, lane);
       else load_kv_block(blk, kpre, vpre, valid + kb * 32, kb, lane);
     };
-    const int kb0 = kb_lo + wave;
-    const int kbs = kb_lo + kCompWaves;  // wave 0's second block, staged in LDS if from the prefix
-    const bool staged = kbs < kb_hi && kbs < nkb_pre;
-    if (item == (int)blockIdx.x) PHASE_TS_CW(s, l, kPhSplit, 10);
-    if (staged) {
-      // copy wave: K fragments of key tiles 2kbs, 2kbs+1 and V fragments of block kbs are two
-      // contiguous runs of 16
-      lds_burst(smem + kLdsStage, kpre + (size_t)(2 * kbs) * 8 * 512, 16);
-      lds_copy(smem + kLdsStage + 4096, vpre + (size_t)kbs * 16 * 512, 16);
-    }
-    if (item == (int)blockIdx.x) PHASE_TS_CW(s, l, kPhSplit, 11);
-    // waves 1 and 2 load their first block before the wait if it is from the static prefix; wave 0
-    // polls, so it issues nothing ahead of its polls
+    // Blocks: the copy wave attends the split's first block if it is from the static prefix (it
+    // loads it before the polls and before its gate_up copies, so the copies never delay it);
+    // compute wave w attends blocks first + o(w), + 3, ... with o = 2, 0, 1 for waves 0, 1, 2
+    // (wave 0 polls, so it gets the block it loads last).  Waves 1 and 2 load their first block
+    // ahead of the polls when it is from the prefix.
+    const bool cw_block = kb_lo < kb_hi && kb_lo < nkb_pre;
+    const int first = kb_lo + (cw_block ? 1 : 0);
+    const int kb0 = copy_wave() ? kb_lo : first + (wave == 0 ? 2 : wave - 1);
+    const bool has_block = copy_wave() ? cw_block : kb0 < kb_hi;
     KvBlock blk;
-    if (comp && wave != 0 && kb0 < kb_hi && kb0 < nkb_pre) load(blk, kb0);
+    if (wave != 0 && has_block && kb0 < nkb_pre) load(blk, kb0);
+    if (!burst) {
+      copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
+      burst = true;
+    }
     PHASE_TS(s, l, kPhSplit, 1);
     if (!waited) {
       if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
@@ -841,79 +884,78 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     }
     PHASE_TS(s, l, kPhSplit, 2);
     // the row block's query fragments -> LDS (direct-to-LDS, compute waves), then the blocks not
-    // yet loaded; the copy wave's staged block lands too
+    // yet loaded
     const u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
-    uint32_t sv0 = 0, sv1 = 0;  // key-valid bytes of the staged block (wave 0)
     if (comp) {
       const int wu = __builtin_amdgcn_readfirstlane(wave);  // LDS addresses of direct-to-LDS loads are wave-uniform
       for (int f = wu; f < 8; f += kCompWaves)
         __builtin_amdgcn_global_load_lds(const_cast<u16*>(qs + afrag_offset(rbq, f, kHeadDim / 32)) + lane * 8, s_q + (size_t)f * 512, 16,
                                          0, 0);
-      if (kb0 < kb_hi && (wave == 0 || kb0 >= nkb_pre)) load(blk, kb0);
-      if (staged && wave == 0) {
-        sv0 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + g * 4);
-        sv1 = *reinterpret_cast<const uint32_t*>(valid + kbs * 32 + 16 + g * 4);
-      }
+      if (has_block && (wave == 0 || kb0 >= nkb_pre)) load(blk, kb0);
+      wait_vmcnt<0>();  // the query fragments have landed in LDS (and this wave's block)
     }
-    wait_vmcnt<0>();
     __syncthreads();
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 oacc[16];
 #pragma unroll
     for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (comp) {
+    if (copy_wave()) {
+      if (has_block) attend_block_lds(blk, s_q, lane, m_run, l_run, oacc);
+    } else {
       for (int kb = kb0; kb < kb_hi; kb += kCompWaves) {
-        if (kb != kb0) {
-          if (kb == kbs && staged) {
-            // the staged block, in load_kv_block's register order
-#pragma unroll
-            for (int f = 0; f < 16; ++f) blk.k[f] = *reinterpret_cast<const bf16x8*>(stg + (size_t)f * 512 + lane * 8);
-#pragma unroll
-            for (int f = 0; f < 16; ++f) blk.v[f] = *reinterpret_cast<const bf16x8*>(stg + (size_t)(16 + f) * 512 + lane * 8);
-            blk.valid0 = sv0;
-            blk.valid1 = sv1;
-          } else {
-            load(blk, kb);
-          }
-        }
+        if (kb != kb0) load(blk, kb);
         attend_block_lds(blk, s_q, lane, m_run, l_run, oacc);
       }
-      l_run += __shfl_xor(l_run, 16);
-      l_run += __shfl_xor(l_run, 32);
     }
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 4);
-    // ---- merge the 3 waves: waves 1 and 2 put their O fragments and (max, sum) per row in LDS;
-    // wave 0 combines them with its own and stores the split's partial: fp32 [16 rows][D], row
-    // r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
-    __syncthreads();  // s_q and the staged block are dead; s_o aliases s_q
-    if (comp && g == 0) {
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (item == (int)blockIdx.x) {
+      PHASE_TS(s, l, kPhSplit, 4);
+      PHASE_TS_W(1, s, l, kPhSplit, 7);
+      PHASE_TS_W(2, s, l, kPhSplit, 8);
+      PHASE_TS_W(3, s, l, kPhSplit, 9);
+    }
+    // ---- merge the 4 waves: waves 1..3 put their O fragments, every wave its (max, sum) per row,
+    // in LDS (no slot aliases s_q); wave 0 combines them and stores the split's partial: fp32 [16
+    // rows][D], row r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
+    if (g == 0) {
       s_m[wave * 16 + r16] = m_run;
       s_l[wave * 16 + r16] = l_run;
     }
-    if (wave == 1 || wave == 2) {
+    if (wave != 0) {
+      float* so = o_slot(wave);
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(s_o + (((size_t)(wave - 1) * 16 + dt) * 64 + lane) * 4) = oacc[dt];
+      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(so + ((size_t)dt * 64 + lane) * 4) = oacc[dt];
     }
     __syncthreads();
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
     if (tid < 64) {
-      float mw[3], Mx = -INFINITY, Lx = 0.f, ww[3];
+      float mw[4], Mx = -INFINITY, Lx = 0.f, ww[4];
 #pragma unroll
-      for (int v = 0; v < 3; ++v) {
+      for (int v = 0; v < 4; ++v) {
         mw[v] = s_m[v * 16 + r16];
         Mx = fmaxf(Mx, mw[v]);
       }
 #pragma unroll
-      for (int v = 0; v < 3; ++v) {
+      for (int v = 0; v < 4; ++v) {
         ww[v] = (mw[v] == -INFINITY) ? 0.f : __expf(mw[v] - Mx);
         Lx += s_l[v * 16 + r16] * ww[v];
       }
-      float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim + (size_t)r16 * kHeadDim + g * 4;
+      float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim;  // + row r16, dims g*4 + dt*16
+      // four d-tiles at a time: all twelve LDS reads in flight before the first use
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) {
-        const f32x4 o1 = *reinterpret_cast<const f32x4*>(s_o + ((size_t)dt * 64 + lane) * 4);
-        const f32x4 o2 = *reinterpret_cast<const f32x4*>(s_o + ((size_t)(16 + dt) * 64 + lane) * 4);
-        const f32x4 o = oacc[dt] * ww[0] + o1 * ww[1] + o2 * ww[2];
-        st_f32x4(part + dt * 16, float4{o[0], o[1], o[2], o[3]});
+      for (int d0 = 0; d0 < 16; d0 += 4) {
+        f32x4 ov[3][4];
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ov[v][j] = *reinterpret_cast<const f32x4*>(o_slot(v + 1) + ((size_t)(d0 + j) * 64 + lane) * 4);
+        sched_fence();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 o = oacc[d0 + j] * ww[0] + ov[0][j] * ww[1] + ov[1][j] * ww[2] + ov[2][j] * ww[3];
+          st_f32x4(part, (size_t)r16 * kHeadDim + g * 4 + (d0 + j) * 16, float4{o[0], o[1], o[2], o[3]});
+        }
       }
       if (g == 0) {
         st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + r16, Mx);
@@ -925,6 +967,8 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
     __syncthreads();  // the LDS tiles are reused by the next item
   }
+  // workgroups without a split item: their gate_up copies
+  if (!burst) copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
   // on work of its own.  All four waves merge (the copy wave has nothing in flight by now): thread
@@ -980,16 +1024,13 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       u16 v8[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) v8[q] = s_ob[j * kHeadDim + d + q];
-      st_bf16x8(os + afrag_index(r, head * kHeadDim + d, kHeads * kHeadDim / 32), v8);
+      st_bf16x8(os, afrag_index(r, head * kHeadDim + d, kHeads * kHeadDim / 32), v8);
     }
     publish(a, fmerge + hp * a.nbp_pad + bp, a.epoch);
     if (first_merge) PHASE_TS(s, l, kPhMerge, 6);
     first_merge = false;
     __syncthreads();  // s_ob is reused by the next role
   }
-  PHASE_TS_CW(s, l, kPhMerge, 10);
-  copy_norm_w<kModeGateUp>(a, l, 1, smem);  // B6 gate_up(l) tile 1 -> A upper half
-  PHASE_TS_CW(s, l, kPhMerge, 11);
   return true;
 }
 
@@ -1008,12 +1049,18 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = blockIdx.x;
   PHASE_TS(s, l, PH, 0);
-  PHASE_TS_CW(s, l, PH, 10);
+  // copy wave, ahead of the polls: down_proj: the next layer's qkv tiles (its gate_up MFMA is
+  // done); o_proj: the rest of this layer's gate_up tiles (attention no longer uses A)
   if constexpr (kDown) {
     int ln;
-    if (next_layer(a, s, l, &ln)) copy_norm_w<kModeQkv>(a, ln, 1, smem);  // B3 next qkv tile 1 -> A
+    if (next_layer(a, s, l, &ln)) {
+      copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
+      copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
+    }
+  } else {
+    copy_norm_w<kModeGateUp, 16, 16>(a, l, 0, smem);
+    copy_norm_w<kModeGateUp, 0, 32>(a, l, 1, smem);
   }
-  PHASE_TS_CW(s, l, PH, 11);
   if (item >= kTiles * kKSplit) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const bool comp = tid < kCompThreads;
@@ -1031,14 +1078,21 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
     if (!wait_flags(a, dep, kDown ? 64 : a.nbp, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
+  // the finisher's residual rows (written before anything this phase waited for), gate and
+  // 1 + scale: loaded by wave 0 right after the polls, used much later
+  const u16* hres = kDown ? a.hmid + slw * (size_t)R * kWidth : a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
+  u16x8 hpre0 = {}, hpre1 = {};
   if (tid < 64) {
-    // the finisher's gate and 1 + scale (loaded after the polls, used much later)
     const float* gmod = a.table + ((size_t)s * NN + 2 * l + (kDown ? 1 : 0)) * kModW + 2 * kWidth + col;
     const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + (kDown ? 2 : 1)) * kModW + col;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
       if (next_g) s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
+    }
+    if (lane < kHorizon) {
+      hpre0 = *reinterpret_cast<const u16x8*>(hres + afrag_index(lane, col, kWidth / 32));
+      hpre1 = *reinterpret_cast<const u16x8*>(hres + afrag_index(lane, col + 8, kWidth / 32));
     }
   }
   const u16* lw = reinterpret_cast<const u16*>(smem + (kDown ? kLdsB : kLdsC));  // this item's K-quarter fragments
@@ -1080,9 +1134,8 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
       // partial [quarter][tile][row][16]: 64 rows x 4 float4
       for (int e = tid; e < 256; e += kCompThreads) {
         const int row = e >> 2, q4 = e & 3;
-        float* pp = dpart + (((size_t)ksp * kTiles + nt) * R + b * kRowsPerSample + row) * 16 + 4 * q4;
         const float* tr = T + row * TS + 4 * q4;
-        st_f32x4(pp, float4{tr[0], tr[1], tr[2], tr[3]});
+        st_f32x4(dpart, (((size_t)ksp * kTiles + nt) * R + b * kRowsPerSample + row) * 16 + 4 * q4, float4{tr[0], tr[1], tr[2], tr[3]});
       }
     }
     __syncthreads();  // T is reused by the next sample
@@ -1092,16 +1145,13 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   if (!last_arrival(a, a.counters + ctr, (unsigned)kKSplit, s_flag)) return true;
   PHASE_TS(s, l, PH, 7);
   if (tid < 64) {
-    const u16* hres;
     u16 *hout, *gout;
     float* rout;
     if (kDown) {
-      hres = a.hmid + slw * (size_t)R * kWidth;
       hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
       gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
       rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
     } else {
-      hres = a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
       hout = a.hmid + slw * (size_t)R * kWidth;
       gout = a.gmid + slw * (size_t)R * kWidth;
       rout = a.ssmid + slw * kTiles * R;
@@ -1123,8 +1173,8 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
 #pragma unroll
           for (int i = 0; i < 4; ++i) pv[q][i] = *reinterpret_cast<const float4*>(pp + 4 * i);
         }
-        const u16x8 hold0 = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col, kWidth / 32));
-        const u16x8 hold1 = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + 8, kWidth / 32));
+        const u16x8 hold0 = b == 0 ? hpre0 : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col, kWidth / 32));
+        const u16x8 hold1 = b == 0 ? hpre1 : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + 8, kWidth / 32));
         u16 hn[16], gn[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -1142,11 +1192,11 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
           gn[i] = f2bf(fmul(hf, s1[i]));
           ss += hf * hf;
         }
-        st_bf16x8(hout + afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn));
-        st_bf16x8(hout + afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn + 8));
+        st_bf16x8(hout, afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn));
+        st_bf16x8(hout, afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn + 8));
         if (next_g) {
-          st_bf16x8(gout + afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn));
-          st_bf16x8(gout + afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn + 8));
+          st_bf16x8(gout, afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn));
+          st_bf16x8(gout, afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn + 8));
         }
       }
       // tile-major statistics: this tile's sums of the sample's 64 rows are one 256-byte run
@@ -1171,8 +1221,8 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   __shared__ __align__(16) float smem[kLdsFloats];
   __shared__ int s_flag;
   // the copy wave: step 0, layer 0 qkv and o_proj weights
-  copy_norm_w<kModeQkv>(a, 0, 0, smem);
-  copy_norm_w<kModeQkv>(a, 0, 1, smem);
+  copy_norm_w<kModeQkv, 0, 32>(a, 0, 0, smem);
+  copy_norm_w<kModeQkv, 0, 31>(a, 0, 1, smem);
   copy_residual_w<kHeads * kHeadDim / 32>(a, 0, smem);
   bool ok = true;
   for (int s = 0; s <= a.steps && ok; ++s) {
