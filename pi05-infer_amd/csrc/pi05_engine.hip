@@ -67,14 +67,14 @@ struct Plan {
   // graph schedule
   size_t kv = 0, valid = 0, h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0;
   // persistent schedule
-  int s_pre = 0, nsplit_p = 1, nsplit_pad = 4, nbp = 0, nbp_pad = 4, R = 0, fstride = 256, max_items = 0;
+  int s_pre = 0, nsplit_p = 1, nsplit_pad = 4, nbp = 0, nbp_pad = 4, R = 0, fstride = 256;
   size_t p_kv = 0, p_valid = 0, p_h = 0, p_g = 0, p_ss = 0, p_hmid = 0, p_ssmid = 0, p_q = 0, p_suf = 0, p_act = 0;
-  size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_ctr = 0, p_euler = 0;
+  size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_euler = 0;
   size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf + bias; }
   size_t graph_bytes() const { return 2 * kv + valid + h + rowss + q + o + act + part + 2 * partml + x + trace; }
   size_t persistent_bytes() const {
     return 2 * p_kv + p_valid + p_h + p_g + p_ss + p_hmid + p_g + p_ssmid + 2 * p_q + 2 * p_suf + p_act + p_apart + p_apartml +
-           p_dpart + p_x + p_flags + p_ctr + p_euler + 256;
+           p_dpart + p_x + p_flags + p_euler + 256;
   }
 };
 
@@ -135,13 +135,13 @@ Plan make_plan(const pi05_dims& d) {
   p.nbp = d.batch * (kHorizon / 2);
   p.nbp_pad = (p.nbp + 3) / 4 * 4;
   const size_t R = p.R;
-  p.max_items = p.M > 256 ? p.M : 256;
   // flag words per phase instance: the largest item count of any phase (io rows, attention split
   // and merge flags, 256 GEMM items), 16-byte aligned sub-ranges
   size_t fw = 256;
   fw = std::max(fw, (size_t)p.M);
   fw = std::max(fw, (size_t)p.nbp * p.nsplit_pad);
   fw = std::max(fw, (size_t)4 * p.nbp_pad);
+  fw = std::max(fw, (size_t)256 + 4 * (kWidth / 16));  // o_proj / down_proj K-quarter flags
   p.fstride = (int)round_up(fw, 256);
   p.p_kv = L * d.batch * p.s_pre * kHeadDim * 2;
   p.p_valid = round_up((size_t)d.batch * (p.s_pre + 64), 256);
@@ -160,7 +160,6 @@ Plan make_plan(const pi05_dims& d) {
   // 7 phases per (step, layer), 8 replicas each; 1 KiB of slack for the 16-byte flag loads past
   // a range's end
   p.p_flags = (T + 1) * (L + 1) * 7 * 8 * (size_t)p.fstride * 4 + 1024;
-  p.p_ctr = round_up(T * L * 2 * (kWidth / 16) * 4, 256);
   p.p_euler = round_up(T * 4 * 4, 256);
   return p;
 }
@@ -386,8 +385,6 @@ void carve_persistent(pi05_ctx* c) {
   a = MegaArgs{};
   a.err = reinterpret_cast<unsigned*>(take(256));
   a.flags = reinterpret_cast<unsigned*>(take(p.p_flags));
-  a.counters = reinterpret_cast<unsigned*>(take(p.p_ctr));
-  a.ctr_down_off = (size_t)d.num_steps * d.depth * (kWidth / 16);
   a.fstride = p.fstride;
   a.depth = d.depth;
   a.steps = d.num_steps;
@@ -451,7 +448,7 @@ hipError_t alloc_schedule(pi05_ctx* c) {
     ALLOC(x, p.x);
     ALLOC(trace, p.trace);
   } else {
-    // zero-filled: flags and counters must start at 0 (epoch 0 never matches a launch)
+    // zero-filled: flags must start at 0 (epoch 0 never matches a launch)
     ALLOC(pbase, p.persistent_bytes() + 64 * 256);
     if (ae == hipSuccess) carve_persistent(c);
     if (ae == hipSuccess) {
@@ -473,11 +470,10 @@ hipError_t alloc_schedule(pi05_ctx* c) {
   return ae;
 }
 
-// After a launch whose waits timed out: bring flags, counters and the error word back to zero.
+// After a launch whose waits timed out: bring the flags and the error word back to zero.
 hipError_t reset_persistent(pi05_ctx* c, hipStream_t st) {
   const Plan& p = c->plan;
   hipError_t e = hipMemsetAsync(c->mega.flags, 0, p.p_flags, st);
-  if (e == hipSuccess) e = hipMemsetAsync(c->mega.counters, 0, p.p_ctr, st);
   if (e == hipSuccess) e = hipMemsetAsync(c->mega.err, 0, 256, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   c->epoch = 0;
@@ -946,8 +942,8 @@ int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* cons
 namespace {
 
 int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t st) {
-  if (c->epoch >= (1u << 31) / (unsigned)c->plan.max_items) {
-    // keep epoch * items below 2^31: restart the count from zeroed counters
+  if (c->epoch >= (1u << 31)) {
+    // the epoch never wraps to 0 (the value of untouched flags): restart from zeroed flags
     HIPCHK(c, reset_persistent(c, st));
   }
   MegaArgs a = c->mega;
@@ -966,8 +962,7 @@ int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t 
     *c->host_err = 0;
     return c->fail(PI05_E_HIP, "denoise kernel: a workgroup timed out waiting for its inputs (state reset%s)",
                    e == hipSuccess ? "" : ", reset failed");
-  }
-  return PI05_OK;
+  }  return PI05_OK;
 }
 
 }  // namespace

@@ -101,12 +101,10 @@ struct AttnArgs {
 constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gate, then 4096 up
 
 struct MegaArgs {
-  unsigned epoch;      // this launch's flag value (1, 2, ...); flags/counters start at 0
+  unsigned epoch;      // this launch's flag value (1, 2, ...); flags start at 0
   unsigned* err;       // set to 1 by a workgroup whose wait timed out
-  unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][fstride]
-  unsigned* counters;  // K-quarter election counters [steps*depth][64] o_proj, then down
-  size_t ctr_down_off;
-  int fstride;         // flag words per phase instance (multiple of 256)
+  unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][8 copies][fstride]
+  int fstride;         // flag words per phase instance and copy (multiple of 256)
   int depth, steps, batch, R, nbp, nsplit, nsplit_pad, nbp_pad, s_pre;
   float eps;
   const float* table;     // [steps][2*depth+1][3W] adaRMS modulation rows: scale | shift | gate

@@ -27,6 +27,8 @@
 //
 // Every wait is bounded: on timeout the kernel records an error and all workgroups leave.
 
+#include <type_traits>
+
 #include "pi05_blocks.h"
 #include "pi05_kernels.h"
 
@@ -169,6 +171,9 @@ constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sa
 // XCD share a replica (workgroups are dispatched to the 8 XCDs round robin), so no flag line is
 // polled by more than a few dozen workgroups.
 constexpr int kFlagCopies = 8;
+// o_proj / down_proj: words [0, 64) flag the finished tiles; words kPartFlags + 4*tile + q - 1
+// flag K quarter q = 1..3 of a tile for its finisher (quarter 0)
+constexpr int kPartFlags = 256;
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
@@ -227,19 +232,11 @@ __device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsig
   if (threadIdx.x < kFlagCopies) st_u32(flag + (size_t)threadIdx.x * a.fstride, epoch);
 }
 
-// Last-arrival election on a device-scope counter that every launch advances by `n` per slot;
-// the compute waves' stores are complete before the workgroup counts itself in.
-__device__ bool last_arrival(const MegaArgs& a, unsigned* ctr, unsigned n, int* s_flag) {
+// The same for a flag that only workgroups of this XCD poll: one replica, this XCD's.
+__device__ __forceinline__ void publish_local(const MegaArgs& a, unsigned* flag, unsigned epoch) {
   if (!copy_wave()) wait_stores();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = old == a.epoch * n - 1u;
-  }
-  __syncthreads();
-  const bool last = *s_flag != 0;
-  __syncthreads();
-  return last;
+  if (threadIdx.x == 0) st_u32(flag + (size_t)(blockIdx.x % kFlagCopies) * a.fstride, epoch);
 }
 
 // ---- LDS map (floats) -------------------------------------------------------------------------
@@ -248,10 +245,10 @@ __device__ bool last_arrival(const MegaArgs& a, unsigned* ctr, unsigned n, int* 
 //   B: down_proj weight fragments (32 KiB)
 //   C: o_proj weight fragments (16 KiB)
 //   then the working area of the current phase.
-// Copy schedule (copy wave, per layer l).  A 63-copy burst takes about 1.3 us to issue and its
-// fragments land 2-3 us later, so every burst is issued just before a flag wait (the copy wave
-// reaches the wait's barrier while the producers are still working) and never between two
-// compute barriers, where it would hold up the compute waves:
+// Copy schedule (copy wave, per layer l).  A copy takes about 25 ns to issue and lands 2-3 us
+// later, so every burst is issued just before a flag wait (the copy wave reaches the next barrier
+// while the producers are still working) and never between two compute barriers, where it would
+// hold up the compute waves:
 //   qkv(l) wait      : all copies landed (qkv(l), o_proj(l) weights); down(l) -> B (32)
 //   attention(l) wait: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's own
 //                      KV block loads
@@ -841,10 +838,12 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   unsigned* fsplit = flag_base(a, s, l, kPhSplit);
   unsigned* fmerge = flag_base(a, s, l, kPhMerge);
   u16* s_q = reinterpret_cast<u16*>(smem + kLdsWork);  // [8 fragments][512] bf16 (2048 floats)
-  // O fragments of waves 1..3 ([16 d-tiles][64 lanes][4] each): waves 1, 2 in the upper half of
-  // A, wave 3 behind s_q; then the running max and sum of every wave
-  auto o_slot = [&](int w) { return w < 3 ? smem + kLdsA1 + (w - 1) * 4096 : smem + kLdsWork + 2048; };
-  float* s_m = smem + kLdsWork + 2048 + 4096;  // [4][16]
+  // per wave, the 12 O d-tiles the other waves combine ([12][64 lanes][4] each): waves 1, 2 in the
+  // upper half of A, waves 0, 3 behind s_q; then the running max and sum of every wave
+  auto o_slot = [&](int w) -> float* {
+    return w == 1 ? smem + kLdsA1 : w == 2 ? smem + kLdsA1 + 3072 : smem + kLdsWork + 2048 + (w == 0 ? 0 : 3072);
+  };
+  float* s_m = smem + kLdsWork + 2048 + 6144;  // [4][16]
   float* s_l = s_m + 64;                       // [4][16]
   PHASE_TS(s, l, kPhSplit, 0);
   bool waited = false, burst = false;
@@ -915,21 +914,27 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       PHASE_TS_W(2, s, l, kPhSplit, 8);
       PHASE_TS_W(3, s, l, kPhSplit, 9);
     }
-    // ---- merge the 4 waves: waves 1..3 put their O fragments, every wave its (max, sum) per row,
-    // in LDS (no slot aliases s_q); wave 0 combines them and stores the split's partial: fp32 [16
-    // rows][D], row r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
+    // ---- merge the 4 waves: wave w combines d-tiles 4w .. 4w+3 of all four waves.  Every wave
+    // puts the 12 d-tiles the others combine (slot index: d-tiles below its own four, then those
+    // above) and its (max, sum) per row in LDS (no slot aliases s_q), then combines its four in
+    // wave order and stores them: fp32 [16 rows][D], row r16 = lane % 16 holding dims
+    // dt*16 + g*4 .. +3 of d-tile dt
     if (g == 0) {
       s_m[wave * 16 + r16] = m_run;
       s_l[wave * 16 + r16] = l_run;
     }
-    if (wave != 0) {
+    {
       float* so = o_slot(wave);
 #pragma unroll
-      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(so + ((size_t)dt * 64 + lane) * 4) = oacc[dt];
+      for (int dt = 0; dt < 16; ++dt) {
+        if ((dt >> 2) == wave) continue;
+        const int si = dt < 4 * wave ? dt : dt - 4;
+        *reinterpret_cast<f32x4*>(so + ((size_t)si * 64 + lane) * 4) = oacc[dt];
+      }
     }
     __syncthreads();
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
-    if (tid < 64) {
+    {
       float mw[4], Mx = -INFINITY, Lx = 0.f, ww[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -942,22 +947,31 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
         Lx += s_l[v * 16 + r16] * ww[v];
       }
       float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim;  // + row r16, dims g*4 + dt*16
-      // four d-tiles at a time: all twelve LDS reads in flight before the first use
+      auto combine = [&](auto wc) {
+        constexpr int W = decltype(wc)::value;
+        f32x4 ov[4][4];
 #pragma unroll
-      for (int d0 = 0; d0 < 16; d0 += 4) {
-        f32x4 ov[3][4];
+        for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int v = 0; v < 3; ++v)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) ov[v][j] = *reinterpret_cast<const f32x4*>(o_slot(v + 1) + ((size_t)(d0 + j) * 64 + lane) * 4);
-        sched_fence();
+          for (int j = 0; j < 4; ++j) {
+            const int dt = 4 * W + j;
+            if (v == W) ov[v][j] = oacc[dt];
+            else ov[v][j] = *reinterpret_cast<const f32x4*>(o_slot(v) + ((size_t)(dt < 4 * v ? dt : dt - 4) * 64 + lane) * 4);
+          }
+        sched_fence();  // all twelve LDS reads in flight before the first use
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const f32x4 o = oacc[d0 + j] * ww[0] + ov[0][j] * ww[1] + ov[1][j] * ww[2] + ov[2][j] * ww[3];
-          st_f32x4(part, (size_t)r16 * kHeadDim + g * 4 + (d0 + j) * 16, float4{o[0], o[1], o[2], o[3]});
+          const f32x4 o = ov[0][j] * ww[0] + ov[1][j] * ww[1] + ov[2][j] * ww[2] + ov[3][j] * ww[3];
+          st_f32x4(part, (size_t)r16 * kHeadDim + g * 4 + (4 * W + j) * 16, float4{o[0], o[1], o[2], o[3]});
         }
+      };
+      switch (wave) {
+        case 0: combine(std::integral_constant<int, 0>{}); break;
+        case 1: combine(std::integral_constant<int, 1>{}); break;
+        case 2: combine(std::integral_constant<int, 2>{}); break;
+        default: combine(std::integral_constant<int, 3>{}); break;
       }
-      if (g == 0) {
+      if (wave == 0 && g == 0) {
         st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + r16, Mx);
         st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + 16 + r16, Lx);
       }
@@ -1036,10 +1050,11 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
 
 // =============================================================================================
 // o_proj (K = 2048) and down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves
-// split the quarter.  The last quarter to arrive adds the four partials in order and applies the
-// gated residual h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 503, 511), then
-// writes the new residual rows, g = bf16(h * (1 + scale)) of the next norm, and the tile's row
-// sums of squares.
+// split the quarter.  Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on
+// the same XCD) keeps its own, waits for the other three, adds the four in quarter order and
+// applies the gated residual h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 503,
+// 511), then writes the new residual rows, g = bf16(h * (1 + scale)) of the next norm, and the
+// tile's row sums of squares.
 // =============================================================================================
 template <bool kDown>
 __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
@@ -1070,7 +1085,7 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   const size_t slw = (size_t)s * L + l;
   // wave 0 (lane = row of the sample): gate and 1 + scale of the tile's 16 columns
   const int col = nt * 16;
-  float4 g4[4] = {}, s14[4] = {};
+  float4 g4[2] = {}, s14[2] = {};
   const bool next_g = !kDown || l + 1 < L;  // the last layer's output feeds the final norm only
   PHASE_TS(s, l, PH, 1);
   {
@@ -1078,29 +1093,29 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
     if (!wait_flags(a, dep, kDown ? 64 : a.nbp, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
-  // the finisher's residual rows (written before anything this phase waited for), gate and
-  // 1 + scale: loaded by wave 0 right after the polls, used much later
+  // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
+  // gate and 1 + scale: loaded by waves 0 and 1 right after the polls, used much later
   const u16* hres = kDown ? a.hmid + slw * (size_t)R * kWidth : a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
-  u16x8 hpre0 = {}, hpre1 = {};
-  if (tid < 64) {
-    const float* gmod = a.table + ((size_t)s * NN + 2 * l + (kDown ? 1 : 0)) * kModW + 2 * kWidth + col;
-    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + (kDown ? 2 : 1)) * kModW + col;
+  const bool fin_thread = ksp == 0 && tid < 128;
+  const int frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;  // finisher thread: row, first of its 8 columns
+  u16x8 hpre = {};
+  if (fin_thread) {
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l + (kDown ? 1 : 0)) * kModW + 2 * kWidth + col + fc0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + (kDown ? 2 : 1)) * kModW + col + fc0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
       if (next_g) s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
     }
-    if (lane < kHorizon) {
-      hpre0 = *reinterpret_cast<const u16x8*>(hres + afrag_index(lane, col, kWidth / 32));
-      hpre1 = *reinterpret_cast<const u16x8*>(hres + afrag_index(lane, col + 8, kWidth / 32));
-    }
+    if (frow < kHorizon) hpre = *reinterpret_cast<const u16x8*>(hres + afrag_index(frow, col + fc0, kWidth / 32));
   }
   const u16* lw = reinterpret_cast<const u16*>(smem + (kDown ? kLdsB : kLdsC));  // this item's K-quarter fragments
   const u16* act = kDown ? a.act + slw * (size_t)R * kMlp : a.o + slw * (size_t)R * (kHeads * kHeadDim);
   // this phase's K-quarter partials [quarter][tile][row][16] (written once per launch)
   float* dpart = a.dpart + (slw * 2 + (kDown ? 1 : 0)) * (size_t)kKSplit * kTiles * R * 16;
   float* red = smem + kLdsWork;
-  float* T = red + kCompWaves * 4 * 256;  // [64][TS]
+  float* T = red + kCompWaves * 4 * 256;  // [64][TS], then the finisher's [2][64] row sums
+  const bool own_lds = ksp == 0 && a.batch == 1;  // the finisher keeps its own partial in T
   const int r16 = lane & 15;
   for (int b = 0; b < a.batch; ++b) {
     if (comp) {
@@ -1130,7 +1145,7 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
     __syncthreads();
     reduce_to_tile<1, TS>(red, T);
     __syncthreads();
-    if (comp) {
+    if (comp && !own_lds) {
       // partial [quarter][tile][row][16]: 64 rows x 4 float4
       for (int e = tid; e < 256; e += kCompThreads) {
         const int row = e >> 2, q4 = e & 3;
@@ -1138,13 +1153,22 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
         st_f32x4(dpart, (((size_t)ksp * kTiles + nt) * R + b * kRowsPerSample + row) * 16 + 4 * q4, float4{tr[0], tr[1], tr[2], tr[3]});
       }
     }
-    __syncthreads();  // T is reused by the next sample
+    if (!own_lds || b + 1 < a.batch) __syncthreads();  // T is reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
-  const size_t ctr = (kDown ? a.ctr_down_off : 0) + slw * kTiles + nt;
-  if (!last_arrival(a, a.counters + ctr, (unsigned)kKSplit, s_flag)) return true;
+  unsigned* fl = flag_base(a, s, l, PH);
+  if (ksp != 0) {
+    // this quarter's partial is stored: flag it for the tile's finisher (quarter 0, same XCD)
+    publish_local(a, fl + kPartFlags + 4 * nt + (ksp - 1), a.epoch);
+    return true;
+  }
+  // ---- the finisher (quarter 0): its own partial stays in LDS at B = 1; it waits for the other
+  // three, adds the four in quarter order and writes the tile.  Waves 0 and 1: lane = row,
+  // columns half*8 .. +7.
+  if (!own_lds && comp) wait_stores();  // its own partials, reloaded below
+  if (!wait_flags(a, fl + kPartFlags + 4 * nt, kKSplit - 1, s_flag)) return false;
   PHASE_TS(s, l, PH, 7);
-  if (tid < 64) {
+  {
     u16 *hout, *gout;
     float* rout;
     if (kDown) {
@@ -1156,51 +1180,46 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
       gout = a.gmid + slw * (size_t)R * kWidth;
       rout = a.ssmid + slw * kTiles * R;
     }
-    const float gate[16] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
-                            round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w),
-                            round_bf(g4[2].x), round_bf(g4[2].y), round_bf(g4[2].z), round_bf(g4[2].w),
-                            round_bf(g4[3].x), round_bf(g4[3].y), round_bf(g4[3].z), round_bf(g4[3].w)};
-    const float s1[16] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w,
-                          s14[2].x, s14[2].y, s14[2].z, s14[2].w, s14[3].x, s14[3].y, s14[3].z, s14[3].w};
+    const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
+                           round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
+    const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
+    float* s_ss = T + 64 * TS;  // [2 halves][64 rows]
     for (int b = 0; b < a.batch; ++b) {
-      const int r = b * kRowsPerSample + lane;
+      const int r = b * kRowsPerSample + frow;
       float ss = 0.f;
-      if (lane < kHorizon) {
-        float4 pv[kKSplit][4];
+      if (fin_thread && frow < kHorizon) {
+        float pv[kKSplit][8];
 #pragma unroll
         for (int q = 0; q < kKSplit; ++q) {
-          const float* pp = dpart + (((size_t)q * kTiles + nt) * R + r) * 16;
+          if (q == 0 && own_lds) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) pv[q][i] = *reinterpret_cast<const float4*>(pp + 4 * i);
-        }
-        const u16x8 hold0 = b == 0 ? hpre0 : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col, kWidth / 32));
-        const u16x8 hold1 = b == 0 ? hpre1 : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + 8, kWidth / 32));
-        u16 hn[16], gn[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float y = 0.f;
-#pragma unroll
-          for (int q = 0; q < kKSplit; ++q) {
-            const float4 v = pv[q][i >> 2];
-            const float vi = (i & 3) == 0 ? v.x : (i & 3) == 1 ? v.y : (i & 3) == 2 ? v.z : v.w;
-            y = q == 0 ? vi : y + vi;
+            for (int i = 0; i < 8; ++i) pv[0][i] = T[frow * TS + fc0 + i];
+          } else {
+            const float* pp = dpart + (((size_t)q * kTiles + nt) * R + r) * 16 + fc0;
+            const float4 v0 = *reinterpret_cast<const float4*>(pp), v1 = *reinterpret_cast<const float4*>(pp + 4);
+            pv[q][0] = v0.x, pv[q][1] = v0.y, pv[q][2] = v0.z, pv[q][3] = v0.w;
+            pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
           }
-          const float hold = bf2f(i < 8 ? hold0[i] : hold1[i - 8]);
+        }
+        const u16x8 hold = b == 0 ? hpre : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
+        u16 hn[8], gn[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float y = ((pv[0][i] + pv[1][i]) + pv[2][i]) + pv[3][i];
           const float prod = round_bf(fmul(round_bf(y), gate[i]));
-          hn[i] = f2bf(fadd(hold, prod));
+          hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
           const float hf = bf2f(hn[i]);
           gn[i] = f2bf(fmul(hf, s1[i]));
           ss += hf * hf;
         }
-        st_bf16x8(hout, afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn));
-        st_bf16x8(hout, afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(hn + 8));
-        if (next_g) {
-          st_bf16x8(gout, afrag_index(r, col, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn));
-          st_bf16x8(gout, afrag_index(r, col + 8, kWidth / 32), *reinterpret_cast<const u16(*)[8]>(gn + 8));
-        }
+        st_bf16x8(hout, afrag_index(r, col + fc0, kWidth / 32), hn);
+        if (next_g) st_bf16x8(gout, afrag_index(r, col + fc0, kWidth / 32), gn);
       }
+      if (fin_thread) s_ss[(fc0 >> 3) * 64 + frow] = ss;
+      __syncthreads();
       // tile-major statistics: this tile's sums of the sample's 64 rows are one 256-byte run
-      st_f32(rout + (size_t)nt * R + r, ss);
+      if (tid < 64) st_f32(rout + (size_t)nt * R + r, s_ss[frow] + s_ss[64 + frow]);
+      __syncthreads();  // s_ss is reused by the next sample
     }
   }
   PHASE_TS(s, l, PH, 8);
@@ -1213,8 +1232,8 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
 // the kernel
 // =============================================================================================
 static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
-static_assert(kCompWaves * 4 * 256 + 64 * 17 <= kWorkFloats, "residual working area");
-static_assert(2 * 16 * 256 + 2 * 48 <= kWorkFloats && 2048 <= 2 * 16 * 256, "attention working area");
+static_assert(kCompWaves * 4 * 256 + 64 * 17 + 128 <= kWorkFloats, "residual working area");
+static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
 
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
