@@ -159,7 +159,7 @@ Plan make_plan(const pi05_dims& d) {
   p.p_x = round_up(T * p.M * kActDim * 4, 256);
   // 7 phases per (step, layer), 8 replicas each; 1 KiB of slack for the 16-byte flag loads past
   // a range's end
-  p.p_flags = (T + 1) * (L + 1) * 7 * 8 * (size_t)p.fstride * 4 + 1024;
+  p.p_flags = (T + 1) * (L + 1) * 7 * kFlagCopies * (size_t)p.fstride * 4 + 1024;
   p.p_euler = round_up(T * 4 * 4, 256);
   return p;
 }

@@ -87,6 +87,11 @@ struct AttnArgs {
   int rows, s_pad, nsplit;
 };
 
+// Every completion flag of the persistent kernel is kept in kFlagCopies replicas; workgroup w polls
+// replica w mod kFlagCopies, so each replica is polled by 8 workgroups of one XCD (workgroups are
+// dispatched to the 8 XCDs round robin).  Fewer pollers per line make a flag visible sooner.
+constexpr int kFlagCopies = 32;
+
 // The whole Euler loop as one cooperative kernel.  Activations live in per-(Euler step s,
 // layer l) slices ("slw" = s * depth + l; h / ss slices are per (s, l') with l' in [0, depth],
 // l' = depth being the last layer's output) that are written once per launch.  Rows are padded
@@ -103,7 +108,7 @@ constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gat
 struct MegaArgs {
   unsigned epoch;      // this launch's flag value (1, 2, ...); flags start at 0
   unsigned* err;       // set to 1 by a workgroup whose wait timed out
-  unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][8 copies][fstride]
+  unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][kFlagCopies][fstride]
   int fstride;         // flag words per phase instance and copy (multiple of 256)
   int depth, steps, batch, R, nbp, nsplit, nsplit_pad, nbp_pad, s_pre;
   float eps;

@@ -167,10 +167,7 @@ constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sa
 
 // Flags of one phase instance: kFlagCopies replicas of a.fstride words, word i = item i
 // (attention: split flags at bp * nsplit_pad + split, merge flags at head_pair * nbp_pad + bp).
-// A producer sets every replica; workgroup w polls replica w mod 8, i.e. the 32 workgroups of one
-// XCD share a replica (workgroups are dispatched to the 8 XCDs round robin), so no flag line is
-// polled by more than a few dozen workgroups.
-constexpr int kFlagCopies = 8;
+// A producer sets every replica; workgroup w polls replica w mod kFlagCopies.
 // o_proj / down_proj: words [0, 64) flag the finished tiles; words kPartFlags + 4*tile + q - 1
 // flag K quarter q = 1..3 of a tile for its finisher (quarter 0)
 constexpr int kPartFlags = 256;
@@ -214,6 +211,7 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
           ok = 0;
           break;
         }
+        asm volatile("" ::: "memory");  // every poll is a fresh load
       }
     }
     if (lane == 0) *s_flag = ok;
