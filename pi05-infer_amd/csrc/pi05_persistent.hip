@@ -862,14 +862,15 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     // Blocks: the copy wave attends the split's first block if it is from the static prefix (it
     // loads it before the polls and before its gate_up copies, so the copies never delay it);
     // compute wave w attends blocks first + o(w), + 3, ... with o = 2, 0, 1 for waves 0, 1, 2
-    // (wave 0 polls, so it gets the block it loads last).  Waves 1 and 2 load their first block
-    // ahead of the polls when it is from the prefix.
+    // (wave 0 gets the fourth, which a split most often lacks).  Every wave loads its first block
+    // ahead of the polls when it is from the prefix (wave 0's polls then complete after it lands).
     const bool cw_block = kb_lo < kb_hi && kb_lo < nkb_pre;
     const int first = kb_lo + (cw_block ? 1 : 0);
     const int kb0 = copy_wave() ? kb_lo : first + (wave == 0 ? 2 : wave - 1);
     const bool has_block = copy_wave() ? cw_block : kb0 < kb_hi;
+    const bool pre = has_block && kb0 < nkb_pre;
     KvBlock blk;
-    if (wave != 0 && has_block && kb0 < nkb_pre) load(blk, kb0);
+    if (pre) load(blk, kb0);
     if (!burst) {
       copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
       burst = true;
@@ -888,7 +889,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       for (int f = wu; f < 8; f += kCompWaves)
         __builtin_amdgcn_global_load_lds(const_cast<u16*>(qs + afrag_offset(rbq, f, kHeadDim / 32)) + lane * 8, s_q + (size_t)f * 512, 16,
                                          0, 0);
-      if (has_block && (wave == 0 || kb0 >= nkb_pre)) load(blk, kb0);
+      if (has_block && !pre) load(blk, kb0);
       wait_vmcnt<0>();  // the query fragments have landed in LDS (and this wave's block)
     }
     __syncthreads();
