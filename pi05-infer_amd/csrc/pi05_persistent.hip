@@ -143,23 +143,24 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 
 // MFMA steps S2.. of an operand block af[4][KSW]: step s2 reads its NT weight fragments from
 // LDS (wk(t, s2)) and accumulates the four m-tiles.
-template <int KSW, int NT, int S2, class WK>
-__device__ __forceinline__ void mfma_steps(f32x4 (&acc)[4][NT], bf16x8 (&af)[4][KSW], WK wk) {
+template <int KSW, int NT, int S2, int MT, class WK>
+__device__ __forceinline__ void mfma_steps(f32x4 (&acc)[MT][NT], bf16x8 (&af)[MT][KSW], WK wk) {
   if constexpr (S2 < KSW) {
     bf16x8 wf[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) wf[t] = wk(t, S2);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[mt][t] = mfma16x16x32(af[mt][S2], wf[t], acc[mt][t]);
-    mfma_steps<KSW, NT, S2 + 1>(acc, af, wk);
+    mfma_steps<KSW, NT, S2 + 1, MT>(acc, af, wk);
   }
 }
 
 // ---- phases, items and flags ------------------------------------------------------------------
 enum { kPhIo = 0, kPhQkv = 1, kPhSplit = 2, kPhMerge = 3, kPhO = 4, kPhGu = 5, kPhDown = 6, kNumPh = 7 };
-constexpr int kQkvItems = 80;        // 72 RoPE pairs of q/k tiles + 8 pairs of v tiles
+constexpr int kQkvPairs = 80;        // 72 RoPE pairs of q/k tiles + 8 pairs of v tiles
+constexpr int kQkvItems = 2 * kQkvPairs;  // each pair in two items: rows 0..31 and rows 32..49
 constexpr int kTiles = kWidth / 16;  // 64 output tiles of o_proj / down_proj
 constexpr int kGuItems = kMlp / 16;  // 256 (gate tile j, up tile j)
 constexpr int kKSplit = 4;           // K quarters of o_proj / down_proj
@@ -287,7 +288,7 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 template <int MODE>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = blockIdx.x;
+  const int p = MODE == kModeQkv ? (int)blockIdx.x % kQkvPairs : (int)blockIdx.x;  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -328,27 +329,28 @@ __device__ __forceinline__ bool next_layer(const MegaArgs& a, int s, int l, int*
   return s + 1 < a.steps;
 }
 
-template <int NT>
-__device__ __forceinline__ void store_wave_partials(float* red, const f32x4 (&acc)[4][NT], int wave, int lane) {
+template <int MT, int NT>
+__device__ __forceinline__ void store_wave_partials(float* red, const f32x4 (&acc)[MT][NT], int wave, int lane) {
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(red + (((size_t)(wave * 4 + mt) * NT + t) * 64 + lane) * 4) = acc[mt][t];
+    for (int t = 0; t < NT; ++t) *reinterpret_cast<f32x4*>(red + (((size_t)(wave * MT + mt) * NT + t) * 64 + lane) * 4) = acc[mt][t];
 }
 
-// Sum the compute waves' D fragments (red[wave][mt][t][lane], f32x4) in wave order and scatter
-// them row-major into the LDS tile T[64][TS] (column t*16 + n), which must not alias red.  Thread
-// tid < 256 owns m-tile tid/64, lane tid%64 of every tile t (the copy wave takes m-tile 3: LDS
-// work only).
-template <int NT, int TS>
+// Sum the compute waves' D fragments (red[wave][mt][t][lane], f32x4, MT m-tiles) in wave order
+// and scatter them row-major into the LDS tile T[16 MT][TS] (column t*16 + n), which must not
+// alias red.  Thread tid < 64 MT owns m-tile tid/64, lane tid%64 of every tile t (with MT = 4 the
+// copy wave takes m-tile 3: LDS work only).
+template <int MT, int NT, int TS>
 __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
   const int tid = threadIdx.x;
   const int mt = tid >> 6, ln = tid & 63;
+  if (mt >= MT) return;
   f32x4 r[kCompWaves][NT];
 #pragma unroll
   for (int w = 0; w < kCompWaves; ++w)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) r[w][t] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * 4 + mt) * NT + t) * 64 + ln) * 4);
+    for (int t = 0; t < NT; ++t) r[w][t] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * MT + mt) * NT + t) * 64 + ln) * 4);
   sched_fence();  // every read in flight before the first sum
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -548,11 +550,17 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
 template <int MODE>
 __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32, TS = 33;
+  // m-tiles per item: qkv items are one half of a sample's rows (m-tiles 2h, 2h+1), gate_up all four
+  constexpr int MT = MODE == kModeQkv ? 2 : 4;
   constexpr int PH = MODE == kModeQkv ? kPhQkv : kPhGu;
   const int L = a.depth, R = a.R;
   const int n_items = MODE == kModeQkv ? kQkvItems : kGuItems;
-  const int p = blockIdx.x;
-  const bool has_item = p < n_items;
+  const int item = (int)blockIdx.x;
+  const bool has_item = item < n_items;
+  const int p = MODE == kModeQkv ? item % kQkvPairs : item;  // tile pair (qkv) / item
+  const int mh = MODE == kModeQkv ? item / kQkvPairs : 0;    // qkv: half of the rows
+  const int rb = 32 * mh;                          // the item's first row within a sample
+  const int nrow = MT * 16 < kHorizon - rb ? MT * 16 : kHorizon - rb;  // its action-token rows
   PHASE_TS(s, l, PH, 0);
   // copy wave: this phase's weights (region A) and everything issued before them have landed;
   // then the bursts of this phase start
@@ -589,20 +597,20 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     gin = a.gmid + slw * R * kWidth;
     ssin = a.ssmid + slw * kTiles * R;
   }
-  float* s_rstd = smem + kLdsWork;  // [64]
+  float* s_rstd = smem + kLdsWork;  // [64] (item rows)
   float* s_bias = s_rstd + 64;      // [32] shift . W^T of the item's two tiles
   float* s_rs = s_bias + 32;        // [3][64] row sums of squares over tiles 22w .. 22w+21
-  float* red = s_rs + 192;          // [3 waves][4 m-tiles][NT][64 lanes][4]
-  float* T = red + kCompWaves * 4 * NT * 256;  // [64][TS]
+  float* red = s_rs + 192;          // [3 waves][MT m-tiles][NT][64 lanes][4]
+  float* T = red + kCompWaves * MT * NT * 256;  // [16 MT][TS] (item rows)
   // static operands, loaded ahead of the polls by waves 1 and 2 (wave 0 polls, so it issues
   // nothing before them): wave 2's qkv tile-1 fragment of k-step 31 (not in LDS), and the RoPE
   // cos/sin chunks of the first sample for the epilogue threads 64..163 (row, half)
   bf16x8 w31 = {};
   u16x8 rcs[4] = {};
-  const int et = tid - 64;  // RoPE epilogue thread: row et/2, half et%2
-  const bool rope_thread = MODE == kModeQkv && rotated && et >= 0 && et < 2 * kHorizon;
+  const int et = tid - 64;  // RoPE epilogue thread: item row et/2, half et%2
+  const bool rope_thread = MODE == kModeQkv && rotated && et >= 0 && et < 2 * nrow;
   auto load_rope = [&](int b) {
-    const size_t cr = (size_t)(b * kHorizon + (et >> 1)) * kHeadDim + dt * 16 + (et & 1) * 8;
+    const size_t cr = (size_t)(b * kHorizon + rb + (et >> 1)) * kHeadDim + dt * 16 + (et & 1) * 8;
     rcs[0] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr);
     rcs[1] = *reinterpret_cast<const u16x8*>(a.sin_tab + cr);
     rcs[2] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr + kHalfDim);
@@ -628,9 +636,9 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
   for (int b = 0; b < a.batch; ++b) {
     const int m0 = b * kRowsPerSample;
-    // the row statistics first (wave w: tiles 22w .. 22w+21, lane = row), then the A fragments
-    // (k-step 32 of wave 2 and the padded rows read as zeros), all without branches
-    f32x4 acc[4][NT];
+    // the row statistics first (wave w: tiles 22w .. 22w+21, lane = item row), then the A
+    // fragments (k-step 32 of wave 2 and the padded rows read as zeros), all without branches
+    f32x4 acc[MT][NT];
     if (comp) {
       const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
       const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
@@ -638,15 +646,15 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
 #pragma unroll
       for (int t = 0; t < 22; ++t) {
         const int tile = 22 * wave + t;
-        buf_f32(st[t], rsrc_s, tile < kTiles ? ((tile * R + b * kRowsPerSample + lane) * 4) : kOob);
+        buf_f32(st[t], rsrc_s, tile < kTiles && lane < 16 * MT ? ((tile * R + m0 + rb + lane) * 4) : kOob);
       }
-      bf16x8 hr[4][KSW];
+      bf16x8 hr[MT][KSW];
 #pragma unroll
       for (int s2 = 0; s2 < KSW; ++s2)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const bool ok = r16 < kHorizon - mt * 16 && ks0 + s2 < KSTEPS;
-          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+        for (int mt = 0; mt < MT; ++mt) {
+          const bool ok = r16 < nrow - mt * 16 && ks0 + s2 < KSTEPS;
+          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + 2 * mh + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
         }
       sched_fence();
       float v = 0.f;
@@ -654,12 +662,12 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
       for (int t = 0; t < 22; ++t) v += st[t];
       s_rs[wave * 64 + lane] = v;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       // zero A for wave 2's surplus step: any finite weights (k-step 31's); qkv tile 1's k-step 31
       // fragment is wave 2's register copy
-      mfma_steps<KSW, NT, 0>(acc, hr, [&](int t, int s2) {
+      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
         const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
         if (MODE == kModeQkv && t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
         return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
@@ -668,10 +676,10 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     if (b == 0) PHASE_TS(s, l, PH, 4);
     __syncthreads();  // every wave is done with region A; the row sums are in LDS
     if (b == 0) PHASE_TS(s, l, PH, 3);
-    if (comp) store_wave_partials<NT>(red, acc, wave, lane);
-    if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
+    if (comp) store_wave_partials<MT, NT>(red, acc, wave, lane);
+    if (tid < 16 * MT) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
     __syncthreads();
-    reduce_to_tile<NT, TS>(red, T);
+    reduce_to_tile<MT, NT, TS>(red, T);
     __syncthreads();
     if (b == 0) PHASE_TS(s, l, PH, 7);
     if constexpr (MODE == kModeQkv) {
@@ -704,24 +712,25 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
           const int d = dt * 16 + half * 8;
           if (head < kHeads) {
             u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
-            const int qrow = (m0 + row) * kQRowsPerTok + head;
+            const int qrow = (m0 + rb + row) * kQRowsPerTok + head;
             st_bf16x8(qs, afrag_index(qrow, d, kHeadDim / 32), olo);
             st_bf16x8(qs, afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
           } else {
             u16* kc = a.ksuf + (slw * a.batch + b) * 64 * kHeadDim;
-            st_bf16x8(kc, kfrag_index(row, d), olo);
-            st_bf16x8(kc, kfrag_index(row, d + kHalfDim), ohi);
+            st_bf16x8(kc, kfrag_index(rb + row, d), olo);
+            st_bf16x8(kc, kfrag_index(rb + row, d + kHalfDim), ohi);
           }
         }
       } else if (comp) {
-        // v: chunk -> (dim dcol of the tile pair, key group (kb, g) of the permuted V fragment)
-        for (int ci = tid; ci < 256; ci += kCompThreads) {
-          const int dcol = ci & 31, kg = ci >> 5, kb = kg >> 2, gg = kg & 3;
+        // v: chunk -> (dim dcol of the tile pair, key group (kb, g) of the permuted V fragment);
+        // this item's rows are the keys of 32-key block kb = mh
+        for (int ci = tid; ci < 128; ci += kCompThreads) {
+          const int dcol = ci & 31, kb = mh, gg = ci >> 5;
           u16 v8[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
-            const int key = vkey(kb, gg, q);
-            v8[q] = key < kHorizon ? f2bf(__builtin_fmaf(s_rstd[key], T[key * TS + dcol], s_bias[dcol])) : (u16)0;
+            const int key = vkey(kb, gg, q);  // key rb + (key - rb) of the sample
+            v8[q] = key < kHorizon ? f2bf(__builtin_fmaf(s_rstd[key - rb], T[(key - rb) * TS + dcol], s_bias[dcol])) : (u16)0;
           }
           const int dv = (tile0 - 144) * 16 + dcol;
           u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
@@ -756,7 +765,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     __syncthreads();  // T and s_rstd are reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
-  publish(a, flag_base(a, s, l, PH) + p, a.epoch);
+  publish(a, flag_base(a, s, l, PH) + item, a.epoch);
   PHASE_TS(s, l, PH, 6);
   return true;
 }
@@ -1133,7 +1142,7 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
       // zero A for the surplus steps: any finite weights (the quarter's last k-step)
-      mfma_steps<KSW, 1, 0>(acc, af, [&](int, int s2) {
+      mfma_steps<KSW, 1, 0, 4>(acc, af, [&](int, int s2) {
         const int kc = kw0 + s2 < KQ ? kw0 + s2 : KQ - 1;
         return *reinterpret_cast<const bf16x8*>(lw + (size_t)kc * 512 + lane * 8);
       });
@@ -1142,7 +1151,7 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
     }
     if (b == 0) PHASE_TS(s, l, PH, 4);
     __syncthreads();
-    reduce_to_tile<1, TS>(red, T);
+    reduce_to_tile<4, 1, TS>(red, T);
     __syncthreads();
     if (comp && !own_lds) {
       // partial [quarter][tile][row][16]: 64 rows x 4 float4
