@@ -161,6 +161,10 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[MT][NT], bf16x8 (&af)[MT
 enum { kPhIo = 0, kPhQkv = 1, kPhSplit = 2, kPhMerge = 3, kPhO = 4, kPhGu = 5, kPhDown = 6, kNumPh = 7 };
 constexpr int kQkvPairs = 80;        // 72 RoPE pairs of q/k tiles + 8 pairs of v tiles
 constexpr int kQkvItems = 2 * kQkvPairs;  // each pair in two items: rows 0..31 and rows 32..49
+// qkv item i runs on workgroup kQkvWg0 + i: not on workgroups 0..63, which finish the previous
+// layer's down_proj tiles (the two items of a pair share an XCD: 80 is a multiple of 8)
+constexpr int kQkvWg0 = 64;
+__device__ __forceinline__ int qkv_item() { return (int)blockIdx.x - kQkvWg0; }
 constexpr int kTiles = kWidth / 16;  // 64 output tiles of o_proj / down_proj
 constexpr int kGuItems = kMlp / 16;  // 256 (gate tile j, up tile j)
 constexpr int kKSplit = 4;           // K quarters of o_proj / down_proj
@@ -288,7 +292,7 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 template <int MODE>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = MODE == kModeQkv ? (int)blockIdx.x % kQkvPairs : (int)blockIdx.x;  // qkv: the tile pair
+  const int p = MODE == kModeQkv ? qkv_item() % kQkvPairs : (int)blockIdx.x;  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -302,7 +306,8 @@ __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int 
 }
 template <int MODE, int F0, int N>
 __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
-  if (!copy_wave() || blockIdx.x >= (MODE == kModeQkv ? kQkvItems : kGuItems)) return;
+  if (!copy_wave()) return;
+  if (MODE == kModeQkv ? (unsigned)qkv_item() >= (unsigned)kQkvItems : blockIdx.x >= kGuItems) return;
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE>(a, l, which) + F0 * 512);
 }
 
@@ -555,8 +560,8 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   constexpr int PH = MODE == kModeQkv ? kPhQkv : kPhGu;
   const int L = a.depth, R = a.R;
   const int n_items = MODE == kModeQkv ? kQkvItems : kGuItems;
-  const int item = (int)blockIdx.x;
-  const bool has_item = item < n_items;
+  const int item = MODE == kModeQkv ? qkv_item() : (int)blockIdx.x;
+  const bool has_item = item >= 0 && item < n_items;
   const int p = MODE == kModeQkv ? item % kQkvPairs : item;  // tile pair (qkv) / item
   const int mh = MODE == kModeQkv ? item / kQkvPairs : 0;    // qkv: half of the rows
   const int rb = 32 * mh;                          // the item's first row within a sample
