@@ -155,7 +155,7 @@ Plan make_plan(const pi05_dims& d) {
   p.p_act = T * L * R * kMlp * 2;
   p.p_apart = T * L * p.nsplit_p * p.nbp * 16 * kHeadDim * 4;
   p.p_apartml = round_up(T * L * p.nsplit_p * p.nbp * 32 * 4, 256);
-  p.p_dpart = T * L * 2 * 4 * (kWidth / 16) * R * 16 * 4;
+  p.p_dpart = T * L * 4 * (kWidth / 16) * R * 16 * 4;
   p.p_x = round_up(T * p.M * kActDim * 4, 256);
   // 7 phases per (step, layer), 8 replicas each; 1 KiB of slack for the 16-byte flag loads past
   // a range's end

@@ -139,7 +139,7 @@ struct MegaArgs {
   u16* act;               // [steps][depth] A fragments of [R, I]
   float* apart;           // [steps][depth][nsplit][nbp][16][D] attention split partials
   float* apart_ml;        // [steps][depth][nsplit][nbp][2][16] running max | sum of the splits
-  float* dpart;           // [steps][depth][o_proj | down][4][64][R][16] K-quarter partials
+  float* dpart;           // [steps][depth][4][64][R][16] down_proj K-quarter partials
   float* x;               // [steps][B*50, a] actions after step s (slot 0 unused)
   float* x_io;            // [B*50, a] caller's buffer: noise on entry, actions on exit
   float* trace;           // [steps][B*50, a] caller's velocity buffer (nullable)

@@ -168,15 +168,18 @@ constexpr int kQkvWg0 = 64;
 __device__ __forceinline__ int qkv_item() { return (int)blockIdx.x - kQkvWg0; }
 constexpr int kTiles = kWidth / 16;  // 64 output tiles of o_proj / down_proj
 constexpr int kGuItems = kMlp / 16;  // 256 (gate tile j, up tile j)
-constexpr int kKSplit = 4;           // K quarters of o_proj / down_proj
+constexpr int kKSplit = 4;           // K quarters of down_proj
+constexpr int kHeadPairs = kHeads / 2;  // attention merges: (row block, pair of heads)
 constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sample
 
 // Flags of one phase instance: kFlagCopies replicas of a.fstride words, word i = item i
-// (attention: split flags at bp * nsplit_pad + split, merge flags at head_pair * nbp_pad + bp).
+// (attention: split flags at bp * nsplit_pad + split, merge flags at 4 * bp + head_pair).
 // A producer sets every replica; workgroup w polls replica w mod kFlagCopies.
-// o_proj / down_proj: words [0, 64) flag the finished tiles; words kPartFlags + 4*tile + q - 1
-// flag K quarter q = 1..3 of a tile for its finisher (quarter 0)
+// o_proj: words [0, 256) flag the items (m-tile mq, tile nt) at 64 mq + nt.  down_proj: words
+// [0, 64) flag the finished tiles; words kPartFlags + 4*tile + q - 1 flag K quarter q = 1..3 of a
+// tile for its finisher (quarter 0)
 constexpr int kPartFlags = 256;
+constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-tile of a sample, tile)
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
@@ -247,23 +250,21 @@ __device__ __forceinline__ void publish_local(const MegaArgs& a, unsigned* flag,
 //   A: qkv or gate_up weight fragments of this workgroup's item: two 32-fragment tiles (64 KiB);
 //      during attention its upper half holds the O fragments of waves 1 and 2
 //   B: down_proj weight fragments (32 KiB)
-//   C: o_proj weight fragments (16 KiB)
-//   then the working area of the current phase.
+//   then the working area of the current phase.  (o_proj holds its weights in registers.)
 // Copy schedule (copy wave, per layer l).  A copy takes about 25 ns to issue and lands 2-3 us
 // later, so every burst is issued just before a flag wait (the copy wave reaches the next barrier
 // while the producers are still working) and never between two compute barriers, where it would
 // hold up the compute waves:
-//   qkv(l) wait      : all copies landed (qkv(l), o_proj(l) weights); down(l) -> B (32)
+//   qkv(l) wait      : all copies landed (qkv(l) weights); down(l) -> B (32)
 //   attention(l) wait: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's own
 //                      KV block loads
-//   o_proj(l) wait   : gate_up(l) tile 0 fragments 16..31 (16) and tile 1 (32) -> A
-//   gate_up(l) wait  : all copies landed (gate_up(l) weights); o_proj(l+1) -> C (16)
+//   merge(l) wait    : gate_up(l) tile 0 fragments 16..31 (16) and tile 1 (32) -> A
+//   gate_up(l) wait  : all copies landed (gate_up(l) weights)
 //   down(l) wait     : qkv(l+1) tile 0 (32) and tile 1 fragments 0..30 (31) -> A
 // so at most 63 copies are ever in flight and a burst never waits for the one before it.
 constexpr int kLdsA = 0;
 constexpr int kLdsB = kLdsA + 16384;
-constexpr int kLdsC = kLdsB + 8192;
-constexpr int kLdsWork = kLdsC + 4096;
+constexpr int kLdsWork = kLdsB + 8192;
 constexpr int kWorkFloats = 8736;
 constexpr int kLdsFloats = kLdsWork + kWorkFloats;
 static_assert(kLdsFloats * 4 <= 160 * 1024, "LDS budget of a gfx950 workgroup");
@@ -315,17 +316,15 @@ __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE>(a, l, which) + F0 * 512);
 }
 
-// o_proj (KSTEPS = 64, region C) or down_proj (KSTEPS = 128, region B) weights of item
-// blockIdx.x = (tile, K quarter).
+// down_proj weights of item blockIdx.x = (tile, K quarter) -> region B.
 template <int KSTEPS>
 __device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
-  constexpr bool kDown = KSTEPS == kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit;
   const int item = blockIdx.x;
   if (!copy_wave() || item >= kTiles * kKSplit) return;
   const int nt = item % kTiles, ksp = item / kTiles;
-  const u16* tile = a.wpack + (size_t)l * kLayerElems + (kDown ? kOffDown : kOffO) + (size_t)nt * KSTEPS * 512 + (size_t)ksp * KQ * 512;
-  lds_burst<KQ>(smem + (kDown ? kLdsB : kLdsC), tile);
+  const u16* tile = a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)nt * KSTEPS * 512 + (size_t)ksp * KQ * 512;
+  lds_burst<KQ>(smem + kLdsB, tile);
 }
 
 // The layer after (s, l): (s, l + 1), or (s + 1, 0) after the last layer; false past the loop.
@@ -577,9 +576,6 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     wait_vmcnt<0>();
     if constexpr (MODE == kModeQkv) {
       copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
-    } else {
-      int ln;
-      if (next_layer(a, s, l, &ln)) copy_residual_w<kHeads * kHeadDim / 32>(a, ln, smem);  // B1 o_proj -> C
     }
   }
   if (!has_item) return true;
@@ -632,7 +628,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   PHASE_TS(s, l, PH, 1);
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
-    const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kTiles) : kTiles;
+    const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kTiles) : kOItems;
     if (!wait_flags(a, dep, ndep, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
@@ -998,8 +994,11 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
     __syncthreads();  // the LDS tiles are reused by the next item
   }
-  // workgroups without a split item: their gate_up copies
+  // the rest of gate_up(l) -> region A, whose upper half the split items no longer use (the
+  // workgroups without a split item: all of it), ahead of the merge polls
   if (!burst) copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
+  copy_norm_w<kModeGateUp, 16, 16>(a, l, 0, smem);
+  copy_norm_w<kModeGateUp, 0, 32>(a, l, 1, smem);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
   // on work of its own.  All four waves merge (the copy wave has nothing in flight by now): thread
@@ -1007,7 +1006,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   // loads every split's (max, sum, O) at once.
   bool first_merge = true;
   u16* s_ob = reinterpret_cast<u16*>(smem + kLdsWork);  // [4 rows][D] bf16
-  for (int role = blockIdx.x; role < kKSplit * nbp; role += gridDim.x) {
+  for (int role = blockIdx.x; role < kHeadPairs * nbp; role += gridDim.x) {
     const int bp = role % nbp, hp = role / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
     if (first_merge) PHASE_TS(s, l, kPhMerge, 1);
@@ -1057,7 +1056,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       for (int q = 0; q < 8; ++q) v8[q] = s_ob[j * kHeadDim + d + q];
       st_bf16x8(os, afrag_index(r, head * kHeadDim + d, kHeads * kHeadDim / 32), v8);
     }
-    publish(a, fmerge + hp * a.nbp_pad + bp, a.epoch);
+    publish(a, fmerge + 4 * bp + hp, a.epoch);
     if (first_merge) PHASE_TS(s, l, kPhMerge, 6);
     first_merge = false;
     __syncthreads();  // s_ob is reused by the next role
@@ -1066,32 +1065,141 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
 }
 
 // =============================================================================================
-// o_proj (K = 2048) and down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves
-// split the quarter.  Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on
-// the same XCD) keeps its own, waits for the other three, adds the four in quarter order and
-// applies the gated residual h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 503,
-// 511), then writes the new residual rows, g = bf16(h * (1 + scale)) of the next norm, and the
-// tile's row sums of squares.
+// o_proj (K = 2048) and the gated residual after attention: item = (m-tile mq of every sample,
+// 16-column tile nt), 256 items, no K split.  The three compute waves split K (22 k-steps each;
+// wave 2's last two are surplus and read A as zeros) and load their weight fragments into
+// registers ahead of the polls, so only the attention output is fetched after them.  Per sample:
+// wait for the merges of the m-tile's row blocks (all four head pairs), MFMA in four independent
+// chains, add the waves in LDS, then h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249,
+// 503), g = bf16(h * (1 + scale)) of the pre-MLP norm and the tile's row sums of squares.
 // =============================================================================================
-template <bool kDown>
-__device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
-  constexpr int KSTEPS = kDown ? kMlp / 32 : kHeads * kHeadDim / 32;
+__device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = (KSTEPS + kCompWaves - 1) / kCompWaves, TS = 17;
+  constexpr int NCH = 4;  // independent accumulation chains per wave
+  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  const int item = blockIdx.x;
+  PHASE_TS(s, l, kPhO, 0);
+  if (item >= kOItems) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const bool comp = tid < kCompThreads;
+  const int nt = item % kTiles, mq = item / kTiles;
+  const int col = nt * 16, ks0 = wave * KSW, r16 = lane & 15;
+  const int nrow = kHorizon - 16 * mq < 16 ? kHorizon - 16 * mq : 16;  // action rows of the m-tile
+  const int np = (nrow + 1) / 2;                                         // its two-token row blocks
+  const size_t slw = (size_t)s * L + l;
+  // the wave's weight fragments (surplus k-steps: the last one again)
+  bf16x8 wf[KSW];
+  if (comp) {
+    const brsrc rw = make_rsrc(a.wpack + (size_t)l * kLayerElems + kOffO + (size_t)nt * KSTEPS * 512, (size_t)KSTEPS * 1024);
+#pragma unroll
+    for (int s2 = 0; s2 < KSW; ++s2) buf_frag(wf[s2], rw, ((ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1) * 512 + lane * 8) * 2);
+  }
+  // epilogue threads: row et/2 of the m-tile, columns (et%2)*8 .. +7; gate and 1 + scale ahead
+  // of the polls
+  const int et = tid, erow = et >> 1, ec0 = (et & 1) * 8;
+  const bool ep_thread = et < 32;
+  const u16* hres = a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
+  float4 g4[2] = {}, s14[2] = {};
+  if (ep_thread) {
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + ec0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + ec0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
+      s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
+    }
+  }
+  PHASE_TS(s, l, kPhO, 1);
+  const u16* act = a.o + slw * (size_t)R * (KSTEPS * 32);
+  u16* hout = a.hmid + slw * (size_t)R * kWidth;
+  u16* gout = a.gmid + slw * (size_t)R * kWidth;
+  float* rout = a.ssmid + slw * kTiles * R;
+  const unsigned* fmerge = flag_base(a, s, l, kPhMerge);
+  float* red = smem + kLdsWork;         // [3 waves][64 lanes][4]
+  float* T = red + kCompWaves * 256;    // [16][TS]
+  float* s_ss = T + 16 * TS;            // [2 halves][16 rows]
+  const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
+                         round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
+  const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
+  for (int b = 0; b < a.batch; ++b) {
+    const int m = 4 * b + mq;  // m-tile of the activations
+    // merge flags 4 * bp + hp: the m-tile's row blocks bp = 25 b + 8 mq .. are one contiguous run
+    if (!wait_flags(a, fmerge + 4 * (b * kPairs + 8 * mq), 4 * np, s_flag)) return false;
+    if (b == 0) PHASE_TS(s, l, kPhO, 2);
+    // the residual rows: the merges waited for imply every earlier phase of the layer, so the
+    // previous layer's down_proj has written them (this workgroup may have had no qkv item)
+    const int r = 16 * m + erow;
+    u16x8 hold = {};
+    if (ep_thread && erow < nrow) hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + ec0, kWidth / 32));
+    if (comp) {
+      const brsrc ra = make_rsrc(act, (size_t)R * KSTEPS * 64);
+      bf16x8 af[KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) {
+        const bool ok = r16 < nrow && ks0 + s2 < KSTEPS;
+        buf_frag(af[s2], ra, ok ? (int)((afrag_offset(m, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+      }
+      sched_fence();
+      f32x4 acc[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) acc[s2 % NCH] = mfma16x16x32(af[s2], wf[s2], acc[s2 % NCH]);
+      *reinterpret_cast<f32x4*>(red + ((size_t)wave * 64 + lane) * 4) = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    if (b == 0) PHASE_TS(s, l, kPhO, 4);
+    __syncthreads();
+    reduce_to_tile<1, 1, TS>(red, T);
+    __syncthreads();
+    float ss = 0.f;
+    if (ep_thread && erow < nrow) {
+      u16 hn[8], gn[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float prod = round_bf(fmul(round_bf(T[erow * TS + ec0 + i]), gate[i]));
+        hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
+        const float hf = bf2f(hn[i]);
+        gn[i] = f2bf(fmul(hf, s1[i]));
+        ss += hf * hf;
+      }
+      st_bf16x8(hout, afrag_index(r, col + ec0, kWidth / 32), hn);
+      st_bf16x8(gout, afrag_index(r, col + ec0, kWidth / 32), gn);
+    }
+    if (ep_thread) s_ss[(et & 1) * 16 + erow] = ss;
+    __syncthreads();
+    // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
+    if (tid < 16) st_f32(rout + (size_t)nt * R + 16 * m + tid, s_ss[tid] + s_ss[16 + tid]);
+    __syncthreads();  // red, T and s_ss are reused by the next sample
+  }
+  PHASE_TS(s, l, kPhO, 5);
+  publish(a, flag_base(a, s, l, kPhO) + item, a.epoch);
+  PHASE_TS(s, l, kPhO, 6);
+  return true;
+}
+
+// =============================================================================================
+// down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves split the quarter.
+// Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on the same XCD) keeps
+// its own, waits for the other three, adds the four in quarter order and applies the gated
+// residual h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 511), then writes the
+// new residual rows, g = bf16(h * (1 + scale)) of the next layer's first norm, and the tile's row
+// sums of squares.  (Without the K split, 128 k-steps of weights and a 16-row A block per item
+// measured slower: the loads queue behind each other in the workgroup.)
+// =============================================================================================
+__device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 17;
-  constexpr int PH = kDown ? kPhDown : kPhO;
+  constexpr int PH = kPhDown;
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = blockIdx.x;
   PHASE_TS(s, l, PH, 0);
-  // copy wave, ahead of the polls: down_proj: the next layer's qkv tiles (its gate_up MFMA is
-  // done); o_proj: the rest of this layer's gate_up tiles (attention no longer uses A)
-  if constexpr (kDown) {
+  // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
+  {
     int ln;
     if (next_layer(a, s, l, &ln)) {
       copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
       copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
     }
-  } else {
-    copy_norm_w<kModeGateUp, 16, 16>(a, l, 0, smem);
-    copy_norm_w<kModeGateUp, 0, 32>(a, l, 1, smem);
   }
   if (item >= kTiles * kKSplit) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -1103,22 +1211,22 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   // wave 0 (lane = row of the sample): gate and 1 + scale of the tile's 16 columns
   const int col = nt * 16;
   float4 g4[2] = {}, s14[2] = {};
-  const bool next_g = !kDown || l + 1 < L;  // the last layer's output feeds the final norm only
+  const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
   PHASE_TS(s, l, PH, 1);
   {
-    const unsigned* dep = kDown ? flag_base(a, s, l, kPhGu) + ksp * 64 : flag_base(a, s, l, kPhMerge) + ksp * a.nbp_pad;
-    if (!wait_flags(a, dep, kDown ? 64 : a.nbp, s_flag)) return false;
+    // the gate_up items of this quarter's 1024 activation columns
+    if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
   // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
   // gate and 1 + scale: loaded by waves 0 and 1 right after the polls, used much later
-  const u16* hres = kDown ? a.hmid + slw * (size_t)R * kWidth : a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
+  const u16* hres = a.hmid + slw * (size_t)R * kWidth;
   const bool fin_thread = ksp == 0 && tid < 128;
   const int frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;  // finisher thread: row, first of its 8 columns
   u16x8 hpre = {};
   if (fin_thread) {
-    const float* gmod = a.table + ((size_t)s * NN + 2 * l + (kDown ? 1 : 0)) * kModW + 2 * kWidth + col + fc0;
-    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + (kDown ? 2 : 1)) * kModW + col + fc0;
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
@@ -1126,10 +1234,10 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
     }
     if (frow < kHorizon) hpre = *reinterpret_cast<const u16x8*>(hres + afrag_index(frow, col + fc0, kWidth / 32));
   }
-  const u16* lw = reinterpret_cast<const u16*>(smem + (kDown ? kLdsB : kLdsC));  // this item's K-quarter fragments
-  const u16* act = kDown ? a.act + slw * (size_t)R * kMlp : a.o + slw * (size_t)R * (kHeads * kHeadDim);
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // this item's K-quarter fragments
+  const u16* act = a.act + slw * (size_t)R * kMlp;
   // this phase's K-quarter partials [quarter][tile][row][16] (written once per launch)
-  float* dpart = a.dpart + (slw * 2 + (kDown ? 1 : 0)) * (size_t)kKSplit * kTiles * R * 16;
+  float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;
   float* red = smem + kLdsWork;
   float* T = red + kCompWaves * 4 * 256;  // [64][TS], then the finisher's [2][64] row sums
   const bool own_lds = ksp == 0 && a.batch == 1;  // the finisher keeps its own partial in T
@@ -1186,17 +1294,9 @@ __device__ bool phase_residual(const MegaArgs& a, int s, int l, float* smem, int
   if (!wait_flags(a, fl + kPartFlags + 4 * nt, kKSplit - 1, s_flag)) return false;
   PHASE_TS(s, l, PH, 7);
   {
-    u16 *hout, *gout;
-    float* rout;
-    if (kDown) {
-      hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
-      gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
-      rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
-    } else {
-      hout = a.hmid + slw * (size_t)R * kWidth;
-      gout = a.gmid + slw * (size_t)R * kWidth;
-      rout = a.ssmid + slw * kTiles * R;
-    }
+    u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
+    u16* gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
+    float* rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
     const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
                            round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
     const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
@@ -1259,15 +1359,14 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   // the copy wave: step 0, layer 0 qkv and o_proj weights
   copy_norm_w<kModeQkv, 0, 32>(a, 0, 0, smem);
   copy_norm_w<kModeQkv, 0, 31>(a, 0, 1, smem);
-  copy_residual_w<kHeads * kHeadDim / 32>(a, 0, smem);
   bool ok = true;
   for (int s = 0; s <= a.steps && ok; ++s) {
     ok = phase_io(a, s, smem, &s_flag);
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
       ok = phase_norm_gemm<kModeQkv>(a, s, l, smem, &s_flag) && phase_attn(a, s, l, smem, &s_flag) &&
-           phase_residual<false>(a, s, l, smem, &s_flag) && phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag) &&
-           phase_residual<true>(a, s, l, smem, &s_flag);
+           phase_oproj(a, s, l, smem, &s_flag) && phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag) &&
+           phase_down(a, s, l, smem, &s_flag);
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released

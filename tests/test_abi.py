@@ -96,8 +96,8 @@ def test_device_bytes_covers_weights_and_cache(lib):
     # shift . W^T per (step, layer): 2560 q|k|v + 2 x 4096 gate|up columns, fp32
     need += 10 * 18 * (2560 + 2 * 4096) * 4
     # per-(step, layer) split partials: attention (9 key splits x 25 row blocks x 16 rows x 256
-    # fp32) and the o_proj / down_proj K quarters (2 x 4 x 64 tiles x 64 rows x 16 fp32)
-    need += 10 * 18 * (9 * 25 * 16 * 256 + 2 * 4 * 64 * 64 * 16) * 4
+    # fp32) and the down_proj K quarters (4 x 64 tiles x 64 rows x 16 fp32)
+    need += 10 * 18 * (9 * 25 * 16 * 256 + 4 * 64 * 64 * 16) * 4
     # completion flags: (steps + 1) x (depth + 1) x 7 phases x 32 replicas x 512 words
     need += 11 * 19 * 7 * 32 * 512 * 4
     got = _ext.device_bytes(d)
