@@ -15,7 +15,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
-SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip"]
+SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip", "pi05_prefill.hip"]
+LIBS = ["-lhipblaslt"]  # the prefill's plain GEMMs
 BENCH_SRC = "denoise_bench.hip"
 BENCH_OUT = os.path.join(HERE, "pi05_infer", "denoise_bench")
 
@@ -49,8 +50,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], "-o", OUT + ".tmp"],
-         verbose)
+    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], *LIBS, "-o",
+          OUT + ".tmp"], verbose)
     os.replace(OUT + ".tmp", OUT)
     bench_flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
     _run([hipcc(), *bench_flags, f"-I{INCLUDE}", os.path.join(CSRC, BENCH_SRC), f"-L{os.path.dirname(OUT)}", "-lpi05_denoise",

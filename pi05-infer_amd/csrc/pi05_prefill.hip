@@ -1,0 +1,700 @@
+// Prefix-LM prefill on gfx950: PaliGemma's Gemma-2B language model over the prefix embeddings,
+// producing the per-layer K/V cache the denoise loop consumes (_build_prefix_cache,
+// engine.py:770-794).  Layer l (modeling_gemma.py:460-517):
+//   n  = RMSNorm(h)                          rmsnorm_kernel
+//   qkv = n . [Wq; Wk; Wv]^T                 hipBLASLt (bf16 in/out, fp32 accumulation)
+//   q, k <- RoPE; k, v -> cache              rope_kv_kernel
+//   o  = softmax(q k^T / 16 + mask) v        prefix_attn_kernel (MFMA, K/V staged through LDS)
+//   h += o . Wo^T; n = RMSNorm(h)            hipBLASLt + rmsnorm_kernel (residual fused)
+//   gu = n . [Wg; Wu]^T                      hipBLASLt, N = 32768 in one GEMM
+//   a  = gelu_tanh(g) * u                    geglu_kernel
+//   h += a . Wd^T; n = RMSNorm(h)            hipBLASLt + rmsnorm_kernel
+// The last layer computes only its K/V (patches/prefix_last_layer.py:84-112).  Every valid
+// token attends to every valid token of its sample (pi0_pytorch.py:236-250); positions are
+// cumsum(pad) - 1 (engine.py:776).
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pi05_blocks.h"
+#include "pi05_prefill.h"
+
+namespace pi05 {
+namespace {
+
+constexpr int kPW = 2048;                    // prefix-LM width
+constexpr int kPI = 16384;                   // GeGLU intermediate
+constexpr int kPHD = kHeads * kHeadDim;      // 2048 attention output columns
+constexpr int kPQkvN = kPHD + 2 * kHeadDim;  // 2560 fused q|k|v columns
+constexpr int kPKvN = 2 * kHeadDim;          // 512: k|v columns (the K/V-only last layer)
+constexpr int kPGuN = 2 * kPI;               // 32768 fused gate|up columns
+// per-layer packed weights (bf16 elements): [q; k; v] | o | [gate; up] | down, nn.Linear layout
+constexpr size_t kPOffQkv = 0;
+constexpr size_t kPOffO = kPOffQkv + (size_t)kPQkvN * kPW;
+constexpr size_t kPOffGu = kPOffO + (size_t)kPW * kPHD;
+constexpr size_t kPOffD = kPOffGu + (size_t)kPGuN * kPW;
+constexpr size_t kPLayerElems = kPOffD + (size_t)kPW * kPI;
+constexpr int kAttnMtPerWg = 8;  // attention m-tiles (16 query rows: 2 tokens x 8 heads) per workgroup
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt not waited for (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
+constexpr int kWaitVm0 = (7 << 4) | (15 << 8);
+
+thread_local std::string g_prefix_err;
+
+// ---------------------------------------------------------------------------------------------
+// positions cumsum(pad) - 1 and key-valid bytes of one sample (one workgroup per sample)
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void positions_kernel(const uint8_t* pad, int P, int s_pad, int* pos, uint8_t* valid) {
+  const int b = blockIdx.x, t = threadIdx.x;
+  __shared__ int s_cnt[256];
+  const uint8_t* pb = pad + (size_t)b * P;
+  const int per = (P + 255) / 256, p0 = t * per, p1 = p0 + per < P ? p0 + per : P;
+  int cnt = 0;
+  for (int p = p0; p < p1; ++p) cnt += pb[p] ? 1 : 0;
+  s_cnt[t] = cnt;
+  __syncthreads();
+  // inclusive scan over the 256 chunk counts (Hillis-Steele)
+  for (int off = 1; off < 256; off <<= 1) {
+    const int v = t >= off ? s_cnt[t - off] : 0;
+    __syncthreads();
+    s_cnt[t] += v;
+    __syncthreads();
+  }
+  int run = s_cnt[t] - cnt;  // valid tokens before this chunk
+  for (int p = p0; p < p1; ++p) {
+    run += pb[p] ? 1 : 0;
+    pos[(size_t)b * s_pad + p] = run - 1;
+  }
+  for (int key = t; key < s_pad; key += 256) valid[(size_t)b * s_pad + key] = key < P && pb[key] ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// h = bf16(x + y) (y optional), n = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w))
+// (modeling_gemma.py:82-99 regular branch; _gated_residual without gate, 231-249).  One
+// workgroup per row of 2048: 8 contiguous elements per thread.  h_out may alias x.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y, const float* w, u16* h_out, u16* n_out, float eps) {
+  const size_t off = (size_t)blockIdx.x * kPW + threadIdx.x * 8;
+  __shared__ float s_part[4];
+  const u16x8 xv = *reinterpret_cast<const u16x8*>(x + off);
+  float h[8];
+  if (y) {
+    const u16x8 yv = *reinterpret_cast<const u16x8*>(y + off);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = round_bf(fadd(bf2f(xv[i]), bf2f(yv[i])));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = bf2f(xv[i]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += h[i] * h[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float var = ((s_part[0] + s_part[1]) + (s_part[2] + s_part[3])) * (1.0f / kPW);
+  const float rs = 1.0f / sqrtf(var + eps);
+  const float4 w0 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8);
+  const float4 w1 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8 + 4);
+  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  u16x8 hv, nv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    hv[i] = f2bf(h[i]);
+    nv[i] = f2bf(fmul(fmul(h[i], rs), fadd(1.0f, wv[i])));
+  }
+  if (y && h_out) *reinterpret_cast<u16x8*>(h_out + off) = hv;
+  *reinterpret_cast<u16x8*>(n_out + off) = nv;
+}
+
+// ---------------------------------------------------------------------------------------------
+// RoPE and the K/V write.  One workgroup per token row (b, p).  qkv row: [q (8 heads x 256) | k |
+// v] (ldq = 2560), or [k | v] (ldq = 512, kv_only).  RoPE in fp32 on the bf16 values with bf16
+// cos/sin of freq = inv_freq[d mod 128] * pos, rounded once (modeling_gemma.py:169-216): q to the
+// attention's A-fragment layout (row = token * 8 + head), k and v to the attention's packed K/V
+// block and to the caller's cache [B, 1, P, D].
+// ---------------------------------------------------------------------------------------------
+struct RopeKvArgs {
+  const u16* qkv;
+  int ldq, kv_only, P, s_pad;
+  const int* pos;
+  const float* inv_freq;
+  u16 *qf, *kf, *vf;   // per sample: q fragments [s_pad*8 rows][256], K / V blocks [s_pad keys][256]
+  u16 *kout, *vout;    // caller's cache of this layer
+  int64_t kv_bs, kv_rs;
+};
+
+__device__ __forceinline__ void rope4(const u16* src, float pos, const float* inv_freq, int lo, u16 (&olo)[4], u16 (&ohi)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float freq = fmul(inv_freq[lo + i], pos);
+    const float c = round_bf(cosf(freq)), s = round_bf(sinf(freq));
+    const float xl = bf2f(src[lo + i]), xh = bf2f(src[kHalfDim + lo + i]);
+    olo[i] = f2bf(fsub(fmul(xl, c), fmul(xh, s)));
+    ohi[i] = f2bf(fadd(fmul(xh, c), fmul(xl, s)));
+  }
+}
+
+__device__ __forceinline__ void store4(u16* dst, const u16 (&v)[4]) {
+  *reinterpret_cast<u16x4*>(dst) = u16x4{v[0], v[1], v[2], v[3]};
+}
+
+__global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
+  const int row = blockIdx.x, b = row / a.P, p = row % a.P, t = threadIdx.x;
+  const u16* src = a.qkv + (size_t)row * a.ldq;
+  const float pos = (float)a.pos[(size_t)b * a.s_pad + p];
+  const u16* ksrc = src + (a.kv_only ? 0 : kPHD);
+  const u16* vsrc = ksrc + kHeadDim;
+  if (!a.kv_only) {
+    // q: thread t -> head t/32, dims 4(t%32) .. +3 and their partners + 128
+    const int head = t >> 5, lo = (t & 31) * 4;
+    u16 olo[4], ohi[4];
+    rope4(src + head * kHeadDim, pos, a.inv_freq, lo, olo, ohi);
+    u16* qb = a.qf + (size_t)b * a.s_pad * kHeads * kHeadDim;
+    const int qrow = p * kHeads + head;
+    store4(qb + afrag_index(qrow, lo, kHeadDim / 32), olo);
+    store4(qb + afrag_index(qrow, lo + kHalfDim, kHeadDim / 32), ohi);
+  }
+  const size_t cache = (size_t)b * a.kv_bs + (size_t)p * a.kv_rs;
+  if (t < 32) {
+    const int lo = t * 4;
+    u16 olo[4], ohi[4];
+    rope4(ksrc, pos, a.inv_freq, lo, olo, ohi);
+    u16* kb = a.kf + (size_t)b * a.s_pad * kHeadDim;
+    store4(kb + kfrag_index(p, lo), olo);
+    store4(kb + kfrag_index(p, lo + kHalfDim), ohi);
+    store4(a.kout + cache + lo, olo);
+    store4(a.kout + cache + lo + kHalfDim, ohi);
+  } else if (t >= 64 && t < 128) {
+    const int d0 = (t - 64) * 4;
+    u16 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = vsrc[d0 + i];
+    u16* vb = a.vf + (size_t)b * a.s_pad * kHeadDim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vb[vfrag_index(p, d0 + i)] = v[i];
+    store4(a.vout + cache + d0, v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Masked MQA attention over the prefix (modeling_gemma.py:219-275): 8 query heads share the one
+// K/V head, so a 16-row m-tile holds 2 tokens x 8 heads against the same keys.  Workgroup = 8
+// m-tiles of one sample, wave w owns m-tiles 2w, 2w+1 (query fragments in registers).  Key blocks
+// of 32 (16 KiB of K + 16 KiB of V fragments) are staged into LDS with direct-to-LDS loads, double
+// buffered, and every wave runs the online-softmax block update of the denoise attention
+// (attend_block) on both of its m-tiles.  Masked keys are skipped; a query row with no valid key
+// (a padded token) is written as zeros.
+// ---------------------------------------------------------------------------------------------
+struct AttnArgs {
+  const u16 *qf, *kf, *vf;
+  const uint8_t* valid;
+  u16* out;  // [B*P, 2048]
+  int P, s_pad, n_mt, items;
+};
+
+__global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
+  __shared__ __align__(16) u16 s_kv[2][32][512];
+  const int b = blockIdx.x / a.items, item = blockIdx.x % a.items;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
+  const int wu = __builtin_amdgcn_readfirstlane(wave);
+  const int mt0 = item * kAttnMtPerWg + 2 * wave;
+  const u16* qb = a.qf + (size_t)b * a.s_pad * kHeads * kHeadDim;
+  const u16* kb0 = a.kf + (size_t)b * a.s_pad * kHeadDim;
+  const u16* vb0 = a.vf + (size_t)b * a.s_pad * kHeadDim;
+  const uint8_t* valid = a.valid + (size_t)b * a.s_pad;
+  const int nkb = a.s_pad / 32;
+  bf16x8 qf[2][8];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qf[m][ds] = mt0 + m < a.n_mt ? load_frag(qb + afrag_offset(mt0 + m, ds, kHeadDim / 32) + lane * 8) : zero_frag();
+  // wave w copies fragments 8w .. 8w+7 of a block (K fragments 0..15, then V fragments)
+  auto stage = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f = wu * 8 + i;
+      const u16* src = f < 16 ? kb0 + ((size_t)2 * kb * 8 + f) * 512 : vb0 + ((size_t)kb * 16 + (f - 16)) * 512;
+      __builtin_amdgcn_global_load_lds(const_cast<u16*>(src) + lane * 8, &s_kv[buf][f][0], 16, 0, 0);
+    }
+  };
+  stage(0, 0);
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  f32x4 oacc[2][16];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int d = 0; d < 16; ++d) oacc[m][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = 0; kb < nkb; ++kb) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of block kb have landed
+    __syncthreads();  // every wave's copies of block kb have landed; buffer (kb+1)&1 is no longer read
+    if (kb + 1 < nkb) stage(kb + 1, (kb + 1) & 1);
+    const int buf = kb & 1;
+    KvBlock blk;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      blk.k[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][i][lane * 8]);
+      blk.v[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][16 + i][lane * 8]);
+    }
+    blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
+    blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      if (mt0 + m < a.n_mt) attend_block(blk, qf[m], m_run[m], l_run[m], oacc[m]);
+  }
+  // O = acc / l: lane (row r16 = token 2 mt + r16/8, head r16 % 8) holds dims 16 dt + 4 g .. +3
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int mt = mt0 + m;
+    if (mt >= a.n_mt) continue;
+    float l = l_run[m];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const int r16 = lane & 15, token = 2 * mt + (r16 >> 3), head = r16 & 7;
+    if (token >= a.P) continue;
+    u16* orow = a.out + ((size_t)b * a.P + token) * kPHD + head * kHeadDim + g * 4;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const f32x4 o = oacc[m][dt];
+      *reinterpret_cast<u16x4*>(orow + dt * 16) = u16x4{f2bf(o[0] * inv), f2bf(o[1] * inv), f2bf(o[2] * inv), f2bf(o[3] * inv)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// act = bf16(gelu_tanh(g) * u) over gu rows [g (16384) | u (16384)] (modeling_gemma.py:147 with
+// the fused pointwise rounding: fp32 on the bf16 GEMM outputs, one rounding)
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void geglu_kernel(const u16* gu, u16* act, size_t chunks) {
+  for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (size_t)gridDim.x * 256) {
+    const size_t row = c / (kPI / 8), j = (c % (kPI / 8)) * 8;
+    const u16x8 gv = *reinterpret_cast<const u16x8*>(gu + row * kPGuN + j);
+    const u16x8 uv = *reinterpret_cast<const u16x8*>(gu + row * kPGuN + kPI + j);
+    u16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = f2bf(fmul(gelu_tanh(bf2f(gv[i])), bf2f(uv[i])));
+    *reinterpret_cast<u16x8*>(act + row * kPI + j) = o;
+  }
+}
+
+// out[i] = bf16(table[ids[i]] * sqrt(2048)); an id outside [0, vocab) zero-fills its row and
+// sets *err.
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u16* table, int64_t vocab, u16* out, unsigned* err) {
+  const int64_t i = blockIdx.x;
+  const int32_t id = ids[i];
+  const bool ok = id >= 0 && id < vocab;
+  if (!ok && threadIdx.x == 0) *err = 1u;
+  const size_t d = (size_t)threadIdx.x * 8;
+  u16x8 o = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (ok) {
+    const u16x8 v = *reinterpret_cast<const u16x8*>(table + (size_t)id * kPW + d);
+    const float scale = 45.254833995939045f;  // sqrt(2048) as an fp32 scalar
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = f2bf(fmul(bf2f(v[k]), scale));
+  }
+  *reinterpret_cast<u16x8*>(out + i * kPW + d) = o;
+}
+
+// ---------------------------------------------------------------------------------------------
+// hipBLASLt plans: C[M, N] (row-major) = A[M, K] (row-major) . W[N, K]^T (nn.Linear), bf16 in and
+// out, fp32 accumulation.  In hipBLASLt's column-major terms that is C^T (N x M) = W (stored K x N,
+// transposed) . A^T (stored K x M).
+// ---------------------------------------------------------------------------------------------
+struct GemmPlan {
+  int M = 0, N = 0, K = 0;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t ws = 0;
+};
+
+bool lt_ok(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS; }
+
+bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan* p, std::string* err) {
+  p->M = M, p->N = N, p->K = K;
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (!lt_ok(hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
+      !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lw, HIP_R_16BF, K, N, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->la, HIP_R_16BF, K, M, K)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, HIP_R_16BF, N, M, N))) {
+    *err = "hipBLASLt descriptor creation failed";
+    return false;
+  }
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) {
+    *err = "hipBLASLt preference creation failed";
+    return false;
+  }
+  uint64_t wsb = ws_max;
+  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
+  hipblasLtMatmulHeuristicResult_t res[8];
+  int n = 0;
+  const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->lw, p->la, p->lc, p->lc, pref, 8, res, &n);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  for (int i = 0; lt_ok(s) && i < n; ++i) {
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) {
+      p->algo = res[i].algo;
+      p->ws = res[i].workspaceSize;
+      return true;
+    }
+  }
+  *err = "hipBLASLt found no bf16 GEMM algorithm for M=" + std::to_string(M) + " N=" + std::to_string(N) + " K=" + std::to_string(K);
+  return false;
+}
+
+void free_plan(GemmPlan* p) {
+  if (p->desc) hipblasLtMatmulDescDestroy(p->desc);
+  if (p->lw) hipblasLtMatrixLayoutDestroy(p->lw);
+  if (p->la) hipblasLtMatrixLayoutDestroy(p->la);
+  if (p->lc) hipblasLtMatrixLayoutDestroy(p->lc);
+  *p = GemmPlan{};
+}
+
+struct LayerBind {
+  const void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+  const float *ln1 = nullptr, *ln2 = nullptr;
+};
+
+// Device layout of one context: sizes in bytes.
+struct PrefixPlan {
+  int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0;
+  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws;
+  size_t total() const { return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + 16 * 256; }
+};
+constexpr size_t kWorkspace = 64ull << 20;
+
+size_t rup(size_t x) { return (x + 255) / 256 * 256; }
+
+PrefixPlan plan_of(const pi05_prefix_dims& d) {
+  PrefixPlan p;
+  p.L = d.depth, p.B = d.batch, p.P = d.prefix_len, p.M = d.batch * d.prefix_len;
+  p.s_pad = (d.prefix_len + 31) / 32 * 32;
+  p.n_mt = (d.prefix_len + 1) / 2;
+  p.items = (p.n_mt + kAttnMtPerWg - 1) / kAttnMtPerWg;
+  const size_t M = p.M;
+  p.w = rup((size_t)p.L * kPLayerElems * 2);
+  p.ln = rup((size_t)p.L * 2 * kPW * 4);
+  p.h = rup(M * kPW * 2);
+  p.qkv = rup(M * kPQkvN * 2);
+  p.attn = rup(M * kPHD * 2);
+  p.gu = rup(M * kPGuN * 2);
+  p.act = rup(M * kPI * 2);
+  p.qf = rup((size_t)p.B * p.s_pad * kHeads * kHeadDim * 2);
+  p.kv = rup((size_t)p.B * p.s_pad * kHeadDim * 2);
+  p.pos = rup((size_t)p.B * p.s_pad * 4);
+  p.valid = rup((size_t)p.B * p.s_pad);
+  p.invf = rup(kHalfDim * 4);
+  p.err = 256;
+  p.ws = kWorkspace;
+  return p;
+}
+
+bool check_prefix_dims(const pi05_prefix_dims* d, std::string* msg) {
+  if (!d) {
+    *msg = "dims is NULL";
+    return false;
+  }
+  if (d->width != kPW || d->num_heads != kHeads || d->num_kv_heads != 1 || d->head_dim != kHeadDim || d->mlp_dim != kPI) {
+    *msg = "prefix geometry must be width 2048, 8 heads, 1 KV head, head_dim 256, mlp_dim 16384";
+    return false;
+  }
+  if (d->depth < 1 || d->depth > 64) {
+    *msg = "depth must be in [1, 64]";
+    return false;
+  }
+  if (d->batch < 1 || d->prefix_len < 1 || (int64_t)d->batch * d->prefix_len > (1 << 16)) {
+    *msg = "batch and prefix_len must be >= 1 with batch * prefix_len <= 65536";
+    return false;
+  }
+  if (!(d->rms_eps > 0.f) || !(d->rope_theta > 1.f) || (d->skip_last_layer != 0 && d->skip_last_layer != 1)) {
+    *msg = "rms_eps must be > 0, rope_theta > 1, skip_last_layer 0 or 1";
+    return false;
+  }
+  return true;
+}
+
+// 1 / (theta ** (arange(0, D, 2) / D)) in fp32, as transformers' default RoPE computes it.
+void prefix_inv_freq(float theta, float* out) {
+  for (int i = 0; i < kHalfDim; ++i) {
+    const float ex = (float)(2 * i) / (float)kHeadDim;
+    out[i] = 1.0f / (float)std::pow((double)theta, (double)ex);
+  }
+}
+
+}  // namespace
+}  // namespace pi05
+
+using namespace pi05;
+
+struct pi05_prefix_ctx {
+  pi05_prefix_dims d{};
+  PrefixPlan plan;
+  int device = -1;
+  std::string err;
+  std::vector<LayerBind> binds;
+  bool refreshed = false;
+  char* base = nullptr;
+  u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
+  u16 *qf = nullptr, *kf = nullptr, *vf = nullptr;
+  float *ln = nullptr, *inv_freq = nullptr;
+  int* pos = nullptr;
+  uint8_t* valid = nullptr;
+  unsigned* err_flag = nullptr;
+  void* ws = nullptr;
+  hipblasLtHandle_t lt = nullptr;
+  GemmPlan g_qkv, g_kv, g_o, g_gu, g_d;
+};
+
+namespace {
+
+int fail(pi05_prefix_ctx* c, int code, const std::string& m) {
+  if (c) c->err = m;
+  else g_prefix_err = m;
+  return code;
+}
+
+int hip_fail(pi05_prefix_ctx* c, const char* what, hipError_t e) {
+  return fail(c, PI05_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int gemm(pi05_prefix_ctx* c, const GemmPlan& p, const u16* W, const u16* A, u16* C, hipStream_t st) {
+  const float alpha = 1.f, beta = 0.f;
+  const hipblasStatus_t s = hipblasLtMatmul(c->lt, p.desc, &alpha, W, p.lw, A, p.la, &beta, C, p.lc, C, p.lc, &p.algo,
+                                            c->ws, p.ws, st);
+  if (!lt_ok(s)) return fail(c, PI05_E_HIP, "hipblasLtMatmul failed (status " + std::to_string((int)s) + ")");
+  return PI05_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void pi05_prefix_default_dims(pi05_prefix_dims* d) {
+  if (!d) return;
+  *d = pi05_prefix_dims{};
+  d->width = kPW;
+  d->depth = 18;
+  d->num_heads = kHeads;
+  d->num_kv_heads = 1;
+  d->head_dim = kHeadDim;
+  d->mlp_dim = kPI;
+  d->batch = 1;
+  d->prefix_len = 968;
+  d->rms_eps = 1e-6f;
+  d->rope_theta = 10000.0f;
+  d->skip_last_layer = 1;
+}
+
+int pi05_prefix_check_dims(const pi05_prefix_dims* dims) {
+  std::string m;
+  if (!check_prefix_dims(dims, &m)) return fail(nullptr, PI05_E_INVALID, m);
+  return PI05_OK;
+}
+
+size_t pi05_prefix_device_bytes(const pi05_prefix_dims* dims) {
+  std::string m;
+  if (!check_prefix_dims(dims, &m)) return 0;
+  return plan_of(*dims).total();
+}
+
+const char* pi05_prefix_last_error(const pi05_prefix_ctx* ctx) { return ctx ? ctx->err.c_str() : g_prefix_err.c_str(); }
+
+int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
+  if (!out) return fail(nullptr, PI05_E_INVALID, "out is NULL");
+  *out = nullptr;
+  std::string m;
+  if (!check_prefix_dims(dims, &m)) return fail(nullptr, PI05_E_INVALID, m);
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(nullptr, PI05_E_NODEVICE, std::string("no HIP device: ") + hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, PI05_E_NODEVICE, std::string("device is not gfx950 (MI355X): ") + (e == hipSuccess ? prop.gcnArchName : hipGetErrorString(e)));
+  pi05_prefix_ctx* c = new pi05_prefix_ctx();
+  c->d = *dims;
+  c->device = dev;
+  c->plan = plan_of(*dims);
+  c->binds.resize(dims->depth);
+  const PrefixPlan& p = c->plan;
+  e = hipMalloc(&c->base, p.total());
+  if (e != hipSuccess) {
+    delete c;
+    return fail(nullptr, PI05_E_NOMEM, std::string("prefix context allocation failed: ") + hipGetErrorString(e));
+  }
+  char* q = c->base;
+  auto take = [&](size_t bytes) {
+    char* r = q;
+    q += bytes;
+    return r;
+  };
+  c->w = reinterpret_cast<u16*>(take(p.w));
+  c->ln = reinterpret_cast<float*>(take(p.ln));
+  c->h = reinterpret_cast<u16*>(take(p.h));
+  c->n = reinterpret_cast<u16*>(take(p.h));
+  c->y = reinterpret_cast<u16*>(take(p.h));
+  c->qkv = reinterpret_cast<u16*>(take(p.qkv));
+  c->attn = reinterpret_cast<u16*>(take(p.attn));
+  c->gu = reinterpret_cast<u16*>(take(p.gu));
+  c->act = reinterpret_cast<u16*>(take(p.act));
+  c->qf = reinterpret_cast<u16*>(take(p.qf));
+  c->kf = reinterpret_cast<u16*>(take(p.kv));
+  c->vf = reinterpret_cast<u16*>(take(p.kv));
+  c->pos = reinterpret_cast<int*>(take(p.pos));
+  c->valid = reinterpret_cast<uint8_t*>(take(p.valid));
+  c->inv_freq = reinterpret_cast<float*>(take(p.invf));
+  c->err_flag = reinterpret_cast<unsigned*>(take(p.err));
+  c->ws = take(p.ws);
+  // query rows and keys past P stay zero (finite and masked) for the life of the context
+  e = hipMemset(c->qf, 0, p.qf);
+  if (e == hipSuccess) e = hipMemset(c->kf, 0, p.kv);
+  if (e == hipSuccess) e = hipMemset(c->vf, 0, p.kv);
+  if (e == hipSuccess) e = hipMemset(c->err_flag, 0, p.err);
+  float invf[kHalfDim];
+  prefix_inv_freq(dims->rope_theta, invf);
+  if (e == hipSuccess) e = hipMemcpy(c->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hipFree(c->base);
+    delete c;
+    return fail(nullptr, PI05_E_HIP, std::string("prefix context initialisation failed: ") + hipGetErrorString(e));
+  }
+  std::string perr;
+  const int M = p.M;
+  if (!lt_ok(hipblasLtCreate(&c->lt)) || !make_plan(c->lt, M, kPQkvN, kPW, kWorkspace, &c->g_qkv, &perr) ||
+      !make_plan(c->lt, M, kPKvN, kPW, kWorkspace, &c->g_kv, &perr) || !make_plan(c->lt, M, kPW, kPHD, kWorkspace, &c->g_o, &perr) ||
+      !make_plan(c->lt, M, kPGuN, kPW, kWorkspace, &c->g_gu, &perr) || !make_plan(c->lt, M, kPW, kPI, kWorkspace, &c->g_d, &perr)) {
+    if (perr.empty()) perr = "hipblasLtCreate failed";
+    pi05_prefix_destroy(c);
+    return fail(nullptr, PI05_E_HIP, perr);
+  }
+  *out = c;
+  return PI05_OK;
+}
+
+int pi05_prefix_destroy(pi05_prefix_ctx* c) {
+  if (!c) return PI05_OK;  // like free(NULL)
+  free_plan(&c->g_qkv);
+  free_plan(&c->g_kv);
+  free_plan(&c->g_o);
+  free_plan(&c->g_gu);
+  free_plan(&c->g_d);
+  if (c->lt) hipblasLtDestroy(c->lt);
+  if (c->base) hipFree(c->base);
+  delete c;
+  return PI05_OK;
+}
+
+int pi05_prefix_bind_layer(pi05_prefix_ctx* c, int layer, const void* wq, const void* wk, const void* wv, const void* wo,
+                           const void* wgate, const void* wup, const void* wdown, const float* ln1_w, const float* ln2_w) {
+  if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (layer < 0 || layer >= c->d.depth) return fail(c, PI05_E_INVALID, "layer out of range");
+  const void* ptrs[] = {wq, wk, wv, wo, wgate, wup, wdown, ln1_w, ln2_w};
+  for (const void* p : ptrs) {
+    if (!p) return fail(c, PI05_E_INVALID, "a weight pointer is NULL");
+    if (reinterpret_cast<uintptr_t>(p) % 16) return fail(c, PI05_E_INVALID, "weight pointers must be 16-byte aligned");
+  }
+  c->binds[layer] = LayerBind{wq, wk, wv, wo, wgate, wup, wdown, ln1_w, ln2_w};
+  c->refreshed = false;
+  return PI05_OK;
+}
+
+int pi05_prefix_refresh_weights(pi05_prefix_ctx* c, void* stream) {
+  if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  for (int l = 0; l < c->d.depth; ++l)
+    if (!c->binds[l].wq) return fail(c, PI05_E_STATE, "layer " + std::to_string(l) + " is not bound");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipMemcpyKind k = hipMemcpyDeviceToDevice;
+  for (int l = 0; l < c->d.depth; ++l) {
+    const LayerBind& b = c->binds[l];
+    u16* w = c->w + (size_t)l * kPLayerElems;
+    const size_t sq = (size_t)kPHD * kPW * 2, sk = (size_t)kHeadDim * kPW * 2, sg = (size_t)kPI * kPW * 2;
+    hipError_t e = hipMemcpyAsync(w + kPOffQkv, b.wq, sq, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffQkv + (size_t)kPHD * kPW, b.wk, sk, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffQkv + (size_t)(kPHD + kHeadDim) * kPW, b.wv, sk, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffO, b.wo, (size_t)kPW * kPHD * 2, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffGu, b.wg, sg, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffGu + (size_t)kPI * kPW, b.wu, sg, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kPOffD, b.wd, (size_t)kPW * kPI * 2, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->ln + (size_t)l * 2 * kPW, b.ln1, kPW * 4, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->ln + (size_t)l * 2 * kPW + kPW, b.ln2, kPW * 4, k, st);
+    if (e != hipSuccess) return hip_fail(c, "weight packing", e);
+  }
+  c->refreshed = true;
+  return PI05_OK;
+}
+
+int pi05_prefix_embed_tokens(pi05_prefix_ctx* c, const int32_t* ids, int64_t n_tokens, const void* table, int64_t vocab,
+                             void* out, void* stream) {
+  if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (!ids || !table || !out) return fail(c, PI05_E_INVALID, "ids, table and out must be non-NULL");
+  if (n_tokens < 1 || n_tokens > (1 << 24) || vocab < 1) return fail(c, PI05_E_INVALID, "n_tokens must be in [1, 2^24] and vocab >= 1");
+  if (reinterpret_cast<uintptr_t>(table) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return fail(c, PI05_E_INVALID, "table and out must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemsetAsync(c->err_flag, 0, 4, st);
+  if (e != hipSuccess) return hip_fail(c, "embed", e);
+  embed_kernel<<<(unsigned)n_tokens, 256, 0, st>>>(ids, static_cast<const u16*>(table), vocab, static_cast<u16*>(out), c->err_flag);
+  unsigned flag = 0;
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(&flag, c->err_flag, 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_fail(c, "embed", e);
+  if (flag) return fail(c, PI05_E_INVALID, "a token id is outside [0, vocab)");
+  return PI05_OK;
+}
+
+int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* prefix_pad, void* const* k_layers,
+                        void* const* v_layers, int64_t kv_batch_stride, int64_t kv_row_stride, void* stream) {
+  if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (!embeds || !prefix_pad || !k_layers || !v_layers) return fail(c, PI05_E_INVALID, "embeds, prefix_pad, k_layers and v_layers must be non-NULL");
+  const PrefixPlan& p = c->plan;
+  if (reinterpret_cast<uintptr_t>(embeds) % 16) return fail(c, PI05_E_INVALID, "embeds must be 16-byte aligned");
+  if (kv_row_stride < kHeadDim || kv_row_stride % 4) return fail(c, PI05_E_INVALID, "kv_row_stride must be >= head_dim and a multiple of 4");
+  if (p.B > 1 && kv_batch_stride < (int64_t)p.P * kv_row_stride) return fail(c, PI05_E_INVALID, "kv_batch_stride must cover prefix_len rows");
+  if (kv_batch_stride % 4) return fail(c, PI05_E_INVALID, "kv_batch_stride must be a multiple of 4");
+  for (int l = 0; l < p.L; ++l) {
+    if (!k_layers[l] || !v_layers[l]) return fail(c, PI05_E_INVALID, "a K/V layer pointer is NULL");
+    if (reinterpret_cast<uintptr_t>(k_layers[l]) % 8 || reinterpret_cast<uintptr_t>(v_layers[l]) % 8)
+      return fail(c, PI05_E_INVALID, "K/V layer pointers must be 8-byte aligned");
+  }
+  if (!c->refreshed) return fail(c, PI05_E_STATE, "weights are not bound and refreshed");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u16* emb = static_cast<const u16*>(embeds);
+  const float eps = c->d.rms_eps;
+  positions_kernel<<<p.B, 256, 0, st>>>(prefix_pad, p.P, p.s_pad, c->pos, c->valid);
+  rmsnorm_kernel<<<p.M, 256, 0, st>>>(emb, nullptr, c->ln, nullptr, c->n, eps);
+  for (int l = 0; l < p.L; ++l) {
+    const u16* w = c->w + (size_t)l * kPLayerElems;
+    const float* ln = c->ln + (size_t)l * 2 * kPW;
+    const bool kv_only = c->d.skip_last_layer && l == p.L - 1;
+    RopeKvArgs ra{c->qkv, kv_only ? kPKvN : kPQkvN, kv_only ? 1 : 0, p.P, p.s_pad, c->pos, c->inv_freq,
+                  c->qf, c->kf, c->vf, static_cast<u16*>(k_layers[l]), static_cast<u16*>(v_layers[l]), kv_batch_stride, kv_row_stride};
+    int rc = kv_only ? gemm(c, c->g_kv, w + kPOffQkv + (size_t)kPHD * kPW, c->n, c->qkv, st) : gemm(c, c->g_qkv, w + kPOffQkv, c->n, c->qkv, st);
+    if (rc != PI05_OK) return rc;
+    rope_kv_kernel<<<p.M, 256, 0, st>>>(ra);
+    if (kv_only) break;
+    AttnArgs aa{c->qf, c->kf, c->vf, c->valid, c->attn, p.P, p.s_pad, p.n_mt, p.items};
+    prefix_attn_kernel<<<p.B * p.items, 256, 0, st>>>(aa);
+    if ((rc = gemm(c, c->g_o, w + kPOffO, c->attn, c->y, st)) != PI05_OK) return rc;
+    rmsnorm_kernel<<<p.M, 256, 0, st>>>(l == 0 ? emb : c->h, c->y, ln + kPW, c->h, c->n, eps);
+    if ((rc = gemm(c, c->g_gu, w + kPOffGu, c->n, c->gu, st)) != PI05_OK) return rc;
+    const size_t chunks = (size_t)p.M * (kPI / 8);
+    geglu_kernel<<<(unsigned)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096), 256, 0, st>>>(c->gu, c->act, chunks);
+    if ((rc = gemm(c, c->g_d, w + kPOffD, c->act, c->y, st)) != PI05_OK) return rc;
+    if (l + 1 < p.L) rmsnorm_kernel<<<p.M, 256, 0, st>>>(c->h, c->y, c->ln + (size_t)(l + 1) * 2 * kPW, c->h, c->n, eps);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(c, "prefill launch", e);
+  return PI05_OK;
+}
+
+}  // extern "C"

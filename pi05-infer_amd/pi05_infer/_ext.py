@@ -1,4 +1,5 @@
-"""ctypes binding of ``libpi05_denoise.so`` (the C ABI in ``include/pi05_denoise.h``).
+"""ctypes binding of ``libpi05_denoise.so`` (the C ABIs in ``include/pi05_denoise.h`` and
+``include/pi05_prefill.h``).
 
 The shared library is built in-tree next to this file (``build_lib.py``).  There is no fallback:
 if the library is missing or fails to load, every entry point raises.
@@ -45,6 +46,20 @@ EXPORTED_SYMBOLS = (
     "pi05_rope_inv_freq",
 )
 
+# every exported symbol of include/pi05_prefill.h
+PREFIX_EXPORTED_SYMBOLS = (
+    "pi05_prefix_default_dims",
+    "pi05_prefix_check_dims",
+    "pi05_prefix_device_bytes",
+    "pi05_prefix_create",
+    "pi05_prefix_destroy",
+    "pi05_prefix_last_error",
+    "pi05_prefix_bind_layer",
+    "pi05_prefix_refresh_weights",
+    "pi05_prefix_embed_tokens",
+    "pi05_prefix_forward",
+)
+
 
 class Pi05Error(RuntimeError):
     """A non-zero status from the engine's C ABI."""
@@ -74,6 +89,22 @@ class Pi05Dims(ctypes.Structure):
     ]
 
 
+class Pi05PrefixDims(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("mlp_dim", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("prefix_len", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("skip_last_layer", ctypes.c_int32),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -90,6 +121,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib = ctypes.CDLL(path)
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     dims_p = ctypes.POINTER(Pi05Dims)
+    pdims_p = ctypes.POINTER(Pi05PrefixDims)
     sig = {
         "pi05_abi_version": (i32, []),
         "pi05_default_dims": (None, [dims_p]),
@@ -112,6 +144,16 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_euler_schedule": (i32, [i32, vp]),
         "pi05_time_embedding": (i32, [dims_p, ctypes.c_float, vp]),
         "pi05_rope_inv_freq": (i32, [dims_p, vp]),
+        "pi05_prefix_default_dims": (None, [pdims_p]),
+        "pi05_prefix_check_dims": (i32, [pdims_p]),
+        "pi05_prefix_device_bytes": (ctypes.c_size_t, [pdims_p]),
+        "pi05_prefix_create": (i32, [pdims_p, ctypes.POINTER(vp)]),
+        "pi05_prefix_destroy": (i32, [vp]),
+        "pi05_prefix_last_error": (ctypes.c_char_p, [vp]),
+        "pi05_prefix_bind_layer": (i32, [vp, i32] + [vp] * 9),
+        "pi05_prefix_refresh_weights": (i32, [vp, vp]),
+        "pi05_prefix_embed_tokens": (i32, [vp, vp, i64, vp, i64, vp, vp]),
+        "pi05_prefix_forward": (i32, [vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -308,6 +350,112 @@ class DenoiseContext:
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.lib.pi05_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------------------------ prefill
+
+
+def _check_prefix(lib: ctypes.CDLL, rc: int, ctx: Optional[int]) -> None:
+    if rc != PI05_OK:
+        msg = lib.pi05_prefix_last_error(ctx)
+        raise Pi05Error(rc, msg.decode() if msg else "")
+
+
+def prefix_default_dims() -> Pi05PrefixDims:
+    lib = load_library()
+    d = Pi05PrefixDims()
+    lib.pi05_prefix_default_dims(ctypes.byref(d))
+    return d
+
+
+def prefix_check_dims(dims: Pi05PrefixDims) -> None:
+    lib = load_library()
+    _check_prefix(lib, lib.pi05_prefix_check_dims(ctypes.byref(dims)), None)
+
+
+def prefix_device_bytes(dims: Pi05PrefixDims) -> int:
+    return int(load_library().pi05_prefix_device_bytes(ctypes.byref(dims)))
+
+
+class PrefixContext:
+    """One prefix-LM prefill context: a (batch, prefix_len) signature on the current device."""
+
+    def __init__(self, dims: Pi05PrefixDims, device: torch.device):
+        self.lib = load_library()
+        self.dims = dims
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        _check_prefix(self.lib, self.lib.pi05_prefix_check_dims(ctypes.byref(self.dims)), None)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _check_prefix(self.lib, self.lib.pi05_prefix_create(ctypes.byref(self.dims), ctypes.byref(handle)), None)
+        self.handle = handle.value
+
+    def _call(self, rc: int) -> None:
+        _check_prefix(self.lib, rc, self.handle)
+
+    def bind_layer(self, i: int, wq, wk, wv, wo, wgate, wup, wdown, ln1_w, ln2_w) -> None:
+        bf, f32, dev = torch.bfloat16, torch.float32, self.device
+        ptrs = [
+            _ptr(wq, bf, "wq", dev), _ptr(wk, bf, "wk", dev), _ptr(wv, bf, "wv", dev), _ptr(wo, bf, "wo", dev),
+            _ptr(wgate, bf, "wgate", dev), _ptr(wup, bf, "wup", dev), _ptr(wdown, bf, "wdown", dev),
+            _ptr(ln1_w, f32, "ln1_w", dev), _ptr(ln2_w, f32, "ln2_w", dev),
+        ]
+        self._call(self.lib.pi05_prefix_bind_layer(self.handle, i, *ptrs))
+
+    def refresh_weights(self, stream=None) -> None:
+        self._call(self.lib.pi05_prefix_refresh_weights(self.handle, _stream_ptr(stream)))
+
+    def embed_tokens(self, ids: torch.Tensor, table: torch.Tensor, stream=None) -> torch.Tensor:
+        """``bf16(table[ids] * sqrt(W))`` for int32/int64 ids of any shape -> ``[*ids.shape, W]``."""
+        ids32 = ids.to(device=self.device, dtype=torch.int32).contiguous()
+        tp = _ptr(table, torch.bfloat16, "table", self.device)
+        out = torch.empty((*ids.shape, self.dims.width), dtype=torch.bfloat16, device=self.device)
+        self._call(self.lib.pi05_prefix_embed_tokens(self.handle, ids32.data_ptr(), ids32.numel(), tp, table.shape[0],
+                                                     out.data_ptr(), _stream_ptr(stream)))
+        return out
+
+    def forward(self, embeds: torch.Tensor, prefix_pad: torch.Tensor, k_layers: Sequence[torch.Tensor],
+                v_layers: Sequence[torch.Tensor], stream=None) -> None:
+        """embeds [B, P, W] bf16, prefix_pad [B, P] bool/uint8 -> K/V written into k_layers / v_layers
+        (per layer bf16 [B, 1, P, D] views with the same strides)."""
+        d = self.dims
+        if tuple(embeds.shape) != (d.batch, d.prefix_len, d.width):
+            raise ValueError(f"embeds shape {tuple(embeds.shape)} != {(d.batch, d.prefix_len, d.width)}")
+        ep = _ptr(embeds, torch.bfloat16, "embeds", self.device)
+        pad = prefix_pad.to(torch.uint8) if prefix_pad.dtype == torch.bool else prefix_pad
+        if pad.dtype != torch.uint8 or tuple(pad.shape) != (d.batch, d.prefix_len):
+            raise ValueError(f"prefix_pad must be bool/uint8 [{d.batch}, {d.prefix_len}]")
+        pad = pad.to(self.device).contiguous()
+        if len(k_layers) != d.depth or len(v_layers) != d.depth:
+            raise ValueError(f"expected {d.depth} K and V layers")
+        ref = k_layers[0]
+        if tuple(ref.shape) != (d.batch, 1, d.prefix_len, d.head_dim):
+            raise ValueError(f"K layer shape {tuple(ref.shape)} != {(d.batch, 1, d.prefix_len, d.head_dim)}")
+        bstride, rstride = ref.stride(0), ref.stride(2)
+        for name, layers in (("K", k_layers), ("V", v_layers)):
+            for i, t in enumerate(layers):
+                if t.dtype != torch.bfloat16 or t.device != self.device:
+                    raise TypeError(f"{name}[{i}] must be bf16 on {self.device}")
+                if tuple(t.shape) != tuple(ref.shape) or t.stride(0) != bstride or t.stride(2) != rstride or t.stride(3) != 1:
+                    raise ValueError(f"{name}[{i}] shape/strides differ from layer 0")
+        karr = (ctypes.c_void_p * d.depth)(*[t.data_ptr() for t in k_layers])
+        varr = (ctypes.c_void_p * d.depth)(*[t.data_ptr() for t in v_layers])
+        self._pad = pad
+        self._call(self.lib.pi05_prefix_forward(self.handle, ep, pad.data_ptr(), karr, varr, bstride, rstride,
+                                                _stream_ptr(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.pi05_prefix_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

@@ -1,0 +1,158 @@
+"""GPU parity of the prefix-LM prefill (Gemma-2B over the prefix) against the CPU oracle, through
+the C ABI (include/pi05_prefill.h).
+
+Tolerance, as for the denoise path (bf16 on the GPU, fp32 with bf16 rounding points in the
+oracle): per layer, the K and V of the valid prefix tokens have cosine similarity >= 0.9999 with
+the oracle's and max-abs error <= 2e-2 of the oracle tensor's range.  The token embedding is
+exact (one fp32 product rounded to bf16).  Padded tokens' K/V are don't-care (no valid query ever
+attends to them) and are only required to be finite.
+"""
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+from oracle import denoise_oracle as O
+from oracle import prefix_oracle as PO
+from pi05_infer import _ext
+from pi05_infer import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+REL_MAXABS = 2e-2
+G = PO.PrefixGeometry()
+
+
+def _close(ref: torch.Tensor, got: torch.Tensor, what: str) -> None:
+    ref = ref.double().flatten().cpu()
+    got = got.double().flatten().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    cos = torch.nn.functional.cosine_similarity(ref, got, dim=0).item()
+    maxabs = (ref - got).abs().max().item()
+    rng = (ref.max() - ref.min()).item()
+    print(f"{what}: cos={cos:.7f} maxabs={maxabs:.3e} range={rng:.3f}", flush=True)
+    assert cos >= COS_MIN, f"{what}: cosine {cos} < {COS_MIN}"
+    assert maxabs <= REL_MAXABS * rng, f"{what}: max-abs {maxabs} > {REL_MAXABS} * range {rng}"
+
+
+def _context(depth: int, batch: int, plen: int, layers, skip_last: int = 1) -> tuple:
+    d = _ext.prefix_default_dims()
+    d.depth, d.batch, d.prefix_len, d.skip_last_layer = depth, batch, plen, skip_last
+    ctx = _ext.PrefixContext(d, torch.device("cuda"))
+    keep = []
+    for i, w in enumerate(layers):
+        t = {k: (v.to(torch.bfloat16) if k not in ("ln1", "ln2") else v.float()).cuda().contiguous() for k, v in w.items()}
+        keep.append(t)
+        ctx.bind_layer(i, t["wq"], t["wk"], t["wv"], t["wo"], t["wg"], t["wu"], t["wd"], t["ln1"], t["ln2"])
+    ctx.refresh_weights()
+    torch.cuda.synchronize()
+    return ctx, keep
+
+
+def _run(ctx, embeds: torch.Tensor, pad: torch.Tensor, depth: int):
+    b, p, _ = embeds.shape
+    ks = [torch.full((b, 1, p, G.head_dim), float("nan"), dtype=torch.bfloat16, device="cuda") for _ in range(depth)]
+    vs = [torch.full((b, 1, p, G.head_dim), float("nan"), dtype=torch.bfloat16, device="cuda") for _ in range(depth)]
+    ctx.forward(embeds.to(torch.bfloat16).cuda().contiguous(), pad.cuda(), ks, vs)
+    torch.cuda.synchronize()
+    return ks, vs
+
+
+def _compare(ref_cache, ks, vs, pad, name):
+    for l, (kr, vr) in enumerate(ref_cache):
+        for b in range(pad.shape[0]):
+            valid = pad[b].bool()
+            for what, r, g in (("K", kr, ks[l]), ("V", vr, vs[l])):
+                gb = g[b, 0].float().cpu()
+                assert torch.isfinite(gb).all(), f"{name} layer {l} {what}[{b}]: non-finite (padded rows included)"
+                _close(r[b, 0][valid], gb[valid], f"{name} layer {l} {what}[{b}]")
+
+
+@pytest.fixture(scope="module")
+def layers3():
+    return PO.random_layers(G, 3, seed=11)
+
+
+def test_prefill_parity_single_sample(layers3):
+    print("case prefill: depth 3, B=1, P=96, all valid", flush=True)
+    torch.manual_seed(0)
+    emb = O._bf(torch.randn(1, 96, G.width))
+    pad = torch.ones(1, 96, dtype=torch.bool)
+    ref = PO.prefill(layers3, G, emb, pad)
+    ctx, _keep = _context(3, 1, 96, layers3)
+    ks, vs = _run(ctx, emb, pad, 3)
+    _compare(ref, ks, vs, pad, "B1P96")
+
+
+def test_prefill_parity_ragged_batch(layers3):
+    print("case prefill: depth 3, B=2, P=77 (odd, not a multiple of 32), sample 1 padded from 57", flush=True)
+    torch.manual_seed(1)
+    emb = O._bf(torch.randn(2, 77, G.width))
+    pad = torch.ones(2, 77, dtype=torch.bool)
+    pad[1, 57:] = False
+    ref = PO.prefill(layers3, G, emb, pad)
+    ctx, _keep = _context(3, 2, 77, layers3)
+    ks, vs = _run(ctx, emb, pad, 3)
+    _compare(ref, ks, vs, pad, "B2P77")
+
+
+def test_kv_only_last_layer_matches_full_layer(layers3):
+    print("case prefill: last layer K/V only vs full", flush=True)
+    torch.manual_seed(2)
+    emb = O._bf(torch.randn(1, 40, G.width))
+    pad = torch.ones(1, 40, dtype=torch.bool)
+    ctx1, k1 = _context(3, 1, 40, layers3, skip_last=1)
+    a = _run(ctx1, emb, pad, 3)
+    ctx0, k0 = _context(3, 1, 40, layers3, skip_last=0)
+    b = _run(ctx0, emb, pad, 3)
+    for l in range(3):
+        assert torch.equal(a[0][l], b[0][l]) and torch.equal(a[1][l], b[1][l])
+
+
+def test_embed_tokens_exact_and_rejects_bad_ids():
+    print("case prefill: language-token embedding", flush=True)
+    torch.manual_seed(3)
+    d = _ext.prefix_default_dims()
+    d.depth, d.prefix_len = 1, 8
+    ctx = _ext.PrefixContext(d, torch.device("cuda"))
+    table = O._bf(torch.randn(1000, G.width))
+    ids = torch.randint(0, 1000, (2, 13))
+    got = ctx.embed_tokens(ids.cuda(), table.to(torch.bfloat16).cuda())
+    ref = PO.embed_tokens(ids, table, G.width)
+    assert torch.equal(got.float().cpu(), ref)
+    bad = ids.clone()
+    bad[1, 4] = 1000
+    with pytest.raises(_ext.Pi05Error):
+        ctx.embed_tokens(bad.cuda(), table.to(torch.bfloat16).cuda())
+
+
+def test_prefill_then_denoise_matches_oracle_chain(layers3):
+    """The prefill's cache fed to the denoise engine (pi05_prime_prefix) against the oracle chain:
+    oracle prefill -> oracle denoise."""
+    print("case prefill -> denoise: depth 3, B=1, P=64 (10 padded), 4 steps", flush=True)
+    from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+
+    torch.manual_seed(4)
+    P, steps = 64, 4
+    emb = O._bf(torch.randn(1, P, G.width))
+    pad = torch.ones(1, P, dtype=torch.bool)
+    pad[0, 54:] = False
+    ref_cache = PO.prefill(layers3, G, emb, pad)
+    k_ref = torch.cat([k for k, _ in ref_cache], dim=1)  # [B, L, P, D]
+    v_ref = torch.cat([v for _, v in ref_cache], dim=1)
+    eg = replace(S.ExpertGeometry(), depth=3)
+    w = S.make_weights(eg)
+    x1 = S.make_noise(eg, 1)
+    og = O.geometry_from(eg)
+    table = O.adarms_table(w, og, steps)
+    act_ref, _ = O.sample_actions(w, og, k_ref, v_ref, pad, x1, steps, table)
+    ctx, _keep = _context(3, 1, P, layers3)
+    ks, vs = _run(ctx, emb, pad, 3)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
+    model.load_state_dict(w)
+    model.to("cuda")
+    act, _ = model.sample_actions_with_velocities(Observation(ks, vs, pad.cuda()), x1.cuda())
+    torch.cuda.synchronize()
+    _close(act_ref, act, "prefill->denoise actions")
