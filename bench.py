@@ -3,12 +3,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4]
                     [--schedule persistent|graph] [--no-cpu-baseline]
+    python bench.py --workload prefill [--steps K] [--warmup W] [--no-cpu-baseline]
 
 One bench "step" is one predict's denoise: the 10-step flow-matching Euler loop of the 18-layer
 expert over a static prefix KV cache, with weights, KV and noise already resident in HBM.  In the
 default (persistent) schedule that is ONE launch of the cooperative denoise kernel; in the graph
 schedule one hipGraph replay.  Random-init weights (seed 0), N(0,1) bf16 prefix KV (seed 1),
 N(0,1) noise (seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
+
+``--workload prefill`` measures the prefix-LM prefill instead (Gemma-2B over a 968-token prefix,
+bs=1, 17 full layers + the last layer's K/V): one step is one prefill, MFMA-bound, reported
+against the bf16 dense MFMA peak.
 """
 
 from __future__ import annotations
@@ -33,6 +38,112 @@ CONFIGS = {
 }
 METRIC = "denoise ms/predict (10 steps, bs=1, 968 prefix) + % peak HBM GB/s"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PREFILL_METRIC = "prefix prefill ms (Gemma-2B, bs=1, 968 tokens) + % peak bf16 MFMA"
+
+
+def prefill_flops(depth: int, batch: int, prefix_len: int, skip_last: bool = True) -> int:
+    """FLOPs of one prefill: per full layer the q|k|v, o_proj, gate|up and down_proj GEMMs and the
+    attention's Q.K^T and P.V over every (query, key) pair; the last layer's K/V projection only."""
+    W, H, D, I = 2048, 8, 256, 16384
+    M = batch * prefix_len
+    gemm = 2 * M * W * ((H + 2) * D + H * D + 2 * I) + 2 * M * I * W
+    attn = 2 * 2 * batch * prefix_len * prefix_len * D * H
+    full = depth - 1 if skip_last else depth
+    return full * (gemm + attn) + (2 * M * W * 2 * D if skip_last else 0)
+
+
+def bench_prefill(args) -> int:
+    import torch
+
+    from pi05_infer import _ext
+
+    d = _ext.prefix_default_dims()
+    B, P, L = d.batch, d.prefix_len, d.depth
+    dev = torch.device("cuda", torch.cuda.current_device())
+    ctx = _ext.PrefixContext(d, dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape, std=0.02, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(dtype)
+
+    layers = []
+    for i in range(L):
+        w = dict(wq=rnd(2048, 2048), wk=rnd(256, 2048), wv=rnd(256, 2048), wo=rnd(2048, 2048), wg=rnd(16384, 2048),
+                 wu=rnd(16384, 2048), wd=rnd(2048, 16384), ln1=rnd(2048, std=0.1, dtype=torch.float32),
+                 ln2=rnd(2048, std=0.1, dtype=torch.float32))
+        ctx.bind_layer(i, w["wq"], w["wk"], w["wv"], w["wo"], w["wg"], w["wu"], w["wd"], w["ln1"], w["ln2"])
+        layers.append(w)
+    ctx.refresh_weights()
+    emb = torch.randn(B, P, 2048, generator=gen, device=dev).to(torch.bfloat16)
+    pad = torch.ones(B, P, dtype=torch.bool, device=dev)
+    ks = [torch.empty(B, 1, P, 256, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    vs = [torch.empty(B, 1, P, 256, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        ctx.forward(emb, pad, ks, vs, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        ctx.forward(emb, pad, ks, vs, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = prefill_flops(L, B, P)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import prefix_oracle as PO
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        g = PO.PrefixGeometry()
+        w0 = {k: v.float().cpu() for k, v in layers[0].items()}
+        h = emb.float().cpu()
+        pos, mask4d = PO.prefix_masks(pad.cpu())
+        from oracle import denoise_oracle as O
+
+        cos, sin = O.rope_cos_sin(pos, g.head_dim, g.rope_theta)
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            PO.prefix_layer(w0, g, h, cos, sin, mask4d)
+            times.append(time.perf_counter() - t0)
+        layer_ms = statistics.median(times) * 1e3
+        cpu = {
+            "value": round(layer_ms * (L - 1) + layer_ms * 512 / (2560 + 2048 + 32768 + 16384), 1),
+            "unit": "ms/prefill",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one full decoder layer of the fp32 CPU oracle at B={B}, P={P} (median of 2), scaled to "
+                      f"{L - 1} full layers + the K/V-only last layer; host {cpu_model()}",
+        }
+    out = {
+        "metric": PREFILL_METRIC,
+        "value": round(ms, 4),
+        "unit": "ms/prefill",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init Gemma-2B weights N(0, 0.02), N(0,1) bf16 prefix embeddings, seed 0)",
+        "config": {"workload": f"Gemma-2B prefix prefill, depth {L} (last layer K/V only), bs={B}, {P} tokens",
+                   "batch": B, "prefix_len": P},
+        "roofline": {"kernel": "whole prefill (hipBLASLt GEMMs + HIP kernels)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None, "flops_per_prefill": flops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+    torch.cuda.synchronize()
+    return 0
 
 
 def algorithmic_bytes_per_predict(depth: int, batch: int, prefix_len: int, steps: int) -> int:
@@ -81,12 +192,15 @@ def main() -> int:
                     help="execution schedule (default: the library's choice, persistent on MI355X)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-predicts", type=int, default=8, help="predicts in the CPU-baseline sample")
+    ap.add_argument("--workload", default="denoise", choices=["denoise", "prefill"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs the denoise loop on one GPU; runs with --gpus > 1 are not "
               "supported (data-parallel sharding over samples needs no communication, see DESIGN.md).",
               file=sys.stderr)
         return 2
+    if args.workload == "prefill":
+        return bench_prefill(args)
 
     import torch
 

@@ -189,18 +189,23 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
 // of 32 (16 KiB of K + 16 KiB of V fragments) are staged into LDS with direct-to-LDS loads, double
 // buffered, and every wave runs the online-softmax block update of the denoise attention
 // (attend_block) on both of its m-tiles.  Masked keys are skipped; a query row with no valid key
-// (a padded token) is written as zeros.
+// (a padded token) is written as zeros.  With nsplit > 1 the key blocks are split over nsplit
+// workgroups per m-tile group (so that short prefixes still fill the GPU), which store their
+// unnormalised fp32 O and running (max, sum) per row for attn_merge_kernel.
 // ---------------------------------------------------------------------------------------------
 struct AttnArgs {
   const u16 *qf, *kf, *vf;
   const uint8_t* valid;
-  u16* out;  // [B*P, 2048]
-  int P, s_pad, n_mt, items;
+  u16* out;    // [B*P, 2048] (nsplit == 1)
+  float* po;   // [nsplit][B][n_mt*16 rows][256] partial O (nsplit > 1); row = token * 8 + head
+  float* pml;  // [nsplit][B][n_mt*16 rows][2] running max, sum
+  int B, P, s_pad, n_mt, items, nsplit;
 };
 
 __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) u16 s_kv[2][32][512];
-  const int b = blockIdx.x / a.items, item = blockIdx.x % a.items;
+  const int split = blockIdx.x % a.nsplit, bi = blockIdx.x / a.nsplit;
+  const int b = bi / a.items, item = bi % a.items;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
   const int wu = __builtin_amdgcn_readfirstlane(wave);
   const int mt0 = item * kAttnMtPerWg + 2 * wave;
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
   const u16* kb0 = a.kf + (size_t)b * a.s_pad * kHeadDim;
   const u16* vb0 = a.vf + (size_t)b * a.s_pad * kHeadDim;
   const uint8_t* valid = a.valid + (size_t)b * a.s_pad;
-  const int nkb = a.s_pad / 32;
+  const int nkb = a.s_pad / 32, kb_lo = split * nkb / a.nsplit, kb_hi = (split + 1) * nkb / a.nsplit;
   bf16x8 qf[2][8];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
@@ -224,17 +229,17 @@ __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
       __builtin_amdgcn_global_load_lds(const_cast<u16*>(src) + lane * 8, &s_kv[buf][f][0], 16, 0, 0);
     }
   };
-  stage(0, 0);
+  stage(kb_lo, kb_lo & 1);
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
   f32x4 oacc[2][16];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int d = 0; d < 16; ++d) oacc[m][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = 0; kb < nkb; ++kb) {
+  for (int kb = kb_lo; kb < kb_hi; ++kb) {
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of block kb have landed
     __syncthreads();  // every wave's copies of block kb have landed; buffer (kb+1)&1 is no longer read
-    if (kb + 1 < nkb) stage(kb + 1, (kb + 1) & 1);
+    if (kb + 1 < kb_hi) stage(kb + 1, (kb + 1) & 1);
     const int buf = kb & 1;
     KvBlock blk;
 #pragma unroll
@@ -256,9 +261,20 @@ __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
     float l = l_run[m];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
     const int r16 = lane & 15, token = 2 * mt + (r16 >> 3), head = r16 & 7;
     if (token >= a.P) continue;
+    if (a.nsplit > 1) {
+      const size_t row = ((size_t)split * a.B + b) * ((size_t)a.n_mt * 16) + (size_t)mt * 16 + r16;
+      float* prow = a.po + row * kHeadDim + g * 4;
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(prow + dt * 16) = oacc[m][dt];
+      if (g == 0) {
+        a.pml[row * 2] = m_run[m];
+        a.pml[row * 2 + 1] = l;
+      }
+      continue;
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
     u16* orow = a.out + ((size_t)b * a.P + token) * kPHD + head * kHeadDim + g * 4;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
@@ -266,6 +282,32 @@ __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
       *reinterpret_cast<u16x4*>(orow + dt * 16) = u16x4{f2bf(o[0] * inv), f2bf(o[1] * inv), f2bf(o[2] * inv), f2bf(o[3] * inv)};
     }
   }
+}
+
+// The key splits of one token row (b, token): out = sum_s O_s w_s / sum_s l_s w_s with
+// w_s = exp(m_s - max_s m_s), splits in order; thread t: head t/32, dims 8(t%32) .. +7.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* po, const float* pml, u16* out, int B, int P, int n_mt, int nsplit) {
+  const int b = blockIdx.x / P, token = blockIdx.x % P, t = threadIdx.x;
+  const int head = t >> 5, d0 = (t & 31) * 8;
+  const size_t rows = (size_t)n_mt * 16, row = (size_t)token * kHeads + head;
+  float M = -INFINITY;
+  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pml[(((size_t)sp * B + b) * rows + row) * 2]);
+  float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const size_t r = ((size_t)sp * B + b) * rows + row;
+    const float ms = pml[r * 2];
+    const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+    L += pml[r * 2 + 1] * w;
+    const float4 v0 = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0);
+    const float4 v1 = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0 + 4);
+    o[0] += v0.x * w, o[1] += v0.y * w, o[2] += v0.z * w, o[3] += v0.w * w;
+    o[4] += v1.x * w, o[5] += v1.y * w, o[6] += v1.z * w, o[7] += v1.w * w;
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  u16x8 r8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r8[i] = f2bf(o[i] * inv);
+  *reinterpret_cast<u16x8*>(out + ((size_t)b * P + token) * kPHD + head * kHeadDim + d0) = r8;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -313,7 +355,10 @@ struct GemmPlan {
   hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
   hipblasLtMatmulAlgo_t algo{};
   size_t ws = 0;
+  std::vector<hipblasLtMatmulHeuristicResult_t> cands;  // heuristic candidates, timed by tune_plan
+  float ms = 0.f;                                        // the chosen algorithm's time
 };
+constexpr int kGemmCandidates = 256;
 
 bool lt_ok(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS; }
 
@@ -336,19 +381,53 @@ bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan
   }
   uint64_t wsb = ws_max;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
-  hipblasLtMatmulHeuristicResult_t res[8];
+  std::vector<hipblasLtMatmulHeuristicResult_t> res(kGemmCandidates);
   int n = 0;
-  const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->lw, p->la, p->lc, p->lc, pref, 8, res, &n);
+  const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->lw, p->la, p->lc, p->lc, pref, kGemmCandidates, res.data(), &n);
   hipblasLtMatmulPreferenceDestroy(pref);
-  for (int i = 0; lt_ok(s) && i < n; ++i) {
-    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) {
-      p->algo = res[i].algo;
-      p->ws = res[i].workspaceSize;
-      return true;
-    }
+  for (int i = 0; lt_ok(s) && i < n; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) p->cands.push_back(res[i]);
+  if (!p->cands.empty()) {
+    p->algo = p->cands[0].algo;  // the heuristic's first choice until tune_plan has timed them all
+    p->ws = p->cands[0].workspaceSize;
+    return true;
   }
   *err = "hipBLASLt found no bf16 GEMM algorithm for M=" + std::to_string(M) + " N=" + std::to_string(N) + " K=" + std::to_string(K);
   return false;
+}
+
+// Time every candidate algorithm on the context's own buffers (3 runs after one warm-up; the
+// values are irrelevant to the timing) and keep the fastest.  Candidates that fail to launch are
+// skipped; the heuristic's first choice stays if all fail.
+bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const void* A, void* C, void* ws, hipStream_t st) {
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return false;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    hipEventDestroy(e0);
+    return false;
+  }
+  const float alpha = 1.f, beta = 0.f;
+  float best = 1e30f;
+  for (const auto& c : p->cands) {
+    bool ok = lt_ok(hipblasLtMatmul(h, p->desc, &alpha, W, p->lw, A, p->la, &beta, C, p->lc, C, p->lc, &c.algo, ws, c.workspaceSize, st));
+    if (!ok) continue;
+    hipEventRecord(e0, st);
+    for (int r = 0; r < 3 && ok; ++r)
+      ok = lt_ok(hipblasLtMatmul(h, p->desc, &alpha, W, p->lw, A, p->la, &beta, C, p->lc, C, p->lc, &c.algo, ws, c.workspaceSize, st));
+    hipEventRecord(e1, st);
+    if (hipEventSynchronize(e1) != hipSuccess) break;
+    float ms = 0.f;
+    if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+    if (ms < best) {
+      best = ms;
+      p->algo = c.algo;
+      p->ws = c.workspaceSize;
+    }
+  }
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  p->ms = best / 3.f;
+  return hipGetLastError() == hipSuccess;
 }
 
 void free_plan(GemmPlan* p) {
@@ -366,9 +445,11 @@ struct LayerBind {
 
 // Device layout of one context: sizes in bytes.
 struct PrefixPlan {
-  int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0;
-  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws;
-  size_t total() const { return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + 16 * 256; }
+  int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0, nsplit = 1;
+  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws, po, pml;
+  size_t total() const {
+    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + po + pml + 16 * 256;
+  }
 };
 constexpr size_t kWorkspace = 64ull << 20;
 
@@ -380,6 +461,13 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   p.s_pad = (d.prefix_len + 31) / 32 * 32;
   p.n_mt = (d.prefix_len + 1) / 2;
   p.items = (p.n_mt + kAttnMtPerWg - 1) / kAttnMtPerWg;
+  // key splits: as many as keep every attention workgroup in one round on 256 CUs (one
+  // workgroup per CU), at most 8 and at most one per key block
+  const int nkb = p.s_pad / 32;
+  p.nsplit = 256 / (p.B * p.items);
+  if (p.nsplit > 8) p.nsplit = 8;
+  if (p.nsplit > nkb) p.nsplit = nkb;
+  if (p.nsplit < 1) p.nsplit = 1;
   const size_t M = p.M;
   p.w = rup((size_t)p.L * kPLayerElems * 2);
   p.ln = rup((size_t)p.L * 2 * kPW * 4);
@@ -395,6 +483,9 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   p.invf = rup(kHalfDim * 4);
   p.err = 256;
   p.ws = kWorkspace;
+  const size_t rows = (size_t)p.B * p.n_mt * 16;
+  p.po = p.nsplit > 1 ? rup((size_t)p.nsplit * rows * kHeadDim * 4) : 0;
+  p.pml = p.nsplit > 1 ? rup((size_t)p.nsplit * rows * 2 * 4) : 0;
   return p;
 }
 
@@ -445,7 +536,7 @@ struct pi05_prefix_ctx {
   char* base = nullptr;
   u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
   u16 *qf = nullptr, *kf = nullptr, *vf = nullptr;
-  float *ln = nullptr, *inv_freq = nullptr;
+  float *ln = nullptr, *inv_freq = nullptr, *po = nullptr, *pml = nullptr;
   int* pos = nullptr;
   uint8_t* valid = nullptr;
   unsigned* err_flag = nullptr;
@@ -554,11 +645,11 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   c->inv_freq = reinterpret_cast<float*>(take(p.invf));
   c->err_flag = reinterpret_cast<unsigned*>(take(p.err));
   c->ws = take(p.ws);
-  // query rows and keys past P stay zero (finite and masked) for the life of the context
-  e = hipMemset(c->qf, 0, p.qf);
-  if (e == hipSuccess) e = hipMemset(c->kf, 0, p.kv);
-  if (e == hipSuccess) e = hipMemset(c->vf, 0, p.kv);
-  if (e == hipSuccess) e = hipMemset(c->err_flag, 0, p.err);
+  c->po = reinterpret_cast<float*>(take(p.po));
+  c->pml = reinterpret_cast<float*>(take(p.pml));
+  // everything starts zeroed: query rows and keys past P stay zero (finite and masked) for the
+  // life of the context, and the GEMM tuning below reads defined values
+  e = hipMemset(c->base, 0, p.total());
   float invf[kHalfDim];
   prefix_inv_freq(dims->rope_theta, invf);
   if (e == hipSuccess) e = hipMemcpy(c->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice);
@@ -575,6 +666,14 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
     if (perr.empty()) perr = "hipblasLtCreate failed";
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, perr);
+  }
+  // pick each GEMM's fastest algorithm on this device and shape
+  const bool tuned = tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr) && tune_plan(c->lt, &c->g_kv, c->w, c->n, c->qkv, c->ws, nullptr) &&
+                     tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_gu, c->w, c->n, c->gu, c->ws, nullptr) &&
+                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr);
+  if (!tuned) {
+    pi05_prefix_destroy(c);
+    return fail(nullptr, PI05_E_HIP, "GEMM algorithm tuning failed");
   }
   *out = c;
   return PI05_OK;
@@ -682,8 +781,9 @@ int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* p
     if (rc != PI05_OK) return rc;
     rope_kv_kernel<<<p.M, 256, 0, st>>>(ra);
     if (kv_only) break;
-    AttnArgs aa{c->qf, c->kf, c->vf, c->valid, c->attn, p.P, p.s_pad, p.n_mt, p.items};
-    prefix_attn_kernel<<<p.B * p.items, 256, 0, st>>>(aa);
+    AttnArgs aa{c->qf, c->kf, c->vf, c->valid, c->attn, c->po, c->pml, p.B, p.P, p.s_pad, p.n_mt, p.items, p.nsplit};
+    prefix_attn_kernel<<<p.B * p.items * p.nsplit, 256, 0, st>>>(aa);
+    if (p.nsplit > 1) attn_merge_kernel<<<p.M, 256, 0, st>>>(c->po, c->pml, c->attn, p.B, p.P, p.n_mt, p.nsplit);
     if ((rc = gemm(c, c->g_o, w + kPOffO, c->attn, c->y, st)) != PI05_OK) return rc;
     rmsnorm_kernel<<<p.M, 256, 0, st>>>(l == 0 ? emb : c->h, c->y, ln + kPW, c->h, c->n, eps);
     if ((rc = gemm(c, c->g_gu, w + kPOffGu, c->n, c->gu, st)) != PI05_OK) return rc;

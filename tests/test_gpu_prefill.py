@@ -107,8 +107,11 @@ def test_kv_only_last_layer_matches_full_layer(layers3):
     a = _run(ctx1, emb, pad, 3)
     ctx0, k0 = _context(3, 1, 40, layers3, skip_last=0)
     b = _run(ctx0, emb, pad, 3)
+    # each context tunes its own GEMM algorithms (and the K/V-only layer runs an N=512 GEMM), so
+    # accumulation orders may differ: equal up to bf16 rounding of the GEMM outputs
     for l in range(3):
-        assert torch.equal(a[0][l], b[0][l]) and torch.equal(a[1][l], b[1][l])
+        _close(b[0][l].float(), a[0][l].float(), f"K/V-only vs full: layer {l} K")
+        _close(b[1][l].float(), a[1][l].float(), f"K/V-only vs full: layer {l} V")
 
 
 def test_embed_tokens_exact_and_rejects_bad_ids():
