@@ -8,10 +8,11 @@ compile, engine.py:1003-1059), ``invalidate_weight_derived_caches`` (engine.py:5
 ``predict_action_batch`` (engine.py:321-342).
 
 Every denoise computation happens in ``libpi05_denoise.so``; PyTorch only provides device
-memory, streams and the random noise draw.  The prefix (SigLIP + PaliGemma prefill,
-engine.py:770-794) is not built here: an observation carries the prefix KV cache and pad mask
-that ``_build_prefix_cache`` would produce (the reference's frozen-prefix mode,
-tools/bitexact_compiled_toggles.py:354-376).
+memory, streams and the random noise draw.  An observation carries either the prefix KV cache and
+pad mask that ``_build_prefix_cache`` produces (the reference's frozen-prefix mode,
+tools/bitexact_compiled_toggles.py:354-376), or the prefix embeddings and pad mask, in which case
+the attached ``PrefixLM`` (prefix.py) runs the Gemma-2B prefill on the GPU first.  SigLIP is not
+part of this engine: image embeddings come with the observation.
 """
 
 from __future__ import annotations
@@ -53,17 +54,21 @@ class OpenPi0InferConfig:
 @dataclass
 class Observation:
     """What ``sample_actions`` consumes: the prefix KV cache of ``_build_prefix_cache`` (per layer
-    K and V bf16 ``[B, 1, P, D]``, or stacked ``[B, L, P, D]``), its pad mask ``[B, P]`` and the
-    robot state (unused by pi0.5's suffix, pi0_pytorch.py:269-287)."""
+    K and V bf16 ``[B, 1, P, D]``, or stacked ``[B, L, P, D]``) or the prefix embeddings
+    ``[B, P, 2048]`` (``embed_prefix``'s output, pi0_pytorch.py:190-255; prefix_k/prefix_v None),
+    the pad mask ``[B, P]`` and the robot state (unused by pi0.5's suffix, pi0_pytorch.py:269-287)."""
 
     prefix_k: Any
     prefix_v: Any
     prefix_pad_masks: torch.Tensor
     state: Optional[torch.Tensor] = None
     extra: dict = field(default_factory=dict)
+    prefix_embs: Optional[torch.Tensor] = None
 
     @classmethod
     def from_dict(cls, d: dict) -> "Observation":
+        if "prefix_embs" in d:
+            return cls(None, None, d["prefix_pad_masks"], d.get("state"), prefix_embs=d["prefix_embs"])
         if "past_key_values" in d:
             kv = d["past_key_values"]
             ks = [p[0] for p in kv]
@@ -101,6 +106,7 @@ class OpenPi0Inference:
         self._torch_compile_mode = None
         self.training = False
         self.schedule: Optional[str] = None  # None: the library's default for the device
+        self.prefix_lm = None  # optional PrefixLM (prefix.py): prefix embeddings -> KV cache
 
     # ------------------------------------------------------------------ parameters
     def expected_parameters(self) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
@@ -146,7 +152,17 @@ class OpenPi0Inference:
             self.params = {k: v.to(device).contiguous() for k, v in self.params.items()}
             self.device = device
             self._drop_contexts()
+            if self.prefix_lm is not None:
+                self.prefix_lm.to(device)
         return self
+
+    def attach_prefix_lm(self, prefix_lm) -> None:
+        """Run the Gemma-2B prefill (prefix.PrefixLM) for observations that carry prefix
+        embeddings instead of a KV cache; its depth must equal the expert's."""
+        if prefix_lm.geometry.depth != self.geometry.depth:
+            raise ValueError("prefix LM and action expert must have the same depth (one KV layer per expert layer)")
+        prefix_lm.to(self.device)
+        self.prefix_lm = prefix_lm
 
     def eval(self):
         self.training = False
@@ -216,9 +232,16 @@ class OpenPi0Inference:
 
     def _run(self, observation, noise, trace: bool):
         obs = Observation.from_dict(observation) if isinstance(observation, dict) else observation
-        ks = _split_layers(obs.prefix_k, self.geometry.depth)
-        vs = _split_layers(obs.prefix_v, self.geometry.depth)
         pad = obs.prefix_pad_masks
+        if obs.prefix_k is None:
+            if obs.prefix_embs is None or self.prefix_lm is None:
+                raise ValueError("the observation has no prefix KV cache; prefix embeddings need an attached PrefixLM")
+            _, pad, kv = self.prefix_lm.build_prefix_cache(obs.prefix_embs, pad)
+            ks = [k for k, _ in kv]
+            vs = [v for _, v in kv]
+        else:
+            ks = _split_layers(obs.prefix_k, self.geometry.depth)
+            vs = _split_layers(obs.prefix_v, self.geometry.depth)
         bsize, plen = pad.shape
         device = self.device
         cfg = self.config
@@ -284,6 +307,8 @@ class OpenPi0Inference:
 
     def close(self) -> None:
         self._drop_contexts()
+        if self.prefix_lm is not None:
+            self.prefix_lm.close()
 
 
 Engine = OpenPi0Inference

@@ -151,11 +151,23 @@ def test_prefill_then_denoise_matches_oracle_chain(layers3):
     og = O.geometry_from(eg)
     table = O.adarms_table(w, og, steps)
     act_ref, _ = O.sample_actions(w, og, k_ref, v_ref, pad, x1, steps, table)
-    ctx, _keep = _context(3, 1, P, layers3)
-    ks, vs = _run(ctx, emb, pad, 3)
+    # through the Python API: the observation carries prefix embeddings, the attached PrefixLM
+    # builds the cache (build_prefix_cache), the expert denoises on it
+    from pi05_infer.prefix import PrefixGeometry, PrefixLM, layer_param_names
+
+    plm = PrefixLM(PrefixGeometry(depth=3))
+    sd = {}
+    for i, lw in enumerate(layers3):
+        n = layer_param_names(i)
+        for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "ln1", "ln2"):
+            sd[n[k]] = lw[k]
+    missing, _ = plm.load_state_dict(sd)
+    assert missing == [PO.layer_names(0)["wq"].split("layers.")[0] + "embed_tokens.weight"]
     model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
     model.load_state_dict(w)
     model.to("cuda")
-    act, _ = model.sample_actions_with_velocities(Observation(ks, vs, pad.cuda()), x1.cuda())
+    model.attach_prefix_lm(plm)
+    obs = Observation(None, None, pad.cuda(), prefix_embs=emb.to(torch.bfloat16).cuda())
+    act, _ = model.sample_actions_with_velocities(obs, x1.cuda())
     torch.cuda.synchronize()
     _close(act_ref, act, "prefill->denoise actions")
