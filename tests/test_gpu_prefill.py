@@ -171,3 +171,51 @@ def test_prefill_then_denoise_matches_oracle_chain(layers3):
     act, _ = model.sample_actions_with_velocities(obs, x1.cuda())
     torch.cuda.synchronize()
     _close(act_ref, act, "prefill->denoise actions")
+
+
+def test_full_depth_prefill_then_denoise_c5_geometry():
+    """All 18 Gemma-2B layers (17 full + the K/V-only last) into the 18-layer expert: the cache's
+    rounding noise grows with depth, so the bar is the north star's on the denoise output (actions
+    and every step's velocity), with the per-layer K/V cosine reported."""
+    print("case prefill -> denoise: depth 18, B=1, P=96 (16 padded), 10 steps", flush=True)
+    from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+    from pi05_infer.prefix import PrefixGeometry, PrefixLM, layer_param_names
+
+    torch.manual_seed(5)
+    P, steps = 96, 10
+    layers = PO.random_layers(G, 18, seed=21)
+    print("  weights generated", flush=True)
+    emb = O._bf(torch.randn(1, P, G.width))
+    pad = torch.ones(1, P, dtype=torch.bool)
+    pad[0, 80:] = False
+    ref_cache = PO.prefill(layers, G, emb, pad)
+    print("  oracle prefill done", flush=True)
+    plm = PrefixLM(PrefixGeometry())
+    plm.load_state_dict({layer_param_names(i)[k]: lw[k] for i, lw in enumerate(layers) for k in lw})
+    del layers
+    eg = S.ExpertGeometry()
+    w = S.make_weights(eg)
+    x1 = S.make_noise(eg, 1)
+    og = O.geometry_from(eg)
+    table = O.adarms_table(w, og, steps)
+    k_ref = torch.cat([k for k, _ in ref_cache], dim=1)
+    v_ref = torch.cat([v for _, v in ref_cache], dim=1)
+    act_ref, vs_ref = O.sample_actions(w, og, k_ref, v_ref, pad, x1, steps, table)
+    print("  oracle denoise done", flush=True)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
+    model.load_state_dict(w)
+    model.to("cuda")
+    model.attach_prefix_lm(plm)
+    _, _, kv = plm.build_prefix_cache(emb.to(torch.bfloat16).cuda(), pad.cuda())
+    valid = pad[0]
+    for l in (0, 5, 11, 17):
+        for what, r, g in (("K", ref_cache[l][0], kv[l][0]), ("V", ref_cache[l][1], kv[l][1])):
+            rr, gg = r[0, 0][valid].double().flatten(), g[0, 0].float().cpu()[valid].double().flatten()
+            print(f"  layer {l} {what}: cos={torch.nn.functional.cosine_similarity(rr, gg, dim=0).item():.7f}", flush=True)
+    obs = Observation(None, None, pad.cuda(), prefix_embs=emb.to(torch.bfloat16).cuda())
+    act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
+    torch.cuda.synchronize()
+    for s in range(steps):
+        _close(vs_ref[s], vs[s], f"depth-18 prefill->denoise step {s} velocity")
+    _close(act_ref, act, "depth-18 prefill->denoise actions")
+    model.close()
