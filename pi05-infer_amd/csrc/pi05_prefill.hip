@@ -75,14 +75,30 @@ __global__ __launch_bounds__(256) void positions_kernel(const uint8_t* pad, int 
 // ---------------------------------------------------------------------------------------------
 // h = bf16(x + y) (y optional), n = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w))
 // (modeling_gemma.py:82-99 regular branch; _gated_residual without gate, 231-249).  One
-// workgroup per row of 2048: 8 contiguous elements per thread.  h_out may alias x.
+// workgroup per row of 2048: 8 contiguous elements per thread.  h_out may alias x.  With ys, y is
+// the bf16 rounding of the sum of nsplit fp32 split-K partials ys[s * split_stride + ...], added
+// in split order (the GEMM's own rounding of its full sum).
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y, const float* w, u16* h_out, u16* n_out, float eps) {
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y, const float* w, u16* h_out, u16* n_out, float eps,
+                                                      const float* ys = nullptr, int nsplit = 0, size_t split_stride = 0) {
   const size_t off = (size_t)blockIdx.x * kPW + threadIdx.x * 8;
   __shared__ float s_part[4];
   const u16x8 xv = *reinterpret_cast<const u16x8*>(x + off);
   float h[8];
-  if (y) {
+  if (ys) {
+    float acc[8];
+    {
+      const float4 a0 = *reinterpret_cast<const float4*>(ys + off), a1 = *reinterpret_cast<const float4*>(ys + off + 4);
+      acc[0] = a0.x, acc[1] = a0.y, acc[2] = a0.z, acc[3] = a0.w, acc[4] = a1.x, acc[5] = a1.y, acc[6] = a1.z, acc[7] = a1.w;
+    }
+    for (int sp = 1; sp < nsplit; ++sp) {
+      const float* q = ys + (size_t)sp * split_stride + off;
+      const float4 a0 = *reinterpret_cast<const float4*>(q), a1 = *reinterpret_cast<const float4*>(q + 4);
+      acc[0] += a0.x, acc[1] += a0.y, acc[2] += a0.z, acc[3] += a0.w, acc[4] += a1.x, acc[5] += a1.y, acc[6] += a1.z, acc[7] += a1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = round_bf(fadd(bf2f(xv[i]), round_bf(acc[i])));
+  } else if (y) {
     const u16x8 yv = *reinterpret_cast<const u16x8*>(y + off);
 #pragma unroll
     for (int i = 0; i < 8; ++i) h[i] = round_bf(fadd(bf2f(xv[i]), bf2f(yv[i])));
@@ -108,7 +124,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y
     hv[i] = f2bf(h[i]);
     nv[i] = f2bf(fmul(fmul(h[i], rs), fadd(1.0f, wv[i])));
   }
-  if (y && h_out) *reinterpret_cast<u16x8*>(h_out + off) = hv;
+  if ((y || ys) && h_out) *reinterpret_cast<u16x8*>(h_out + off) = hv;
   *reinterpret_cast<u16x8*>(n_out + off) = nv;
 }
 
@@ -362,17 +378,36 @@ constexpr int kGemmCandidates = 256;
 
 bool lt_ok(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS; }
 
-bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan* p, std::string* err) {
+// batch > 1: split-K over `batch` K-slices of width K of row-major operands whose rows are ld_k
+// long (slice i starts at element i * K of every row), fp32 partial outputs [batch][M][N].
+bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan* p, std::string* err, int batch = 1, int ld_k = 0) {
+  if (ld_k == 0) ld_k = K;
   p->M = M, p->N = N, p->K = K;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  const hipDataType ct = batch > 1 ? HIP_R_32F : HIP_R_16BF;
   if (!lt_ok(hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) ||
       !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
       !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lw, HIP_R_16BF, K, N, K)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->la, HIP_R_16BF, K, M, K)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, HIP_R_16BF, N, M, N))) {
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lw, HIP_R_16BF, K, N, ld_k)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->la, HIP_R_16BF, K, M, ld_k)) ||
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, ct, N, M, N))) {
     *err = "hipBLASLt descriptor creation failed";
     return false;
+  }
+  if (batch > 1) {
+    const int32_t bc = batch;
+    const int64_t sk = K, sc = (int64_t)N * M;
+    for (hipblasLtMatrixLayout_t l : {p->lw, p->la, p->lc}) {
+      if (!lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)))) {
+        *err = "hipBLASLt batch layout failed";
+        return false;
+      }
+      const int64_t st = l == p->lc ? sc : sk;
+      if (!lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st, sizeof(st)))) {
+        *err = "hipBLASLt batch layout failed";
+        return false;
+      }
+    }
   }
   hipblasLtMatmulPreference_t pref = nullptr;
   if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) {
@@ -446,12 +481,13 @@ struct LayerBind {
 // Device layout of one context: sizes in bytes.
 struct PrefixPlan {
   int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0, nsplit = 1;
-  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws, po, pml;
+  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws, po, pml, dpart;
   size_t total() const {
-    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + po + pml + 16 * 256;
+    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + po + pml + dpart + 16 * 256;
   }
 };
 constexpr size_t kWorkspace = 64ull << 20;
+constexpr int kDownSplits = 4;  // down_proj split-K candidate: 4 slices of K = 4096
 
 size_t rup(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -486,6 +522,7 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   const size_t rows = (size_t)p.B * p.n_mt * 16;
   p.po = p.nsplit > 1 ? rup((size_t)p.nsplit * rows * kHeadDim * 4) : 0;
   p.pml = p.nsplit > 1 ? rup((size_t)p.nsplit * rows * 2 * 4) : 0;
+  p.dpart = rup((size_t)kDownSplits * M * kPW * 4);
   return p;
 }
 
@@ -536,13 +573,14 @@ struct pi05_prefix_ctx {
   char* base = nullptr;
   u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
   u16 *qf = nullptr, *kf = nullptr, *vf = nullptr;
-  float *ln = nullptr, *inv_freq = nullptr, *po = nullptr, *pml = nullptr;
+  float *ln = nullptr, *inv_freq = nullptr, *po = nullptr, *pml = nullptr, *dpart = nullptr;
+  bool down_split = false;  // down_proj as kDownSplits fp32 split-K GEMMs reduced in the residual norm
   int* pos = nullptr;
   uint8_t* valid = nullptr;
   unsigned* err_flag = nullptr;
   void* ws = nullptr;
   hipblasLtHandle_t lt = nullptr;
-  GemmPlan g_qkv, g_kv, g_o, g_gu, g_d;
+  GemmPlan g_qkv, g_kv, g_o, g_gu, g_d, g_dsk;
 };
 
 namespace {
@@ -557,7 +595,7 @@ int hip_fail(pi05_prefix_ctx* c, const char* what, hipError_t e) {
   return fail(c, PI05_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-int gemm(pi05_prefix_ctx* c, const GemmPlan& p, const u16* W, const u16* A, u16* C, hipStream_t st) {
+int gemm(pi05_prefix_ctx* c, const GemmPlan& p, const u16* W, const u16* A, void* C, hipStream_t st) {
   const float alpha = 1.f, beta = 0.f;
   const hipblasStatus_t s = hipblasLtMatmul(c->lt, p.desc, &alpha, W, p.lw, A, p.la, &beta, C, p.lc, C, p.lc, &p.algo,
                                             c->ws, p.ws, st);
@@ -647,6 +685,7 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   c->ws = take(p.ws);
   c->po = reinterpret_cast<float*>(take(p.po));
   c->pml = reinterpret_cast<float*>(take(p.pml));
+  c->dpart = reinterpret_cast<float*>(take(p.dpart));
   // everything starts zeroed: query rows and keys past P stay zero (finite and masked) for the
   // life of the context, and the GEMM tuning below reads defined values
   e = hipMemset(c->base, 0, p.total());
@@ -662,7 +701,8 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   const int M = p.M;
   if (!lt_ok(hipblasLtCreate(&c->lt)) || !make_plan(c->lt, M, kPQkvN, kPW, kWorkspace, &c->g_qkv, &perr) ||
       !make_plan(c->lt, M, kPKvN, kPW, kWorkspace, &c->g_kv, &perr) || !make_plan(c->lt, M, kPW, kPHD, kWorkspace, &c->g_o, &perr) ||
-      !make_plan(c->lt, M, kPGuN, kPW, kWorkspace, &c->g_gu, &perr) || !make_plan(c->lt, M, kPW, kPI, kWorkspace, &c->g_d, &perr)) {
+      !make_plan(c->lt, M, kPGuN, kPW, kWorkspace, &c->g_gu, &perr) || !make_plan(c->lt, M, kPW, kPI, kWorkspace, &c->g_d, &perr) ||
+      !make_plan(c->lt, M, kPW, kPI / kDownSplits, kWorkspace, &c->g_dsk, &perr, kDownSplits, kPI)) {
     if (perr.empty()) perr = "hipblasLtCreate failed";
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, perr);
@@ -670,11 +710,15 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   // pick each GEMM's fastest algorithm on this device and shape
   const bool tuned = tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr) && tune_plan(c->lt, &c->g_kv, c->w, c->n, c->qkv, c->ws, nullptr) &&
                      tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_gu, c->w, c->n, c->gu, c->ws, nullptr) &&
-                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr);
+                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_dsk, c->w, c->act, c->dpart, c->ws, nullptr);
   if (!tuned) {
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, "GEMM algorithm tuning failed");
   }
+  // split-K down_proj when its GEMM plus the extra partial traffic of the fused reduction
+  // ((kDownSplits * 4 - 2) bytes per output element at ~4 TB/s) beats the single bf16 GEMM
+  const float extra_ms = (float)((double)(kDownSplits * 4 - 2) * M * kPW / 4e12 * 1e3);
+  c->down_split = c->g_dsk.ms + extra_ms < c->g_d.ms;
   *out = c;
   return PI05_OK;
 }
@@ -686,6 +730,7 @@ int pi05_prefix_destroy(pi05_prefix_ctx* c) {
   free_plan(&c->g_o);
   free_plan(&c->g_gu);
   free_plan(&c->g_d);
+  free_plan(&c->g_dsk);
   if (c->lt) hipblasLtDestroy(c->lt);
   if (c->base) hipFree(c->base);
   delete c;
@@ -789,8 +834,15 @@ int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* p
     if ((rc = gemm(c, c->g_gu, w + kPOffGu, c->n, c->gu, st)) != PI05_OK) return rc;
     const size_t chunks = (size_t)p.M * (kPI / 8);
     geglu_kernel<<<(unsigned)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096), 256, 0, st>>>(c->gu, c->act, chunks);
-    if ((rc = gemm(c, c->g_d, w + kPOffD, c->act, c->y, st)) != PI05_OK) return rc;
-    if (l + 1 < p.L) rmsnorm_kernel<<<p.M, 256, 0, st>>>(c->h, c->y, c->ln + (size_t)(l + 1) * 2 * kPW, c->h, c->n, eps);
+    if (c->down_split) {
+      if ((rc = gemm(c, c->g_dsk, w + kPOffD, c->act, c->dpart, st)) != PI05_OK) return rc;
+      if (l + 1 < p.L)
+        rmsnorm_kernel<<<p.M, 256, 0, st>>>(c->h, nullptr, c->ln + (size_t)(l + 1) * 2 * kPW, c->h, c->n, eps, c->dpart, kDownSplits,
+                                            (size_t)p.M * kPW);
+    } else {
+      if ((rc = gemm(c, c->g_d, w + kPOffD, c->act, c->y, st)) != PI05_OK) return rc;
+      if (l + 1 < p.L) rmsnorm_kernel<<<p.M, 256, 0, st>>>(c->h, c->y, c->ln + (size_t)(l + 1) * 2 * kPW, c->h, c->n, eps);
+    }
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(c, "prefill launch", e);

@@ -67,6 +67,7 @@ def test_device_bytes_covers_weights_and_activations(lib):
     need += M * (3 * 2048 + 2560 + 2048 + 32768 + 16384) * 2  # h, n, y, q|k|v, attention out, gate|up, GeGLU out
     need += 992 * 8 * 256 * 2 + 2 * 992 * 256 * 2  # attention q fragments and K/V blocks (P padded to 992)
     need += 4 * 968 * 8 * (256 + 2) * 4  # 4 key splits (61 workgroups x 4 fill 244 CUs): fp32 partial O, max, sum
+    need += 4 * 968 * 2048 * 4  # down_proj split-K fp32 partials (4 slices)
     got = _ext.prefix_device_bytes(d)
     assert need <= got <= need + 80 * 2**20  # + GEMM workspace and small tables
     d.batch = 2
