@@ -575,12 +575,13 @@ struct pi05_prefix_ctx {
   u16 *qf = nullptr, *kf = nullptr, *vf = nullptr;
   float *ln = nullptr, *inv_freq = nullptr, *po = nullptr, *pml = nullptr, *dpart = nullptr;
   bool down_split = false;  // down_proj as kDownSplits fp32 split-K GEMMs reduced in the residual norm
+  bool o_split = false;     // o_proj likewise
   int* pos = nullptr;
   uint8_t* valid = nullptr;
   unsigned* err_flag = nullptr;
   void* ws = nullptr;
   hipblasLtHandle_t lt = nullptr;
-  GemmPlan g_qkv, g_kv, g_o, g_gu, g_d, g_dsk;
+  GemmPlan g_qkv, g_kv, g_o, g_gu, g_d, g_dsk, g_osk;
 };
 
 namespace {
@@ -702,7 +703,8 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   if (!lt_ok(hipblasLtCreate(&c->lt)) || !make_plan(c->lt, M, kPQkvN, kPW, kWorkspace, &c->g_qkv, &perr) ||
       !make_plan(c->lt, M, kPKvN, kPW, kWorkspace, &c->g_kv, &perr) || !make_plan(c->lt, M, kPW, kPHD, kWorkspace, &c->g_o, &perr) ||
       !make_plan(c->lt, M, kPGuN, kPW, kWorkspace, &c->g_gu, &perr) || !make_plan(c->lt, M, kPW, kPI, kWorkspace, &c->g_d, &perr) ||
-      !make_plan(c->lt, M, kPW, kPI / kDownSplits, kWorkspace, &c->g_dsk, &perr, kDownSplits, kPI)) {
+      !make_plan(c->lt, M, kPW, kPI / kDownSplits, kWorkspace, &c->g_dsk, &perr, kDownSplits, kPI) ||
+      !make_plan(c->lt, M, kPW, kPHD / kDownSplits, kWorkspace, &c->g_osk, &perr, kDownSplits, kPHD)) {
     if (perr.empty()) perr = "hipblasLtCreate failed";
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, perr);
@@ -710,7 +712,8 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   // pick each GEMM's fastest algorithm on this device and shape
   const bool tuned = tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr) && tune_plan(c->lt, &c->g_kv, c->w, c->n, c->qkv, c->ws, nullptr) &&
                      tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_gu, c->w, c->n, c->gu, c->ws, nullptr) &&
-                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_dsk, c->w, c->act, c->dpart, c->ws, nullptr);
+                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_dsk, c->w, c->act, c->dpart, c->ws, nullptr) &&
+                     tune_plan(c->lt, &c->g_osk, c->w, c->attn, c->dpart, c->ws, nullptr);
   if (!tuned) {
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, "GEMM algorithm tuning failed");
@@ -719,6 +722,7 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   // ((kDownSplits * 4 - 2) bytes per output element at ~4 TB/s) beats the single bf16 GEMM
   const float extra_ms = (float)((double)(kDownSplits * 4 - 2) * M * kPW / 4e12 * 1e3);
   c->down_split = c->g_dsk.ms + extra_ms < c->g_d.ms;
+  c->o_split = c->g_osk.ms + extra_ms < c->g_o.ms;
   *out = c;
   return PI05_OK;
 }
@@ -731,6 +735,7 @@ int pi05_prefix_destroy(pi05_prefix_ctx* c) {
   free_plan(&c->g_gu);
   free_plan(&c->g_d);
   free_plan(&c->g_dsk);
+  free_plan(&c->g_osk);
   if (c->lt) hipblasLtDestroy(c->lt);
   if (c->base) hipFree(c->base);
   delete c;
@@ -829,8 +834,13 @@ int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* p
     AttnArgs aa{c->qf, c->kf, c->vf, c->valid, c->attn, c->po, c->pml, p.B, p.P, p.s_pad, p.n_mt, p.items, p.nsplit};
     prefix_attn_kernel<<<p.B * p.items * p.nsplit, 256, 0, st>>>(aa);
     if (p.nsplit > 1) attn_merge_kernel<<<p.M, 256, 0, st>>>(c->po, c->pml, c->attn, p.B, p.P, p.n_mt, p.nsplit);
-    if ((rc = gemm(c, c->g_o, w + kPOffO, c->attn, c->y, st)) != PI05_OK) return rc;
-    rmsnorm_kernel<<<p.M, 256, 0, st>>>(l == 0 ? emb : c->h, c->y, ln + kPW, c->h, c->n, eps);
+    if (c->o_split) {
+      if ((rc = gemm(c, c->g_osk, w + kPOffO, c->attn, c->dpart, st)) != PI05_OK) return rc;
+      rmsnorm_kernel<<<p.M, 256, 0, st>>>(l == 0 ? emb : c->h, nullptr, ln + kPW, c->h, c->n, eps, c->dpart, kDownSplits, (size_t)p.M * kPW);
+    } else {
+      if ((rc = gemm(c, c->g_o, w + kPOffO, c->attn, c->y, st)) != PI05_OK) return rc;
+      rmsnorm_kernel<<<p.M, 256, 0, st>>>(l == 0 ? emb : c->h, c->y, ln + kPW, c->h, c->n, eps);
+    }
     if ((rc = gemm(c, c->g_gu, w + kPOffGu, c->n, c->gu, st)) != PI05_OK) return rc;
     const size_t chunks = (size_t)p.M * (kPI / 8);
     geglu_kernel<<<(unsigned)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096), 256, 0, st>>>(c->gu, c->act, chunks);
