@@ -15,8 +15,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
-SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip", "pi05_prefill.hip"]
-LIBS = ["-lhipblaslt"]  # the prefill's plain GEMMs
+SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip", "pi05_prefill.hip", "pi05_siglip.hip"]
+LIBS = ["-lhipblaslt"]  # the plain GEMMs of the prefill and the vision tower
 BENCH_SRC = "denoise_bench.hip"
 BENCH_OUT = os.path.join(HERE, "pi05_infer", "denoise_bench")
 

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "pi05_blocks.h"
+#include "pi05_gemm.h"
 #include "pi05_prefill.h"
 
 namespace pi05 {
@@ -360,119 +361,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u1
   *reinterpret_cast<u16x8*>(out + i * kPW + d) = o;
 }
 
-// ---------------------------------------------------------------------------------------------
-// hipBLASLt plans: C[M, N] (row-major) = A[M, K] (row-major) . W[N, K]^T (nn.Linear), bf16 in and
-// out, fp32 accumulation.  In hipBLASLt's column-major terms that is C^T (N x M) = W (stored K x N,
-// transposed) . A^T (stored K x M).
-// ---------------------------------------------------------------------------------------------
-struct GemmPlan {
-  int M = 0, N = 0, K = 0;
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
-  hipblasLtMatmulAlgo_t algo{};
-  size_t ws = 0;
-  std::vector<hipblasLtMatmulHeuristicResult_t> cands;  // heuristic candidates, timed by tune_plan
-  float ms = 0.f;                                        // the chosen algorithm's time
-};
-constexpr int kGemmCandidates = 256;
-
-bool lt_ok(hipblasStatus_t s) { return s == HIPBLAS_STATUS_SUCCESS; }
-
-// batch > 1: split-K over `batch` K-slices of width K of row-major operands whose rows are ld_k
-// long (slice i starts at element i * K of every row), fp32 partial outputs [batch][M][N].
-bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan* p, std::string* err, int batch = 1, int ld_k = 0) {
-  if (ld_k == 0) ld_k = K;
-  p->M = M, p->N = N, p->K = K;
-  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-  const hipDataType ct = batch > 1 ? HIP_R_32F : HIP_R_16BF;
-  if (!lt_ok(hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F)) ||
-      !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
-      !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lw, HIP_R_16BF, K, N, ld_k)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->la, HIP_R_16BF, K, M, ld_k)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, ct, N, M, N))) {
-    *err = "hipBLASLt descriptor creation failed";
-    return false;
-  }
-  if (batch > 1) {
-    const int32_t bc = batch;
-    const int64_t sk = K, sc = (int64_t)N * M;
-    for (hipblasLtMatrixLayout_t l : {p->lw, p->la, p->lc}) {
-      if (!lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)))) {
-        *err = "hipBLASLt batch layout failed";
-        return false;
-      }
-      const int64_t st = l == p->lc ? sc : sk;
-      if (!lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &st, sizeof(st)))) {
-        *err = "hipBLASLt batch layout failed";
-        return false;
-      }
-    }
-  }
-  hipblasLtMatmulPreference_t pref = nullptr;
-  if (!lt_ok(hipblasLtMatmulPreferenceCreate(&pref))) {
-    *err = "hipBLASLt preference creation failed";
-    return false;
-  }
-  uint64_t wsb = ws_max;
-  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
-  std::vector<hipblasLtMatmulHeuristicResult_t> res(kGemmCandidates);
-  int n = 0;
-  const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->lw, p->la, p->lc, p->lc, pref, kGemmCandidates, res.data(), &n);
-  hipblasLtMatmulPreferenceDestroy(pref);
-  for (int i = 0; lt_ok(s) && i < n; ++i)
-    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) p->cands.push_back(res[i]);
-  if (!p->cands.empty()) {
-    p->algo = p->cands[0].algo;  // the heuristic's first choice until tune_plan has timed them all
-    p->ws = p->cands[0].workspaceSize;
-    return true;
-  }
-  *err = "hipBLASLt found no bf16 GEMM algorithm for M=" + std::to_string(M) + " N=" + std::to_string(N) + " K=" + std::to_string(K);
-  return false;
-}
-
-// Time every candidate algorithm on the context's own buffers (3 runs after one warm-up; the
-// values are irrelevant to the timing) and keep the fastest.  Candidates that fail to launch are
-// skipped; the heuristic's first choice stays if all fail.
-bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const void* A, void* C, void* ws, hipStream_t st) {
-  hipEvent_t e0, e1;
-  if (hipEventCreate(&e0) != hipSuccess) return false;
-  if (hipEventCreate(&e1) != hipSuccess) {
-    hipEventDestroy(e0);
-    return false;
-  }
-  const float alpha = 1.f, beta = 0.f;
-  float best = 1e30f;
-  for (const auto& c : p->cands) {
-    bool ok = lt_ok(hipblasLtMatmul(h, p->desc, &alpha, W, p->lw, A, p->la, &beta, C, p->lc, C, p->lc, &c.algo, ws, c.workspaceSize, st));
-    if (!ok) continue;
-    hipEventRecord(e0, st);
-    for (int r = 0; r < 3 && ok; ++r)
-      ok = lt_ok(hipblasLtMatmul(h, p->desc, &alpha, W, p->lw, A, p->la, &beta, C, p->lc, C, p->lc, &c.algo, ws, c.workspaceSize, st));
-    hipEventRecord(e1, st);
-    if (hipEventSynchronize(e1) != hipSuccess) break;
-    float ms = 0.f;
-    if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
-    if (ms < best) {
-      best = ms;
-      p->algo = c.algo;
-      p->ws = c.workspaceSize;
-    }
-  }
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
-  p->ms = best / 3.f;
-  return hipGetLastError() == hipSuccess;
-}
-
-void free_plan(GemmPlan* p) {
-  if (p->desc) hipblasLtMatmulDescDestroy(p->desc);
-  if (p->lw) hipblasLtMatrixLayoutDestroy(p->lw);
-  if (p->la) hipblasLtMatrixLayoutDestroy(p->la);
-  if (p->lc) hipblasLtMatrixLayoutDestroy(p->lc);
-  *p = GemmPlan{};
-}
-
 struct LayerBind {
   const void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
   const float *ln1 = nullptr, *ln2 = nullptr;
@@ -596,10 +484,15 @@ int hip_fail(pi05_prefix_ctx* c, const char* what, hipError_t e) {
   return fail(c, PI05_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+GemmOpts split_opts(int ld_k) {
+  GemmOpts o;
+  o.batch = kDownSplits;
+  o.ld_k = ld_k;
+  return o;
+}
+
 int gemm(pi05_prefix_ctx* c, const GemmPlan& p, const u16* W, const u16* A, void* C, hipStream_t st) {
-  const float alpha = 1.f, beta = 0.f;
-  const hipblasStatus_t s = hipblasLtMatmul(c->lt, p.desc, &alpha, W, p.lw, A, p.la, &beta, C, p.lc, C, p.lc, &p.algo,
-                                            c->ws, p.ws, st);
+  const hipblasStatus_t s = run_plan(c->lt, p, p.algo, p.ws, W, A, C, nullptr, c->ws, st);
   if (!lt_ok(s)) return fail(c, PI05_E_HIP, "hipblasLtMatmul failed (status " + std::to_string((int)s) + ")");
   return PI05_OK;
 }
@@ -703,8 +596,8 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   if (!lt_ok(hipblasLtCreate(&c->lt)) || !make_plan(c->lt, M, kPQkvN, kPW, kWorkspace, &c->g_qkv, &perr) ||
       !make_plan(c->lt, M, kPKvN, kPW, kWorkspace, &c->g_kv, &perr) || !make_plan(c->lt, M, kPW, kPHD, kWorkspace, &c->g_o, &perr) ||
       !make_plan(c->lt, M, kPGuN, kPW, kWorkspace, &c->g_gu, &perr) || !make_plan(c->lt, M, kPW, kPI, kWorkspace, &c->g_d, &perr) ||
-      !make_plan(c->lt, M, kPW, kPI / kDownSplits, kWorkspace, &c->g_dsk, &perr, kDownSplits, kPI) ||
-      !make_plan(c->lt, M, kPW, kPHD / kDownSplits, kWorkspace, &c->g_osk, &perr, kDownSplits, kPHD)) {
+      !make_plan(c->lt, M, kPW, kPI / kDownSplits, kWorkspace, &c->g_dsk, &perr, split_opts(kPI)) ||
+      !make_plan(c->lt, M, kPW, kPHD / kDownSplits, kWorkspace, &c->g_osk, &perr, split_opts(kPHD))) {
     if (perr.empty()) perr = "hipblasLtCreate failed";
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, perr);

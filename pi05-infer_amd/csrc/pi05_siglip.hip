@@ -1,0 +1,538 @@
+// The pi0.5 vision tower on gfx950: SigLIP So400m/14 + PaliGemma's projector (get_image_features,
+// gemma_pytorch.py:106-107; the tower itself is transformers' SiglipVisionModel).  Per image:
+//   patches (fp32 im2col) . Wpatch^T          hipBLASLt fp32 GEMM
+//   h = bf16(conv + bpatch + pos)              embed_kernel
+//   27 x [ n = LN1(h); q|k|v = n.W^T + b      hipBLASLt (bias epilogue)
+//          attention, 16 heads of 72          qkv_layout_kernel + vision_attn_kernel (MFMA)
+//          h = bf16(h + o.Wo^T + bo); n = LN2 hipBLASLt + layernorm_kernel (residual fused)
+//          a = gelu_tanh(n.W1^T + b1)          hipBLASLt + gelu_kernel
+//          h = bf16(h + a.W2^T + b2) ]         hipBLASLt + layernorm_kernel (next LN1 / post_layernorm)
+//   out = (n.Wproj^T + bproj) * out_scale     hipBLASLt (+ scale_kernel)
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pi05_blocks.h"
+#include "pi05_gemm.h"
+#include "pi05_siglip.h"
+
+namespace pi05 {
+namespace {
+
+constexpr int kVW = 1152, kVH = 16, kVD = 72, kVI = 4304, kVPatch = 14, kVImg = 224, kVC = 3, kVProj = 2048;
+constexpr int kVGrid = kVImg / kVPatch, kVS = kVGrid * kVGrid;  // 16 x 16 = 256 patches
+constexpr int kVPD = kVC * kVPatch * kVPatch;                   // 588 values per patch
+constexpr int kVQkvN = 3 * kVW;                                 // 3456 fused q|k|v columns
+// attention operands, per (image, head): head dim padded to 96 for Q.K^T (3 k-steps of 32) and to
+// 80 for P.V (5 d-tiles of 16); the padding stays zero
+constexpr int kVKs = 3, kVDt = 5;
+constexpr size_t kVQHead = (size_t)kVS * kVKs * 32;  // elements of one head's Q (or K) fragments
+constexpr size_t kVVHead = (size_t)(kVS / 32) * kVDt * 512;
+// per-layer packed bf16 weights: [Wq; Wk; Wv] | Wo | W1 | W2; fp32 parameters: bqkv | bo | b1 | b2 |
+// ln1w | ln1b | ln2w | ln2b
+constexpr size_t kVOffQkv = 0, kVOffO = kVOffQkv + (size_t)kVQkvN * kVW, kVOff1 = kVOffO + (size_t)kVW * kVW,
+                 kVOff2 = kVOff1 + (size_t)kVI * kVW, kVLayerElems = kVOff2 + (size_t)kVW * kVI;
+constexpr size_t kVPOffBqkv = 0, kVPOffBo = kVQkvN, kVPOffB1 = kVPOffBo + kVW, kVPOffB2 = kVPOffB1 + kVI,
+                 kVPOffLn1w = kVPOffB2 + kVW, kVPOffLn1b = kVPOffLn1w + kVW, kVPOffLn2w = kVPOffLn1b + kVW,
+                 kVPOffLn2b = kVPOffLn2w + kVW, kVLayerParams = kVPOffLn2b + kVW;
+constexpr size_t kVWorkspace = 32ull << 20;
+
+thread_local std::string g_vision_err;
+
+// K fragment (key, d) of one head over 96 padded dims: fragment (key tile, d-step) is the MFMA A
+// operand of S^T = K Q^T; V fragment (key, d) of the 5 d-tiles with the 32-key permutation vkey
+// (the P^T operand is the S^T accumulator a lane already holds).
+__host__ __device__ constexpr size_t kfrag3(int key, int d) {
+  return ((size_t)(key >> 4) * kVKs + (d >> 5)) * 512 + (size_t)(((d & 31) >> 3) * 16 + (key & 15)) * 8 + (d & 7);
+}
+__host__ __device__ constexpr size_t vfrag5(int key, int d) {
+  const int kb = key >> 5, r = key & 31, g = (r & 15) >> 2, j = r < 16 ? (r & 3) : 4 + (r & 3);
+  return ((size_t)kb * kVDt + (d >> 4)) * 512 + (size_t)(g * 16 + (d & 15)) * 8 + j;
+}
+
+// im2col: patches[(n, p)][c*196 + ky*14 + kx] = pixels[n][c][14 py + ky][14 px + kx], p = 16 py + px
+__global__ __launch_bounds__(256) void im2col_kernel(const float* px, float* patches, int n_img) {
+  const size_t total = (size_t)n_img * kVS * kVPD;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const size_t row = i / kVPD;
+    const int col = (int)(i % kVPD), n = (int)(row / kVS), p = (int)(row % kVS);
+    const int c = col / (kVPatch * kVPatch), ky = (col / kVPatch) % kVPatch, kx = col % kVPatch;
+    const int y = (p / kVGrid) * kVPatch + ky, x = (p % kVGrid) * kVPatch + kx;
+    patches[i] = px[(((size_t)n * kVC + c) * kVImg + y) * kVImg + x];
+  }
+}
+
+// h = bf16(conv + patch bias + position embedding) (SiglipVisionEmbeddings, fp32 until here)
+__global__ __launch_bounds__(256) void embed_kernel(const float* conv, const float* pb, const float* pos, u16* h, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const int c = (int)(i % kVW), p = (int)((i / kVW) % kVS);
+    h[i] = f2bf(conv[i] + pb[c] + pos[(size_t)p * kVW + c]);
+  }
+}
+
+// h = bf16(x + y) (y optional), n = bf16((h - mean) / sqrt(var + eps) * w + b), fp32 statistics
+// (nn.LayerNorm).  One workgroup of 192 threads per 1152-wide row, 6 elements per thread.
+__global__ __launch_bounds__(192) void layernorm_kernel(const u16* x, const u16* y, const float* w, const float* b, u16* h_out, u16* n_out,
+                                                       float eps) {
+  const size_t off = (size_t)blockIdx.x * kVW + threadIdx.x * 6;
+  __shared__ float s_part[3];
+  float h[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) h[i] = y ? round_bf(fadd(bf2f(x[off + i]), bf2f(y[off + i]))) : bf2f(x[off + i]);
+  auto block_sum = [&](float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();  // s_part of a previous reduction has been read
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (s_part[0] + s_part[1]) + s_part[2];
+  };
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) s += h[i];
+  const float mean = block_sum(s) * (1.0f / kVW);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) q += (h[i] - mean) * (h[i] - mean);
+  const float rstd = 1.0f / sqrtf(block_sum(q) * (1.0f / kVW) + eps);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int c = threadIdx.x * 6 + i;
+    if (y && h_out) h_out[off + i] = f2bf(h[i]);
+    n_out[off + i] = f2bf(fadd(fmul(fmul(fsub(h[i], mean), rstd), w[c]), b[c]));
+  }
+}
+
+// q, k, v of one token row -> the attention's fragment layouts (one workgroup per row)
+__global__ __launch_bounds__(256) void qkv_layout_kernel(const u16* qkv, u16* qf, u16* kf, u16* vf) {
+  const int row = blockIdx.x, n = row / kVS, tok = row % kVS;
+  const u16* src = qkv + (size_t)row * kVQkvN;
+  for (int i = threadIdx.x; i < kVW; i += 256) {
+    const int hd = i / kVD, d = i % kVD;
+    const size_t head = (size_t)n * kVH + hd;
+    qf[head * kVQHead + afrag_index(tok, d, kVKs)] = src[i];
+    kf[head * kVQHead + kfrag3(tok, d)] = src[kVW + i];
+    vf[head * kVVHead + vfrag5(tok, d)] = src[2 * kVW + i];
+  }
+}
+
+// MHA over one image's 256 patches: workgroup = (image, head, quarter of the queries), wave w owns
+// query m-tile 4 quarter + w; every wave streams the head's 8 key blocks of 32 (K and V fragments
+// from L2) through the online-softmax block update with fp32 scores scaled by 72^-0.5 (no bf16
+// rounding of the scores: the reference runs SDPA's flash kernel), P rounded to bf16 for P.V.
+__global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qf, const u16* kf, const u16* vf, u16* out) {
+  const int quarter = blockIdx.x & 3, head = (blockIdx.x >> 2) % kVH, n = (blockIdx.x >> 2) / kVH;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, mt = quarter * 4 + wave;
+  const size_t hb = (size_t)n * kVH + head;
+  const u16* qb = qf + hb * kVQHead;
+  const u16* kb = kf + hb * kVQHead;
+  const u16* vb = vf + hb * kVVHead;
+  bf16x8 q[kVKs];
+#pragma unroll
+  for (int ds = 0; ds < kVKs; ++ds) q[ds] = load_frag(qb + afrag_offset(mt, ds, kVKs) + lane * 8);
+  const float scale = 0.11785113019775793f;  // 72 ** -0.5
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 oacc[kVDt];
+#pragma unroll
+  for (int d = 0; d < kVDt; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int blk = 0; blk < kVS / 32; ++blk) {
+    bf16x8 k[2 * kVKs], v[kVDt];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ds = 0; ds < kVKs; ++ds) k[t * kVKs + ds] = load_frag(kb + ((size_t)(2 * blk + t) * kVKs + ds) * 512 + lane * 8);
+#pragma unroll
+    for (int dt = 0; dt < kVDt; ++dt) v[dt] = load_frag(vb + ((size_t)blk * kVDt + dt) * 512 + lane * 8);
+    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ds = 0; ds < kVKs; ++ds)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) sacc[t] = mfma16x16x32(k[t * kVKs + ds], q[ds], sacc[t]);
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = sacc[0][i] * scale;
+      s[4 + i] = sacc[1][i] * scale;
+    }
+    float bm = s[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float m_new = fmaxf(m_run, bm);
+    const float alpha = __expf(m_run - m_new);  // m_run = -inf on the first block: alpha = 0
+    float e[8], esum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      e[i] = __expf(s[i] - m_new);
+      esum += e[i];
+    }
+    l_run = l_run * alpha + esum;
+    m_run = m_new;
+    u16x8 pf;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pf[i] = f2bf(e[i]);
+    const bf16x8 pfrag = as_bf16x8(pf);
+#pragma unroll
+    for (int dt = 0; dt < kVDt; ++dt) oacc[dt] = mfma16x16x32(v[dt], pfrag, oacc[dt] * alpha);
+  }
+  float l = l_run;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  const float inv = 1.0f / l;
+  const int tok = mt * 16 + (lane & 15), g = lane >> 4;
+  u16* orow = out + ((size_t)n * kVS + tok) * kVW + head * kVD;
+#pragma unroll
+  for (int dt = 0; dt < kVDt; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = dt * 16 + g * 4 + i;
+      if (d < kVD) orow[d] = f2bf(oacc[dt][i] * inv);
+    }
+}
+
+// bf16(gelu_tanh(x)) in place (transformers' gelu_pytorch_tanh on the bf16 fc1 output)
+__global__ __launch_bounds__(256) void gelu_kernel(u16* x, size_t total) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) x[i] = f2bf(gelu_tanh(bf2f(x[i])));
+}
+
+__global__ __launch_bounds__(256) void scale_kernel(u16* x, size_t total, float s) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) x[i] = f2bf(bf2f(x[i]) * s);
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const u16* src, float* dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = bf2f(src[i]);
+}
+
+struct VLayerBind {
+  const void* p[16] = {};  // wq bq wk bk wv bv wo bo w1 b1 w2 b2 ln1w ln1b ln2w ln2b
+};
+
+struct VisionPlan {
+  int L = 0, N = 0, M = 0;
+  size_t w, par, head, h, qkv, qf, vfb, act, patches, conv, ws;
+  size_t total() const { return w + par + head + 4 * h + qkv + 2 * qf + vfb + act + patches + conv + ws + 16 * 256; }
+};
+
+size_t vrup(size_t x) { return (x + 255) / 256 * 256; }
+
+VisionPlan vplan_of(const pi05_vision_dims& d) {
+  VisionPlan p;
+  p.L = d.depth, p.N = d.n_images, p.M = d.n_images * kVS;
+  const size_t M = p.M;
+  p.w = vrup((size_t)p.L * kVLayerElems * 2);
+  p.par = vrup((size_t)p.L * kVLayerParams * 4);
+  // heads: patch_w [W, 588] + patch_b + pos [256, W] + post w/b (fp32), proj_w bf16, proj_b fp32
+  p.head = vrup(((size_t)kVW * kVPD + kVW + (size_t)kVS * kVW + 2 * kVW + kVProj) * 4 + (size_t)kVProj * kVW * 2);
+  p.h = vrup(M * kVW * 2);
+  p.qkv = vrup(M * kVQkvN * 2);
+  p.qf = vrup((size_t)p.N * kVH * kVQHead * 2);
+  p.vfb = vrup((size_t)p.N * kVH * kVVHead * 2);
+  p.act = vrup(M * kVI * 2);
+  p.patches = vrup(M * kVPD * 4);
+  p.conv = vrup(M * kVW * 4);
+  p.ws = kVWorkspace;
+  return p;
+}
+
+bool check_vision_dims(const pi05_vision_dims* d, std::string* m) {
+  if (!d) {
+    *m = "dims is NULL";
+    return false;
+  }
+  if (d->width != kVW || d->num_heads != kVH || d->mlp_dim != kVI || d->patch != kVPatch || d->image != kVImg || d->channels != kVC ||
+      d->proj_dim != kVProj) {
+    *m = "vision geometry must be width 1152, 16 heads, mlp_dim 4304, patch 14, image 224, 3 channels, proj_dim 2048";
+    return false;
+  }
+  if (d->depth < 1 || d->depth > 64 || d->n_images < 1 || d->n_images > 64) {
+    *m = "depth must be in [1, 64] and n_images in [1, 64]";
+    return false;
+  }
+  if (!(d->ln_eps > 0.f) || !(d->out_scale > 0.f)) {
+    *m = "ln_eps and out_scale must be > 0";
+    return false;
+  }
+  return true;
+}
+
+unsigned grid_for(size_t total) {
+  const size_t g = (total + 255) / 256;
+  return (unsigned)(g < 8192 ? g : 8192);
+}
+
+}  // namespace
+}  // namespace pi05
+
+using namespace pi05;
+
+struct pi05_vision_ctx {
+  pi05_vision_dims d{};
+  VisionPlan plan;
+  std::string err;
+  std::vector<VLayerBind> binds;
+  const float *b_patch_w = nullptr, *b_patch_b = nullptr, *b_pos = nullptr;
+  const void *b_post_w = nullptr, *b_post_b = nullptr, *b_proj_w = nullptr, *b_proj_b = nullptr;
+  bool refreshed = false;
+  char* base = nullptr;
+  u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *attn = nullptr, *qkv = nullptr, *qf = nullptr, *kf = nullptr, *vf = nullptr,
+      *act = nullptr, *proj_w = nullptr;
+  float *par = nullptr, *patch_w = nullptr, *patch_b = nullptr, *pos = nullptr, *post_w = nullptr, *post_b = nullptr, *proj_b = nullptr,
+        *patches = nullptr, *conv = nullptr;
+  void* ws = nullptr;
+  hipblasLtHandle_t lt = nullptr;
+  GemmPlan g_patch, g_qkv, g_o, g_fc1, g_fc2, g_proj;
+};
+
+namespace {
+
+int vfail(pi05_vision_ctx* c, int code, const std::string& m) {
+  if (c) c->err = m;
+  else g_vision_err = m;
+  return code;
+}
+
+int vgemm(pi05_vision_ctx* c, const GemmPlan& p, const void* W, const void* A, void* C, const float* bias, hipStream_t st) {
+  const hipblasStatus_t s = run_plan(c->lt, p, p.algo, p.ws, W, A, C, bias, c->ws, st);
+  if (!lt_ok(s)) return vfail(c, PI05_E_HIP, "hipblasLtMatmul failed (status " + std::to_string((int)s) + ")");
+  return PI05_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void pi05_vision_default_dims(pi05_vision_dims* d) {
+  if (!d) return;
+  *d = pi05_vision_dims{kVW, 27, kVH, kVI, kVPatch, kVImg, kVC, kVProj, 3, 1e-6f, 1.0f};
+}
+
+int pi05_vision_check_dims(const pi05_vision_dims* dims) {
+  std::string m;
+  if (!check_vision_dims(dims, &m)) return vfail(nullptr, PI05_E_INVALID, m);
+  return PI05_OK;
+}
+
+size_t pi05_vision_device_bytes(const pi05_vision_dims* dims) {
+  std::string m;
+  if (!check_vision_dims(dims, &m)) return 0;
+  return vplan_of(*dims).total();
+}
+
+const char* pi05_vision_last_error(const pi05_vision_ctx* ctx) { return ctx ? ctx->err.c_str() : g_vision_err.c_str(); }
+
+int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
+  if (!out) return vfail(nullptr, PI05_E_INVALID, "out is NULL");
+  *out = nullptr;
+  std::string m;
+  if (!check_vision_dims(dims, &m)) return vfail(nullptr, PI05_E_INVALID, m);
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return vfail(nullptr, PI05_E_NODEVICE, std::string("no HIP device: ") + hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess || strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return vfail(nullptr, PI05_E_NODEVICE, std::string("device is not gfx950 (MI355X): ") + (e == hipSuccess ? prop.gcnArchName : hipGetErrorString(e)));
+  pi05_vision_ctx* c = new pi05_vision_ctx();
+  c->d = *dims;
+  c->plan = vplan_of(*dims);
+  c->binds.resize(dims->depth);
+  const VisionPlan& p = c->plan;
+  e = hipMalloc(&c->base, p.total());
+  if (e != hipSuccess) {
+    delete c;
+    return vfail(nullptr, PI05_E_NOMEM, std::string("vision context allocation failed: ") + hipGetErrorString(e));
+  }
+  char* q = c->base;
+  auto take = [&](size_t bytes) {
+    char* r = q;
+    q += bytes;
+    return r;
+  };
+  c->w = reinterpret_cast<u16*>(take(p.w));
+  c->par = reinterpret_cast<float*>(take(p.par));
+  char* hd = take(p.head);
+  c->patch_w = reinterpret_cast<float*>(hd);
+  c->patch_b = c->patch_w + (size_t)kVW * kVPD;
+  c->pos = c->patch_b + kVW;
+  c->post_w = c->pos + (size_t)kVS * kVW;
+  c->post_b = c->post_w + kVW;
+  c->proj_b = c->post_b + kVW;
+  c->proj_w = reinterpret_cast<u16*>(c->proj_b + kVProj);
+  c->h = reinterpret_cast<u16*>(take(p.h));
+  c->n = reinterpret_cast<u16*>(take(p.h));
+  c->y = reinterpret_cast<u16*>(take(p.h));
+  c->attn = reinterpret_cast<u16*>(take(p.h));
+  c->qkv = reinterpret_cast<u16*>(take(p.qkv));
+  c->qf = reinterpret_cast<u16*>(take(p.qf));
+  c->kf = reinterpret_cast<u16*>(take(p.qf));
+  c->vf = reinterpret_cast<u16*>(take(p.vfb));
+  c->act = reinterpret_cast<u16*>(take(p.act));
+  c->patches = reinterpret_cast<float*>(take(p.patches));
+  c->conv = reinterpret_cast<float*>(take(p.conv));
+  c->ws = take(p.ws);
+  // zeroed once: the padded head dims of the attention operands stay zero, tuning reads defined data
+  e = hipMemset(c->base, 0, p.total());
+  if (e != hipSuccess) {
+    hipFree(c->base);
+    delete c;
+    return vfail(nullptr, PI05_E_HIP, std::string("vision context initialisation failed: ") + hipGetErrorString(e));
+  }
+  std::string perr;
+  const int M = p.M;
+  GemmOpts f32;
+  f32.ab = HIP_R_32F;
+  f32.c = HIP_R_32F;
+  GemmOpts bias;
+  bias.bias = true;
+  bool ok = lt_ok(hipblasLtCreate(&c->lt)) && make_plan(c->lt, M, kVW, kVPD, kVWorkspace, &c->g_patch, &perr, f32) &&
+            make_plan(c->lt, M, kVQkvN, kVW, kVWorkspace, &c->g_qkv, &perr, bias) && make_plan(c->lt, M, kVW, kVW, kVWorkspace, &c->g_o, &perr, bias) &&
+            make_plan(c->lt, M, kVI, kVW, kVWorkspace, &c->g_fc1, &perr, bias) && make_plan(c->lt, M, kVW, kVI, kVWorkspace, &c->g_fc2, &perr, bias) &&
+            make_plan(c->lt, M, kVProj, kVW, kVWorkspace, &c->g_proj, &perr, bias);
+  if (ok) {
+    const float* bz = c->par;  // any fp32 vector long enough (zeros) stands in for the biases while timing
+    ok = tune_plan(c->lt, &c->g_patch, c->patch_w, c->patches, c->conv, c->ws, nullptr) &&
+         tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr, bz) &&
+         tune_plan(c->lt, &c->g_fc1, c->w, c->n, c->act, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_fc2, c->w, c->act, c->y, c->ws, nullptr, bz) &&
+         tune_plan(c->lt, &c->g_proj, c->proj_w, c->n, c->act, c->ws, nullptr, bz);
+    if (!ok && perr.empty()) perr = "GEMM algorithm tuning failed";
+  }
+  if (!ok) {
+    if (perr.empty()) perr = "hipblasLtCreate failed";
+    pi05_vision_destroy(c);
+    return vfail(nullptr, PI05_E_HIP, perr);
+  }
+  *out = c;
+  return PI05_OK;
+}
+
+int pi05_vision_destroy(pi05_vision_ctx* c) {
+  if (!c) return PI05_OK;
+  for (GemmPlan* g : {&c->g_patch, &c->g_qkv, &c->g_o, &c->g_fc1, &c->g_fc2, &c->g_proj}) free_plan(g);
+  if (c->lt) hipblasLtDestroy(c->lt);
+  if (c->base) hipFree(c->base);
+  delete c;
+  return PI05_OK;
+}
+
+int pi05_vision_bind_layer(pi05_vision_ctx* c, int layer, const void* wq, const void* bq, const void* wk, const void* bk, const void* wv,
+                           const void* bv, const void* wo, const void* bo, const void* w1, const void* b1, const void* w2, const void* b2,
+                           const void* ln1_w, const void* ln1_b, const void* ln2_w, const void* ln2_b) {
+  if (!c) return vfail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (layer < 0 || layer >= c->d.depth) return vfail(c, PI05_E_INVALID, "layer out of range");
+  const void* ps[16] = {wq, bq, wk, bk, wv, bv, wo, bo, w1, b1, w2, b2, ln1_w, ln1_b, ln2_w, ln2_b};
+  VLayerBind b;
+  for (int i = 0; i < 16; ++i) {
+    if (!ps[i]) return vfail(c, PI05_E_INVALID, "a weight pointer is NULL");
+    if (reinterpret_cast<uintptr_t>(ps[i]) % 16) return vfail(c, PI05_E_INVALID, "weight pointers must be 16-byte aligned");
+    b.p[i] = ps[i];
+  }
+  c->binds[layer] = b;
+  c->refreshed = false;
+  return PI05_OK;
+}
+
+int pi05_vision_bind_heads(pi05_vision_ctx* c, const float* patch_w, const float* patch_b, const float* pos, const void* post_w,
+                           const void* post_b, const void* proj_w, const void* proj_b) {
+  if (!c) return vfail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  const void* ps[7] = {patch_w, patch_b, pos, post_w, post_b, proj_w, proj_b};
+  for (const void* x : ps) {
+    if (!x) return vfail(c, PI05_E_INVALID, "a weight pointer is NULL");
+    if (reinterpret_cast<uintptr_t>(x) % 16) return vfail(c, PI05_E_INVALID, "weight pointers must be 16-byte aligned");
+  }
+  c->b_patch_w = patch_w, c->b_patch_b = patch_b, c->b_pos = pos;
+  c->b_post_w = post_w, c->b_post_b = post_b, c->b_proj_w = proj_w, c->b_proj_b = proj_b;
+  c->refreshed = false;
+  return PI05_OK;
+}
+
+int pi05_vision_refresh_weights(pi05_vision_ctx* c, void* stream) {
+  if (!c) return vfail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (!c->b_patch_w) return vfail(c, PI05_E_STATE, "heads are not bound");
+  for (int l = 0; l < c->d.depth; ++l)
+    if (!c->binds[l].p[0]) return vfail(c, PI05_E_STATE, "layer " + std::to_string(l) + " is not bound");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipMemcpyKind k = hipMemcpyDeviceToDevice;
+  hipError_t e = hipSuccess;
+  auto to_f32 = [&](const void* src, float* dst, size_t n) {
+    bf16_to_f32_kernel<<<grid_for(n), 256, 0, st>>>(static_cast<const u16*>(src), dst, n);
+  };
+  for (int l = 0; l < c->d.depth && e == hipSuccess; ++l) {
+    const VLayerBind& b = c->binds[l];
+    u16* w = c->w + (size_t)l * kVLayerElems;
+    float* pr = c->par + (size_t)l * kVLayerParams;
+    const size_t ww = (size_t)kVW * kVW * 2;
+    e = hipMemcpyAsync(w + kVOffQkv, b.p[0], ww, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOffQkv + (size_t)kVW * kVW, b.p[2], ww, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOffQkv + (size_t)2 * kVW * kVW, b.p[4], ww, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOffO, b.p[6], ww, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOff1, b.p[8], (size_t)kVI * kVW * 2, k, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOff2, b.p[10], (size_t)kVW * kVI * 2, k, st);
+    to_f32(b.p[1], pr + kVPOffBqkv, kVW);
+    to_f32(b.p[3], pr + kVPOffBqkv + kVW, kVW);
+    to_f32(b.p[5], pr + kVPOffBqkv + 2 * kVW, kVW);
+    to_f32(b.p[7], pr + kVPOffBo, kVW);
+    to_f32(b.p[9], pr + kVPOffB1, kVI);
+    to_f32(b.p[11], pr + kVPOffB2, kVW);
+    to_f32(b.p[12], pr + kVPOffLn1w, kVW);
+    to_f32(b.p[13], pr + kVPOffLn1b, kVW);
+    to_f32(b.p[14], pr + kVPOffLn2w, kVW);
+    to_f32(b.p[15], pr + kVPOffLn2b, kVW);
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(c->patch_w, c->b_patch_w, (size_t)kVW * kVPD * 4, k, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(c->patch_b, c->b_patch_b, kVW * 4, k, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(c->pos, c->b_pos, (size_t)kVS * kVW * 4, k, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(c->proj_w, c->b_proj_w, (size_t)kVProj * kVW * 2, k, st);
+  if (e == hipSuccess) {
+    to_f32(c->b_post_w, c->post_w, kVW);
+    to_f32(c->b_post_b, c->post_b, kVW);
+    to_f32(c->b_proj_b, c->proj_b, kVProj);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return vfail(c, PI05_E_HIP, std::string("weight packing: ") + hipGetErrorString(e));
+  c->refreshed = true;
+  return PI05_OK;
+}
+
+int pi05_vision_forward(pi05_vision_ctx* c, const float* pixels, void* out, void* stream) {
+  if (!c) return vfail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  if (!pixels || !out) return vfail(c, PI05_E_INVALID, "pixels and out must be non-NULL");
+  if (reinterpret_cast<uintptr_t>(out) % 16) return vfail(c, PI05_E_INVALID, "out must be 16-byte aligned");
+  if (!c->refreshed) return vfail(c, PI05_E_STATE, "weights are not bound and refreshed");
+  const VisionPlan& p = c->plan;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const float eps = c->d.ln_eps;
+  const size_t M = p.M;
+  int rc;
+  im2col_kernel<<<grid_for(M * kVPD), 256, 0, st>>>(pixels, c->patches, p.N);
+  if ((rc = vgemm(c, c->g_patch, c->patch_w, c->patches, c->conv, nullptr, st)) != PI05_OK) return rc;
+  embed_kernel<<<grid_for(M * kVW), 256, 0, st>>>(c->conv, c->patch_b, c->pos, c->h, M * kVW);
+  const float* pr0 = c->par;
+  layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, nullptr, pr0 + kVPOffLn1w, pr0 + kVPOffLn1b, nullptr, c->n, eps);
+  for (int l = 0; l < p.L; ++l) {
+    const u16* w = c->w + (size_t)l * kVLayerElems;
+    const float* pr = c->par + (size_t)l * kVLayerParams;
+    if ((rc = vgemm(c, c->g_qkv, w + kVOffQkv, c->n, c->qkv, pr + kVPOffBqkv, st)) != PI05_OK) return rc;
+    qkv_layout_kernel<<<(unsigned)M, 256, 0, st>>>(c->qkv, c->qf, c->kf, c->vf);
+    vision_attn_kernel<<<(unsigned)(p.N * kVH * 4), 256, 0, st>>>(c->qf, c->kf, c->vf, c->attn);
+    if ((rc = vgemm(c, c->g_o, w + kVOffO, c->attn, c->y, pr + kVPOffBo, st)) != PI05_OK) return rc;
+    layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, c->y, pr + kVPOffLn2w, pr + kVPOffLn2b, c->h, c->n, eps);
+    if ((rc = vgemm(c, c->g_fc1, w + kVOff1, c->n, c->act, pr + kVPOffB1, st)) != PI05_OK) return rc;
+    gelu_kernel<<<grid_for(M * kVI), 256, 0, st>>>(c->act, M * kVI);
+    if ((rc = vgemm(c, c->g_fc2, w + kVOff2, c->act, c->y, pr + kVPOffB2, st)) != PI05_OK) return rc;
+    const bool last = l + 1 == p.L;
+    const float* nw = last ? c->post_w : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1w;
+    const float* nb = last ? c->post_b : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1b;
+    layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, c->y, nw, nb, c->h, c->n, eps);
+  }
+  if ((rc = vgemm(c, c->g_proj, c->proj_w, c->n, out, c->proj_b, st)) != PI05_OK) return rc;
+  if (c->d.out_scale != 1.0f) scale_kernel<<<grid_for(M * kVProj), 256, 0, st>>>(static_cast<u16*>(out), M * kVProj, c->d.out_scale);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return vfail(c, PI05_E_HIP, std::string("vision launch: ") + hipGetErrorString(e));
+  return PI05_OK;
+}
+
+}  // extern "C"

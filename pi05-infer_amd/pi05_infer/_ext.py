@@ -1,5 +1,5 @@
-"""ctypes binding of ``libpi05_denoise.so`` (the C ABIs in ``include/pi05_denoise.h`` and
-``include/pi05_prefill.h``).
+"""ctypes binding of ``libpi05_denoise.so`` (the C ABIs in ``include/pi05_denoise.h``,
+``include/pi05_prefill.h`` and ``include/pi05_siglip.h``).
 
 The shared library is built in-tree next to this file (``build_lib.py``).  There is no fallback:
 if the library is missing or fails to load, every entry point raises.
@@ -60,6 +60,20 @@ PREFIX_EXPORTED_SYMBOLS = (
     "pi05_prefix_forward",
 )
 
+# every exported symbol of include/pi05_siglip.h
+VISION_EXPORTED_SYMBOLS = (
+    "pi05_vision_default_dims",
+    "pi05_vision_check_dims",
+    "pi05_vision_device_bytes",
+    "pi05_vision_create",
+    "pi05_vision_destroy",
+    "pi05_vision_last_error",
+    "pi05_vision_bind_layer",
+    "pi05_vision_bind_heads",
+    "pi05_vision_refresh_weights",
+    "pi05_vision_forward",
+)
+
 
 class Pi05Error(RuntimeError):
     """A non-zero status from the engine's C ABI."""
@@ -105,6 +119,22 @@ class Pi05PrefixDims(ctypes.Structure):
     ]
 
 
+class Pi05VisionDims(ctypes.Structure):
+    _fields_ = [
+        ("width", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("mlp_dim", ctypes.c_int32),
+        ("patch", ctypes.c_int32),
+        ("image", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("proj_dim", ctypes.c_int32),
+        ("n_images", ctypes.c_int32),
+        ("ln_eps", ctypes.c_float),
+        ("out_scale", ctypes.c_float),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -122,6 +152,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     dims_p = ctypes.POINTER(Pi05Dims)
     pdims_p = ctypes.POINTER(Pi05PrefixDims)
+    vdims_p = ctypes.POINTER(Pi05VisionDims)
     sig = {
         "pi05_abi_version": (i32, []),
         "pi05_default_dims": (None, [dims_p]),
@@ -154,6 +185,16 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_prefix_refresh_weights": (i32, [vp, vp]),
         "pi05_prefix_embed_tokens": (i32, [vp, vp, i64, vp, i64, vp, vp]),
         "pi05_prefix_forward": (i32, [vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp]),
+        "pi05_vision_default_dims": (None, [vdims_p]),
+        "pi05_vision_check_dims": (i32, [vdims_p]),
+        "pi05_vision_device_bytes": (ctypes.c_size_t, [vdims_p]),
+        "pi05_vision_create": (i32, [vdims_p, ctypes.POINTER(vp)]),
+        "pi05_vision_destroy": (i32, [vp]),
+        "pi05_vision_last_error": (ctypes.c_char_p, [vp]),
+        "pi05_vision_bind_layer": (i32, [vp, i32] + [vp] * 16),
+        "pi05_vision_bind_heads": (i32, [vp] + [vp] * 7),
+        "pi05_vision_refresh_weights": (i32, [vp, vp]),
+        "pi05_vision_forward": (i32, [vp, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -456,6 +497,95 @@ class PrefixContext:
     def close(self) -> None:
         if getattr(self, "handle", None):
             self.lib.pi05_prefix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------------------------ vision tower
+
+
+def _check_vision(lib: ctypes.CDLL, rc: int, ctx: Optional[int]) -> None:
+    if rc != PI05_OK:
+        msg = lib.pi05_vision_last_error(ctx)
+        raise Pi05Error(rc, msg.decode() if msg else "")
+
+
+def vision_default_dims() -> Pi05VisionDims:
+    lib = load_library()
+    d = Pi05VisionDims()
+    lib.pi05_vision_default_dims(ctypes.byref(d))
+    return d
+
+
+def vision_check_dims(dims: Pi05VisionDims) -> None:
+    lib = load_library()
+    _check_vision(lib, lib.pi05_vision_check_dims(ctypes.byref(dims)), None)
+
+
+def vision_device_bytes(dims: Pi05VisionDims) -> int:
+    return int(load_library().pi05_vision_device_bytes(ctypes.byref(dims)))
+
+
+class VisionContext:
+    """One SigLIP + projector context: an image count on the current device."""
+
+    def __init__(self, dims: Pi05VisionDims, device: torch.device):
+        self.lib = load_library()
+        self.dims = dims
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        _check_vision(self.lib, self.lib.pi05_vision_check_dims(ctypes.byref(self.dims)), None)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _check_vision(self.lib, self.lib.pi05_vision_create(ctypes.byref(self.dims), ctypes.byref(handle)), None)
+        self.handle = handle.value
+
+    def _call(self, rc: int) -> None:
+        _check_vision(self.lib, rc, self.handle)
+
+    def bind_layer(self, i: int, wq, bq, wk, bk, wv, bv, wo, bo, w1, b1, w2, b2, ln1_w, ln1_b, ln2_w, ln2_b) -> None:
+        """Encoder layer i, every tensor bf16 (the reference's dtype for the encoder)."""
+        names = ("wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo", "w1", "b1", "w2", "b2", "ln1_w", "ln1_b", "ln2_w", "ln2_b")
+        ts = (wq, bq, wk, bk, wv, bv, wo, bo, w1, b1, w2, b2, ln1_w, ln1_b, ln2_w, ln2_b)
+        ptrs = [_ptr(t, torch.bfloat16, n, self.device) for t, n in zip(ts, names)]
+        self._call(self.lib.pi05_vision_bind_layer(self.handle, i, *ptrs))
+
+    def bind_heads(self, patch_w, patch_b, pos, post_w, post_b, proj_w, proj_b) -> None:
+        """Patch/position embeddings fp32, post_layernorm and projector bf16."""
+        f32, bf, dev = torch.float32, torch.bfloat16, self.device
+        ptrs = [_ptr(patch_w, f32, "patch_w", dev), _ptr(patch_b, f32, "patch_b", dev), _ptr(pos, f32, "pos", dev),
+                _ptr(post_w, bf, "post_w", dev), _ptr(post_b, bf, "post_b", dev), _ptr(proj_w, bf, "proj_w", dev),
+                _ptr(proj_b, bf, "proj_b", dev)]
+        self._call(self.lib.pi05_vision_bind_heads(self.handle, *ptrs))
+
+    def refresh_weights(self, stream=None) -> None:
+        self._call(self.lib.pi05_vision_refresh_weights(self.handle, _stream_ptr(stream)))
+
+    def forward(self, pixels: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """pixels [N, 3, 224, 224] fp32 -> image embeddings [N, 256, proj_dim] bf16."""
+        d = self.dims
+        shape = (d.n_images, d.channels, d.image, d.image)
+        if tuple(pixels.shape) != shape:
+            raise ValueError(f"pixels shape {tuple(pixels.shape)} != {shape}")
+        pp = _ptr(pixels, torch.float32, "pixels", self.device)
+        n_patches = (d.image // d.patch) ** 2
+        if out is None:
+            out = torch.empty((d.n_images, n_patches, d.proj_dim), dtype=torch.bfloat16, device=self.device)
+        elif tuple(out.shape) != (d.n_images, n_patches, d.proj_dim):
+            raise ValueError(f"out shape {tuple(out.shape)} != {(d.n_images, n_patches, d.proj_dim)}")
+        op = _ptr(out, torch.bfloat16, "out", self.device)
+        self._call(self.lib.pi05_vision_forward(self.handle, pp, op, _stream_ptr(stream)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.pi05_vision_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

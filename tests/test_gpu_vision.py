@@ -1,0 +1,129 @@
+"""GPU parity of the vision tower (SigLIP So400m/14 + PaliGemma projector) against the CPU oracle
+(oracle/siglip_oracle.py), through the C ABI (include/pi05_siglip.h).
+
+Tolerance, as for the denoise path (bf16 on the GPU, fp32 with bf16 rounding points in the
+oracle): the image embeddings have cosine similarity >= 0.9999 with the oracle's and max-abs
+error <= 2e-2 of the oracle tensor's range, per image.  Through all 27 layers the bf16 rounding
+noise alone takes the cosine below 0.9999: the oracle against itself with fp64-accumulated GEMMs
+(every rounding point unchanged) reaches 0.99989 on the full-depth case, and with P rounded to
+bf16 before P.V (flash attention's order) 0.99988.  The full-depth bar is therefore cos >= 0.9998
+(the max-abs bar is unchanged).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import siglip_oracle as SO
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+REL_MAXABS = 2e-2
+COS_MIN_FULL_DEPTH = 0.9998
+G = SO.SiglipGeometry()
+
+
+def _close(ref: torch.Tensor, got: torch.Tensor, what: str, cos_min: float = COS_MIN) -> None:
+    ref = ref.double().flatten().cpu()
+    got = got.double().flatten().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite values"
+    cos = torch.nn.functional.cosine_similarity(ref, got, dim=0).item()
+    maxabs = (ref - got).abs().max().item()
+    rng = (ref.max() - ref.min()).item()
+    print(f"{what}: cos={cos:.7f} maxabs={maxabs:.3e} range={rng:.3f}", flush=True)
+    assert cos >= cos_min, f"{what}: cosine {cos} < {cos_min}"
+    assert maxabs <= REL_MAXABS * rng, f"{what}: max-abs {maxabs} > {REL_MAXABS} * range {rng}"
+
+
+def _context(layers, heads, n_images: int, out_scale: float = 1.0):
+    from pi05_infer import _ext
+
+    d = _ext.vision_default_dims()
+    d.depth, d.n_images, d.out_scale = len(layers), n_images, out_scale
+    ctx = _ext.VisionContext(d, torch.device("cuda"))
+    keep = []
+    order = ("wq", "bq", "wk", "bk", "wv", "bv", "wout", "bout", "w1", "b1", "w2", "b2", "ln1w", "ln1b", "ln2w", "ln2b")
+    for i, w in enumerate(layers):
+        t = [w[k].to(torch.bfloat16).cuda().contiguous() for k in order]
+        keep.append(t)
+        ctx.bind_layer(i, *t)
+    f32 = lambda x: x.float().cuda().contiguous()  # noqa: E731
+    bf = lambda x: x.to(torch.bfloat16).cuda().contiguous()  # noqa: E731
+    h = [f32(heads["patch_w"]), f32(heads["patch_b"]), f32(heads["pos"]), bf(heads["post_w"]), bf(heads["post_b"]),
+         bf(heads["proj_w"]), bf(heads["proj_b"])]
+    keep.append(h)
+    ctx.bind_heads(*h)
+    ctx.refresh_weights()
+    torch.cuda.synchronize()
+    return ctx, keep
+
+
+def _pixels(n: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(n, 3, G.image, G.image, generator=g) * 2 - 1
+
+
+@pytest.fixture(scope="module")
+def weights2():
+    return SO.random_weights(G, 2, seed=21, std=0.03)
+
+
+def test_vision_parity_three_images(weights2):
+    print("case vision: depth 2, 3 images", flush=True)
+    layers, heads = weights2
+    px = _pixels(3, 0)
+    ref = SO.image_features(px, layers, heads, G)
+    ctx, _keep = _context(layers, heads, 3)
+    got = ctx.forward(px.cuda())
+    torch.cuda.synchronize()
+    assert got.shape == (3, 256, 2048) and got.dtype == torch.bfloat16
+    for i in range(3):
+        _close(ref[i], got[i].float(), f"depth 2 image {i}")
+    again = ctx.forward(px.cuda())  # a second call on the same context is identical
+    torch.cuda.synchronize()
+    assert torch.equal(again, got)
+    ctx.close()
+
+
+def test_vision_single_image_with_projector_scale(weights2):
+    print("case vision: depth 2, 1 image, out_scale 2048^-1/2", flush=True)
+    layers, heads = weights2
+    px = _pixels(1, 1)
+    s = 1.0 / math.sqrt(2048.0)
+    ref = SO.image_features(px, layers, heads, G, out_scale=s)
+    ctx, _keep = _context(layers, heads, 1, out_scale=s)
+    got = ctx.forward(px.cuda())
+    torch.cuda.synchronize()
+    _close(ref[0], got[0].float(), "depth 2 image 0 scaled")
+    ctx.close()
+
+
+def test_vision_images_are_independent(weights2):
+    print("case vision: depth 2, image order", flush=True)
+    layers, heads = weights2
+    px = _pixels(3, 2)
+    ctx3, _k3 = _context(layers, heads, 3)
+    ctx1, _k1 = _context(layers, heads, 1)
+    all3 = ctx3.forward(px.cuda())
+    one = ctx1.forward(px[2:3].cuda())
+    torch.cuda.synchronize()
+    # image 2 alone and as the third of three: same values up to the GEMM algorithms' summation order
+    _close(one[0].float(), all3[2].float(), "image 2 alone vs in a batch of 3")
+    ctx3.close()
+    ctx1.close()
+
+
+def test_vision_full_depth_three_images():
+    print("case vision: depth 27, 3 images", flush=True)
+    layers, heads = SO.random_weights(G, G.depth, seed=27, std=0.03)
+    px = _pixels(3, 3)
+    ctx, _keep = _context(layers, heads, 3)
+    got = ctx.forward(px.cuda())
+    torch.cuda.synchronize()
+    ctx.close()
+    del _keep
+    ref = SO.image_features(px, layers, heads, G)
+    for i in range(3):
+        _close(ref[i], got[i].float(), f"depth 27 image {i}", COS_MIN_FULL_DEPTH)
