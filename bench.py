@@ -4,6 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c1|c2|c3|c4]
                     [--schedule persistent|graph] [--no-cpu-baseline]
     python bench.py --workload prefill [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --workload vision [--steps K] [--warmup W] [--no-cpu-baseline]
 
 One bench "step" is one predict's denoise: the 10-step flow-matching Euler loop of the 18-layer
 expert over a static prefix KV cache, with weights, KV and noise already resident in HBM.  In the
@@ -13,7 +14,8 @@ N(0,1) noise (seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
 
 ``--workload prefill`` measures the prefix-LM prefill instead (Gemma-2B over a 968-token prefix,
 bs=1, 17 full layers + the last layer's K/V): one step is one prefill, MFMA-bound, reported
-against the bf16 dense MFMA peak.
+against the bf16 dense MFMA peak.  ``--workload vision`` measures the vision tower (SigLIP
+So400m/14 + projector over 3 camera views of 224 x 224, M = 768 patches) the same way.
 """
 
 from __future__ import annotations
@@ -40,6 +42,109 @@ METRIC = "denoise ms/predict (10 steps, bs=1, 968 prefix) + % peak HBM GB/s"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL_METRIC = "prefix prefill ms (Gemma-2B, bs=1, 968 tokens) + % peak bf16 MFMA"
+VISION_METRIC = "vision tower ms (SigLIP So400m/14 + projector, 3 views of 224x224) + % peak bf16 MFMA"
+
+
+def vision_flops(depth: int, n_images: int) -> int:
+    """FLOPs of one vision-tower call: per layer q, k, v, out (1152 x 1152), fc1, fc2 (1152 x 4304)
+    and the attention's Q.K^T and P.V over 16 heads of 72; the patch convolution (588 -> 1152) and
+    the projector (1152 -> 2048) once."""
+    W, I, S, H, D = 1152, 4304, 256, 16, 72
+    M = n_images * S
+    layer = 2 * M * W * (4 * W + 2 * I) + 2 * 2 * n_images * H * S * S * D
+    return depth * layer + 2 * M * 588 * W + 2 * M * W * 2048
+
+
+def bench_vision(args) -> int:
+    import torch
+
+    from pi05_infer import _ext
+    from pi05_infer.vision import HEAD_KEYS, HEAD_PARAM_NAMES, LAYER_KEYS, VisionGeometry, layer_param_names, make_weights
+
+    d = _ext.vision_default_dims()
+    N, L = d.n_images, d.depth
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = VisionGeometry()
+    w = make_weights(g, seed=0, device=dev, std=0.02)
+    ctx = _ext.VisionContext(d, dev)
+    for i in range(L):
+        n = layer_param_names(i)
+        ctx.bind_layer(i, *(w[n[k]] for k in LAYER_KEYS))
+    ctx.bind_heads(*(w[HEAD_PARAM_NAMES[k]] for k in HEAD_KEYS))
+    ctx.refresh_weights()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    px = torch.rand(N, 3, 224, 224, generator=gen, device=dev) * 2 - 1
+    out = torch.empty(N, 256, 2048, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        ctx.forward(px, out, stream=stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        ctx.forward(px, out, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = vision_flops(L, N)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import siglip_oracle as SO
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        og = SO.SiglipGeometry()
+        n0 = layer_param_names(0)
+        okeys = dict(zip(LAYER_KEYS, ("wq", "bq", "wk", "bk", "wv", "bv", "wout", "bout", "w1", "b1", "w2", "b2", "ln1w",
+                                      "ln1b", "ln2w", "ln2b")))
+        w0 = {okeys[k]: w[n0[k]].float().cpu() for k in LAYER_KEYS}
+        heads = {k: w[HEAD_PARAM_NAMES[k]].float().cpu() for k in HEAD_KEYS}
+        pxc = px.cpu()
+        t0 = time.perf_counter()
+        h = SO.embeddings(pxc, heads, og)
+        x = SO.layer_norm(h, heads["post_w"], heads["post_b"], og.ln_eps)
+        SO.linear_bias(x, heads["proj_w"], heads["proj_b"])
+        heads_ms = (time.perf_counter() - t0) * 1e3
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            SO.encoder_layer(w0, og, h)
+            times.append(time.perf_counter() - t0)
+        layer_ms = statistics.median(times) * 1e3
+        cpu = {
+            "value": round(layer_ms * L + heads_ms, 1),
+            "unit": "ms/call",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one encoder layer of the fp32 CPU oracle over {N} images (median of 2) scaled to {L} layers, "
+                      f"plus the embeddings, post-norm and projector once; host {cpu_model()}",
+        }
+    out_line = {
+        "metric": VISION_METRIC,
+        "value": round(ms, 4),
+        "unit": "ms/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init SigLIP/projector weights N(0, 0.02), uniform [-1, 1] pixels, seeds 0/1)",
+        "config": {"workload": f"SigLIP So400m/14 depth {L} + projector, {N} images of 224x224 (M = {N * 256})",
+                   "n_images": N},
+        "roofline": {"kernel": "whole tower (hipBLASLt GEMMs + HIP kernels)", "bound": "mfma",
+                     "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None, "flops_per_call": flops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out_line), flush=True)
+    ctx.close()
+    torch.cuda.synchronize()
+    return 0
 
 
 def prefill_flops(depth: int, batch: int, prefix_len: int, skip_last: bool = True) -> int:
@@ -192,15 +297,17 @@ def main() -> int:
                     help="execution schedule (default: the library's choice, persistent on MI355X)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-predicts", type=int, default=8, help="predicts in the CPU-baseline sample")
-    ap.add_argument("--workload", default="denoise", choices=["denoise", "prefill"])
+    ap.add_argument("--workload", default="denoise", choices=["denoise", "prefill", "vision"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs the denoise loop on one GPU; runs with --gpus > 1 are not "
-              "supported (data-parallel sharding over samples needs no communication, see DESIGN.md).",
+              "supported (data-parallel sharding over samples needs no communication).",
               file=sys.stderr)
         return 2
     if args.workload == "prefill":
         return bench_prefill(args)
+    if args.workload == "vision":
+        return bench_vision(args)
 
     import torch
 

@@ -11,8 +11,11 @@ Every denoise computation happens in ``libpi05_denoise.so``; PyTorch only provid
 memory, streams and the random noise draw.  An observation carries either the prefix KV cache and
 pad mask that ``_build_prefix_cache`` produces (the reference's frozen-prefix mode,
 tools/bitexact_compiled_toggles.py:354-376), or the prefix embeddings and pad mask, in which case
-the attached ``PrefixLM`` (prefix.py) runs the Gemma-2B prefill on the GPU first.  SigLIP is not
-part of this engine: image embeddings come with the observation.
+the attached ``PrefixLM`` (prefix.py) runs the Gemma-2B prefill on the GPU first, or the camera
+images and tokenized prompt, in which case ``embed_prefix`` (pi0_pytorch.py:190-255) runs the
+attached ``VisionTower`` (vision.py, SigLIP + projector) and the token embedding before the
+prefill.  Image preprocessing (resize, augmentation, HWC -> CHW) happens before the observation
+reaches the engine: images arrive as ``[B, 3, 224, 224]`` in [-1, 1].
 """
 
 from __future__ import annotations
@@ -53,20 +56,33 @@ class OpenPi0InferConfig:
 
 @dataclass
 class Observation:
-    """What ``sample_actions`` consumes: the prefix KV cache of ``_build_prefix_cache`` (per layer
-    K and V bf16 ``[B, 1, P, D]``, or stacked ``[B, L, P, D]``) or the prefix embeddings
-    ``[B, P, 2048]`` (``embed_prefix``'s output, pi0_pytorch.py:190-255; prefix_k/prefix_v None),
-    the pad mask ``[B, P]`` and the robot state (unused by pi0.5's suffix, pi0_pytorch.py:269-287)."""
+    """What ``sample_actions`` consumes, one of three prefix forms: the prefix KV cache of
+    ``_build_prefix_cache`` (per layer K and V bf16 ``[B, 1, P, D]``, or stacked ``[B, L, P, D]``)
+    with its pad mask ``[B, P]``; the prefix embeddings ``[B, P, 2048]`` (``embed_prefix``'s
+    output, pi0_pytorch.py:190-255) with the pad mask; or the camera views (``images``: per view
+    ``[B, 3, 224, 224]`` in [-1, 1], ``image_masks``: per view ``[B]`` bool) and the tokenized
+    prompt ``[B, T]`` with its mask, as ``_preprocess_observation`` returns them
+    (pi0_pytorch.py:165-174).  The robot state is unused by pi0.5's suffix (pi0_pytorch.py:269-287)."""
 
     prefix_k: Any
     prefix_v: Any
-    prefix_pad_masks: torch.Tensor
+    prefix_pad_masks: Optional[torch.Tensor]
     state: Optional[torch.Tensor] = None
     extra: dict = field(default_factory=dict)
     prefix_embs: Optional[torch.Tensor] = None
+    images: Optional[list] = None
+    image_masks: Optional[list] = None
+    tokenized_prompt: Optional[torch.Tensor] = None
+    tokenized_prompt_mask: Optional[torch.Tensor] = None
 
     @classmethod
     def from_dict(cls, d: dict) -> "Observation":
+        if "images" in d:
+            imgs, masks = d["images"], d["image_masks"]
+            imgs = list(imgs.values()) if isinstance(imgs, dict) else list(imgs)
+            masks = list(masks.values()) if isinstance(masks, dict) else list(masks)
+            return cls(None, None, None, d.get("state"), images=imgs, image_masks=masks,
+                       tokenized_prompt=d["tokenized_prompt"], tokenized_prompt_mask=d["tokenized_prompt_mask"])
         if "prefix_embs" in d:
             return cls(None, None, d["prefix_pad_masks"], d.get("state"), prefix_embs=d["prefix_embs"])
         if "past_key_values" in d:
@@ -107,6 +123,7 @@ class OpenPi0Inference:
         self.training = False
         self.schedule: Optional[str] = None  # None: the library's default for the device
         self.prefix_lm = None  # optional PrefixLM (prefix.py): prefix embeddings -> KV cache
+        self.vision_tower = None  # optional VisionTower (vision.py): camera images -> image embeddings
 
     # ------------------------------------------------------------------ parameters
     def expected_parameters(self) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
@@ -154,6 +171,8 @@ class OpenPi0Inference:
             self._drop_contexts()
             if self.prefix_lm is not None:
                 self.prefix_lm.to(device)
+            if self.vision_tower is not None:
+                self.vision_tower.to(device)
         return self
 
     def attach_prefix_lm(self, prefix_lm) -> None:
@@ -163,6 +182,39 @@ class OpenPi0Inference:
             raise ValueError("prefix LM and action expert must have the same depth (one KV layer per expert layer)")
         prefix_lm.to(self.device)
         self.prefix_lm = prefix_lm
+
+    def attach_vision_tower(self, vision_tower) -> None:
+        """Run SigLIP + the projector (vision.VisionTower) for observations that carry camera
+        images; the projector's width must equal the prefix LM's."""
+        vision_tower.to(self.device)
+        self.vision_tower = vision_tower
+
+    @torch.no_grad()
+    def embed_prefix(self, images, img_masks, lang_tokens, lang_masks):
+        """``(prefix_embs, prefix_pad_masks, prefix_att_masks)`` as pi0_pytorch.py:190-255 builds
+        them: one vision-tower call over all views stacked on the batch dim, each view's 256 image
+        embeddings padded by its image mask, then the scaled token embeddings padded by the prompt
+        mask; the attention mask is all zeros (full attention over the prefix)."""
+        if self.vision_tower is None or self.prefix_lm is None:
+            raise ValueError("embed_prefix needs an attached VisionTower and PrefixLM")
+        bsize = images[0].shape[0]
+        all_embs = self.vision_tower.embed_image(torch.cat(list(images), dim=0) if len(images) > 1 else images[0])
+        n_img = all_embs.shape[1]
+        embs, pads = [], []
+        for v, m in enumerate(img_masks):
+            embs.append(all_embs[v * bsize : (v + 1) * bsize])
+            pads.append(m.to(device=all_embs.device, dtype=torch.bool)[:, None].expand(bsize, n_img))
+        embs.append(self.prefix_lm.embed_language_tokens(lang_tokens, prefix_len=len(images) * n_img + lang_tokens.shape[1]))
+        pads.append(lang_masks.to(device=all_embs.device, dtype=torch.bool))
+        embs = torch.cat(embs, dim=1)
+        pads = torch.cat(pads, dim=1)
+        return embs, pads, torch.zeros_like(pads)
+
+    def _build_prefix_cache(self, images, img_masks, lang_tokens, lang_masks):
+        """``(prefix_output, prefix_pad_masks, past_key_values)`` from camera images and prompt
+        (engine.py:770-794): ``embed_prefix`` then the prefill."""
+        embs, pads, _ = self.embed_prefix(images, img_masks, lang_tokens, lang_masks)
+        return self.prefix_lm.build_prefix_cache(embs, pads)
 
     def eval(self):
         self.training = False
@@ -233,7 +285,12 @@ class OpenPi0Inference:
     def _run(self, observation, noise, trace: bool):
         obs = Observation.from_dict(observation) if isinstance(observation, dict) else observation
         pad = obs.prefix_pad_masks
-        if obs.prefix_k is None:
+        if obs.prefix_k is None and obs.prefix_embs is None and obs.images is not None:
+            _, pad, kv = self._build_prefix_cache(obs.images, obs.image_masks, obs.tokenized_prompt,
+                                                  obs.tokenized_prompt_mask)
+            ks = [k for k, _ in kv]
+            vs = [v for _, v in kv]
+        elif obs.prefix_k is None:
             if obs.prefix_embs is None or self.prefix_lm is None:
                 raise ValueError("the observation has no prefix KV cache; prefix embeddings need an attached PrefixLM")
             _, pad, kv = self.prefix_lm.build_prefix_cache(obs.prefix_embs, pad)
@@ -309,6 +366,8 @@ class OpenPi0Inference:
         self._drop_contexts()
         if self.prefix_lm is not None:
             self.prefix_lm.close()
+        if self.vision_tower is not None:
+            self.vision_tower.close()
 
 
 Engine = OpenPi0Inference

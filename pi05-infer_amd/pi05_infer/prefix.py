@@ -3,8 +3,8 @@ model over the prefix embeddings, producing the KV cache the denoise loop consum
 
 Mirrors the reference's ``_build_prefix_cache`` (engine.py:770-794) from the prefix embeddings on:
 ``embed_language_tokens`` + the ``sqrt(width)`` scaling of ``embed_prefix`` (pi0_pytorch.py:225-228)
-and the prefill itself.  SigLIP (the image embeddings) is not part of this engine: callers pass the
-image embeddings, or any ``[B, P, 2048]`` bf16 prefix embedding, and the pad mask.  Every computation
+and the prefill itself.  The image embeddings come from the vision tower (vision.py), assembled by
+the engine's ``embed_prefix``; any ``[B, P, 2048]`` bf16 prefix embedding with its pad mask works.  Every computation
 runs in ``libpi05_denoise.so`` (include/pi05_prefill.h); there is no fallback.
 """
 
@@ -145,12 +145,16 @@ class PrefixLM:
         return ctx
 
     @torch.no_grad()
-    def embed_language_tokens(self, tokens: torch.Tensor) -> torch.Tensor:
+    def embed_language_tokens(self, tokens: torch.Tensor, prefix_len: Optional[int] = None) -> torch.Tensor:
         """``embed_tokens(tokens) * sqrt(width)`` in bf16 (gemma_pytorch.py:109-110 with
-        pi0_pytorch.py:225-228's scaling)."""
+        pi0_pytorch.py:225-228's scaling).  ``prefix_len``: the length of the prefix these tokens
+        end, so the context the prefill will use serves the lookup too."""
         if EMBED_NAME not in self.params:
             raise RuntimeError("embed_tokens weight not loaded")
-        ctx = next(iter(self._contexts.values()), None) or self._context(1, 1)
+        if prefix_len is not None:
+            ctx = self._context(tokens.shape[0], prefix_len)
+        else:
+            ctx = next(iter(self._contexts.values()), None) or self._context(1, 1)
         return ctx.embed_tokens(tokens, self.params[EMBED_NAME])
 
     @torch.no_grad()

@@ -127,3 +127,79 @@ def test_vision_full_depth_three_images():
     ref = SO.image_features(px, layers, heads, G)
     for i in range(3):
         _close(ref[i], got[i].float(), f"depth 27 image {i}", COS_MIN_FULL_DEPTH)
+
+
+def test_images_and_prompt_to_actions_matches_oracle_chain(weights2):
+    """A whole predict from camera images and a tokenized prompt through the Python API
+    (``embed_prefix`` -> prefill -> denoise) against the oracle chain: the prefix embeddings'
+    language part and pad mask exactly, the image part to the tolerance, the actions to the
+    north-star bar.  The second view is masked out (a missing camera)."""
+    print("case images -> actions: vision depth 2, prefix/expert depth 3, B=1, 2 views + 24 tokens, 4 steps",
+          flush=True)
+    from dataclasses import replace
+
+    from oracle import denoise_oracle as O
+    from oracle import prefix_oracle as PO
+    from pi05_infer import synthetic as S
+    from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+    from pi05_infer.prefix import EMBED_NAME, PrefixGeometry, PrefixLM
+    from pi05_infer.prefix import layer_param_names as prefix_names
+    from pi05_infer.vision import HEAD_PARAM_NAMES, VisionGeometry, VisionTower
+    from pi05_infer.vision import layer_param_names as vision_names
+
+    layers_v, heads_v = weights2
+    B, T, steps, vocab = 1, 24, 4, 1000
+    views = [_pixels(B, 10), _pixels(B, 11)]
+    img_masks = [torch.ones(B, dtype=torch.bool), torch.zeros(B, dtype=torch.bool)]
+    g = torch.Generator().manual_seed(12)
+    tokens = torch.randint(0, vocab, (B, T), generator=g)
+    lang_mask = torch.ones(B, T, dtype=torch.bool)
+    lang_mask[0, 18:] = False
+    pg = PrefixGeometry(depth=3, vocab_size=vocab)
+    og_p = PO.PrefixGeometry()
+    layers_p = PO.random_layers(og_p, 3, seed=13)
+    table = O._bf(torch.randn(vocab, pg.width, generator=g))
+
+    # oracle chain
+    feats = SO.image_features(torch.cat(views), layers_v, heads_v, G)
+    emb_ref = torch.cat([feats[:B], feats[B:], PO.embed_tokens(tokens, table, pg.width)], dim=1)
+    pad_ref = torch.cat([img_masks[0][:, None].expand(B, 256), img_masks[1][:, None].expand(B, 256), lang_mask], dim=1)
+    ref_cache = PO.prefill(layers_p, og_p, emb_ref, pad_ref)
+    k_ref = torch.cat([k for k, _ in ref_cache], dim=1)
+    v_ref = torch.cat([v for _, v in ref_cache], dim=1)
+    eg = replace(S.ExpertGeometry(), depth=3)
+    w = S.make_weights(eg)
+    x1 = S.make_noise(eg, 1)
+    og = O.geometry_from(eg)
+    act_ref, _ = O.sample_actions(w, og, k_ref, v_ref, pad_ref, x1, steps, O.adarms_table(w, og, steps))
+
+    # the engine with a vision tower and a prefix LM attached
+    vt = VisionTower(VisionGeometry(depth=2))
+    rename = {"wout": "wo", "bout": "bo", "ln1w": "ln1_w", "ln1b": "ln1_b", "ln2w": "ln2_w", "ln2b": "ln2_b"}
+    sd = {vision_names(i)[rename.get(k, k)]: t for i, lw in enumerate(layers_v) for k, t in lw.items()}
+    sd.update({HEAD_PARAM_NAMES[k]: t for k, t in heads_v.items()})
+    missing, _ = vt.load_state_dict(sd, strict=True)
+    assert missing == []
+    plm = PrefixLM(pg)
+    psd = {prefix_names(i)[k]: lw[k] for i, lw in enumerate(layers_p) for k in lw}
+    psd[EMBED_NAME] = table
+    assert plm.load_state_dict(psd, strict=True)[0] == []
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
+    model.load_state_dict(w)
+    model.to("cuda")
+    model.attach_prefix_lm(plm)
+    model.attach_vision_tower(vt)
+    cuda_views = [v.cuda() for v in views]
+    embs, pads, att = model.embed_prefix(cuda_views, [m.cuda() for m in img_masks], tokens.cuda(), lang_mask.cuda())
+    torch.cuda.synchronize()
+    assert embs.shape == (B, 512 + T, 2048) and embs.dtype == torch.bfloat16
+    assert torch.equal(pads.cpu(), pad_ref) and not att.any()
+    assert torch.equal(embs[:, 512:].float().cpu(), emb_ref[:, 512:])  # token embedding: exact
+    _close(emb_ref[:, :256], embs[:, :256].float(), "embed_prefix view 0")
+    obs = Observation.from_dict({"images": {"base_0_rgb": cuda_views[0], "left_wrist_0_rgb": cuda_views[1]},
+                                 "image_masks": {"base_0_rgb": img_masks[0].cuda(), "left_wrist_0_rgb": img_masks[1].cuda()},
+                                 "tokenized_prompt": tokens.cuda(), "tokenized_prompt_mask": lang_mask.cuda()})
+    act, _ = model.sample_actions_with_velocities(obs, x1.cuda())
+    torch.cuda.synchronize()
+    _close(act_ref, act, "images+prompt -> actions")
+    model.close()
