@@ -7,9 +7,12 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace pi05 {
@@ -21,7 +24,7 @@ struct GemmPlan {
   hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
   hipblasLtMatmulAlgo_t algo{};
   size_t ws = 0;
-  std::vector<hipblasLtMatmulHeuristicResult_t> cands;  // heuristic candidates, timed by tune_plan
+  std::vector<hipblasLtMatmulHeuristicResult_t> cands;  // heuristic picks + other supported solutions, timed by tune_plan
   float ms = 0.f;                                        // the chosen algorithm's time
 };
 constexpr int kGemmCandidates = 256;
@@ -34,6 +37,7 @@ struct GemmOpts {
   hipDataType ab = HIP_R_16BF;  // operand type (HIP_R_32F for an fp32 GEMM)
   hipDataType c = HIP_R_16BF;   // output type (split-K partials: HIP_R_32F)
   bool bias = false;            // fp32 per-column bias before the rounding
+  int ld_c = 0;                 // row length of the output (0: N)
 };
 
 inline bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, GemmPlan* p, std::string* err, GemmOpts o = GemmOpts{}) {
@@ -45,7 +49,7 @@ inline bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, G
       !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta))) ||
       !lt_ok(hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb))) ||
       !lt_ok(hipblasLtMatrixLayoutCreate(&p->lw, o.ab, K, N, ld_k)) || !lt_ok(hipblasLtMatrixLayoutCreate(&p->la, o.ab, K, M, ld_k)) ||
-      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, ct, N, M, N))) {
+      !lt_ok(hipblasLtMatrixLayoutCreate(&p->lc, ct, N, M, o.ld_c ? o.ld_c : N))) {
     *err = "hipBLASLt descriptor creation failed";
     return false;
   }
@@ -81,8 +85,30 @@ inline bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, G
   int n = 0;
   const hipblasStatus_t s = hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->lw, p->la, p->lc, p->lc, pref, kGemmCandidates, res.data(), &n);
   hipblasLtMatmulPreferenceDestroy(pref);
+  std::vector<int> seen;
   for (int i = 0; lt_ok(s) && i < n; ++i)
-    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) p->cands.push_back(res[i]);
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_max) {
+      p->cands.push_back(res[i]);
+      seen.push_back(hipblaslt_ext::getIndexFromAlgo(res[i].algo));
+    }
+  // every other solution the library holds for this problem type that accepts this problem
+  // (split-K / stream-K variants the heuristic leaves out fill the GPU at small M x N)
+  std::vector<hipblasLtMatmulHeuristicResult_t> all;
+  const hipDataType ct_all = ct;
+  if (lt_ok(hipblaslt_ext::getAllAlgos(h, hipblaslt_ext::GemmType::HIPBLASLT_GEMM, ta, tb, o.ab, o.ab, ct_all, ct_all, HIPBLAS_COMPUTE_32F, all))) {
+    const float alpha = 1.f, beta = 0.f;
+    for (auto& r : all) {
+      const int idx = hipblaslt_ext::getIndexFromAlgo(r.algo);
+      if (std::find(seen.begin(), seen.end(), idx) != seen.end()) continue;
+      size_t wsz = 0;
+      if (!lt_ok(hipblaslt_ext::matmulIsAlgoSupported(h, p->desc, &alpha, p->lw, p->la, &beta, p->lc, p->lc, r.algo, wsz)) || wsz > ws_max)
+        continue;
+      r.workspaceSize = wsz;
+      r.state = HIPBLAS_STATUS_SUCCESS;
+      p->cands.push_back(r);
+      seen.push_back(idx);
+    }
+  }
   if (!p->cands.empty()) {
     p->algo = p->cands[0].algo;  // the heuristic's first choice until tune_plan has timed them all
     p->ws = p->cands[0].workspaceSize;
@@ -103,8 +129,9 @@ inline hipblasStatus_t run_plan(hipblasLtHandle_t h, const GemmPlan& p, const hi
   return hipblasLtMatmul(h, p.desc, &alpha, W, p.lw, A, p.la, &beta, C, p.lc, C, p.lc, &algo, ws, ws_bytes, st);
 }
 
-// Time every candidate algorithm on real buffers (3 runs after one warm-up; values do not affect
-// the timing) and keep the fastest; candidates that fail to launch are skipped.
+// Time every candidate algorithm on real buffers (2 runs after one warm-up; values do not affect
+// the timing), re-time the 4 fastest over 15 runs each and keep the best; candidates that fail to
+// launch are skipped.
 inline bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const void* A, void* C, void* ws, hipStream_t st,
                       const float* bias = nullptr) {
   hipEvent_t e0, e1;
@@ -113,25 +140,35 @@ inline bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const voi
     hipEventDestroy(e0);
     return false;
   }
-  float best = 1e30f;
-  for (const auto& c : p->cands) {
+  auto time_algo = [&](const hipblasLtMatmulHeuristicResult_t& c, int reps, float* ms) {
     bool ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, W, A, C, bias, ws, st));
-    if (!ok) continue;
+    if (!ok) return false;
     hipEventRecord(e0, st);
-    for (int r = 0; r < 3 && ok; ++r) ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, W, A, C, bias, ws, st));
+    for (int r = 0; r < reps && ok; ++r) ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, W, A, C, bias, ws, st));
     hipEventRecord(e1, st);
-    if (hipEventSynchronize(e1) != hipSuccess) break;
+    if (hipEventSynchronize(e1) != hipSuccess || !ok || hipEventElapsedTime(ms, e0, e1) != hipSuccess) return false;
+    *ms /= (float)reps;
+    return true;
+  };
+  std::vector<std::pair<float, size_t>> timed;
+  for (size_t i = 0; i < p->cands.size(); ++i) {
     float ms = 0.f;
-    if (!ok || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+    if (time_algo(p->cands[i], 2, &ms)) timed.emplace_back(ms, i);
+  }
+  std::sort(timed.begin(), timed.end());
+  float best = 1e30f;
+  for (size_t k = 0; k < timed.size() && k < 4; ++k) {
+    float ms = 0.f;
+    if (!time_algo(p->cands[timed[k].second], 15, &ms)) continue;
     if (ms < best) {
       best = ms;
-      p->algo = c.algo;
-      p->ws = c.workspaceSize;
+      p->algo = p->cands[timed[k].second].algo;
+      p->ws = p->cands[timed[k].second].workspaceSize;
     }
   }
   hipEventDestroy(e0);
   hipEventDestroy(e1);
-  p->ms = best / 3.f;
+  p->ms = best;
   return hipGetLastError() == hipSuccess;
 }
 

@@ -3,10 +3,11 @@
 //   patches (fp32 im2col) . Wpatch^T          hipBLASLt fp32 GEMM
 //   h = bf16(conv + bpatch + pos)              embed_kernel
 //   27 x [ n = LN1(h); q|k|v = n.W^T + b      hipBLASLt (bias epilogue)
-//          attention, 16 heads of 72          qkv_layout_kernel + vision_attn_kernel (MFMA)
-//          h = bf16(h + o.Wo^T + bo); n = LN2 hipBLASLt + layernorm_kernel (residual fused)
+//          attention, 16 heads of 72          vision_attn_kernel (MFMA, K/V staged in LDS)
+//          h = bf16(h + o.Wo^T + bo); n = LN2 hipBLASLt (split-K when faster) + layernorm_kernel
 //          a = gelu_tanh(n.W1^T + b1)          hipBLASLt + gelu_kernel
-//          h = bf16(h + a.W2^T + b2) ]         hipBLASLt + layernorm_kernel (next LN1 / post_layernorm)
+//          h = bf16(h + a.W2^T + b2) ]         hipBLASLt (split-K when faster) + layernorm_kernel
+//                                              (the next LN1 / post_layernorm)
 //   out = (n.Wproj^T + bproj) * out_scale     hipBLASLt (+ scale_kernel)
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
@@ -23,35 +24,33 @@ namespace pi05 {
 namespace {
 
 constexpr int kVW = 1152, kVH = 16, kVD = 72, kVI = 4304, kVPatch = 14, kVImg = 224, kVC = 3, kVProj = 2048;
+// the MLP's hidden dim padded to 4352 = 64 x 68 in the fc1 output and the fc2 weight rows (the pad
+// columns stay zero: gelu(0) = 0 and zero products add exactly nothing), so fc2 splits into 4 or 8
+// K slices of 16-byte-aligned width
+constexpr int kVIp = 4352;
 constexpr int kVGrid = kVImg / kVPatch, kVS = kVGrid * kVGrid;  // 16 x 16 = 256 patches
 constexpr int kVPD = kVC * kVPatch * kVPatch;                   // 588 values per patch
 constexpr int kVQkvN = 3 * kVW;                                 // 3456 fused q|k|v columns
 // attention operands, per (image, head): head dim padded to 96 for Q.K^T (3 k-steps of 32) and to
 // 80 for P.V (5 d-tiles of 16); the padding stays zero
 constexpr int kVKs = 3, kVDt = 5;
-constexpr size_t kVQHead = (size_t)kVS * kVKs * 32;  // elements of one head's Q (or K) fragments
-constexpr size_t kVVHead = (size_t)(kVS / 32) * kVDt * 512;
 // per-layer packed bf16 weights: [Wq; Wk; Wv] | Wo | W1 | W2; fp32 parameters: bqkv | bo | b1 | b2 |
 // ln1w | ln1b | ln2w | ln2b
 constexpr size_t kVOffQkv = 0, kVOffO = kVOffQkv + (size_t)kVQkvN * kVW, kVOff1 = kVOffO + (size_t)kVW * kVW,
-                 kVOff2 = kVOff1 + (size_t)kVI * kVW, kVLayerElems = kVOff2 + (size_t)kVW * kVI;
+                 kVOff2 = kVOff1 + (size_t)kVI * kVW, kVLayerElems = kVOff2 + (size_t)kVW * kVIp;
 constexpr size_t kVPOffBqkv = 0, kVPOffBo = kVQkvN, kVPOffB1 = kVPOffBo + kVW, kVPOffB2 = kVPOffB1 + kVI,
                  kVPOffLn1w = kVPOffB2 + kVW, kVPOffLn1b = kVPOffLn1w + kVW, kVPOffLn2w = kVPOffLn1b + kVW,
                  kVPOffLn2b = kVPOffLn2w + kVW, kVLayerParams = kVPOffLn2b + kVW;
 constexpr size_t kVWorkspace = 32ull << 20;
+constexpr int kVMaxSplits = 8;  // split-K candidates: 4 and 8 K slices
 
 thread_local std::string g_vision_err;
 
-// K fragment (key, d) of one head over 96 padded dims: fragment (key tile, d-step) is the MFMA A
-// operand of S^T = K Q^T; V fragment (key, d) of the 5 d-tiles with the 32-key permutation vkey
-// (the P^T operand is the S^T accumulator a lane already holds).
-__host__ __device__ constexpr size_t kfrag3(int key, int d) {
-  return ((size_t)(key >> 4) * kVKs + (d >> 5)) * 512 + (size_t)(((d & 31) >> 3) * 16 + (key & 15)) * 8 + (d & 7);
-}
-__host__ __device__ constexpr size_t vfrag5(int key, int d) {
-  const int kb = key >> 5, r = key & 31, g = (r & 15) >> 2, j = r < 16 ? (r & 3) : 4 + (r & 3);
-  return ((size_t)kb * kVDt + (d >> 4)) * 512 + (size_t)(g * 16 + (d & 15)) * 8 + j;
-}
+// Attention operands in LDS, per (image, head): K over 96 padded head dims as the A operand of
+// S^T = K Q^T (fragment (key tile, d-step)), V over 80 padded dims as the A operand of
+// O^T = V^T P^T (fragment (key block, d-tile)) with the 32-key permutation vkey, so the P^T operand
+// is the S^T accumulator a lane already holds.  The padding dims are zero.
+constexpr int kVKFrags = (kVS / 16) * kVKs, kVVFrags = (kVS / 32) * kVDt;
 
 // im2col: patches[(n, p)][c*196 + ky*14 + kx] = pixels[n][c][14 py + ky][14 px + kx], p = 16 py + px
 __global__ __launch_bounds__(256) void im2col_kernel(const float* px, float* patches, int n_img) {
@@ -73,66 +72,124 @@ __global__ __launch_bounds__(256) void embed_kernel(const float* conv, const flo
   }
 }
 
-// h = bf16(x + y) (y optional), n = bf16((h - mean) / sqrt(var + eps) * w + b), fp32 statistics
-// (nn.LayerNorm).  One workgroup of 192 threads per 1152-wide row, 6 elements per thread.
-__global__ __launch_bounds__(192) void layernorm_kernel(const u16* x, const u16* y, const float* w, const float* b, u16* h_out, u16* n_out,
-                                                       float eps) {
-  const size_t off = (size_t)blockIdx.x * kVW + threadIdx.x * 6;
-  __shared__ float s_part[3];
-  float h[6];
+// h = bf16(x + y), n = bf16((h - mean) / sqrt(var + eps) * w + b) with fp32 statistics
+// (nn.LayerNorm after the residual add).  y is the bf16 Linear output, or (ys != null) the Linear
+// as nsplit fp32 split-K partials reduced here: y = bf16(sum + ybias); neither: h = x.  One wave
+// per 1152-wide row (9 pairs of bf16 per lane), 4 rows per workgroup.
+__global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16* y, const float* ys, int nsplit, size_t split_stride,
+                                                       const float* ybias, const float* w, const float* b, u16* h_out, u16* n_out,
+                                                       float eps, int rows) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const size_t ro = (size_t)row * kVW;
+  // every load of the row is issued before the first use
+  uint32_t xv[9];
 #pragma unroll
-  for (int i = 0; i < 6; ++i) h[i] = y ? round_bf(fadd(bf2f(x[off + i]), bf2f(y[off + i]))) : bf2f(x[off + i]);
-  auto block_sum = [&](float v) {
+  for (int j = 0; j < 9; ++j) xv[j] = *reinterpret_cast<const uint32_t*>(x + ro + 2 * (lane + 64 * j));
+  float h[18];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    __syncthreads();  // s_part of a previous reduction has been read
-    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (s_part[0] + s_part[1]) + s_part[2];
-  };
+  for (int j = 0; j < 9; ++j) h[2 * j] = bf2f((u16)(xv[j] & 0xffff)), h[2 * j + 1] = bf2f((u16)(xv[j] >> 16));
+  if (ys) {
+    float2 acc[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) acc[j] = *reinterpret_cast<const float2*>(ys + ro + 2 * (lane + 64 * j));
+    for (int sp = 1; sp < nsplit; ++sp) {
+      float2 a[9];
+#pragma unroll
+      for (int j = 0; j < 9; ++j) a[j] = *reinterpret_cast<const float2*>(ys + (size_t)sp * split_stride + ro + 2 * (lane + 64 * j));
+#pragma unroll
+      for (int j = 0; j < 9; ++j) acc[j].x += a[j].x, acc[j].y += a[j].y;
+    }
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float2 bb = *reinterpret_cast<const float2*>(ybias + 2 * (lane + 64 * j));
+      h[2 * j] = round_bf(fadd(h[2 * j], round_bf(fadd(acc[j].x, bb.x))));
+      h[2 * j + 1] = round_bf(fadd(h[2 * j + 1], round_bf(fadd(acc[j].y, bb.y))));
+    }
+  } else if (y) {
+    uint32_t yv[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) yv[j] = *reinterpret_cast<const uint32_t*>(y + ro + 2 * (lane + 64 * j));
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      h[2 * j] = round_bf(fadd(h[2 * j], bf2f((u16)(yv[j] & 0xffff))));
+      h[2 * j + 1] = round_bf(fadd(h[2 * j + 1], bf2f((u16)(yv[j] >> 16))));
+    }
+  }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 6; ++i) s += h[i];
-  const float mean = block_sum(s) * (1.0f / kVW);
+  for (int i = 0; i < 18; ++i) s += h[i];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const float mean = s * (1.0f / kVW);
   float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < 6; ++i) q += (h[i] - mean) * (h[i] - mean);
-  const float rstd = 1.0f / sqrtf(block_sum(q) * (1.0f / kVW) + eps);
+  for (int i = 0; i < 18; ++i) q += (h[i] - mean) * (h[i] - mean);
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const int c = threadIdx.x * 6 + i;
-    if (y && h_out) h_out[off + i] = f2bf(h[i]);
-    n_out[off + i] = f2bf(fadd(fmul(fmul(fsub(h[i], mean), rstd), w[c]), b[c]));
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+  const float rstd = 1.0f / sqrtf(q * (1.0f / kVW) + eps);
+  const bool write_h = (y || ys) && h_out;
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int e = 2 * (lane + 64 * j);
+    const float2 wv = *reinterpret_cast<const float2*>(w + e), bv = *reinterpret_cast<const float2*>(b + e);
+    const u16 n0 = f2bf(fadd(fmul(fmul(fsub(h[2 * j], mean), rstd), wv.x), bv.x));
+    const u16 n1 = f2bf(fadd(fmul(fmul(fsub(h[2 * j + 1], mean), rstd), wv.y), bv.y));
+    *reinterpret_cast<uint32_t*>(n_out + ro + e) = (uint32_t)n0 | ((uint32_t)n1 << 16);
+    if (write_h) *reinterpret_cast<uint32_t*>(h_out + ro + e) = (uint32_t)f2bf(h[2 * j]) | ((uint32_t)f2bf(h[2 * j + 1]) << 16);
   }
 }
 
-// q, k, v of one token row -> the attention's fragment layouts (one workgroup per row)
-__global__ __launch_bounds__(256) void qkv_layout_kernel(const u16* qkv, u16* qf, u16* kf, u16* vf) {
-  const int row = blockIdx.x, n = row / kVS, tok = row % kVS;
-  const u16* src = qkv + (size_t)row * kVQkvN;
-  for (int i = threadIdx.x; i < kVW; i += 256) {
-    const int hd = i / kVD, d = i % kVD;
-    const size_t head = (size_t)n * kVH + hd;
-    qf[head * kVQHead + afrag_index(tok, d, kVKs)] = src[i];
-    kf[head * kVQHead + kfrag3(tok, d)] = src[kVW + i];
-    vf[head * kVVHead + vfrag5(tok, d)] = src[2 * kVW + i];
-  }
-}
-
-// MHA over one image's 256 patches: workgroup = (image, head, quarter of the queries), wave w owns
-// query m-tile 4 quarter + w; every wave streams the head's 8 key blocks of 32 (K and V fragments
-// from L2) through the online-softmax block update with fp32 scores scaled by 72^-0.5 (no bf16
+// MHA over one image's 256 patches, straight from the fused q|k|v GEMM output [M, 3456]:
+// workgroup = (image, head, quarter of the queries).  The workgroup stages the head's K and V for
+// all 256 keys into LDS in fragment order (16-byte global loads of 8 head dims of one key); wave w
+// loads its query m-tile 4 quarter + w as B fragments straight from global memory and streams the
+// 8 key blocks of 32 through the online-softmax update: fp32 scores scaled by 72^-0.5 (no bf16
 // rounding of the scores: the reference runs SDPA's flash kernel), P rounded to bf16 for P.V.
-__global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qf, const u16* kf, const u16* vf, u16* out) {
+__global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qkv, u16* out) {
+  __shared__ __align__(16) u16 s_k[kVKFrags * 512];
+  __shared__ __align__(16) u16 s_v[kVVFrags * 512];
   const int quarter = blockIdx.x & 3, head = (blockIdx.x >> 2) % kVH, n = (blockIdx.x >> 2) / kVH;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, mt = quarter * 4 + wave;
-  const size_t hb = (size_t)n * kVH + head;
-  const u16* qb = qf + hb * kVQHead;
-  const u16* kb = kf + hb * kVQHead;
-  const u16* vb = vf + hb * kVVHead;
-  bf16x8 q[kVKs];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, mt = quarter * 4 + wave;
+  const u16* base = qkv + (size_t)n * kVS * kVQkvN + head * kVD;  // row r of the image: q | k | v at +0 | +W | +2W
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  // K: chunk c (dims 8c..8c+7) of key r is lane ((c % 4) * 16 + r % 16) of fragment (r / 16, c / 4);
+  // chunks 9..11 are the zero padding up to 96 dims
+  static_assert(kVS * 12 == 12 * 256 && kVS * 10 == 10 * 256, "one staging pass per thread and chunk slot");
+  u16x8 kv[12], vv[10];  // every global load is issued before the first LDS store
 #pragma unroll
-  for (int ds = 0; ds < kVKs; ++ds) q[ds] = load_frag(qb + afrag_offset(mt, ds, kVKs) + lane * 8);
+  for (int t = 0; t < 12; ++t) {
+    const int i = tid + t * 256, r = i / 12, c = i % 12;
+    kv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + kVW + c * 8) : zero;
+  }
+#pragma unroll
+  for (int t = 0; t < 10; ++t) {
+    const int i = tid + t * 256, r = i / 10, c = i % 10;
+    vv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + 2 * kVW + c * 8) : zero;
+  }
+#pragma unroll
+  for (int t = 0; t < 12; ++t) {
+    const int i = tid + t * 256, r = i / 12, c = i % 12;
+    *reinterpret_cast<u16x8*>(s_k + ((r >> 4) * kVKs + (c >> 2)) * 512 + ((c & 3) * 16 + (r & 15)) * 8) = kv[t];
+  }
+  // V: element (key r, dim d) at fragment (r / 32, d / 16), lane g * 16 + d % 16, slot j (vkey's
+  // inverse); chunk 9 is the zero padding up to 80 dims
+#pragma unroll
+  for (int t = 0; t < 10; ++t) {
+    const int i = tid + t * 256, r = i / 10, c = i % 10;
+    const int rr = r & 31, g = (rr & 15) >> 2, j = rr < 16 ? (rr & 3) : 4 + (rr & 3);
+    u16* dst = s_v + ((r >> 5) * kVDt + (c >> 1)) * 512 + (g * 16 + (c & 1) * 8) * 8 + j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e * 8] = vv[t][e];
+  }
+  bf16x8 q[kVKs];
+  const u16* qrow = base + (size_t)(mt * 16 + (lane & 15)) * kVQkvN;
+#pragma unroll
+  for (int ds = 0; ds < kVKs; ++ds) {
+    const int d = ds * 32 + (lane >> 4) * 8;
+    q[ds] = d < kVD ? load_frag(qrow + d) : zero_frag();
+  }
+  __syncthreads();
   const float scale = 0.11785113019775793f;  // 72 ** -0.5
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 oacc[kVDt];
@@ -143,9 +200,9 @@ __global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qf, const u
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int ds = 0; ds < kVKs; ++ds) k[t * kVKs + ds] = load_frag(kb + ((size_t)(2 * blk + t) * kVKs + ds) * 512 + lane * 8);
+      for (int ds = 0; ds < kVKs; ++ds) k[t * kVKs + ds] = load_frag(s_k + ((2 * blk + t) * kVKs + ds) * 512 + lane * 8);
 #pragma unroll
-    for (int dt = 0; dt < kVDt; ++dt) v[dt] = load_frag(vb + ((size_t)blk * kVDt + dt) * 512 + lane * 8);
+    for (int dt = 0; dt < kVDt; ++dt) v[dt] = load_frag(s_v + (blk * kVDt + dt) * 512 + lane * 8);
     f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int ds = 0; ds < kVKs; ++ds)
@@ -195,8 +252,14 @@ __global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qf, const u
 }
 
 // bf16(gelu_tanh(x)) in place (transformers' gelu_pytorch_tanh on the bf16 fc1 output)
-__global__ __launch_bounds__(256) void gelu_kernel(u16* x, size_t total) {
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) x[i] = f2bf(gelu_tanh(bf2f(x[i])));
+// (8 elements per thread over the padded rows; chunks = elements / 8)
+__global__ __launch_bounds__(256) void gelu_kernel(u16* x, size_t chunks) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (size_t)gridDim.x * 256) {
+    u16x8 v = *reinterpret_cast<const u16x8*>(x + i * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = f2bf(gelu_tanh(bf2f(v[e])));
+    *reinterpret_cast<u16x8*>(x + i * 8) = v;
+  }
 }
 
 __global__ __launch_bounds__(256) void scale_kernel(u16* x, size_t total, float s) {
@@ -213,8 +276,8 @@ struct VLayerBind {
 
 struct VisionPlan {
   int L = 0, N = 0, M = 0;
-  size_t w, par, head, h, qkv, qf, vfb, act, patches, conv, ws;
-  size_t total() const { return w + par + head + 4 * h + qkv + 2 * qf + vfb + act + patches + conv + ws + 16 * 256; }
+  size_t w, par, head, h, qkv, act, part, patches, conv, ws;
+  size_t total() const { return w + par + head + 4 * h + qkv + act + part + patches + conv + ws + 16 * 256; }
 };
 
 size_t vrup(size_t x) { return (x + 255) / 256 * 256; }
@@ -229,9 +292,8 @@ VisionPlan vplan_of(const pi05_vision_dims& d) {
   p.head = vrup(((size_t)kVW * kVPD + kVW + (size_t)kVS * kVW + 2 * kVW + kVProj) * 4 + (size_t)kVProj * kVW * 2);
   p.h = vrup(M * kVW * 2);
   p.qkv = vrup(M * kVQkvN * 2);
-  p.qf = vrup((size_t)p.N * kVH * kVQHead * 2);
-  p.vfb = vrup((size_t)p.N * kVH * kVVHead * 2);
-  p.act = vrup(M * kVI * 2);
+  p.part = vrup((size_t)kVMaxSplits * M * kVW * 4);
+  p.act = vrup(M * kVIp * 2);
   p.patches = vrup(M * kVPD * 4);
   p.conv = vrup(M * kVW * 4);
   p.ws = kVWorkspace;
@@ -259,6 +321,13 @@ bool check_vision_dims(const pi05_vision_dims* d, std::string* m) {
   return true;
 }
 
+GemmOpts split_opts(int nsplit, int ld_k) {
+  GemmOpts o;
+  o.batch = nsplit;
+  o.ld_k = ld_k;
+  return o;
+}
+
 unsigned grid_for(size_t total) {
   const size_t g = (total + 255) / 256;
   return (unsigned)(g < 8192 ? g : 8192);
@@ -278,13 +347,15 @@ struct pi05_vision_ctx {
   const void *b_post_w = nullptr, *b_post_b = nullptr, *b_proj_w = nullptr, *b_proj_b = nullptr;
   bool refreshed = false;
   char* base = nullptr;
-  u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *attn = nullptr, *qkv = nullptr, *qf = nullptr, *kf = nullptr, *vf = nullptr,
-      *act = nullptr, *proj_w = nullptr;
+  u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *attn = nullptr, *qkv = nullptr, *act = nullptr, *proj_w = nullptr;
   float *par = nullptr, *patch_w = nullptr, *patch_b = nullptr, *pos = nullptr, *post_w = nullptr, *post_b = nullptr, *proj_b = nullptr,
-        *patches = nullptr, *conv = nullptr;
+        *part = nullptr, *patches = nullptr, *conv = nullptr;
   void* ws = nullptr;
   hipblasLtHandle_t lt = nullptr;
   GemmPlan g_patch, g_qkv, g_o, g_fc1, g_fc2, g_proj;
+  // out_proj / fc2 as fp32 split-K GEMMs (4 or 8 K slices) reduced in the LayerNorm, when faster
+  GemmPlan g_osk[2], g_fc2sk[2];
+  int o_split = 0, fc2_split = 0;  // chosen slice count (0: the single bf16 GEMM with its bias)
 };
 
 namespace {
@@ -367,14 +438,12 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
   c->y = reinterpret_cast<u16*>(take(p.h));
   c->attn = reinterpret_cast<u16*>(take(p.h));
   c->qkv = reinterpret_cast<u16*>(take(p.qkv));
-  c->qf = reinterpret_cast<u16*>(take(p.qf));
-  c->kf = reinterpret_cast<u16*>(take(p.qf));
-  c->vf = reinterpret_cast<u16*>(take(p.vfb));
   c->act = reinterpret_cast<u16*>(take(p.act));
+  c->part = reinterpret_cast<float*>(take(p.part));
   c->patches = reinterpret_cast<float*>(take(p.patches));
   c->conv = reinterpret_cast<float*>(take(p.conv));
   c->ws = take(p.ws);
-  // zeroed once: the padded head dims of the attention operands stay zero, tuning reads defined data
+  // zeroed once: tuning reads defined data
   e = hipMemset(c->base, 0, p.total());
   if (e != hipSuccess) {
     hipFree(c->base);
@@ -388,17 +457,36 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
   f32.c = HIP_R_32F;
   GemmOpts bias;
   bias.bias = true;
+  GemmOpts fc1o = bias;
+  fc1o.ld_c = kVIp;
+  GemmOpts fc2o = bias;
+  fc2o.ld_k = kVIp;
+  const int splits[2] = {4, 8};
   bool ok = lt_ok(hipblasLtCreate(&c->lt)) && make_plan(c->lt, M, kVW, kVPD, kVWorkspace, &c->g_patch, &perr, f32) &&
             make_plan(c->lt, M, kVQkvN, kVW, kVWorkspace, &c->g_qkv, &perr, bias) && make_plan(c->lt, M, kVW, kVW, kVWorkspace, &c->g_o, &perr, bias) &&
-            make_plan(c->lt, M, kVI, kVW, kVWorkspace, &c->g_fc1, &perr, bias) && make_plan(c->lt, M, kVW, kVI, kVWorkspace, &c->g_fc2, &perr, bias) &&
+            make_plan(c->lt, M, kVI, kVW, kVWorkspace, &c->g_fc1, &perr, fc1o) && make_plan(c->lt, M, kVW, kVIp, kVWorkspace, &c->g_fc2, &perr, fc2o) &&
             make_plan(c->lt, M, kVProj, kVW, kVWorkspace, &c->g_proj, &perr, bias);
+  for (int i = 0; i < 2 && ok; ++i)
+    ok = make_plan(c->lt, M, kVW, kVW / splits[i], kVWorkspace, &c->g_osk[i], &perr, split_opts(splits[i], kVW)) &&
+         make_plan(c->lt, M, kVW, kVIp / splits[i], kVWorkspace, &c->g_fc2sk[i], &perr, split_opts(splits[i], kVIp));
   if (ok) {
     const float* bz = c->par;  // any fp32 vector long enough (zeros) stands in for the biases while timing
     ok = tune_plan(c->lt, &c->g_patch, c->patch_w, c->patches, c->conv, c->ws, nullptr) &&
          tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr, bz) &&
          tune_plan(c->lt, &c->g_fc1, c->w, c->n, c->act, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_fc2, c->w, c->act, c->y, c->ws, nullptr, bz) &&
          tune_plan(c->lt, &c->g_proj, c->proj_w, c->n, c->act, c->ws, nullptr, bz);
+    for (int i = 0; i < 2 && ok; ++i)
+      ok = tune_plan(c->lt, &c->g_osk[i], c->w, c->attn, c->part, c->ws, nullptr) &&
+           tune_plan(c->lt, &c->g_fc2sk[i], c->w, c->act, c->part, c->ws, nullptr);
     if (!ok && perr.empty()) perr = "GEMM algorithm tuning failed";
+    // split-K when the split GEMM plus the partials' extra traffic through the LayerNorm
+    // ((4 nsplit - 2) bytes per output element at ~4 TB/s) beats the single bf16 GEMM
+    auto extra_ms = [&](int ns) { return (float)((double)(4 * ns - 2) * M * kVW / 4e12 * 1e3); };
+    float best_o = c->g_o.ms, best_2 = c->g_fc2.ms;
+    for (int i = 0; i < 2 && ok; ++i) {
+      if (c->g_osk[i].ms + extra_ms(splits[i]) < best_o) best_o = c->g_osk[i].ms + extra_ms(splits[i]), c->o_split = splits[i];
+      if (c->g_fc2sk[i].ms + extra_ms(splits[i]) < best_2) best_2 = c->g_fc2sk[i].ms + extra_ms(splits[i]), c->fc2_split = splits[i];
+    }
   }
   if (!ok) {
     if (perr.empty()) perr = "hipblasLtCreate failed";
@@ -411,7 +499,9 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
 
 int pi05_vision_destroy(pi05_vision_ctx* c) {
   if (!c) return PI05_OK;
-  for (GemmPlan* g : {&c->g_patch, &c->g_qkv, &c->g_o, &c->g_fc1, &c->g_fc2, &c->g_proj}) free_plan(g);
+  for (GemmPlan* g : {&c->g_patch, &c->g_qkv, &c->g_o, &c->g_fc1, &c->g_fc2, &c->g_proj, &c->g_osk[0], &c->g_osk[1], &c->g_fc2sk[0],
+                      &c->g_fc2sk[1]})
+    free_plan(g);
   if (c->lt) hipblasLtDestroy(c->lt);
   if (c->base) hipFree(c->base);
   delete c;
@@ -470,7 +560,7 @@ int pi05_vision_refresh_weights(pi05_vision_ctx* c, void* stream) {
     if (e == hipSuccess) e = hipMemcpyAsync(w + kVOffQkv + (size_t)2 * kVW * kVW, b.p[4], ww, k, st);
     if (e == hipSuccess) e = hipMemcpyAsync(w + kVOffO, b.p[6], ww, k, st);
     if (e == hipSuccess) e = hipMemcpyAsync(w + kVOff1, b.p[8], (size_t)kVI * kVW * 2, k, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(w + kVOff2, b.p[10], (size_t)kVW * kVI * 2, k, st);
+    if (e == hipSuccess) e = hipMemcpy2DAsync(w + kVOff2, (size_t)kVIp * 2, b.p[10], (size_t)kVI * 2, (size_t)kVI * 2, kVW, k, st);
     to_f32(b.p[1], pr + kVPOffBqkv, kVW);
     to_f32(b.p[3], pr + kVPOffBqkv + kVW, kVW);
     to_f32(b.p[5], pr + kVPOffBqkv + 2 * kVW, kVW);
@@ -511,22 +601,36 @@ int pi05_vision_forward(pi05_vision_ctx* c, const float* pixels, void* out, void
   if ((rc = vgemm(c, c->g_patch, c->patch_w, c->patches, c->conv, nullptr, st)) != PI05_OK) return rc;
   embed_kernel<<<grid_for(M * kVW), 256, 0, st>>>(c->conv, c->patch_b, c->pos, c->h, M * kVW);
   const float* pr0 = c->par;
-  layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, nullptr, pr0 + kVPOffLn1w, pr0 + kVPOffLn1b, nullptr, c->n, eps);
+  const unsigned ln_grid = (unsigned)((M + 3) / 4);
+  const size_t pstride = M * kVW;
+  layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, nullptr, nullptr, 0, 0, nullptr, pr0 + kVPOffLn1w, pr0 + kVPOffLn1b, nullptr, c->n, eps, (int)M);
   for (int l = 0; l < p.L; ++l) {
     const u16* w = c->w + (size_t)l * kVLayerElems;
     const float* pr = c->par + (size_t)l * kVLayerParams;
     if ((rc = vgemm(c, c->g_qkv, w + kVOffQkv, c->n, c->qkv, pr + kVPOffBqkv, st)) != PI05_OK) return rc;
-    qkv_layout_kernel<<<(unsigned)M, 256, 0, st>>>(c->qkv, c->qf, c->kf, c->vf);
-    vision_attn_kernel<<<(unsigned)(p.N * kVH * 4), 256, 0, st>>>(c->qf, c->kf, c->vf, c->attn);
-    if ((rc = vgemm(c, c->g_o, w + kVOffO, c->attn, c->y, pr + kVPOffBo, st)) != PI05_OK) return rc;
-    layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, c->y, pr + kVPOffLn2w, pr + kVPOffLn2b, c->h, c->n, eps);
+    vision_attn_kernel<<<(unsigned)(p.N * kVH * 4), 256, 0, st>>>(c->qkv, c->attn);
+    if (c->o_split) {
+      if ((rc = vgemm(c, c->g_osk[c->o_split == 8], w + kVOffO, c->attn, c->part, nullptr, st)) != PI05_OK) return rc;
+      layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, nullptr, c->part, c->o_split, pstride, pr + kVPOffBo, pr + kVPOffLn2w,
+                                                pr + kVPOffLn2b, c->h, c->n, eps, (int)M);
+    } else {
+      if ((rc = vgemm(c, c->g_o, w + kVOffO, c->attn, c->y, pr + kVPOffBo, st)) != PI05_OK) return rc;
+      layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, c->y, nullptr, 0, 0, nullptr, pr + kVPOffLn2w, pr + kVPOffLn2b, c->h, c->n, eps,
+                                                (int)M);
+    }
     if ((rc = vgemm(c, c->g_fc1, w + kVOff1, c->n, c->act, pr + kVPOffB1, st)) != PI05_OK) return rc;
-    gelu_kernel<<<grid_for(M * kVI), 256, 0, st>>>(c->act, M * kVI);
-    if ((rc = vgemm(c, c->g_fc2, w + kVOff2, c->act, c->y, pr + kVPOffB2, st)) != PI05_OK) return rc;
+    gelu_kernel<<<grid_for(M * kVIp / 8), 256, 0, st>>>(c->act, M * kVIp / 8);
     const bool last = l + 1 == p.L;
     const float* nw = last ? c->post_w : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1w;
     const float* nb = last ? c->post_b : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1b;
-    layernorm_kernel<<<(unsigned)M, 192, 0, st>>>(c->h, c->y, nw, nb, c->h, c->n, eps);
+    if (c->fc2_split) {
+      if ((rc = vgemm(c, c->g_fc2sk[c->fc2_split == 8], w + kVOff2, c->act, c->part, nullptr, st)) != PI05_OK) return rc;
+      layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, nullptr, c->part, c->fc2_split, pstride, pr + kVPOffB2, nw, nb, c->h, c->n, eps,
+                                                (int)M);
+    } else {
+      if ((rc = vgemm(c, c->g_fc2, w + kVOff2, c->act, c->y, pr + kVPOffB2, st)) != PI05_OK) return rc;
+      layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, c->y, nullptr, 0, 0, nullptr, nw, nb, c->h, c->n, eps, (int)M);
+    }
   }
   if ((rc = vgemm(c, c->g_proj, c->proj_w, c->n, out, c->proj_b, st)) != PI05_OK) return rc;
   if (c->d.out_scale != 1.0f) scale_kernel<<<grid_for(M * kVProj), 256, 0, st>>>(static_cast<u16*>(out), M * kVProj, c->d.out_scale);

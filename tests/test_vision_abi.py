@@ -62,12 +62,13 @@ def test_invalid_dims_rejected_with_message(lib, field, value, msg):
 def test_device_bytes_covers_weights_and_activations(lib):
     d = _ext.vision_default_dims()
     W, I, P, S = 1152, 4304, 2048, 256
-    need = 27 * (4 * W * W + 2 * I * W) * 2  # packed bf16 q|k|v, out, fc1, fc2 (0.8 GB)
+    Ip = 4352  # the MLP dim padded for 16-byte-aligned split-K slices of fc2
+    need = 27 * (4 * W * W + I * W + W * Ip) * 2  # packed bf16 q|k|v, out, fc1, fc2 (0.8 GB)
     need += 27 * (3 * W + W + I + W + 4 * W) * 4  # fp32 biases and LayerNorm parameters
     need += (W * 588 + W + S * W + 2 * W + P) * 4 + P * W * 2  # patch/position embeddings, post-LN, projector
     M = 3 * S
-    need += M * (4 * W + 3 * W + I) * 2  # h, n, y, attention out, q|k|v, fc1 out
-    need += 3 * 16 * (2 * S * 96 + S * 80) * 2  # per-head Q and K fragments (96 dims), V (80 dims)
+    need += M * (4 * W + 3 * W + Ip) * 2  # h, n, y, attention out, q|k|v, fc1 out
+    need += 8 * M * W * 4  # fp32 split-K partials of out_proj / fc2 (up to 8 slices)
     need += M * (588 + W) * 4  # fp32 patches and patch-embedding output
     got = _ext.vision_device_bytes(d)
     assert need <= got <= need + 40 * 2**20  # + GEMM workspace
