@@ -5,6 +5,7 @@
                     [--schedule persistent|graph] [--no-cpu-baseline]
     python bench.py --workload prefill [--steps K] [--warmup W] [--no-cpu-baseline]
     python bench.py --workload vision [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --workload e2e [--steps K] [--warmup W]
 
 One bench "step" is one predict's denoise: the 10-step flow-matching Euler loop of the 18-layer
 expert over a static prefix KV cache, with weights, KV and noise already resident in HBM.  In the
@@ -15,7 +16,9 @@ N(0,1) noise (seed 2): synthetic data, no checkpoint.  Prints ONE JSON line.
 ``--workload prefill`` measures the prefix-LM prefill instead (Gemma-2B over a 968-token prefix,
 bs=1, 17 full layers + the last layer's K/V): one step is one prefill, MFMA-bound, reported
 against the bf16 dense MFMA peak.  ``--workload vision`` measures the vision tower (SigLIP
-So400m/14 + projector over 3 camera views of 224 x 224, M = 768 patches) the same way.
+So400m/14 + projector over 3 camera views of 224 x 224, M = 768 patches) the same way, and
+``--workload e2e`` a whole ``sample_actions`` from 3 camera images and a 200-token prompt (vision
+tower, token embedding, 968-token prefill, 10-step denoise) through the Python API.
 """
 
 from __future__ import annotations
@@ -43,6 +46,75 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PREFILL_METRIC = "prefix prefill ms (Gemma-2B, bs=1, 968 tokens) + % peak bf16 MFMA"
 VISION_METRIC = "vision tower ms (SigLIP So400m/14 + projector, 3 views of 224x224) + % peak bf16 MFMA"
+
+
+E2E_METRIC = "end-to-end sample_actions ms/predict (3 images 224x224 + 200 tokens -> 968-token prefix, 10 steps, bs=1)"
+
+
+def bench_e2e(args) -> int:
+    import torch
+
+    from pi05_infer import synthetic as S
+    from pi05_infer.builder import build_model
+    from pi05_infer.engine import Observation
+    from pi05_infer.prefix import PrefixGeometry, PrefixLM
+    from pi05_infer.prefix import make_weights as prefix_weights
+    from pi05_infer.vision import VisionGeometry, VisionTower
+    from pi05_infer.vision import make_weights as vision_weights
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    steps, B, views, T = 10, 1, 3, 200
+    model = build_model("random:0", "pi05_libero", num_steps=steps)
+    model.to(dev)
+    plm = PrefixLM(PrefixGeometry())
+    plm.to(dev)
+    plm.load_state_dict(prefix_weights(PrefixGeometry(), seed=1, device=dev))
+    vt = VisionTower(VisionGeometry())
+    vt.to(dev)
+    vt.load_state_dict(vision_weights(VisionGeometry(), seed=2, device=dev))
+    model.attach_prefix_lm(plm)
+    model.attach_vision_tower(vt)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    images = {f"view{i}": torch.rand(B, 3, 224, 224, generator=gen, device=dev) * 2 - 1 for i in range(views)}
+    masks = {k: torch.ones(B, dtype=torch.bool, device=dev) for k in images}
+    tokens = torch.randint(0, PrefixGeometry().vocab_size, (B, T), generator=gen, device=dev)
+    obs = Observation.from_dict({"images": images, "image_masks": masks, "tokenized_prompt": tokens,
+                                 "tokenized_prompt_mask": torch.ones(B, T, dtype=torch.bool, device=dev)})
+    x1 = S.make_noise(S.ExpertGeometry(), B).to(dev)
+    for _ in range(args.warmup):
+        model.sample_actions(obs, x1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = model.sample_actions(obs, x1)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    assert out["actions"].shape == (B, 50, 32) and bool(torch.isfinite(out["actions"]).all())
+    line = {
+        "metric": E2E_METRIC,
+        "value": round(ms, 3),
+        "unit": "ms/predict",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init expert / Gemma-2B / SigLIP weights seeds 0-2, uniform [-1, 1] images, random token "
+                "ids in [0, 257152), N(0,1) noise)",
+        "config": {"workload": f"sample_actions: SigLIP over {views} views of 224x224 + {T}-token prompt -> "
+                               f"{views * 256 + T}-token Gemma-2B prefill -> {steps}-step denoise, bs={B}",
+                   "batch": B, "prefix_len": views * 256 + T, "num_steps": steps,
+                   "timing": "host wall clock around K back-to-back predicts, synchronized at both ends"},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    model.close()
+    torch.cuda.synchronize()
+    return 0
 
 
 def vision_flops(depth: int, n_images: int) -> int:
@@ -297,7 +369,7 @@ def main() -> int:
                     help="execution schedule (default: the library's choice, persistent on MI355X)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-predicts", type=int, default=8, help="predicts in the CPU-baseline sample")
-    ap.add_argument("--workload", default="denoise", choices=["denoise", "prefill", "vision"])
+    ap.add_argument("--workload", default="denoise", choices=["denoise", "prefill", "vision", "e2e"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs the denoise loop on one GPU; runs with --gpus > 1 are not "
@@ -308,6 +380,8 @@ def main() -> int:
         return bench_prefill(args)
     if args.workload == "vision":
         return bench_vision(args)
+    if args.workload == "e2e":
+        return bench_e2e(args)
 
     import torch
 
