@@ -64,7 +64,7 @@ inline bool make_plan(hipblasLtHandle_t h, int M, int N, int K, size_t ws_max, G
   }
   if (o.batch > 1) {
     const int32_t bc = o.batch;
-    const int64_t sk = K, sc = (int64_t)N * M;
+    const int64_t sk = K, sc = (int64_t)(o.ld_c ? o.ld_c : N) * M;
     for (hipblasLtMatrixLayout_t l : {p->lw, p->la, p->lc}) {
       const int64_t st = l == p->lc ? sc : sk;
       if (!lt_ok(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc))) ||
@@ -131,9 +131,12 @@ inline hipblasStatus_t run_plan(hipblasLtHandle_t h, const GemmPlan& p, const hi
 
 // Time every candidate algorithm on real buffers (2 runs after one warm-up; values do not affect
 // the timing), re-time the 4 fastest over 15 runs each and keep the best; candidates that fail to
-// launch are skipped.
+// launch are skipped.  w_stride / w_count: see w_at below.
 inline bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const void* A, void* C, void* ws, hipStream_t st,
-                      const float* bias = nullptr) {
+                      const float* bias = nullptr, size_t w_stride = 0, int w_count = 1) {
+  // run r reads the weights at W + (r mod w_count) * w_stride: with one weight block per layer the
+  // timed runs stream weights from HBM as the layer loop does, instead of re-reading a cached block
+  auto w_at = [&](int r) { return static_cast<const void*>(static_cast<const char*>(W) + (size_t)(r % w_count) * w_stride); };
   hipEvent_t e0, e1;
   if (hipEventCreate(&e0) != hipSuccess) return false;
   if (hipEventCreate(&e1) != hipSuccess) {
@@ -141,10 +144,10 @@ inline bool tune_plan(hipblasLtHandle_t h, GemmPlan* p, const void* W, const voi
     return false;
   }
   auto time_algo = [&](const hipblasLtMatmulHeuristicResult_t& c, int reps, float* ms) {
-    bool ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, W, A, C, bias, ws, st));
+    bool ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, w_at(w_count - 1), A, C, bias, ws, st));
     if (!ok) return false;
     hipEventRecord(e0, st);
-    for (int r = 0; r < reps && ok; ++r) ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, W, A, C, bias, ws, st));
+    for (int r = 0; r < reps && ok; ++r) ok = lt_ok(run_plan(h, *p, c.algo, c.workspaceSize, w_at(r), A, C, bias, ws, st));
     hipEventRecord(e1, st);
     if (hipEventSynchronize(e1) != hipSuccess || !ok || hipEventElapsedTime(ms, e0, e1) != hipSuccess) return false;
     *ms /= (float)reps;

@@ -603,10 +603,16 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
     return fail(nullptr, PI05_E_HIP, perr);
   }
   // pick each GEMM's fastest algorithm on this device and shape
-  const bool tuned = tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr) && tune_plan(c->lt, &c->g_kv, c->w, c->n, c->qkv, c->ws, nullptr) &&
-                     tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_gu, c->w, c->n, c->gu, c->ws, nullptr) &&
-                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr) && tune_plan(c->lt, &c->g_dsk, c->w, c->act, c->dpart, c->ws, nullptr) &&
-                     tune_plan(c->lt, &c->g_osk, c->w, c->attn, c->dpart, c->ws, nullptr);
+  // (weights rotate over the layers' blocks while timing, as the layer loop streams them)
+  const size_t ls = kPLayerElems * 2;
+  const int nl = dims->depth;
+  const bool tuned = tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_kv, c->w, c->n, c->qkv, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_gu, c->w, c->n, c->gu, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_d, c->w, c->act, c->y, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_dsk, c->w, c->act, c->dpart, c->ws, nullptr, nullptr, ls, nl) &&
+                     tune_plan(c->lt, &c->g_osk, c->w, c->attn, c->dpart, c->ws, nullptr, nullptr, ls, nl);
   if (!tuned) {
     pi05_prefix_destroy(c);
     return fail(nullptr, PI05_E_HIP, "GEMM algorithm tuning failed");

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -42,7 +43,7 @@ constexpr size_t kVPOffBqkv = 0, kVPOffBo = kVQkvN, kVPOffB1 = kVPOffBo + kVW, k
                  kVPOffLn1w = kVPOffB2 + kVW, kVPOffLn1b = kVPOffLn1w + kVW, kVPOffLn2w = kVPOffLn1b + kVW,
                  kVPOffLn2b = kVPOffLn2w + kVW, kVLayerParams = kVPOffLn2b + kVW;
 constexpr size_t kVWorkspace = 32ull << 20;
-constexpr int kVMaxSplits = 8;  // split-K candidates: 4 and 8 K slices
+constexpr int kVMaxSplits = 8;  // split-K candidates: 4 and 8 K slices (out_proj, fc2); 2 and 3 (fc1)
 
 thread_local std::string g_vision_err;
 
@@ -51,6 +52,9 @@ thread_local std::string g_vision_err;
 // O^T = V^T P^T (fragment (key block, d-tile)) with the 32-key permutation vkey, so the P^T operand
 // is the S^T accumulator a lane already holds.  The padding dims are zero.
 constexpr int kVKFrags = (kVS / 16) * kVKs, kVVFrags = (kVS / 32) * kVDt;
+// V fragments in LDS carry 16 bytes of padding after each 16-lane group (a fragment = 4 groups of
+// 272 bytes), so the transposing 2-byte stores of one wave spread over 32 banks
+constexpr int kVVGroup = 136, kVVFrag = 4 * kVVGroup;  // in bf16 elements
 
 // im2col: patches[(n, p)][c*196 + ky*14 + kx] = pixels[n][c][14 py + ky][14 px + kx], p = 16 py + px
 __global__ __launch_bounds__(256) void im2col_kernel(const float* px, float* patches, int n_img) {
@@ -148,37 +152,36 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
 // rounding of the scores: the reference runs SDPA's flash kernel), P rounded to bf16 for P.V.
 __global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qkv, u16* out) {
   __shared__ __align__(16) u16 s_k[kVKFrags * 512];
-  __shared__ __align__(16) u16 s_v[kVVFrags * 512];
+  __shared__ __align__(16) u16 s_v[kVVFrags * kVVFrag];
   const int quarter = blockIdx.x & 3, head = (blockIdx.x >> 2) % kVH, n = (blockIdx.x >> 2) / kVH;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, mt = quarter * 4 + wave;
   const u16* base = qkv + (size_t)n * kVS * kVQkvN + head * kVD;  // row r of the image: q | k | v at +0 | +W | +2W
   const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  // K: chunk c (dims 8c..8c+7) of key r is lane ((c % 4) * 16 + r % 16) of fragment (r / 16, c / 4);
-  // chunks 9..11 are the zero padding up to 96 dims
-  static_assert(kVS * 12 == 12 * 256 && kVS * 10 == 10 * 256, "one staging pass per thread and chunk slot");
+  static_assert((kVS / 16) * kVKs == 4 * 12 && (kVS / 32) * 5 == 4 * 10, "staging: 12 K and 10 V passes per wave");
+  // K: pass (wave, t) fills fragment f = 12 wave + t = (key tile f / 3, d-step f % 3) whole: lane l
+  // loads dims 8 (4 (f % 3) + l / 16) .. +7 of key 16 (f / 3) + l % 16 (zero beyond dim 72) and
+  // stores them at its own 16-byte slot, so each 16-lane store group covers all banks once.
+  // V: pass (wave, t) = combo 10 wave + t = (key block combo / 5, chunk pair combo % 5): lanes 0-31
+  // load the even chunk, lanes 32-63 the odd chunk of the block's 32 keys; element (key r, dim d)
+  // goes to fragment (r / 32, d / 16), group g, lane d % 16, slot j (vkey's inverse).
   u16x8 kv[12], vv[10];  // every global load is issued before the first LDS store
 #pragma unroll
   for (int t = 0; t < 12; ++t) {
-    const int i = tid + t * 256, r = i / 12, c = i % 12;
+    const int f = wave * 12 + t, r = (f / 3) * 16 + (lane & 15), c = (f % 3) * 4 + (lane >> 4);
     kv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + kVW + c * 8) : zero;
   }
 #pragma unroll
   for (int t = 0; t < 10; ++t) {
-    const int i = tid + t * 256, r = i / 10, c = i % 10;
+    const int combo = wave * 10 + t, r = (combo / 5) * 32 + (lane & 31), c = (combo % 5) * 2 + (lane >> 5);
     vv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + 2 * kVW + c * 8) : zero;
   }
 #pragma unroll
-  for (int t = 0; t < 12; ++t) {
-    const int i = tid + t * 256, r = i / 12, c = i % 12;
-    *reinterpret_cast<u16x8*>(s_k + ((r >> 4) * kVKs + (c >> 2)) * 512 + ((c & 3) * 16 + (r & 15)) * 8) = kv[t];
-  }
-  // V: element (key r, dim d) at fragment (r / 32, d / 16), lane g * 16 + d % 16, slot j (vkey's
-  // inverse); chunk 9 is the zero padding up to 80 dims
+  for (int t = 0; t < 12; ++t) *reinterpret_cast<u16x8*>(s_k + (wave * 12 + t) * 512 + lane * 8) = kv[t];
 #pragma unroll
   for (int t = 0; t < 10; ++t) {
-    const int i = tid + t * 256, r = i / 10, c = i % 10;
-    const int rr = r & 31, g = (rr & 15) >> 2, j = rr < 16 ? (rr & 3) : 4 + (rr & 3);
-    u16* dst = s_v + ((r >> 5) * kVDt + (c >> 1)) * 512 + (g * 16 + (c & 1) * 8) * 8 + j;
+    const int combo = wave * 10 + t, r = lane & 31, c = (combo % 5) * 2 + (lane >> 5);
+    const int g = (r & 15) >> 2, j = r < 16 ? (r & 3) : 4 + (r & 3);
+    u16* dst = s_v + ((combo / 5) * kVDt + (c >> 1)) * kVVFrag + g * kVVGroup + (c & 1) * 64 + j;
 #pragma unroll
     for (int e = 0; e < 8; ++e) dst[e * 8] = vv[t][e];
   }
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qkv, u16* o
 #pragma unroll
       for (int ds = 0; ds < kVKs; ++ds) k[t * kVKs + ds] = load_frag(s_k + ((2 * blk + t) * kVKs + ds) * 512 + lane * 8);
 #pragma unroll
-    for (int dt = 0; dt < kVDt; ++dt) v[dt] = load_frag(s_v + (blk * kVDt + dt) * 512 + lane * 8);
+    for (int dt = 0; dt < kVDt; ++dt) v[dt] = load_frag(s_v + (blk * kVDt + dt) * kVVFrag + (lane >> 4) * kVVGroup + (lane & 15) * 8);
     f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int ds = 0; ds < kVKs; ++ds)
@@ -262,6 +265,30 @@ __global__ __launch_bounds__(256) void gelu_kernel(u16* x, size_t chunks) {
   }
 }
 
+// act = bf16(gelu_tanh(bf16(sum of nsplit fp32 fc1 partials + b1))): fc1 run as a split-K GEMM,
+// reduced here with its bias and the one rounding a GEMM epilogue would apply; the pad columns of
+// the 4352-wide rows are written as zeros.
+__global__ __launch_bounds__(256) void gelu_split_kernel(const float* part, int nsplit, size_t split_stride, const float* bias, u16* act,
+                                                        size_t chunks) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (size_t)gridDim.x * 256) {
+    const int col = (int)((i * 8) % kVIp);
+    u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (col < kVI) {
+      float a[8];
+      const float4 p0 = *reinterpret_cast<const float4*>(part + i * 8), p1 = *reinterpret_cast<const float4*>(part + i * 8 + 4);
+      a[0] = p0.x, a[1] = p0.y, a[2] = p0.z, a[3] = p0.w, a[4] = p1.x, a[5] = p1.y, a[6] = p1.z, a[7] = p1.w;
+      for (int sp = 1; sp < nsplit; ++sp) {
+        const float* q = part + (size_t)sp * split_stride + i * 8;
+        const float4 q0 = *reinterpret_cast<const float4*>(q), q1 = *reinterpret_cast<const float4*>(q + 4);
+        a[0] += q0.x, a[1] += q0.y, a[2] += q0.z, a[3] += q0.w, a[4] += q1.x, a[5] += q1.y, a[6] += q1.z, a[7] += q1.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = f2bf(gelu_tanh(round_bf(fadd(a[e], bias[col + e]))));
+    }
+    *reinterpret_cast<u16x8*>(act + i * 8) = v;
+  }
+}
+
 __global__ __launch_bounds__(256) void scale_kernel(u16* x, size_t total, float s) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) x[i] = f2bf(bf2f(x[i]) * s);
 }
@@ -292,7 +319,7 @@ VisionPlan vplan_of(const pi05_vision_dims& d) {
   p.head = vrup(((size_t)kVW * kVPD + kVW + (size_t)kVS * kVW + 2 * kVW + kVProj) * 4 + (size_t)kVProj * kVW * 2);
   p.h = vrup(M * kVW * 2);
   p.qkv = vrup(M * kVQkvN * 2);
-  p.part = vrup((size_t)kVMaxSplits * M * kVW * 4);
+  p.part = vrup(std::max((size_t)kVMaxSplits * M * kVW, (size_t)3 * M * kVIp) * 4);
   p.act = vrup(M * kVIp * 2);
   p.patches = vrup(M * kVPD * 4);
   p.conv = vrup(M * kVW * 4);
@@ -355,7 +382,8 @@ struct pi05_vision_ctx {
   GemmPlan g_patch, g_qkv, g_o, g_fc1, g_fc2, g_proj;
   // out_proj / fc2 as fp32 split-K GEMMs (4 or 8 K slices) reduced in the LayerNorm, when faster
   GemmPlan g_osk[2], g_fc2sk[2];
-  int o_split = 0, fc2_split = 0;  // chosen slice count (0: the single bf16 GEMM with its bias)
+  GemmPlan g_fc1sk[2];  // fc1 as 2 or 3 fp32 split-K GEMMs reduced (+ bias, GELU) in gelu_split_kernel
+  int o_split = 0, fc2_split = 0, fc1_split = 0;  // chosen slice count (0: the single bf16 GEMM with its bias)
 };
 
 namespace {
@@ -466,24 +494,38 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
             make_plan(c->lt, M, kVQkvN, kVW, kVWorkspace, &c->g_qkv, &perr, bias) && make_plan(c->lt, M, kVW, kVW, kVWorkspace, &c->g_o, &perr, bias) &&
             make_plan(c->lt, M, kVI, kVW, kVWorkspace, &c->g_fc1, &perr, fc1o) && make_plan(c->lt, M, kVW, kVIp, kVWorkspace, &c->g_fc2, &perr, fc2o) &&
             make_plan(c->lt, M, kVProj, kVW, kVWorkspace, &c->g_proj, &perr, bias);
-  for (int i = 0; i < 2 && ok; ++i)
+  const int fc1_splits[2] = {2, 3};
+  for (int i = 0; i < 2 && ok; ++i) {
+    GemmOpts f1 = split_opts(fc1_splits[i], kVW);
+    f1.ld_c = kVIp;
     ok = make_plan(c->lt, M, kVW, kVW / splits[i], kVWorkspace, &c->g_osk[i], &perr, split_opts(splits[i], kVW)) &&
-         make_plan(c->lt, M, kVW, kVIp / splits[i], kVWorkspace, &c->g_fc2sk[i], &perr, split_opts(splits[i], kVIp));
+         make_plan(c->lt, M, kVW, kVIp / splits[i], kVWorkspace, &c->g_fc2sk[i], &perr, split_opts(splits[i], kVIp)) &&
+         make_plan(c->lt, M, kVI, kVW / fc1_splits[i], kVWorkspace, &c->g_fc1sk[i], &perr, f1);
+  }
   if (ok) {
     const float* bz = c->par;  // any fp32 vector long enough (zeros) stands in for the biases while timing
+    // (weights rotate over the layers' blocks while timing, as the layer loop streams them)
+    const size_t ls = kVLayerElems * 2;
+    const int nl = p.L;
     ok = tune_plan(c->lt, &c->g_patch, c->patch_w, c->patches, c->conv, c->ws, nullptr) &&
-         tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr, bz) &&
-         tune_plan(c->lt, &c->g_fc1, c->w, c->n, c->act, c->ws, nullptr, bz) && tune_plan(c->lt, &c->g_fc2, c->w, c->act, c->y, c->ws, nullptr, bz) &&
+         tune_plan(c->lt, &c->g_qkv, c->w, c->n, c->qkv, c->ws, nullptr, bz, ls, nl) &&
+         tune_plan(c->lt, &c->g_o, c->w, c->attn, c->y, c->ws, nullptr, bz, ls, nl) &&
+         tune_plan(c->lt, &c->g_fc1, c->w, c->n, c->act, c->ws, nullptr, bz, ls, nl) &&
+         tune_plan(c->lt, &c->g_fc2, c->w, c->act, c->y, c->ws, nullptr, bz, ls, nl) &&
          tune_plan(c->lt, &c->g_proj, c->proj_w, c->n, c->act, c->ws, nullptr, bz);
     for (int i = 0; i < 2 && ok; ++i)
-      ok = tune_plan(c->lt, &c->g_osk[i], c->w, c->attn, c->part, c->ws, nullptr) &&
-           tune_plan(c->lt, &c->g_fc2sk[i], c->w, c->act, c->part, c->ws, nullptr);
+      ok = tune_plan(c->lt, &c->g_osk[i], c->w, c->attn, c->part, c->ws, nullptr, nullptr, ls, nl) &&
+           tune_plan(c->lt, &c->g_fc2sk[i], c->w, c->act, c->part, c->ws, nullptr, nullptr, ls, nl) &&
+           tune_plan(c->lt, &c->g_fc1sk[i], c->w, c->n, c->part, c->ws, nullptr, nullptr, ls, nl);
     if (!ok && perr.empty()) perr = "GEMM algorithm tuning failed";
     // split-K when the split GEMM plus the partials' extra traffic through the LayerNorm
     // ((4 nsplit - 2) bytes per output element at ~4 TB/s) beats the single bf16 GEMM
     auto extra_ms = [&](int ns) { return (float)((double)(4 * ns - 2) * M * kVW / 4e12 * 1e3); };
-    float best_o = c->g_o.ms, best_2 = c->g_fc2.ms;
+    float best_o = c->g_o.ms, best_2 = c->g_fc2.ms, best_1 = c->g_fc1.ms;
     for (int i = 0; i < 2 && ok; ++i) {
+      // fc1: the partials replace the bf16 output that the GELU reads anyway
+      const float x1 = (float)((double)(4 * fc1_splits[i] - 2) * M * kVIp / 4e12 * 1e3);
+      if (c->g_fc1sk[i].ms + x1 < best_1) best_1 = c->g_fc1sk[i].ms + x1, c->fc1_split = fc1_splits[i];
       if (c->g_osk[i].ms + extra_ms(splits[i]) < best_o) best_o = c->g_osk[i].ms + extra_ms(splits[i]), c->o_split = splits[i];
       if (c->g_fc2sk[i].ms + extra_ms(splits[i]) < best_2) best_2 = c->g_fc2sk[i].ms + extra_ms(splits[i]), c->fc2_split = splits[i];
     }
@@ -500,7 +542,7 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
 int pi05_vision_destroy(pi05_vision_ctx* c) {
   if (!c) return PI05_OK;
   for (GemmPlan* g : {&c->g_patch, &c->g_qkv, &c->g_o, &c->g_fc1, &c->g_fc2, &c->g_proj, &c->g_osk[0], &c->g_osk[1], &c->g_fc2sk[0],
-                      &c->g_fc2sk[1]})
+                      &c->g_fc2sk[1], &c->g_fc1sk[0], &c->g_fc1sk[1]})
     free_plan(g);
   if (c->lt) hipblasLtDestroy(c->lt);
   if (c->base) hipFree(c->base);
@@ -618,8 +660,13 @@ int pi05_vision_forward(pi05_vision_ctx* c, const float* pixels, void* out, void
       layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, c->y, nullptr, 0, 0, nullptr, pr + kVPOffLn2w, pr + kVPOffLn2b, c->h, c->n, eps,
                                                 (int)M);
     }
-    if ((rc = vgemm(c, c->g_fc1, w + kVOff1, c->n, c->act, pr + kVPOffB1, st)) != PI05_OK) return rc;
-    gelu_kernel<<<grid_for(M * kVIp / 8), 256, 0, st>>>(c->act, M * kVIp / 8);
+    if (c->fc1_split) {
+      if ((rc = vgemm(c, c->g_fc1sk[c->fc1_split == 3], w + kVOff1, c->n, c->part, nullptr, st)) != PI05_OK) return rc;
+      gelu_split_kernel<<<grid_for(M * kVIp / 8), 256, 0, st>>>(c->part, c->fc1_split, M * kVIp, pr + kVPOffB1, c->act, M * kVIp / 8);
+    } else {
+      if ((rc = vgemm(c, c->g_fc1, w + kVOff1, c->n, c->act, pr + kVPOffB1, st)) != PI05_OK) return rc;
+      gelu_kernel<<<grid_for(M * kVIp / 8), 256, 0, st>>>(c->act, M * kVIp / 8);
+    }
     const bool last = l + 1 == p.L;
     const float* nw = last ? c->post_w : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1w;
     const float* nb = last ? c->post_b : c->par + (size_t)(l + 1) * kVLayerParams + kVPOffLn1b;

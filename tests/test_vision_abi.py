@@ -68,7 +68,7 @@ def test_device_bytes_covers_weights_and_activations(lib):
     need += (W * 588 + W + S * W + 2 * W + P) * 4 + P * W * 2  # patch/position embeddings, post-LN, projector
     M = 3 * S
     need += M * (4 * W + 3 * W + Ip) * 2  # h, n, y, attention out, q|k|v, fc1 out
-    need += 8 * M * W * 4  # fp32 split-K partials of out_proj / fc2 (up to 8 slices)
+    need += max(8 * M * W, 3 * M * Ip) * 4  # fp32 split-K partials: out_proj / fc2 (up to 8 slices), fc1 (up to 3)
     need += M * (588 + W) * 4  # fp32 patches and patch-embedding output
     got = _ext.vision_device_bytes(d)
     assert need <= got <= need + 40 * 2**20  # + GEMM workspace
