@@ -90,6 +90,69 @@ def bench_e2e(args) -> int:
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     assert out["actions"].shape == (B, 50, 32) and bool(torch.isfinite(out["actions"]).all())
+
+    # the same predict phase by phase (each phase timed alone, same clock, same inputs)
+    imgs, img_masks = list(images.values()), list(masks.values())
+
+    def timed(fn, reps=args.steps):
+        fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(reps):
+            r = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) * 1e3 / reps, r
+
+    vis_ms, _ = timed(lambda: vt.embed_image(torch.cat(imgs, dim=0)))
+    emb_ms, (embs, pads, _) = timed(lambda: model.embed_prefix(imgs, img_masks, tokens, obs.tokenized_prompt_mask))
+    pre_ms, (_, _, kv) = timed(lambda: plm.build_prefix_cache(embs, pads))
+    kv_obs = Observation([k for k, _ in kv], [v for _, v in kv], pads)
+    den_ms, _ = timed(lambda: model.sample_actions(kv_obs, x1))
+    phases = {"vision_ms": round(vis_ms, 3), "embed_prefix_ms (vision + token embedding + concat)": round(emb_ms, 3),
+              "prefill_ms": round(pre_ms, 3), "denoise_ms (prime + 10 steps)": round(den_ms, 3)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import denoise_oracle as O
+        from oracle import prefix_oracle as PO
+        from oracle import siglip_oracle as SO
+        from pi05_infer.prefix import layer_param_names as pnames
+        from pi05_infer.vision import HEAD_KEYS, HEAD_PARAM_NAMES, LAYER_KEYS
+        from pi05_infer.vision import layer_param_names as vnames
+
+        threads = max(1, min(16, os.cpu_count() or 1))
+        torch.set_num_threads(threads)
+        # one SigLIP layer, one Gemma-2B layer and one expert predict of the fp32 oracle, scaled
+        okeys = dict(zip(LAYER_KEYS, ("wq", "bq", "wk", "bk", "wv", "bv", "wout", "bout", "w1", "b1", "w2", "b2", "ln1w",
+                                      "ln1b", "ln2w", "ln2b")))
+        v0 = {okeys[k]: vt.params[vnames(0)[k]].float().cpu() for k in LAYER_KEYS}
+        vh = {k: vt.params[HEAD_PARAM_NAMES[k]].float().cpu() for k in HEAD_KEYS}
+        t = time.perf_counter()
+        h = SO.embeddings(torch.cat(imgs).cpu(), vh, SO.SiglipGeometry())
+        SO.encoder_layer(v0, SO.SiglipGeometry(), h)
+        v_layer = time.perf_counter() - t
+        p0 = {k: plm.params[pnames(0)[k]].float().cpu() for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "ln1", "ln2")}
+        g = PO.PrefixGeometry()
+        pos, mask4d = PO.prefix_masks(pads.cpu())
+        cos, sin = O.rope_cos_sin(pos, g.head_dim, g.rope_theta)
+        t = time.perf_counter()
+        PO.prefix_layer(p0, g, embs.float().cpu(), cos, sin, mask4d)
+        p_layer = time.perf_counter() - t
+        w = {n: t_.cpu() for n, t_ in model.params.items()}
+        og = O.geometry_from(S.ExpertGeometry())
+        k_ref = torch.cat([k.cpu() for k, _ in kv], dim=1)
+        v_ref = torch.cat([v.cpu() for _, v in kv], dim=1)
+        t = time.perf_counter()
+        O.sample_actions(w, og, k_ref, v_ref, pads.cpu(), x1.cpu(), steps, O.adarms_table(w, og, steps))
+        d_pred = time.perf_counter() - t
+        cpu = {
+            "value": round((v_layer * 27 + p_layer * 18 + d_pred) * 1e3, 1),
+            "unit": "ms/predict",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": "one SigLIP layer (x27) + one Gemma-2B layer (x18) + one full expert predict of the fp32 CPU "
+                      f"oracle on the same inputs; host {cpu_model()}",
+        }
     line = {
         "metric": E2E_METRIC,
         "value": round(ms, 3),
@@ -108,8 +171,9 @@ def bench_e2e(args) -> int:
                                f"{views * 256 + T}-token Gemma-2B prefill -> {steps}-step denoise, bs={B}",
                    "batch": B, "prefix_len": views * 256 + T, "num_steps": steps,
                    "timing": "host wall clock around K back-to-back predicts, synchronized at both ends"},
+        "phases": phases,
         "roofline": None,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     model.close()
