@@ -203,3 +203,61 @@ def test_images_and_prompt_to_actions_matches_oracle_chain(weights2):
     torch.cuda.synchronize()
     _close(act_ref, act, "images+prompt -> actions")
     model.close()
+
+
+def test_embed_prefix_batch_of_two_matches_each_sample_alone(weights2):
+    """Batched SigLIP over all views (the reference's stacking, pi0_pytorch.py:200-213): at B=2 with
+    2 views the four images go through one vision call; each sample's prefix equals the oracle's and,
+    up to GEMM summation order, its own B=1 prefix (views do not mix across samples)."""
+    print("case embed_prefix: vision depth 2, B=2, 2 views + 8 tokens", flush=True)
+    from oracle import denoise_oracle as O
+    from oracle import prefix_oracle as PO
+    from pi05_infer import synthetic as S
+    from pi05_infer.engine import OpenPi0InferConfig, OpenPi0Inference
+    from pi05_infer.prefix import EMBED_NAME, PrefixGeometry, PrefixLM
+    from pi05_infer.prefix import layer_param_names as prefix_names
+    from pi05_infer.vision import HEAD_PARAM_NAMES, VisionGeometry, VisionTower
+    from pi05_infer.vision import layer_param_names as vision_names
+
+    from dataclasses import replace
+
+    layers_v, heads_v = weights2
+    B, T, vocab = 2, 8, 500
+    views = [_pixels(B, 20), _pixels(B, 21)]
+    masks = [torch.tensor([True, True]), torch.tensor([True, False])]
+    g = torch.Generator().manual_seed(22)
+    tokens = torch.randint(0, vocab, (B, T), generator=g)
+    lang_mask = torch.ones(B, T, dtype=torch.bool)
+    lang_mask[1, 5:] = False
+    table = O._bf(torch.randn(vocab, 2048, generator=g))
+    vt = VisionTower(VisionGeometry(depth=2))
+    rename = {"wout": "wo", "bout": "bo", "ln1w": "ln1_w", "ln1b": "ln1_b", "ln2w": "ln2_w", "ln2b": "ln2_b"}
+    sd = {vision_names(i)[rename.get(k, k)]: t for i, lw in enumerate(layers_v) for k, t in lw.items()}
+    sd.update({HEAD_PARAM_NAMES[k]: t for k, t in heads_v.items()})
+    vt.load_state_dict(sd, strict=True)
+    pg = PrefixGeometry(depth=3, vocab_size=vocab)
+    plm = PrefixLM(pg)
+    layers_p = PO.random_layers(PO.PrefixGeometry(), 3, seed=23)
+    psd = {prefix_names(i)[k]: lw[k] for i, lw in enumerate(layers_p) for k in lw}
+    psd[EMBED_NAME] = table
+    plm.load_state_dict(psd, strict=True)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=2), replace(S.ExpertGeometry(), depth=3))
+    model.load_state_dict(S.make_weights(replace(S.ExpertGeometry(), depth=3)))
+    model.to("cuda")
+    model.attach_prefix_lm(plm)
+    model.attach_vision_tower(vt)
+    embs, pads, _ = model.embed_prefix([v.cuda() for v in views], [m.cuda() for m in masks], tokens.cuda(), lang_mask.cuda())
+    torch.cuda.synchronize()
+    assert embs.shape == (B, 512 + T, 2048)
+    feats = SO.image_features(torch.cat(views), layers_v, heads_v, G)  # view-major: [v0 s0, v0 s1, v1 s0, v1 s1]
+    for b in range(B):
+        ref_pad = torch.cat([masks[0][b].expand(256), masks[1][b].expand(256), lang_mask[b]])
+        assert torch.equal(pads[b].cpu(), ref_pad)
+        assert torch.equal(embs[b, 512:].float().cpu(), PO.embed_tokens(tokens[b], table, 2048))
+        _close(feats[b], embs[b, :256].float(), f"B=2 sample {b} view 0")
+        _close(feats[B + b], embs[b, 256:512].float(), f"B=2 sample {b} view 1")
+        one, _, _ = model.embed_prefix([v[b:b + 1].cuda() for v in views], [m[b:b + 1].cuda() for m in masks],
+                                       tokens[b:b + 1].cuda(), lang_mask[b:b + 1].cuda())
+        torch.cuda.synchronize()
+        _close(one[0, :512].float(), embs[b, :512].float(), f"B=2 sample {b} vs alone")
+    model.close()
