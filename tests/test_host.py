@@ -99,6 +99,41 @@ def test_observation_from_dynamic_cache_dict():
     assert len(obs.prefix_k) == SMALL.depth and torch.equal(obs.prefix_v[1], v[:, 1:2])
 
 
+def test_observation_from_preprocessed_images_dict():
+    """openpi's preprocessed observation: per-view images and masks keep their order."""
+    imgs = {"base_0_rgb": torch.zeros(1, 3, 224, 224), "left_wrist_0_rgb": torch.ones(1, 3, 224, 224)}
+    masks = {"base_0_rgb": torch.tensor([True]), "left_wrist_0_rgb": torch.tensor([False])}
+    obs = Observation.from_dict({"images": imgs, "image_masks": masks, "tokenized_prompt": torch.zeros(1, 4, dtype=torch.long),
+                                 "tokenized_prompt_mask": torch.ones(1, 4, dtype=torch.bool)})
+    assert obs.prefix_k is None and obs.prefix_embs is None and obs.prefix_pad_masks is None
+    assert [float(t.mean()) for t in obs.images] == [0.0, 1.0]
+    assert [bool(m[0]) for m in obs.image_masks] == [True, False]
+
+
+def test_embed_prefix_needs_vision_tower_and_prefix_lm():
+    m = build_model("random", "pi05_libero", geometry=SMALL)
+    with pytest.raises(ValueError, match="VisionTower and PrefixLM"):
+        m.embed_prefix([torch.zeros(1, 3, 224, 224)], [torch.tensor([True])], torch.zeros(1, 4, dtype=torch.long),
+                       torch.ones(1, 4, dtype=torch.bool))
+
+
+def test_vision_tower_weights_and_device_checks():
+    from pi05_infer.vision import VisionGeometry, VisionTower, parameter_specs
+
+    g = VisionGeometry(depth=2)
+    specs = parameter_specs(g)
+    assert len(specs) == 2 * 16 + 7
+    fp32 = [n for n, _, dt in specs if dt == torch.float32]
+    assert all("embeddings" in n for n in fp32) and len(fp32) == 3  # patch weight/bias, position embedding
+    vt = VisionTower(g)
+    missing, _ = vt.load_state_dict({})
+    assert len(missing) == len(specs)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        vt.embed_image(torch.zeros(1, 3, 224, 224))
+    with pytest.raises(ValueError, match="image must be"):
+        vt.embed_image(torch.zeros(1, 3, 112, 112))
+
+
 def test_compat_shims():
     m = build_model("random", "pi05_libero", geometry=SMALL)
     assert not m.is_cuda_graph_enabled()
