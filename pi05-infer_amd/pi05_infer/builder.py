@@ -5,8 +5,10 @@
 a checkpoint directory (``*.safetensors``, or ``model_state_dict/full_weights.pt`` /
 ``actor/model_state_dict/full_weights.pt`` loaded with ``weights_only=True``), or
 ``"random"`` / ``"random:<seed>"`` / ``None`` for the seeded random-init expert used by the
-benchmark (there is no checkpoint download here).  Only the action-expert, time-MLP and action
-projection tensors are read; the prefix towers are not part of this engine.
+benchmark (there is no checkpoint download here).  A checkpoint that also holds PaliGemma's
+language model and vision tower gets them as an attached ``PrefixLM`` and ``VisionTower``, so
+``sample_actions`` runs from camera images and a tokenized prompt, as the reference's model does;
+``prefix_towers=True`` forces that (random-init towers for ``"random"``), ``False`` skips it.
 """
 
 from __future__ import annotations
@@ -56,9 +58,13 @@ def build_model(
     *,
     data_kwargs: Optional[dict] = None,
     geometry: ExpertGeometry = ExpertGeometry(),
+    prefix_towers: Optional[bool] = None,
+    prefix_geometry=None,
+    vision_geometry=None,
     **config_overrides: Any,
 ) -> OpenPi0Inference:
-    """Construct a ready-to-run inference engine (builder.py:34-138)."""
+    """Construct a ready-to-run inference engine (builder.py:34-138).  ``prefix_geometry`` /
+    ``vision_geometry`` default to Gemma-2B and SigLIP So400m/14."""
     if config_name in _PI0_CONFIGS:
         raise NotImplementedError(f"{config_name} is a pi0 config; this engine implements pi0.5 only")
     if config_name not in _PI05_CONFIGS:
@@ -74,6 +80,24 @@ def build_model(
     missing, _ = model.load_state_dict(state, strict=False)
     if missing:
         raise KeyError(f"checkpoint lacks {len(missing)} expert tensors, e.g. {missing[:3]}")
+    from . import prefix, vision
+
+    if prefix_towers is None:
+        prefix_towers = seed is None and any(k.startswith(prefix.PREFIX) for k in state)
+    if prefix_towers:
+        pg = prefix_geometry or prefix.PrefixGeometry(depth=geometry.depth)
+        vg = vision_geometry or vision.VisionGeometry()
+        plm, vt = prefix.PrefixLM(pg), vision.VisionTower(vg)
+        if seed is not None:
+            tower_state = {**prefix.make_weights(pg, seed=seed + 1, device="cpu"), **vision.make_weights(vg, seed=seed + 2, device="cpu")}
+        else:
+            tower_state = state
+        for name, module in (("prefix LM", plm), ("vision tower", vt)):
+            tmissing, _ = module.load_state_dict(tower_state, strict=False)
+            if tmissing:
+                raise KeyError(f"checkpoint lacks {len(tmissing)} {name} tensors, e.g. {tmissing[:3]}")
+        model.attach_prefix_lm(plm)
+        model.attach_vision_tower(vt)
     return model
 
 

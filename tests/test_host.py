@@ -134,6 +134,28 @@ def test_vision_tower_weights_and_device_checks():
         vt.embed_image(torch.zeros(1, 3, 112, 112))
 
 
+def test_build_model_attaches_prefix_towers_from_a_full_checkpoint(tmp_path):
+    """A checkpoint with the language model and vision tower comes back with both attached (tiny
+    tower geometries; the C ABIs check geometry only when a GPU context is made)."""
+    import safetensors.torch
+
+    from pi05_infer import prefix, vision
+
+    pg = prefix.PrefixGeometry(width=32, depth=SMALL.depth, num_heads=2, head_dim=16, mlp_dim=64, vocab_size=50)
+    vg = vision.VisionGeometry(width=32, depth=1, num_heads=2, mlp_dim=48, image=28, proj_dim=32)
+    sd = {**S.make_weights(SMALL, seed=3), **prefix.make_weights(pg, seed=4, device="cpu"), **vision.make_weights(vg, seed=5, device="cpu")}
+    safetensors.torch.save_file({k: v.contiguous() for k, v in sd.items()}, str(tmp_path / "model.safetensors"))
+    m = build_model(str(tmp_path), "pi05_libero", geometry=SMALL, prefix_geometry=pg, vision_geometry=vg)
+    assert m.prefix_lm is not None and m.vision_tower is not None
+    name = prefix.layer_param_names(1)["wq"]
+    assert torch.equal(m.prefix_lm.params[name], sd[name].to(torch.bfloat16))
+    pw = vision.HEAD_PARAM_NAMES["patch_w"]
+    assert m.vision_tower.params[pw].dtype == torch.float32 and torch.equal(m.vision_tower.params[pw], sd[pw])
+    expert_only = build_model(str(tmp_path), "pi05_libero", geometry=SMALL, prefix_towers=False)
+    assert expert_only.prefix_lm is None and expert_only.vision_tower is None
+    assert build_model("random", "pi05_libero", geometry=SMALL).prefix_lm is None
+
+
 def test_compat_shims():
     m = build_model("random", "pi05_libero", geometry=SMALL)
     assert not m.is_cuda_graph_enabled()
