@@ -202,10 +202,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
 // ---------------------------------------------------------------------------------------------
 // Masked MQA attention over the prefix (modeling_gemma.py:219-275): 8 query heads share the one
 // K/V head, so a 16-row m-tile holds 2 tokens x 8 heads against the same keys.  Workgroup = 8
-// m-tiles of one sample, wave w owns m-tiles 2w, 2w+1 (query fragments in registers).  Key blocks
-// of 32 (16 KiB of K + 16 KiB of V fragments) are staged into LDS with direct-to-LDS loads, double
-// buffered, and every wave runs the online-softmax block update of the denoise attention
-// (attend_block) on both of its m-tiles.  Masked keys are skipped; a query row with no valid key
+// m-tiles of one sample in 8 waves, wave w owns m-tile w (query fragments in registers; one m-tile
+// per wave keeps a wave under 256 registers, so two waves share each SIMD and one wave's softmax
+// overlaps the other's MFMAs).  Key blocks of 32 (16 KiB of K + 16 KiB of V fragments) are staged
+// into LDS with direct-to-LDS loads, double buffered, and every wave runs the online-softmax block
+// update of the denoise attention (attend_block) on its m-tile.  Masked keys are skipped; a query row with no valid key
 // (a padded token) is written as zeros.  With nsplit > 1 the key blocks are split over nsplit
 // workgroups per m-tile group (so that short prefixes still fill the GPU), which store their
 // unnormalised fp32 O and running (max, sum) per row for attn_merge_kernel.
@@ -219,40 +220,35 @@ struct AttnArgs {
   int B, P, s_pad, n_mt, items, nsplit;
 };
 
-__global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) u16 s_kv[2][32][512];
   const int split = blockIdx.x % a.nsplit, bi = blockIdx.x / a.nsplit;
   const int b = bi / a.items, item = bi % a.items;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
   const int wu = __builtin_amdgcn_readfirstlane(wave);
-  const int mt0 = item * kAttnMtPerWg + 2 * wave;
+  const int mt = item * kAttnMtPerWg + wave;
   const u16* qb = a.qf + (size_t)b * a.s_pad * kHeads * kHeadDim;
   const u16* kb0 = a.kf + (size_t)b * a.s_pad * kHeadDim;
   const u16* vb0 = a.vf + (size_t)b * a.s_pad * kHeadDim;
   const uint8_t* valid = a.valid + (size_t)b * a.s_pad;
   const int nkb = a.s_pad / 32, kb_lo = split * nkb / a.nsplit, kb_hi = (split + 1) * nkb / a.nsplit;
-  bf16x8 qf[2][8];
+  bf16x8 qf[8];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-      qf[m][ds] = mt0 + m < a.n_mt ? load_frag(qb + afrag_offset(mt0 + m, ds, kHeadDim / 32) + lane * 8) : zero_frag();
-  // wave w copies fragments 8w .. 8w+7 of a block (K fragments 0..15, then V fragments)
+  for (int ds = 0; ds < 8; ++ds) qf[ds] = mt < a.n_mt ? load_frag(qb + afrag_offset(mt, ds, kHeadDim / 32) + lane * 8) : zero_frag();
+  // wave w copies fragments 4w .. 4w+3 of a block (K fragments 0..15, then V fragments)
   auto stage = [&](int kb, int buf) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = wu * 8 + i;
+    for (int i = 0; i < 4; ++i) {
+      const int f = wu * 4 + i;
       const u16* src = f < 16 ? kb0 + ((size_t)2 * kb * 8 + f) * 512 : vb0 + ((size_t)kb * 16 + (f - 16)) * 512;
       __builtin_amdgcn_global_load_lds(const_cast<u16*>(src) + lane * 8, &s_kv[buf][f][0], 16, 0, 0);
     }
   };
   stage(kb_lo, kb_lo & 1);
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-  f32x4 oacc[2][16];
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 oacc[16];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int d = 0; d < 16; ++d) oacc[m][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int kb = kb_lo; kb < kb_hi; ++kb) {
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of block kb have landed
     __syncthreads();  // every wave's copies of block kb have landed; buffer (kb+1)&1 is no longer read
@@ -266,38 +262,32 @@ __global__ __launch_bounds__(256, 1) void prefix_attn_kernel(AttnArgs a) {
     }
     blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
     blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-      if (mt0 + m < a.n_mt) attend_block(blk, qf[m], m_run[m], l_run[m], oacc[m]);
+    if (mt < a.n_mt) attend_block(blk, qf, m_run, l_run, oacc);
   }
   // O = acc / l: lane (row r16 = token 2 mt + r16/8, head r16 % 8) holds dims 16 dt + 4 g .. +3
+  if (mt >= a.n_mt) return;  // after the last barrier
+  float l = l_run;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  const int r16 = lane & 15, token = 2 * mt + (r16 >> 3), head = r16 & 7;
+  if (token >= a.P) return;
+  if (a.nsplit > 1) {
+    const size_t row = ((size_t)split * a.B + b) * ((size_t)a.n_mt * 16) + (size_t)mt * 16 + r16;
+    float* prow = a.po + row * kHeadDim + g * 4;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int mt = mt0 + m;
-    if (mt >= a.n_mt) continue;
-    float l = l_run[m];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const int r16 = lane & 15, token = 2 * mt + (r16 >> 3), head = r16 & 7;
-    if (token >= a.P) continue;
-    if (a.nsplit > 1) {
-      const size_t row = ((size_t)split * a.B + b) * ((size_t)a.n_mt * 16) + (size_t)mt * 16 + r16;
-      float* prow = a.po + row * kHeadDim + g * 4;
-#pragma unroll
-      for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(prow + dt * 16) = oacc[m][dt];
-      if (g == 0) {
-        a.pml[row * 2] = m_run[m];
-        a.pml[row * 2 + 1] = l;
-      }
-      continue;
+    for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(prow + dt * 16) = oacc[dt];
+    if (g == 0) {
+      a.pml[row * 2] = m_run;
+      a.pml[row * 2 + 1] = l;
     }
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    u16* orow = a.out + ((size_t)b * a.P + token) * kPHD + head * kHeadDim + g * 4;
+    return;
+  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  u16* orow = a.out + ((size_t)b * a.P + token) * kPHD + head * kHeadDim + g * 4;
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const f32x4 o = oacc[m][dt];
-      *reinterpret_cast<u16x4*>(orow + dt * 16) = u16x4{f2bf(o[0] * inv), f2bf(o[1] * inv), f2bf(o[2] * inv), f2bf(o[3] * inv)};
-    }
+  for (int dt = 0; dt < 16; ++dt) {
+    const f32x4 o = oacc[dt];
+    *reinterpret_cast<u16x4*>(orow + dt * 16) = u16x4{f2bf(o[0] * inv), f2bf(o[1] * inv), f2bf(o[2] * inv), f2bf(o[3] * inv)};
   }
 }
 
@@ -731,7 +721,7 @@ int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* p
     rope_kv_kernel<<<p.M, 256, 0, st>>>(ra);
     if (kv_only) break;
     AttnArgs aa{c->qf, c->kf, c->vf, c->valid, c->attn, c->po, c->pml, p.B, p.P, p.s_pad, p.n_mt, p.items, p.nsplit};
-    prefix_attn_kernel<<<p.B * p.items * p.nsplit, 256, 0, st>>>(aa);
+    prefix_attn_kernel<<<p.B * p.items * p.nsplit, 512, 0, st>>>(aa);
     if (p.nsplit > 1) attn_merge_kernel<<<p.M, 256, 0, st>>>(c->po, c->pml, c->attn, p.B, p.P, p.n_mt, p.nsplit);
     if (c->o_split) {
       if ((rc = gemm(c, c->g_osk, w + kPOffO, c->attn, c->dpart, st)) != PI05_OK) return rc;
