@@ -220,8 +220,11 @@ struct AttnArgs {
   int B, P, s_pad, n_mt, items, nsplit;
 };
 
+constexpr int kAttnMaxBlocks = 65536 / 32;  // key blocks of the longest prefix (batch * prefix_len <= 65536)
+
 __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) u16 s_kv[2][32][512];
+  __shared__ uint32_t s_bits[kAttnMaxBlocks];  // bit j of word i: key 32 (kb_lo + i) + j is valid
   const int split = blockIdx.x % a.nsplit, bi = blockIdx.x / a.nsplit;
   const int b = bi / a.items, item = bi % a.items;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4;
@@ -232,6 +235,18 @@ __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
   const u16* vb0 = a.vf + (size_t)b * a.s_pad * kHeadDim;
   const uint8_t* valid = a.valid + (size_t)b * a.s_pad;
   const int nkb = a.s_pad / 32, kb_lo = split * nkb / a.nsplit, kb_hi = (split + 1) * nkb / a.nsplit;
+  // the key-valid bytes of the workgroup's key range as one bit-mask word per block, so the block
+  // loop issues no vector loads besides the staging copies (a wait for a mask load would also wait
+  // for the next block's copies)
+  for (int i = tid; i < kb_hi - kb_lo; i += 512) {
+    const uint4 v0 = *reinterpret_cast<const uint4*>(valid + (size_t)(kb_lo + i) * 32);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(valid + (size_t)(kb_lo + i) * 32 + 16);
+    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t bits = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) bits |= (((w[j >> 2] >> (8 * (j & 3))) & 0xff) ? 1u : 0u) << j;
+    s_bits[i] = bits;
+  }
   bf16x8 qf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) qf[ds] = mt < a.n_mt ? load_frag(qb + afrag_offset(mt, ds, kHeadDim / 32) + lane * 8) : zero_frag();
@@ -260,8 +275,11 @@ __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
       blk.k[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][i][lane * 8]);
       blk.v[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][16 + i][lane * 8]);
     }
-    blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
-    blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
+    // attend_block's key-valid bytes: keys 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3
+    const uint32_t bits = s_bits[kb - kb_lo];
+    const uint32_t lo = (bits >> (4 * g)) & 15u, hi = (bits >> (16 + 4 * g)) & 15u;
+    blk.valid0 = (lo & 1u) | ((lo & 2u) << 7) | ((lo & 4u) << 14) | ((lo & 8u) << 21);
+    blk.valid1 = (hi & 1u) | ((hi & 2u) << 7) | ((hi & 4u) << 14) | ((hi & 8u) << 21);
     if (mt < a.n_mt) attend_block(blk, qf, m_run, l_run, oacc);
   }
   // O = acc / l: lane (row r16 = token 2 mt + r16/8, head r16 % 8) holds dims 16 dt + 4 g .. +3
