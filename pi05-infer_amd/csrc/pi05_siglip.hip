@@ -145,41 +145,44 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
 }
 
 // MHA over one image's 256 patches, straight from the fused q|k|v GEMM output [M, 3456]:
-// workgroup = (image, head, quarter of the queries).  The workgroup stages the head's K and V for
-// all 256 keys into LDS in fragment order (16-byte global loads of 8 head dims of one key); wave w
-// loads its query m-tile 4 quarter + w as B fragments straight from global memory and streams the
+// workgroup = (image, head, half of the queries), 8 waves (two per SIMD, so one wave's softmax
+// overlaps the other's MFMAs).  The workgroup stages the head's K and V for all 256 keys into LDS
+// in fragment order (16-byte global loads of 8 head dims of one key); wave w loads its query m-tile
+// 8 half + w as B fragments straight from global memory and streams the
 // 8 key blocks of 32 through the online-softmax update: fp32 scores scaled by 72^-0.5 (no bf16
 // rounding of the scores: the reference runs SDPA's flash kernel), P rounded to bf16 for P.V.
-__global__ __launch_bounds__(256) void vision_attn_kernel(const u16* qkv, u16* out) {
+constexpr int kVAttnWaves = 8, kVKPass = (kVS / 16) * kVKs / kVAttnWaves, kVVPass = (kVS / 32) * kVDt / kVAttnWaves;
+
+__global__ __launch_bounds__(512) void vision_attn_kernel(const u16* qkv, u16* out) {
   __shared__ __align__(16) u16 s_k[kVKFrags * 512];
   __shared__ __align__(16) u16 s_v[kVVFrags * kVVFrag];
-  const int quarter = blockIdx.x & 3, head = (blockIdx.x >> 2) % kVH, n = (blockIdx.x >> 2) / kVH;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, mt = quarter * 4 + wave;
+  const int half = blockIdx.x & 1, head = (blockIdx.x >> 1) % kVH, n = (blockIdx.x >> 1) / kVH;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, mt = half * kVAttnWaves + wave;
   const u16* base = qkv + (size_t)n * kVS * kVQkvN + head * kVD;  // row r of the image: q | k | v at +0 | +W | +2W
   const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  static_assert((kVS / 16) * kVKs == 4 * 12 && (kVS / 32) * 5 == 4 * 10, "staging: 12 K and 10 V passes per wave");
-  // K: pass (wave, t) fills fragment f = 12 wave + t = (key tile f / 3, d-step f % 3) whole: lane l
+  static_assert(kVKPass * kVAttnWaves == (kVS / 16) * kVKs && kVVPass * kVAttnWaves == (kVS / 32) * kVDt, "staging passes");
+  // K: pass (wave, t) fills fragment f = 6 wave + t = (key tile f / 3, d-step f % 3) whole: lane l
   // loads dims 8 (4 (f % 3) + l / 16) .. +7 of key 16 (f / 3) + l % 16 (zero beyond dim 72) and
   // stores them at its own 16-byte slot, so each 16-lane store group covers all banks once.
-  // V: pass (wave, t) = combo 10 wave + t = (key block combo / 5, chunk pair combo % 5): lanes 0-31
+  // V: pass (wave, t) = combo 5 wave + t = (key block combo / 5, chunk pair combo % 5): lanes 0-31
   // load the even chunk, lanes 32-63 the odd chunk of the block's 32 keys; element (key r, dim d)
   // goes to fragment (r / 32, d / 16), group g, lane d % 16, slot j (vkey's inverse).
-  u16x8 kv[12], vv[10];  // every global load is issued before the first LDS store
+  u16x8 kv[kVKPass], vv[kVVPass];  // every global load is issued before the first LDS store
 #pragma unroll
-  for (int t = 0; t < 12; ++t) {
-    const int f = wave * 12 + t, r = (f / 3) * 16 + (lane & 15), c = (f % 3) * 4 + (lane >> 4);
+  for (int t = 0; t < kVKPass; ++t) {
+    const int f = wave * kVKPass + t, r = (f / 3) * 16 + (lane & 15), c = (f % 3) * 4 + (lane >> 4);
     kv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + kVW + c * 8) : zero;
   }
 #pragma unroll
-  for (int t = 0; t < 10; ++t) {
-    const int combo = wave * 10 + t, r = (combo / 5) * 32 + (lane & 31), c = (combo % 5) * 2 + (lane >> 5);
+  for (int t = 0; t < kVVPass; ++t) {
+    const int combo = wave * kVVPass + t, r = (combo / 5) * 32 + (lane & 31), c = (combo % 5) * 2 + (lane >> 5);
     vv[t] = c < 9 ? *reinterpret_cast<const u16x8*>(base + (size_t)r * kVQkvN + 2 * kVW + c * 8) : zero;
   }
 #pragma unroll
-  for (int t = 0; t < 12; ++t) *reinterpret_cast<u16x8*>(s_k + (wave * 12 + t) * 512 + lane * 8) = kv[t];
+  for (int t = 0; t < kVKPass; ++t) *reinterpret_cast<u16x8*>(s_k + (wave * kVKPass + t) * 512 + lane * 8) = kv[t];
 #pragma unroll
-  for (int t = 0; t < 10; ++t) {
-    const int combo = wave * 10 + t, r = lane & 31, c = (combo % 5) * 2 + (lane >> 5);
+  for (int t = 0; t < kVVPass; ++t) {
+    const int combo = wave * kVVPass + t, r = lane & 31, c = (combo % 5) * 2 + (lane >> 5);
     const int g = (r & 15) >> 2, j = r < 16 ? (r & 3) : 4 + (r & 3);
     u16* dst = s_v + ((combo / 5) * kVDt + (c >> 1)) * kVVFrag + g * kVVGroup + (c & 1) * 64 + j;
 #pragma unroll
@@ -650,7 +653,7 @@ int pi05_vision_forward(pi05_vision_ctx* c, const float* pixels, void* out, void
     const u16* w = c->w + (size_t)l * kVLayerElems;
     const float* pr = c->par + (size_t)l * kVLayerParams;
     if ((rc = vgemm(c, c->g_qkv, w + kVOffQkv, c->n, c->qkv, pr + kVPOffBqkv, st)) != PI05_OK) return rc;
-    vision_attn_kernel<<<(unsigned)(p.N * kVH * 4), 256, 0, st>>>(c->qkv, c->attn);
+    vision_attn_kernel<<<(unsigned)(p.N * kVH * 2), 512, 0, st>>>(c->qkv, c->attn);
     if (c->o_split) {
       if ((rc = vgemm(c, c->g_osk[c->o_split == 8], w + kVOffO, c->attn, c->part, nullptr, st)) != PI05_OK) return rc;
       layernorm_kernel<<<ln_grid, 256, 0, st>>>(c->h, nullptr, c->part, c->o_split, pstride, pr + kVPOffBo, pr + kVPOffLn2w,
