@@ -63,14 +63,14 @@ struct HeadBind {
 struct Plan {
   int M = 0, S = 0, s_pad = 0, n_norms = 0, rows = 0, nsplit = 1, mgroups = 1;
   // common
-  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, rope = 0, pos = 0, ptrs = 0, invf = 0, bias = 0;
+  size_t wpack = 0, table = 0, temb = 0, cond = 0, heads = 0, rope = 0, pos = 0, invf = 0, bias = 0;
   // graph schedule
   size_t kv = 0, valid = 0, h = 0, rowss = 0, q = 0, o = 0, act = 0, part = 0, partml = 0, x = 0, trace = 0;
   // persistent schedule
   int s_pre = 0, nsplit_p = 1, nsplit_pad = 4, nbp = 0, nbp_pad = 4, R = 0, fstride = 256;
   size_t p_kv = 0, p_valid = 0, p_h = 0, p_g = 0, p_ss = 0, p_hmid = 0, p_ssmid = 0, p_q = 0, p_suf = 0, p_act = 0;
   size_t p_apart = 0, p_apartml = 0, p_dpart = 0, p_x = 0, p_flags = 0, p_euler = 0;
-  size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + ptrs + invf + bias; }
+  size_t common() const { return wpack + 2 * table + temb + 2 * cond + heads + 2 * rope + pos + invf + bias; }
   size_t graph_bytes() const { return 2 * kv + valid + h + rowss + q + o + act + part + 2 * partml + x + trace; }
   size_t persistent_bytes() const {
     return 2 * p_kv + p_valid + p_h + p_g + p_ss + p_hmid + p_g + p_ssmid + 2 * p_q + 2 * p_suf + p_act + p_apart + p_apartml +
@@ -106,7 +106,6 @@ Plan make_plan(const pi05_dims& d) {
   p.heads = ((size_t)kWidth * kActDim * 2 + kWidth + kActDim) * 4;
   p.rope = (size_t)p.M * kHeadDim * 2;
   p.pos = (size_t)p.M * 4;
-  p.ptrs = 2 * L * sizeof(void*);
   p.invf = (size_t)kHalfDim * 4;
   p.bias = T * L * kBiasCols * 4;
 
@@ -185,7 +184,7 @@ bool check_dims_msg(const pi05_dims* d, std::string* msg) {
   REQ(d->mlp_dim == kMlp, "mlp_dim %d unsupported (compiled for %d)", d->mlp_dim, kMlp);
   REQ(d->action_dim == kActDim, "action_dim %d unsupported (compiled for %d)", d->action_dim, kActDim);
   REQ(d->action_horizon == kHorizon, "action_horizon %d unsupported (compiled for %d)", d->action_horizon, kHorizon);
-  REQ(d->depth >= 1 && d->depth <= 64, "depth %d out of range [1, 64]", d->depth);
+  REQ(d->depth >= 1 && d->depth <= kMaxDepth, "depth %d out of range [1, %d]", d->depth, kMaxDepth);
   REQ(d->batch >= 1 && d->batch <= 64, "batch %d out of range [1, 64]", d->batch);
   REQ(d->prefix_len >= 1 && d->prefix_len <= 16384, "prefix_len %d out of range [1, 16384]", d->prefix_len);
   REQ(d->num_steps >= 1 && d->num_steps <= kMaxSteps, "num_steps %d out of range [1, %d]", d->num_steps, kMaxSteps);
@@ -254,7 +253,6 @@ struct pi05_ctx {
   std::vector<LayerBind> layers;
   HeadBind heads;
   std::vector<float> ts;
-  std::vector<const void*> kv_host_ptrs;
 
   // common
   u16* wpack = nullptr;
@@ -268,7 +266,6 @@ struct pi05_ctx {
   u16* cos_tab = nullptr;
   u16* sin_tab = nullptr;
   int32_t* positions = nullptr;
-  const void** kv_ptrs = nullptr;
   float* inv_freq = nullptr;
 
   // graph schedule
@@ -347,7 +344,7 @@ void free_schedule(pi05_ctx* c) {
 void free_all(pi05_ctx* c) {
   free_schedule(c);
   void* bufs[] = {c->wpack, c->table, c->table_s1, c->bias, c->temb, c->cond1, c->cond, c->heads_buf, c->cos_tab, c->sin_tab,
-                  c->positions, (void*)c->kv_ptrs, c->inv_freq};
+                  c->positions, c->inv_freq};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->host_err) (void)hipHostFree(c->host_err);
@@ -699,7 +696,6 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   c->plan = make_plan(*dims);
   c->layers.resize(dims->depth);
   c->ts = euler_schedule(dims->num_steps);
-  c->kv_host_ptrs.assign(2 * dims->depth, nullptr);
   const Plan& p = c->plan;
   hipError_t ae = hipSuccess;
 #define ALLOC(field, bytes) \
@@ -715,7 +711,6 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   ALLOC(cos_tab, p.rope);
   ALLOC(sin_tab, p.rope);
   ALLOC(positions, p.pos);
-  ALLOC(kv_ptrs, p.ptrs);
   ALLOC(inv_freq, p.invf);
 #undef ALLOC
   if (ae == hipSuccess) {
@@ -899,22 +894,19 @@ int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* cons
   if (kv_row_stride < kHeadDim || kv_row_stride % 8) return c->fail(PI05_E_INVALID, "kv_row_stride %lld must be >= %d and a multiple of 8", (long long)kv_row_stride, kHeadDim);
   if (d.batch > 1 && (kv_batch_stride < (int64_t)d.prefix_len * kv_row_stride || kv_batch_stride % 8))
     return c->fail(PI05_E_INVALID, "kv_batch_stride %lld too small or not a multiple of 8", (long long)kv_batch_stride);
+  // the per-layer pointers go to the kernel by value: nothing to copy, nothing to wait for
+  PrimeKvArgs ka{};
   for (int l = 0; l < d.depth; ++l) {
     if (!k_layers[l] || !v_layers[l]) return c->fail(PI05_E_INVALID, "layer %d K/V pointer is NULL", l);
     if (!aligned16(k_layers[l]) || !aligned16(v_layers[l])) return c->fail(PI05_E_INVALID, "layer %d K/V pointer is not 16-byte aligned", l);
-    c->kv_host_ptrs[l] = k_layers[l];
-    c->kv_host_ptrs[d.depth + l] = v_layers[l];
+    ka.k_ptrs[l] = k_layers[l];
+    ka.v_ptrs[l] = v_layers[l];
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // the pointer table is tiny; a synchronous copy keeps the host vector's lifetime trivial
-  HIPCHK(c, hipMemcpy(c->kv_ptrs, c->kv_host_ptrs.data(), c->plan.ptrs, hipMemcpyHostToDevice));
   const bool persistent = c->schedule == PI05_SCHEDULE_PERSISTENT;
   // graph schedule: one cache of s_pad keys, action keys at [P, P + A);
   // persistent: prefix keys padded to s_pre, action keys in a separate per-step block
   const int kv_keys = persistent ? c->plan.s_pre : c->plan.s_pad;
-  PrimeKvArgs ka{};
-  ka.k_ptrs = c->kv_ptrs;
-  ka.v_ptrs = c->kv_ptrs + d.depth;
   ka.batch_stride = kv_batch_stride;
   ka.row_stride = kv_row_stride;
   ka.kcache = persistent ? const_cast<u16*>(c->mega.kpre) : c->kcache;

@@ -10,9 +10,11 @@ typedef uint16_t u16;
 
 constexpr int kMaxSteps = 32;  // Euler steps the modulation-table builder supports
 
+constexpr int kMaxDepth = 64;  // layers a context may have (the per-layer pointers travel as kernel arguments)
+
 struct PrimeKvArgs {
-  const void* const* k_ptrs;  // device array [depth] of bf16 [B, 1, P, D] bases
-  const void* const* v_ptrs;
+  const void* k_ptrs[kMaxDepth];  // per layer: bf16 [B, 1, P, D] bases (passed by value, no device table)
+  const void* v_ptrs[kMaxDepth];
   int64_t batch_stride;  // elements between samples
   int64_t row_stride;    // elements between prefix positions
   u16* kcache;           // [depth][B] fragment-major blocks of s_pad * D
