@@ -129,7 +129,8 @@ int pi05_get_adarms_table(pi05_ctx* ctx, float* table_out, void* stream);
  * and prefix_pad is a device uint8/bool [B, P] key-padding mask (1 = valid).  Packs the KV into
  * the context's static cache and derives positions, RoPE tables and key masks.  Replaces
  * prime_kv_static + _build_step_invariants (modeling_gemma.py:312-329, 605-615;
- * engine.py:453-524). `k_layers` / `v_layers` are HOST arrays of `depth` device pointers. */
+ * engine.py:453-524). `k_layers` / `v_layers` are HOST arrays of `depth` device pointers, read
+ * during the call only; the packing is enqueued on `stream` (the call does not block). */
 int pi05_prime_prefix(pi05_ctx* ctx, const void* const* k_layers, const void* const* v_layers,
                       int64_t kv_batch_stride, int64_t kv_row_stride, const uint8_t* prefix_pad,
                       void* stream);
