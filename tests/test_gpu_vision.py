@@ -261,3 +261,29 @@ def test_embed_prefix_batch_of_two_matches_each_sample_alone(weights2):
         torch.cuda.synchronize()
         _close(one[0, :512].float(), embs[b, :512].float(), f"B=2 sample {b} vs alone")
     model.close()
+
+
+def test_build_model_with_prefix_towers_predicts_from_images():
+    """build_model(..., prefix_towers=True) on random weights: the attached towers move with
+    .to('cuda') and sample_actions runs from images and a prompt (shape and finiteness; the
+    arithmetic is pinned by the oracle-chain test above)."""
+    print("case build_model with prefix towers: expert/prefix depth 2, vision depth 1, B=1", flush=True)
+    from dataclasses import replace
+
+    from pi05_infer import synthetic as S
+    from pi05_infer.builder import build_model
+    from pi05_infer.prefix import PrefixGeometry
+    from pi05_infer.vision import VisionGeometry
+
+    eg = replace(S.ExpertGeometry(), depth=2)
+    model = build_model("random:7", "pi05_libero", geometry=eg, prefix_towers=True, num_steps=3,
+                        prefix_geometry=PrefixGeometry(depth=2, vocab_size=300), vision_geometry=VisionGeometry(depth=1))
+    model.to("cuda")
+    assert model.vision_tower.device.type == "cuda" and model.prefix_lm.device.type == "cuda"
+    obs = {"images": {"base_0_rgb": _pixels(1, 30).cuda(), "left_wrist_0_rgb": _pixels(1, 31).cuda()},
+           "image_masks": {"base_0_rgb": torch.ones(1, dtype=torch.bool).cuda(), "left_wrist_0_rgb": torch.ones(1, dtype=torch.bool).cuda()},
+           "tokenized_prompt": torch.randint(0, 300, (1, 12)).cuda(), "tokenized_prompt_mask": torch.ones(1, 12, dtype=torch.bool).cuda()}
+    out = model.sample_actions(obs, S.make_noise(eg, 1).cuda())["actions"]
+    torch.cuda.synchronize()
+    assert out.shape == (1, 50, 32) and bool(torch.isfinite(out).all())
+    model.close()
