@@ -287,3 +287,70 @@ def test_build_model_with_prefix_towers_predicts_from_images():
     torch.cuda.synchronize()
     assert out.shape == (1, 50, 32) and bool(torch.isfinite(out).all())
     model.close()
+
+
+def test_full_c5_predict_from_images_matches_oracle_chain():
+    """The whole C5 predict at full depth: SigLIP (27 layers) over 3 images of 224x224 and 200 prompt
+    tokens (20 padded) -> 968-token prefix -> Gemma-2B prefill (18 layers) -> 10-step denoise of the
+    18-layer expert, against the oracle chain on the same random weights.  The north-star bar applies
+    to every step's velocity and to the actions."""
+    print("case C5 chain: vision 27, prefill 18, denoise 18 x 10 steps, 3 views + 200 tokens", flush=True)
+    from oracle import denoise_oracle as O
+    from oracle import prefix_oracle as PO
+    from pi05_infer import synthetic as S
+    from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+    from pi05_infer.prefix import EMBED_NAME, PrefixGeometry, PrefixLM
+    from pi05_infer.prefix import layer_param_names as prefix_names
+    from pi05_infer.vision import HEAD_PARAM_NAMES, VisionGeometry, VisionTower
+    from pi05_infer.vision import layer_param_names as vision_names
+
+    steps, T, vocab = 10, 200, 2000
+    layers_v, heads_v = SO.random_weights(G, G.depth, seed=41, std=0.03)
+    views = [_pixels(1, 42 + i) for i in range(3)]
+    gen = torch.Generator().manual_seed(45)
+    tokens = torch.randint(0, vocab, (1, T), generator=gen)
+    lang_mask = torch.ones(1, T, dtype=torch.bool)
+    lang_mask[0, 180:] = False
+    table = O._bf(torch.randn(vocab, 2048, generator=gen))
+    layers_p = PO.random_layers(PO.PrefixGeometry(), 18, seed=46)
+    print("  weights generated", flush=True)
+
+    feats = SO.image_features(torch.cat(views), layers_v, heads_v, G)
+    emb = torch.cat([feats[0:1], feats[1:2], feats[2:3], PO.embed_tokens(tokens, table, 2048)], dim=1)
+    pad = torch.cat([torch.ones(1, 768, dtype=torch.bool), lang_mask], dim=1)
+    ref_cache = PO.prefill(layers_p, PO.PrefixGeometry(), emb, pad)
+    eg = S.ExpertGeometry()
+    w = S.make_weights(eg)
+    x1 = S.make_noise(eg, 1)
+    og = O.geometry_from(eg)
+    k_ref = torch.cat([k for k, _ in ref_cache], dim=1)
+    v_ref = torch.cat([v for _, v in ref_cache], dim=1)
+    del ref_cache
+    act_ref, vs_ref = O.sample_actions(w, og, k_ref, v_ref, pad, x1, steps, O.adarms_table(w, og, steps))
+    print("  oracle chain done", flush=True)
+
+    vt = VisionTower(VisionGeometry())
+    rename = {"wout": "wo", "bout": "bo", "ln1w": "ln1_w", "ln1b": "ln1_b", "ln2w": "ln2_w", "ln2b": "ln2_b"}
+    sd = {vision_names(i)[rename.get(k, k)]: t for i, lw in enumerate(layers_v) for k, t in lw.items()}
+    sd.update({HEAD_PARAM_NAMES[k]: t for k, t in heads_v.items()})
+    vt.load_state_dict(sd, strict=True)
+    del sd, layers_v
+    plm = PrefixLM(PrefixGeometry(vocab_size=vocab))
+    psd = {prefix_names(i)[k]: lw[k] for i, lw in enumerate(layers_p) for k in lw}
+    psd[EMBED_NAME] = table
+    plm.load_state_dict(psd, strict=True)
+    del psd, layers_p
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
+    model.load_state_dict(w)
+    model.to("cuda")
+    model.attach_prefix_lm(plm)
+    model.attach_vision_tower(vt)
+    obs = Observation.from_dict({"images": {f"view{i}": v.cuda() for i, v in enumerate(views)},
+                                 "image_masks": {f"view{i}": torch.ones(1, dtype=torch.bool).cuda() for i in range(3)},
+                                 "tokenized_prompt": tokens.cuda(), "tokenized_prompt_mask": lang_mask.cuda()})
+    act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
+    torch.cuda.synchronize()
+    for s in range(steps):
+        _close(vs_ref[s], vs[s], f"C5 chain step {s} velocity")
+    _close(act_ref, act, "C5 chain actions")
+    model.close()
