@@ -954,7 +954,8 @@ int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t 
     *c->host_err = 0;
     return c->fail(PI05_E_HIP, "denoise kernel: a workgroup timed out waiting for its inputs (state reset%s)",
                    e == hipSuccess ? "" : ", reset failed");
-  }  return PI05_OK;
+  }
+  return PI05_OK;
 }
 
 }  // namespace
