@@ -175,8 +175,9 @@ def test_prefill_then_denoise_matches_oracle_chain(layers3):
 
 def test_full_depth_prefill_then_denoise_c5_geometry():
     """All 18 Gemma-2B layers (17 full + the K/V-only last) into the 18-layer expert: the cache's
-    rounding noise grows with depth, so the bar is the north star's on the denoise output (actions
-    and every step's velocity), with the per-layer K/V cosine reported."""
+    rounding noise grows with depth, so the parity bar (cos >= 0.9999, max-abs <= 2e-2 of the
+    range) is applied to the denoise output (actions and every step's velocity), with the per-layer
+    K/V cosine reported."""
     print("case prefill -> denoise: depth 18, B=1, P=96 (16 padded), 10 steps", flush=True)
     from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
     from pi05_infer.prefix import PrefixGeometry, PrefixLM, layer_param_names

@@ -133,7 +133,8 @@ def test_images_and_prompt_to_actions_matches_oracle_chain(weights2):
     """A whole predict from camera images and a tokenized prompt through the Python API
     (``embed_prefix`` -> prefill -> denoise) against the oracle chain: the prefix embeddings'
     language part and pad mask exactly, the image part to the tolerance, the actions to the
-    north-star bar.  The second view is masked out (a missing camera)."""
+    parity bar (cos >= 0.9999, max-abs <= 2e-2 of the range).  The second view is masked out (a missing
+    camera)."""
     print("case images -> actions: vision depth 2, prefix/expert depth 3, B=1, 2 views + 24 tokens, 4 steps",
           flush=True)
     from dataclasses import replace
@@ -292,7 +293,8 @@ def test_build_model_with_prefix_towers_predicts_from_images():
 def test_full_c5_predict_from_images_matches_oracle_chain():
     """The whole C5 predict at full depth: SigLIP (27 layers) over 3 images of 224x224 and 200 prompt
     tokens (20 padded) -> 968-token prefix -> Gemma-2B prefill (18 layers) -> 10-step denoise of the
-    18-layer expert, against the oracle chain on the same random weights.  The north-star bar applies
+    18-layer expert, against the oracle chain on the same random weights.  The parity bar (cos >= 0.9999, max-abs <=
+    2e-2 of the range) applies
     to every step's velocity and to the actions."""
     print("case C5 chain: vision 27, prefill 18, denoise 18 x 10 steps, 3 views + 200 tokens", flush=True)
     from oracle import denoise_oracle as O
