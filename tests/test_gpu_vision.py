@@ -290,13 +290,13 @@ def test_build_model_with_prefix_towers_predicts_from_images():
     model.close()
 
 
-def test_full_c5_predict_from_images_matches_oracle_chain():
-    """The whole C5 predict at full depth: SigLIP (27 layers) over 3 images of 224x224 and 200 prompt
+def test_full_predict_3_images_200_tokens_matches_oracle_chain():
+    """A whole predict at full depth: SigLIP (27 layers) over 3 images of 224x224 and 200 prompt
     tokens (20 padded) -> 968-token prefix -> Gemma-2B prefill (18 layers) -> 10-step denoise of the
     18-layer expert, against the oracle chain on the same random weights.  The parity bar (cos >= 0.9999, max-abs <=
     2e-2 of the range) applies
     to every step's velocity and to the actions."""
-    print("case C5 chain: vision 27, prefill 18, denoise 18 x 10 steps, 3 views + 200 tokens", flush=True)
+    print("case full predict: vision 27, prefill 18, denoise 18 x 10 steps, 3 views + 200 tokens", flush=True)
     from oracle import denoise_oracle as O
     from oracle import prefix_oracle as PO
     from pi05_infer import synthetic as S
@@ -353,6 +353,6 @@ def test_full_c5_predict_from_images_matches_oracle_chain():
     act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
     torch.cuda.synchronize()
     for s in range(steps):
-        _close(vs_ref[s], vs[s], f"C5 chain step {s} velocity")
-    _close(act_ref, act, "C5 chain actions")
+        _close(vs_ref[s], vs[s], f"full predict step {s} velocity")
+    _close(act_ref, act, "full predict actions")
     model.close()
