@@ -18,9 +18,12 @@ restates their published algorithm (the same in the installed transformers 5.15,
   LayerNorm eps 1e-6, 16 heads of 72, every Linear with bias;
 * ``post_layernorm``, then ``multi_modal_projector.linear`` (1152 -> 2048, bias), times
   ``out_scale`` (1.0: the image features enter the prefix unscaled, as the language embeddings
-  are scaled explicitly by embed_prefix; transformers versions that divide the projector output by
-  sqrt(2048) correspond to out_scale = 2048 ** -0.5 -- which one the pinned install does is not
-  verifiable here, so the scale is a parameter and that factor is parity unpinned).
+  are scaled explicitly by embed_prefix -- openpi's patched Gemma likewise drops the embedding
+  normalizer, modeling_gemma.py:737-740, and the installed transformers 5.15 get_image_features
+  applies no scale; transformers versions that divide the projector output by sqrt(2048)
+  correspond to out_scale = 2048 ** -0.5 -- which one the pinned install with openpi's replacement
+  files does is not verifiable here, so the scale is a parameter and that factor is parity
+  unpinned).
 
 Rounding ledger (``rnd`` = bf16 rounding; pass ``rnd=lambda x: x`` for the fp32 pin): Linear
 outputs ``bf16(x.W^T + b)`` (bias in fp32 before the one rounding, as a GEMM epilogue adds it);
