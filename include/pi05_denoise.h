@@ -135,14 +135,41 @@ int pi05_prime_prefix(pi05_ctx* ctx, const void* const* k_layers, const void* co
                       int64_t kv_batch_stride, int64_t kv_row_stride, const uint8_t* prefix_pad,
                       void* stream);
 
+/* Copy the step invariants that pi05_prime_prefix derived out of the context, in the reference's
+ * layout (a parity / debug read; it does not change the context).  Replaces reading the buffers
+ * of _build_step_invariants (engine.py:453-524):
+ *   positions_out   int64 [B, A]: sum(prefix_pad[b]) + t, the RoPE positions (engine.py:476-477);
+ *   key_valid_out   uint8 [B, P + A]: 1 where action query rows may attend key j, keys in the
+ *                   reference's order (P prefix keys, then the A action keys): prefix_pad over
+ *                   the prefix, 1 over the action keys -- the zero entries of the additive mask
+ *                   of engine.py:471-478 / pi0_pytorch.py:160-163 (the same for every query row);
+ *   stray_valid_out int32 [1]: padding slots of the context's key table that are marked valid
+ *                   (0 for a correct table).
+ * Device pointers, each nullable (not all).  Requires a primed prefix; enqueued on `stream`. */
+int pi05_get_step_invariants(pi05_ctx* ctx, int64_t* positions_out, uint8_t* key_valid_out,
+                             int32_t* stray_valid_out, void* stream);
+
 /* Run the full num_steps Euler denoise loop (one cooperative kernel, or a hipGraph replay in the
  * graph schedule): x_inout [B, A, a] fp32 holds the initial noise x_1 on entry and the actions
  * x_0 on exit.  v_trace (nullable) [num_steps, B, A, a] fp32 receives each step's velocity.
- * The persistent schedule returns after the kernel has finished (it synchronises `stream` to
- * report a kernel-side timeout as PI05_E_HIP); the graph schedule only enqueues.
+ * Both schedules only enqueue work on `stream`; nothing blocks the host.  Every wait inside the
+ * persistent kernel is bounded: a launch whose wait gives up leaves its outputs invalid and is
+ * reported asynchronously, as PI05_E_HIP from the next pi05_denoise on this context (which then
+ * enqueues nothing) or from pi05_denoise_status.
  * Replaces sample_actions' denoise loop (engine.py:389-405) with sample_mean_var_val /
  * get_velocity / the expert forward (engine.py:629-768, modeling_gemma.py:662-794). */
 int pi05_denoise(pi05_ctx* ctx, float* x_inout, float* v_trace, void* stream);
+
+/* Wait for `stream` and report a timed-out persistent launch of this context that has not been
+ * reported yet (PI05_E_HIP), once.  The reference surfaces device-side failures at the next
+ * synchronising call in the same way (CUDA/torch asynchronous error semantics); this is that
+ * synchronising call for callers that want it per predict. */
+int pi05_denoise_status(pi05_ctx* ctx, void* stream);
+
+/* Test hook: polls after which a wait of the persistent kernel gives up (0 restores the default of
+ * 2^20).  A small value makes waits give up on purpose, so the timeout path can be exercised;
+ * every workgroup still leaves the kernel normally.  No counterpart in the reference. */
+int pi05_debug_set_spin_limit(pi05_ctx* ctx, int polls);
 
 /* Drop the captured graph (it is recaptured on the next pi05_denoise).  Mirrors
  * release_cuda_graph (_vendored/base_policy.py:96-102). */

@@ -244,6 +244,10 @@ void rope_inv_freq(float theta, float* out) {
 
 }  // namespace
 
+// Polls before a wait of the persistent kernel gives up (each poll >= ~1 us; a legitimate wait
+// spans a few phases, so this is a fault detector, not a performance knob).
+constexpr int kDefaultSpinLimit = 1 << 20;
+
 struct pi05_ctx {
   pi05_dims d{};
   Plan plan;
@@ -289,7 +293,9 @@ struct pi05_ctx {
   char* pbase = nullptr;  // one allocation, carved by carve_persistent()
   MegaArgs mega{};
   unsigned epoch = 0;
-  unsigned* host_err = nullptr;  // pinned host word the kernel sets on a timed-out wait
+  unsigned* host_err = nullptr;  // pinned host word: epoch of the last launch whose wait timed out
+  unsigned reported = 0;         // the last such epoch already reported to the caller
+  int spin_limit = kDefaultSpinLimit;
 
   bool weights_ready = false;
   bool primed = false;
@@ -931,30 +937,65 @@ int pi05_prime_prefix(pi05_ctx* c, const void* const* k_layers, const void* cons
   return PI05_OK;
 }
 
+int pi05_get_step_invariants(pi05_ctx* c, int64_t* positions_out, uint8_t* key_valid_out, int32_t* stray_valid_out, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (!positions_out && !key_valid_out && !stray_valid_out) return c->fail(PI05_E_INVALID, "every output is NULL");
+  if (!c->primed) return c->fail(PI05_E_STATE, "prefix not primed (call pi05_prime_prefix)");
+  const bool persistent = c->schedule == PI05_SCHEDULE_PERSISTENT;
+  ExportInvariantsArgs a{};
+  a.positions = c->positions;
+  a.valid = persistent ? c->mega.valid : c->valid;
+  a.pos_out = positions_out;
+  a.valid_out = key_valid_out;
+  a.stray_out = stray_valid_out;
+  a.batch = c->d.batch;
+  a.prefix_len = c->d.prefix_len;
+  // the layouts pi05_prime_prefix wrote: persistent [B][s_pre + 64] with the action keys at
+  // s_pre; graph [B][s_pad] with the action keys at P
+  a.valid_ld = persistent ? c->plan.s_pre + 64 : c->plan.s_pad;
+  a.suffix_base = persistent ? c->plan.s_pre : c->d.prefix_len;
+  HIPCHK(c, launch_export_invariants(a, reinterpret_cast<hipStream_t>(stream)));
+  return PI05_OK;
+}
+
 namespace {
 
+// A timeout recorded by a launch of this context that has not been reported yet: the pinned host
+// word holds the epoch of the last launch whose wait timed out (read without waiting: a launch
+// still running is seen by a later call or by pi05_denoise_status).
+int take_pending_error(pi05_ctx* c) {
+  if (!c->host_err) return PI05_OK;
+  const unsigned e = __atomic_load_n(c->host_err, __ATOMIC_ACQUIRE);
+  if (e == 0 || e == c->reported) return PI05_OK;
+  c->reported = e;
+  return c->fail(PI05_E_HIP, "denoise launch %u on this context timed out waiting for its inputs; its actions are invalid "
+                 "(nothing was enqueued by the call reporting it)", e);
+}
+
 int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t st) {
+  const int pending = take_pending_error(c);
+  if (pending != PI05_OK) return pending;
   if (c->epoch >= (1u << 31)) {
     // the epoch never wraps to 0 (the value of untouched flags): restart from zeroed flags
     HIPCHK(c, reset_persistent(c, st));
+    const int late = take_pending_error(c);
+    *c->host_err = 0;
+    c->reported = 0;
+    if (late != PI05_OK) return late;
   }
   MegaArgs a = c->mega;
   a.epoch = ++c->epoch;
+  a.spin_limit = c->spin_limit;
   a.x_io = x_inout;
   a.trace = v_trace;
   unsigned* host_err_dev = nullptr;
   HIPCHK(c, hipHostGetDevicePointer(reinterpret_cast<void**>(&host_err_dev), c->host_err, 0));
   a.host_err = host_err_dev;
-  *c->host_err = 0;
+  // enqueue only: a timed-out wait is reported by the next call or by pi05_denoise_status
   HIPCHK(c, launch_denoise_loop(a, c->grid, st));
-  // a timed-out wait inside the kernel is only visible after it ends
-  HIPCHK(c, hipStreamSynchronize(st));
-  if (__atomic_load_n(c->host_err, __ATOMIC_ACQUIRE) != 0) {
-    const hipError_t e = reset_persistent(c, st);
-    *c->host_err = 0;
-    return c->fail(PI05_E_HIP, "denoise kernel: a workgroup timed out waiting for its inputs (state reset%s)",
-                   e == hipSuccess ? "" : ", reset failed");
-  }
   return PI05_OK;
 }
 
@@ -977,6 +1018,25 @@ int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
   HIPCHK(c, hipGraphLaunch(c->exec[with_trace ? 1 : 0], st));
   HIPCHK(c, hipMemcpyAsync(x_inout, c->x, c->plan.x, hipMemcpyDeviceToDevice, st));
   if (with_trace) HIPCHK(c, hipMemcpyAsync(v_trace, c->trace, c->plan.trace, hipMemcpyDeviceToDevice, st));
+  return PI05_OK;
+}
+
+int pi05_denoise_status(pi05_ctx* c, void* stream) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  HIPCHK(c, hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  return take_pending_error(c);
+}
+
+int pi05_debug_set_spin_limit(pi05_ctx* c, int polls) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (polls < 0) return c->fail(PI05_E_INVALID, "polls %d < 0", polls);
+  c->spin_limit = polls == 0 ? kDefaultSpinLimit : polls;
   return PI05_OK;
 }
 

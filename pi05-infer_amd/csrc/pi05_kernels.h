@@ -34,6 +34,17 @@ struct PrimeTablesArgs {
   int suffix_base;        // first key of the action tokens in the mask
 };
 
+// The step invariants of a primed context in the reference's key order (a debug / parity copy).
+struct ExportInvariantsArgs {
+  const int32_t* positions;  // [B, A]
+  const uint8_t* valid;      // [B, valid_ld] the context's key-valid table
+  int64_t* pos_out;          // [B, A] (nullable)
+  uint8_t* valid_out;        // [B, P + A] prefix keys, then the A action keys (nullable)
+  int32_t* stray_out;        // [1] padding slots of the table marked valid (nullable)
+  int batch, prefix_len, valid_ld;
+  int suffix_base;           // first slot of the action keys in the table
+};
+
 struct GemvArgs {
   const float* W;     // [rows, K]
   const float* bias;  // [rows]
@@ -109,7 +120,8 @@ constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gat
 
 struct MegaArgs {
   unsigned epoch;      // this launch's flag value (1, 2, ...); flags start at 0
-  unsigned* err;       // set to 1 by a workgroup whose wait timed out
+  unsigned* err;       // set to the launch's epoch by a workgroup whose wait timed out
+  int spin_limit;      // polls before a wait gives up (each poll >= ~1 us)
   unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][kFlagCopies][fstride]
   int fstride;         // flag words per phase instance and copy (multiple of 256)
   int depth, steps, batch, R, nbp, nsplit, nsplit_pad, nbp_pad, s_pre;
@@ -145,7 +157,7 @@ struct MegaArgs {
   float* x;               // [steps][B*50, a] actions after step s (slot 0 unused)
   float* x_io;            // [B*50, a] caller's buffer: noise on entry, actions on exit
   float* trace;           // [steps][B*50, a] caller's velocity buffer (nullable)
-  unsigned* host_err;     // pinned host word, set with err (device-visible mapping)
+  unsigned* host_err;     // pinned host word, set to the epoch with err (device-visible mapping)
 };
 
 // bias[s][l][j] = sum_k shift_{s, norm(j)}[k] * W_l[j][k] from the packed weights, for the fused
@@ -165,6 +177,7 @@ const void* denoise_loop_kernel_ptr();
 hipError_t launch_pack_weight(const void* src, u16* dst, int N, int K, hipStream_t st);
 hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);
 hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t st);
+hipError_t launch_export_invariants(const ExportInvariantsArgs& a, hipStream_t st);
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st);
 // out[r] = in[r] with 1 + scale in place of scale, for rows of [3W] modulation (scale | shift | gate)
 hipError_t launch_scale_plus_one(const float* in, float* out, int rows, hipStream_t st);

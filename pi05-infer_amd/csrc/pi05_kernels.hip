@@ -101,6 +101,35 @@ __global__ void prime_tables_kernel(PrimeTablesArgs a) {
   }
 }
 
+// One workgroup: positions widened to int64, the key-valid table gathered into the reference's
+// key order [prefix keys | action keys], and a count of the table's padding slots that are marked
+// valid (none, unless the table is corrupt).
+__global__ __launch_bounds__(256) void export_invariants_kernel(ExportInvariantsArgs a) {
+  __shared__ int s_stray;
+  if (threadIdx.x == 0) s_stray = 0;
+  __syncthreads();
+  const int nkeys = a.prefix_len + kHorizon;
+  int stray = 0;
+  for (int b = 0; b < a.batch; ++b) {
+    if (a.pos_out)
+      for (int t = threadIdx.x; t < kHorizon; t += blockDim.x) a.pos_out[(size_t)b * kHorizon + t] = a.positions[(size_t)b * kHorizon + t];
+    for (int k = threadIdx.x; k < a.valid_ld; k += blockDim.x) {
+      const uint8_t v = a.valid[(size_t)b * a.valid_ld + k];
+      int j = -1;
+      if (k < a.prefix_len) j = k;
+      else if (k >= a.suffix_base && k < a.suffix_base + kHorizon) j = a.prefix_len + (k - a.suffix_base);
+      if (j >= 0) {
+        if (a.valid_out) a.valid_out[(size_t)b * nkeys + j] = v;
+      } else if (v) {
+        ++stray;
+      }
+    }
+  }
+  atomicAdd(&s_stray, stray);
+  __syncthreads();
+  if (threadIdx.x == 0 && a.stray_out) *a.stray_out = s_stray;
+}
+
 // =============================================================================================
 // adaRMS modulation table (once per weight refresh)
 // =============================================================================================
@@ -689,6 +718,11 @@ hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st) {
 
 hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t st) {
   prime_tables_kernel<<<batch, 256, 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_export_invariants(const ExportInvariantsArgs& a, hipStream_t st) {
+  export_invariants_kernel<<<1, 256, 0, st>>>(a);
   return hipGetLastError();
 }
 

@@ -62,7 +62,6 @@ __device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 16];
 constexpr int kCompWaves = 3;
 constexpr int kCompThreads = kCompWaves * 64;
 constexpr int kThreads = kCompThreads + 64;  // + the copy wave
-constexpr int kSpinLimit = 1 << 20;          // polls (each >= ~1 us): a legitimate wait spans a few phases
 constexpr int kRowsPerSample = 64;           // padded rows per sample (50 action tokens)
 
 // ---- coherent (agent-scope, write-through) accesses -------------------------------------------
@@ -184,9 +183,13 @@ __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, 
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
 
+// A timed-out wait: the launch's epoch goes to the device error word (which every waiting
+// workgroup of this launch checks, so all of them leave) and to the pinned host word (which the
+// host reads after the launch).  Words of earlier launches hold older epochs, so nothing needs
+// clearing between launches.
 __device__ void record_error(const MegaArgs& a) {
-  st_u32(a.err, 1u);
-  __hip_atomic_store(a.host_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  st_u32(a.err, a.epoch);
+  __hip_atomic_store(a.host_err, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Wave 0 polls until flags f[0..n) all hold this launch's epoch (f 16-byte aligned; the 16-byte
@@ -215,7 +218,7 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
         __builtin_amdgcn_s_sleep(1);
         va = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
         if (__all(done(vb))) break;
-        if (spins > kSpinLimit || ((spins & 63) == 62 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) != 0)) {
+        if (spins > a.spin_limit || ((spins & 63) == 62 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
           if (lane == 0) record_error(a);
           ok = 0;
           break;

@@ -35,7 +35,10 @@ EXPORTED_SYMBOLS = (
     "pi05_refresh_weights",
     "pi05_get_adarms_table",
     "pi05_prime_prefix",
+    "pi05_get_step_invariants",
     "pi05_denoise",
+    "pi05_denoise_status",
+    "pi05_debug_set_spin_limit",
     "pi05_release_graph",
     "pi05_set_schedule",
     "pi05_get_schedule",
@@ -166,7 +169,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_refresh_weights": (i32, [vp, vp]),
         "pi05_get_adarms_table": (i32, [vp, vp, vp]),
         "pi05_prime_prefix": (i32, [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp, vp]),
+        "pi05_get_step_invariants": (i32, [vp, vp, vp, vp, vp]),
         "pi05_denoise": (i32, [vp, vp, vp, vp]),
+        "pi05_denoise_status": (i32, [vp, vp]),
+        "pi05_debug_set_spin_limit": (i32, [vp, i32]),
         "pi05_release_graph": (i32, [vp]),
         "pi05_set_schedule": (i32, [vp, i32]),
         "pi05_get_schedule": (i32, [vp]),
@@ -323,6 +329,18 @@ class DenoiseContext:
         self._call(self.lib.pi05_get_adarms_table(self.handle, out.data_ptr(), _stream_ptr(stream)))
         return out
 
+    def step_invariants(self, stream=None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """The primed step invariants in the reference's layout: RoPE positions int64 ``[B, A]``,
+        key-valid uint8 ``[B, P + A]`` (prefix keys, then the action keys) and the number of padding
+        slots of the context's key table marked valid (int32 ``[1]``, 0 for a correct table)."""
+        d = self.dims
+        pos = torch.empty((d.batch, d.action_horizon), dtype=torch.int64, device=self.device)
+        valid = torch.empty((d.batch, d.prefix_len + d.action_horizon), dtype=torch.uint8, device=self.device)
+        stray = torch.empty(1, dtype=torch.int32, device=self.device)
+        self._call(self.lib.pi05_get_step_invariants(self.handle, pos.data_ptr(), valid.data_ptr(), stray.data_ptr(),
+                                                     _stream_ptr(stream)))
+        return pos, valid, stray
+
     def prime_prefix(self, k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.Tensor],
                      prefix_pad: torch.Tensor, stream=None) -> None:
         """k_layers/v_layers: per layer bf16 [B, 1, P, D] (or any view whose last dim is contiguous
@@ -363,6 +381,15 @@ class DenoiseContext:
                 raise ValueError("trace shape mismatch")
             tp = _ptr(trace, torch.float32, "trace", self.device)
         self._call(self.lib.pi05_denoise(self.handle, xp, tp, _stream_ptr(stream)))
+
+    def status(self, stream=None) -> None:
+        """Wait for the stream; raise Pi05Error(PI05_E_HIP) if a denoise launch of this context
+        timed out and was not reported yet (denoise itself only enqueues)."""
+        self._call(self.lib.pi05_denoise_status(self.handle, _stream_ptr(stream)))
+
+    def set_spin_limit(self, polls: int) -> None:
+        """Test hook: polls after which a kernel wait gives up (0 = the default)."""
+        self._call(self.lib.pi05_debug_set_spin_limit(self.handle, polls))
 
     def release_graph(self) -> None:
         self._call(self.lib.pi05_release_graph(self.handle))

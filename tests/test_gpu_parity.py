@@ -2,8 +2,9 @@
 
 Tolerance (the path is bf16 on the GPU, fp32 with bf16 rounding points in the oracle): for every
 per-step velocity and for the final actions, cosine similarity >= 0.9999 and max-abs error
-<= 2e-2 of the oracle's range of that tensor.  Integer work (positions, masks) is checked
-bit-exactly through its effect: ragged prefix padding must match the oracle's masked result.
+<= 2e-2 of the oracle's range of that tensor.  Integer work (RoPE positions, key masks) is read
+back through pi05_get_step_invariants and compared bit-exactly with the oracle's
+position_ids / attention_mask_4d (test_step_invariants_bit_exact).
 """
 
 from dataclasses import replace
@@ -13,7 +14,7 @@ import torch
 
 from oracle import denoise_oracle as O
 from pi05_infer import synthetic as S
-from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference, _split_layers
 
 pytestmark = pytest.mark.gpu
 
@@ -218,4 +219,110 @@ def test_persistent_is_default_and_single_launch(full_weights):
     assert ctx.launches_per_step() == 0
     ctx.set_schedule("graph")
     assert ctx.launches_per_step() in (1 + 2 * 5, 1 + 2 * 6)
+    model.close()
+
+
+INVARIANT_CASES = {
+    # name: (B, P, pad_fn)
+    "full_c1": (1, 968, None),
+    "ragged_tails": (3, 300, lambda p: (p[0, 280:].zero_(), p[1, 100:].zero_())),
+    "interior_holes": (3, 77, lambda p: (p[0, 5:17].zero_(), p[1, ::3].zero_(), p[2, 40:41].zero_())),
+    "padded_head": (2, 64, lambda p: (p[0, :10].zero_(), p[1, 1:].zero_())),
+    "single_key": (1, 1, None),
+    "odd_length": (3, 33, lambda p: p[1, 32:].zero_()),
+}
+
+
+@pytest.mark.parametrize("case", sorted(INVARIANT_CASES))
+def test_step_invariants_bit_exact(full_weights, case):
+    """RoPE positions and key masks are integer work: the context's copies must equal the oracle's
+    position_ids and the zero entries of attention_mask_4d exactly (engine.py:471-478;
+    pi0_pytorch.py:56-85, 160-163), under both schedules, before and after a predict."""
+    B, P, pad_fn = INVARIANT_CASES[case]
+    print(f"case invariants/{case}: B={B}, P={P}", flush=True)
+    g = replace(S.ExpertGeometry(), depth=1)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 1}
+    pad = S.full_prefix_pad(P, B)
+    if pad_fn is not None:
+        pad_fn(pad)
+    pos_ref = O.position_ids(pad, g.action_horizon)
+    allowed_ref = (O.attention_mask_4d(pad, g.action_horizon) == 0.0).to(torch.uint8)  # [B, 1, A, P + A]
+    # every query row sees the same keys: the table is per key
+    assert torch.equal(allowed_ref, allowed_ref[:, :, :1].expand_as(allowed_ref))
+    k, v = S.make_prefix_kv(g, P, B)
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=2), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    obs = Observation(k.cuda(), v.cuda(), pad.cuda())
+    x1 = S.make_noise(g, B).cuda()
+    for sched in SCHEDULES:
+        model.set_schedule(sched)
+        model.sample_actions(obs, x1)
+        ctx = model._context(B, P, 2)
+        for when in ("after predict", "after re-prime"):
+            if when == "after re-prime":
+                ctx.prime_prefix(_split_layers(obs.prefix_k, g.depth), _split_layers(obs.prefix_v, g.depth), obs.prefix_pad_masks)
+            pos, valid, stray = ctx.step_invariants()
+            torch.cuda.synchronize()
+            assert torch.equal(pos.cpu(), pos_ref), f"{case} [{sched}] positions {when}"
+            assert torch.equal(valid.cpu(), allowed_ref[:, 0, 0]), f"{case} [{sched}] key mask {when}"
+            assert stray.item() == 0, f"{case} [{sched}] {stray.item()} padding slots marked valid {when}"
+    model.close()
+
+
+def test_timeout_is_reported_and_the_next_predict_recovers(full_weights):
+    """The persistent kernel's waits are bounded.  With the spin limit cut to a few polls some wait
+    gives up; every workgroup still leaves normally, the launch is reported as PI05_E_HIP (once),
+    and the next predict with the default limit is exact again."""
+    from pi05_infer import _ext
+
+    g = replace(S.ExpertGeometry(), depth=2)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 2}
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=3), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    k, v = S.make_prefix_kv(g, 64)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(64).cuda())
+    x1 = S.make_noise(g).cuda()
+    good = model.sample_actions(obs, x1)["actions"].clone()
+    ctx = model._context(1, 64, 3)
+    assert ctx.schedule == "persistent"
+    ctx.status()  # nothing pending
+    print("forcing a timed-out wait (spin limit 1)", flush=True)
+    ctx.set_spin_limit(1)
+    model.sample_actions(obs, x1)
+    with pytest.raises(_ext.Pi05Error, match="PI05_E_HIP"):
+        ctx.status()
+    ctx.status()  # reported once
+    # reported by the next denoise when nobody asked for the status
+    model.sample_actions(obs, x1)
+    torch.cuda.synchronize()
+    with pytest.raises(_ext.Pi05Error, match="PI05_E_HIP"):
+        model.sample_actions(obs, x1)
+    ctx.set_spin_limit(0)
+    again = model.sample_actions(obs, x1)["actions"]
+    ctx.status()
+    assert torch.equal(again, good)
+    model.close()
+
+
+def test_back_to_back_predicts_without_host_sync(full_weights):
+    """pi05_denoise only enqueues: predicts queued back to back with no host synchronisation in
+    between give the same actions as one predict at a time."""
+    g = replace(S.ExpertGeometry(), depth=3)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 3}
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=4), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    k, v = S.make_prefix_kv(g, 200)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(200).cuda())
+    noises = [S.make_noise(g).cuda() * s for s in (1.0, -0.5, 2.0)]
+    single = []
+    for n in noises:
+        single.append(model.sample_actions(obs, n)["actions"].clone())
+        torch.cuda.synchronize()
+    queued = [model.sample_actions(obs, n)["actions"] for n in noises]
+    torch.cuda.synchronize()
+    for a, b in zip(single, queued):
+        assert torch.equal(a, b)
     model.close()

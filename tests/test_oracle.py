@@ -310,3 +310,164 @@ def test_kv_cache_tail_holds_rotated_suffix_keys():
     assert torch.equal(st.k_cache[0][:, 0, :7], k[:, 0].float())
     assert torch.all(st.k_cache[0][:, 0, 7:].abs().sum(-1) > 0)
     assert torch.all(st.v_cache[0][:, 0, 7:].abs().sum(-1) > 0)
+
+
+# ---------------------------------------------------------------------------- layer composition
+#
+# GemmaDecoderLayer (modeling_gemma.py:486-517): the input norm takes mod[0] and its gate scales
+# the attention branch; the post-attention norm takes mod[1] and its gate scales the MLP branch;
+# GemmaModel hands layer i the slices 2i, 2i+1 and the final norm slice 2L
+# (modeling_gemma.py:773, 782-783).  Each branch is isolated by zeroing the other branch's output
+# projection, and checked against a reference assembled here from library routines
+# (F.rms_norm, F.gelu, F.scaled_dot_product_attention, RoPE as a complex rotation); the
+# variants with the slices or the gates swapped must fail the same check.
+
+
+def _distinct_mods(W, seed=11):
+    """Two modulation rows with clearly different scale / shift / gate per norm."""
+    g = torch.Generator().manual_seed(seed)
+    r = lambda: 0.1 * torch.randn(W, generator=g)
+    mod_a = torch.cat([0.5 + r(), 0.3 + r(), 0.8 + r()])
+    mod_b = torch.cat([-0.4 + r(), -0.2 + r(), 1.5 + r()])
+    return torch.stack([mod_a, mod_b])
+
+
+def _lib_norm(h, mod, eps):
+    W = h.shape[-1]
+    scale, shift, gate = mod[:W], mod[W:2 * W], mod[2 * W:]
+    n = F.rms_norm(h, (W,), eps=eps) * (1 + scale) + shift
+    return n.to(torch.bfloat16).float(), gate.to(torch.bfloat16).float()
+
+
+def _bf(x):
+    return x.to(torch.bfloat16).float()
+
+
+def _lib_rope(x, pos, theta):
+    """x [B, A, H, D]; rotation of (x[d], x[d + D/2]) by pos * theta^(-2d/D), in float64."""
+    D = x.shape[-1]
+    inv = theta ** (-torch.arange(0, D, 2, dtype=torch.float64) / D)
+    ang = pos.double()[:, :, None, None] * inv
+    z = torch.complex(x[..., : D // 2].double(), x[..., D // 2:].double()) * torch.polar(torch.ones_like(ang), ang)
+    return _bf(torch.cat([z.real, z.imag], dim=-1).float())
+
+
+def _lib_attention_branch(w, g, i, h, mod, k_pre, v_pre, pad):
+    """bf16(h + bf16(o_proj(attention(norm(h; mod))) * gate)), library attention in fp32."""
+    p = f"{O.EXPERT_PREFIX}layers.{i}."
+    B, A, _ = h.shape
+    H, D = g.num_heads, g.head_dim
+    n, gate = _lib_norm(h, mod, g.rms_eps)
+    q = _bf(n @ w[p + "self_attn.q_proj.weight"].float().T).reshape(B, A, H, D)
+    k = _bf(n @ w[p + "self_attn.k_proj.weight"].float().T).reshape(B, A, 1, D)
+    v = _bf(n @ w[p + "self_attn.v_proj.weight"].float().T).reshape(B, A, 1, D)
+    pos = pad.sum(-1, keepdim=True) + torch.arange(A)[None, :]
+    q, k = _lib_rope(q, pos, g.rope_theta), _lib_rope(k, pos, g.rope_theta)
+    K = torch.cat([k_pre[:, i].float(), k[:, :, 0]], dim=1)[:, None]  # [B, 1, P + A, D]
+    V = torch.cat([v_pre[:, i].float(), v[:, :, 0]], dim=1)[:, None]
+    allowed = torch.cat([pad, torch.ones(B, A, dtype=torch.bool)], dim=1)[:, None, None, :]
+    o = F.scaled_dot_product_attention(q.transpose(1, 2), K.expand(B, H, -1, -1), V.expand(B, H, -1, -1), attn_mask=allowed)
+    o = _bf(o).transpose(1, 2).reshape(B, A, H * D)
+    y = _bf(o @ w[p + "self_attn.o_proj.weight"].float().T)
+    return _bf(h + _bf(y * gate))
+
+
+def _lib_mlp_branch(w, g, i, h, mod):
+    """bf16(h + bf16(down(bf16(gelu_tanh(bf16(gate_proj(n))) * up_proj(n))) * gate)), n = norm(h; mod)."""
+    p = f"{O.EXPERT_PREFIX}layers.{i}."
+    n, gate = _lib_norm(h, mod, g.rms_eps)
+    gt = _bf(n @ w[p + "mlp.gate_proj.weight"].float().T)
+    up = n @ w[p + "mlp.up_proj.weight"].float().T
+    act = _bf(F.gelu(gt, approximate="tanh") * up)
+    y = _bf(act @ w[p + "mlp.down_proj.weight"].float().T)
+    return _bf(h + _bf(y * gate))
+
+
+def _lib_layer(w, g, i, h, mod2, k_pre, v_pre, pad):
+    return _lib_mlp_branch(w, g, i, _lib_attention_branch(w, g, i, h, mod2[0], k_pre, v_pre, pad), mod2[1])
+
+
+def _agree(got, ref, h):
+    """Cosine and relative max error of the branch contributions (got - h) vs (ref - h)."""
+    a, b = (got - h).double().flatten(), (ref - h).double().flatten()
+    cos = F.cosine_similarity(a, b, dim=0).item()
+    rel = ((a - b).abs().max() / b.abs().max()).item()
+    return cos, rel
+
+
+def _layer_case(P=7, seed=3):
+    g = SMALL
+    og = O.geometry_from(g)
+    # weights large enough that each branch's contribution is not lost in the bf16 residual add
+    w = S.make_weights(g, seed=seed, std=0.15)
+    k, v, _, x = _small_inputs(g, P=P)
+    pad = torch.ones(1, P, dtype=torch.bool)
+    pad[0, 2] = False  # one padded prefix key
+    h = _bf(0.1 * torch.randn(1, g.action_horizon, g.width, generator=torch.Generator().manual_seed(seed)))
+    return g, og, w, k, v, pad, h
+
+
+def test_expert_layer_mlp_branch_uses_second_slice_and_gate():
+    g, og, w, k, v, pad, h = _layer_case()
+    p = f"{O.EXPERT_PREFIX}layers.0."
+    w[p + "self_attn.o_proj.weight"] = torch.zeros_like(w[p + "self_attn.o_proj.weight"])  # attention adds 0
+    mod2 = _distinct_mods(g.width)
+    st = O.prepare_state(og, k, v, pad)
+    got = O.expert_layer(w, og, 0, h, mod2, st)
+    cos, rel = _agree(got, _lib_mlp_branch(w, g, 0, h, mod2[1]), h)
+    assert cos >= 0.9999 and rel <= 2e-2, (cos, rel)
+    # the MLP norm fed the first slice, or the MLP scaled by the attention gate, must fail
+    swapped = torch.stack([mod2[0], mod2[0]])
+    gate_swapped = mod2[1].clone()
+    gate_swapped[2 * g.width:] = mod2[0, 2 * g.width:]
+    for bad in (_lib_mlp_branch(w, g, 0, h, swapped[1]), _lib_mlp_branch(w, g, 0, h, gate_swapped)):
+        cos_b, rel_b = _agree(got, bad, h)
+        assert cos_b < 0.999 or rel_b > 0.1, (cos_b, rel_b)
+
+
+def test_expert_layer_attention_branch_uses_first_slice_and_gate():
+    g, og, w, k, v, pad, h = _layer_case()
+    p = f"{O.EXPERT_PREFIX}layers.0."
+    w[p + "mlp.down_proj.weight"] = torch.zeros_like(w[p + "mlp.down_proj.weight"])  # MLP adds 0
+    mod2 = _distinct_mods(g.width)
+    st = O.prepare_state(og, k, v, pad)
+    got = O.expert_layer(w, og, 0, h, mod2, st)
+    cos, rel = _agree(got, _lib_attention_branch(w, g, 0, h, mod2[0], k, v, pad), h)
+    assert cos >= 0.9999 and rel <= 2e-2, (cos, rel)
+    gate_swapped = mod2[0].clone()
+    gate_swapped[2 * g.width:] = mod2[1, 2 * g.width:]
+    for bad in (_lib_attention_branch(w, g, 0, h, mod2[1], k, v, pad), _lib_attention_branch(w, g, 0, h, gate_swapped, k, v, pad)):
+        cos_b, rel_b = _agree(got, bad, h)
+        assert cos_b < 0.999 or rel_b > 0.1, (cos_b, rel_b)
+
+
+def test_velocity_feeds_layer_i_slices_2i_2i1_and_final_norm_2L():
+    g = SMALL  # depth 2: norms 0..4
+    og = O.geometry_from(g)
+    w = S.make_weights(g, seed=5, std=0.15)
+    k, v, _, x = _small_inputs(g, P=6)
+    pad = torch.ones(1, 6, dtype=torch.bool)
+    gen = torch.Generator().manual_seed(12)
+    mod = torch.stack([torch.cat([(-1) ** j * 0.3 * (j + 1) + 0.1 * torch.randn(g.width, generator=gen),
+                                  0.1 * (j - 2) + 0.1 * torch.randn(g.width, generator=gen),
+                                  0.4 + 0.3 * j + 0.1 * torch.randn(g.width, generator=gen)]) for j in range(og.num_norms)])
+    st = O.prepare_state(og, k, v, pad)
+    got = O.velocity(w, og, x, mod, st)
+
+    def lib_velocity(slices, final):
+        h = _bf(x @ w["action_in_proj.weight"].T + w["action_in_proj.bias"])
+        for i in range(g.depth):
+            h = _lib_layer(w, g, i, h, mod[list(slices(i))], k, v, pad)
+        n, _ = _lib_norm(h, mod[final], g.rms_eps)
+        return n @ w["action_out_proj.weight"].T + w["action_out_proj.bias"]
+
+    ref = lib_velocity(lambda i: (2 * i, 2 * i + 1), 2 * g.depth)
+    cos = F.cosine_similarity(got.double().flatten(), ref.double().flatten(), dim=0).item()
+    rel = ((got - ref).abs().max() / ref.abs().max()).item()
+    assert cos >= 0.9999 and rel <= 2e-2, (cos, rel)
+    for slices, final in (((lambda i: (i, i + 1)), 2 * g.depth), ((lambda i: (2 * i + 1, 2 * i)), 2 * g.depth),
+                          ((lambda i: (2 * i, 2 * i + 1)), 0)):
+        bad = lib_velocity(slices, final)
+        cos_b = F.cosine_similarity(got.double().flatten(), bad.double().flatten(), dim=0).item()
+        rel_b = ((got - bad).abs().max() / bad.abs().max()).item()
+        assert cos_b < 0.999 or rel_b > 0.1, (cos_b, rel_b)
