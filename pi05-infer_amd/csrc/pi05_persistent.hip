@@ -885,7 +885,9 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     const int first = kb_lo + (cw_block ? 1 : 0);
     const int kb0 = copy_wave() ? kb_lo : first + (wave == 0 ? 2 : wave - 1);
     const bool has_block = copy_wave() ? cw_block : kb0 < kb_hi;
-    const bool pre = has_block && kb0 < nkb_pre;
+    // wave 0 polls: anything it loads before its polls completes first (a wave's vector memory
+    // operations complete in issue order), so its block is loaded after the wait
+    const bool pre = has_block && kb0 < nkb_pre && wave != 0;
     KvBlock blk;
     if (pre) load(blk, kb0);
     if (!burst) {

@@ -19,6 +19,7 @@ from typing import Any, Optional
 
 import torch
 
+from . import transforms
 from .engine import OpenPi0InferConfig, OpenPi0Inference
 from .synthetic import ExpertGeometry, make_weights
 
@@ -52,6 +53,20 @@ def _load_checkpoint(checkpoint_dir: str) -> dict[str, torch.Tensor]:
     return sd
 
 
+def _output_transforms(config_name: str, checkpoint_dir: Optional[str], data_kwargs: Optional[dict]) -> list:
+    """Unnormalize with the checkpoint's norm stats (``<checkpoint>/<asset_id>/norm_stats.json``,
+    builder.py:118-121) and the policy's Outputs (builder.py:130-135).  ``data_kwargs`` may name
+    ``norm_stats_path`` (a JSON file or asset directory), ``asset_id``, ``use_quantile_norm`` and
+    ``extra_delta_transform``."""
+    kw = dict(data_kwargs or {})
+    path = kw.get("norm_stats_path")
+    if path is None and checkpoint_dir is not None:
+        path = transforms.find_norm_stats(checkpoint_dir, kw.get("asset_id", transforms.DEFAULT_ASSET_ID))
+    stats = transforms.load_norm_stats(path) if path is not None else None
+    return transforms.output_transforms_for(config_name, stats, use_quantiles=bool(kw.get("use_quantile_norm", True)),
+                                            extra_delta_transform=bool(kw.get("extra_delta_transform", False)))
+
+
 def build_model(
     model_path: Optional[str],
     config_name: str,
@@ -80,6 +95,7 @@ def build_model(
     missing, _ = model.load_state_dict(state, strict=False)
     if missing:
         raise KeyError(f"checkpoint lacks {len(missing)} expert tensors, e.g. {missing[:3]}")
+    model.setup_wrappers(output_transforms=_output_transforms(config_name, None if seed is not None else str(model_path), data_kwargs))
     from . import prefix, vision
 
     if prefix_towers is None:

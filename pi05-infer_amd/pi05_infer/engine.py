@@ -27,6 +27,7 @@ from typing import Any, Optional, Sequence
 import torch
 
 from . import _ext
+from . import transforms as _transforms
 from .synthetic import BF16_KEYS, HEAD_PARAM_NAMES, ExpertGeometry, layer_param_names
 
 logger = logging.getLogger(__name__)
@@ -124,6 +125,9 @@ class OpenPi0Inference:
         self.schedule: Optional[str] = None  # None: the library's default for the device
         self.prefix_lm = None  # optional PrefixLM (prefix.py): prefix embeddings -> KV cache
         self.vision_tower = None  # optional VisionTower (vision.py): camera images -> image embeddings
+        # until setup_wrappers installs the checkpoint's transforms: the policy's Outputs slice only
+        # (no norm stats), so env-facing actions never carry the model's padding dims
+        self.setup_wrappers(output_transforms=_transforms.output_transforms_for(config.config_name, None))
 
     # ------------------------------------------------------------------ parameters
     def expected_parameters(self) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
@@ -350,17 +354,35 @@ class OpenPi0Inference:
             ctx.refresh_weights()
         self._stale_contexts.clear()
 
+    def setup_wrappers(self, transforms: Sequence = (), output_transforms: Sequence = ()) -> None:
+        """Install the per-sample input and output transforms (engine.py:217-223).  The output
+        transforms run in ``output_transform``; the input transforms (openpi's image and prompt
+        preprocessing) are kept for the caller but not applied here: observations reach this engine
+        already preprocessed."""
+        self._input_transforms = list(transforms)
+        self._output_transform = _transforms.compose(output_transforms)
+
     def output_transform(self, outputs: dict) -> dict:
-        """Slice to ``action_chunk`` (engine.py:282); the openpi unnormalize transforms are not part
-        of this engine."""
-        out = dict(outputs)
-        out["actions"] = outputs["actions"][:, : self.config.action_chunk]
+        """Model-space outputs -> env-space outputs (engine.py:269-283): the installed output
+        transforms (Unnormalize with the checkpoint's norm stats, the policy's Outputs slice to the
+        env action dims), applied on the host like the reference, then the first ``action_chunk``
+        actions."""
+        host = {k: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for k, v in outputs.items()}
+        out = self._output_transform(host)
+        out["actions"] = out["actions"][:, : self.config.action_chunk]
         return out
 
     def predict_action_batch(self, env_obs, **kwargs) -> torch.Tensor:
-        """Observation with a prefix cache -> actions ``[B, action_chunk, a]`` (engine.py:321-342)."""
-        outputs = self.sample_actions(env_obs, kwargs.get("noise"))
-        return self.output_transform(outputs)["actions"]
+        """Observation -> env-space actions ``[B, action_chunk, env action dims]`` (engine.py:321-342).
+
+        The reference first turns raw environment observations into the model's ``Observation``
+        (openpi image transforms and prompt tokenisation, engine.py:225-268, 284-319); here the
+        observation arrives in that preprocessed form (prefix cache, prefix embeddings, or images
+        and tokenized prompt), and the rest is the reference's: ``sample_actions``, then
+        ``output_transform({"actions", "state"})``."""
+        obs = Observation.from_dict(env_obs) if isinstance(env_obs, dict) else env_obs
+        outputs = self.sample_actions(obs, kwargs.get("noise"))
+        return self.output_transform({"actions": outputs["actions"], "state": obs.state})["actions"]
 
     def close(self) -> None:
         self._drop_contexts()

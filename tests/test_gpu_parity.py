@@ -326,3 +326,28 @@ def test_back_to_back_predicts_without_host_sync(full_weights):
     for a, b in zip(single, queued):
         assert torch.equal(a, b)
     model.close()
+
+
+def test_predict_action_batch_returns_env_space_actions(full_weights):
+    """predict_action_batch = sample_actions, then the output transforms (engine.py:321-342):
+    Unnormalize with the installed norm stats and the policy's Outputs slice, then the chunk."""
+    from pi05_infer import transforms as T
+
+    g = replace(S.ExpertGeometry(), depth=2)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < 2}
+    model = OpenPi0Inference(OpenPi0InferConfig(config_name="pi05_turtle", num_steps=3, action_chunk=5), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    k, v = S.make_prefix_kv(g, 40)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(40).cuda(), state=torch.zeros(1, 8, device="cuda"))
+    x1 = S.make_noise(g).cuda()
+    raw = model.sample_actions(obs, x1)["actions"].cpu()
+    got = model.predict_action_batch(obs, noise=x1)
+    assert got.shape == (1, 5, 6) and torch.equal(got, raw[:, :5, :6])
+    q01 = torch.linspace(-2, 0, 6, dtype=torch.float64)
+    stats = {"actions": T.NormStats(torch.zeros(6, dtype=torch.float64), torch.ones(6, dtype=torch.float64), q01, q01 + 3)}
+    model.setup_wrappers(output_transforms=T.output_transforms_for("pi05_turtle", stats))
+    got = model.predict_action_batch(obs, noise=x1)
+    ref = (raw[:, :5, :6].double() + 1) / 2 * (3 + 1e-6) + q01
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    model.close()

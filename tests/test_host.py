@@ -166,7 +166,8 @@ def test_compat_shims():
     m.enable_torch_compile("max-autotune")
     assert m.torch_compile_enabled
     out = m.output_transform({"actions": torch.zeros(2, 50, 32)})
-    assert out["actions"].shape == (2, m.config.action_chunk, 32)
+    # the policy's Outputs slice (LiberoOutputs: 7 env action dims) and the action chunk
+    assert out["actions"].shape == (2, m.config.action_chunk, 7)
 
 
 def test_synthetic_recipe_is_deterministic_and_depth_independent():
