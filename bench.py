@@ -120,7 +120,7 @@ def bench_e2e(args) -> int:
         from pi05_infer.vision import HEAD_KEYS, HEAD_PARAM_NAMES, LAYER_KEYS
         from pi05_infer.vision import layer_param_names as vnames
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_threads()
         torch.set_num_threads(threads)
         # one SigLIP layer, one Gemma-2B layer and one expert predict of the fp32 oracle, scaled
         okeys = dict(zip(LAYER_KEYS, ("wq", "bq", "wk", "bk", "wv", "bv", "wout", "bout", "w1", "b1", "w2", "b2", "ln1w",
@@ -229,7 +229,7 @@ def bench_vision(args) -> int:
     if not args.no_cpu_baseline:
         from oracle import siglip_oracle as SO
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_threads()
         torch.set_num_threads(threads)
         og = SO.SiglipGeometry()
         n0 = layer_param_names(0)
@@ -338,7 +338,7 @@ def bench_prefill(args) -> int:
     if not args.no_cpu_baseline:
         from oracle import prefix_oracle as PO
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_threads()
         torch.set_num_threads(threads)
         g = PO.PrefixGeometry()
         w0 = {k: v.float().cpu() for k, v in layers[0].items()}
@@ -397,6 +397,19 @@ def algorithmic_bytes_per_predict(depth: int, batch: int, prefix_len: int, steps
     heads = (W * a * 2 + W + a) * 4
     x = batch * A * a * 4 * 2
     return steps * (weights + kv + mod + heads + x)
+
+
+def host_threads() -> int:
+    """CPU threads for the CPU baseline: the cores this process may run on (its affinity set, which
+    is the host's CPU share where the scheduler restricts it), capped by OMP_NUM_THREADS when set."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def cpu_model() -> str:
@@ -472,19 +485,29 @@ def main() -> int:
     for i in range(args.warmup):
         ctx.denoise(xs[i], stream=stream)
     torch.cuda.synchronize()
-    # timed region: K predicts back to back on `stream`, the stream every launch goes to
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ctx.status()
+    # timed region: K predicts back to back on `stream`, the stream every launch goes to, with an
+    # event between consecutive predicts (K + 1 events: per-predict times and their distribution)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    e0.record(stream)
+    evs[0].record(stream)
     for i in range(args.steps):
         ctx.denoise(xs[args.warmup + i], stream=stream)
-    e1.record(stream)
+        evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    ms_per_predict = e0.elapsed_time(e1) / args.steps
+    ctx.status()  # no launch of the timed region timed out
+    ms_per_predict = evs[0].elapsed_time(evs[-1]) / args.steps
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+
+    def pct(q):
+        return per[min(len(per) - 1, int(round(q * (len(per) - 1))))]
+
+    timing = {"mean": round(ms_per_predict, 4), "p50": round(pct(0.5), 4), "p90": round(pct(0.9), 4),
+              "min": round(per[0], 4), "max": round(per[-1], 4), "unit": "ms/predict", "n": args.steps}
 
     # dominant kernel: in the persistent schedule the whole predict is one launch of
-    # denoise_loop_kernel, so its average launch duration is the timed region / K (each predict's
-    # host-side completion check adds a few microseconds, so this slightly overstates it)
+    # denoise_loop_kernel, so its average launch duration is the timed region / K (back-to-back
+    # launches on one stream; the gap between two launches is included)
     pred_bytes = algorithmic_bytes_per_predict(g.depth, B, P, steps)
     launch_us = ms_per_predict * 1e3
     pred_gbs = pred_bytes / (launch_us * 1e-6) / 1e9
@@ -493,7 +516,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         from oracle import denoise_oracle as O
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_threads()
         torch.set_num_threads(threads)
         w = {n: t.cpu() for n, t in model.params.items()}
         og = O.geometry_from(g)
@@ -510,7 +533,7 @@ def main() -> int:
             "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{args.cpu_predicts} full predicts ({steps} steps, B={B}, P={P}) of the fp32 CPU oracle, median; "
-                      f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}",
+                      f"host {cpu_model()}, os.cpu_count()={os.cpu_count()}, affinity/OMP threads used={threads}",
         }
 
     traffic = read_traffic(f"denoise_loop_{args.config}_traffic.txt") if schedule == "persistent" else None
@@ -522,6 +545,9 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_predict, 4),
+        "step": f"one predict ({steps} Euler steps)",
+        "ms_per_euler_step": round(ms_per_predict / steps, 4),
+        "timing": timing,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,

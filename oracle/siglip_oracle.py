@@ -113,42 +113,62 @@ def layer_norm(x: torch.Tensor, wt: torch.Tensor, b: torch.Tensor, eps: float, r
     return rnd((x - mean) / torch.sqrt(var + eps) * wt + b)
 
 
-def linear_bias(x: torch.Tensor, wt: torch.Tensor, b: torch.Tensor, rnd: Callable = _bf) -> torch.Tensor:
+def linear_bias(x: torch.Tensor, wt: torch.Tensor, b: torch.Tensor, rnd: Callable = _bf, acc64: bool = False) -> torch.Tensor:
+    """``rnd(x W^T + b)``; ``acc64`` accumulates in float64 instead of fp32 (the same rounding
+    points, another summation precision: a measure of how far legitimate implementations of the
+    same rounding ledger drift apart)."""
+    if acc64:
+        return rnd((x.double() @ wt.double().T + b.double()).float())
     return rnd(x @ wt.T + b)
 
 
-def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rnd: Callable = _bf) -> torch.Tensor:
-    """``[N, H, S, Dh]`` each; fp32 scores and softmax, O = rnd(P.V) -> ``[N, S, H*Dh]``."""
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rnd: Callable = _bf, p_bf16: bool = False) -> torch.Tensor:
+    """``[N, H, S, Dh]`` each; fp32 scores and softmax, O = rnd(P.V) -> ``[N, S, H*Dh]``.
+
+    ``p_bf16``: flash attention's rounding point instead of the math path's: the unnormalised
+    probabilities ``exp(s - max)`` are rounded to bf16 before ``P.V`` and the fp32 sum of the
+    unrounded ones normalises the product once (what SDPA's flash / memory-efficient kernels
+    compute; the reference leaves SigLIP's attention implementation unset, gemma_pytorch.py:45-61,
+    so which one runs depends on the installed torch's dispatch).  The engine's kernel rounds here.
+    """
     n, h, s, d = q.shape
-    p = torch.softmax((q @ k.transpose(-1, -2)) * (d ** -0.5), dim=-1)
+    sc = (q @ k.transpose(-1, -2)) * (d ** -0.5)
+    if p_bf16:
+        e = torch.exp(sc - sc.amax(dim=-1, keepdim=True))
+        o = (_bf(e) @ v) / e.sum(dim=-1, keepdim=True)
+        return rnd(o).transpose(1, 2).reshape(n, s, h * d)
+    p = torch.softmax(sc, dim=-1)
     return rnd(p @ v).transpose(1, 2).reshape(n, s, h * d)
 
 
-def encoder_layer(w: dict, g: SiglipGeometry, h: torch.Tensor, rnd: Callable = _bf) -> torch.Tensor:
+def encoder_layer(w: dict, g: SiglipGeometry, h: torch.Tensor, rnd: Callable = _bf, p_bf16: bool = False,
+                  acc64: bool = False) -> torch.Tensor:
     n, s, _ = h.shape
+    lin = lambda x, wn, bn: linear_bias(x, w[wn], w[bn], rnd, acc64)  # noqa: E731
     x = layer_norm(h, w["ln1w"], w["ln1b"], g.ln_eps, rnd)
     heads = lambda t: t.view(n, s, g.num_heads, g.head_dim).transpose(1, 2)
-    q = heads(linear_bias(x, w["wq"], w["bq"], rnd))
-    k = heads(linear_bias(x, w["wk"], w["bk"], rnd))
-    v = heads(linear_bias(x, w["wv"], w["bv"], rnd))
-    h = rnd(h + linear_bias(attention(q, k, v, rnd), w["wout"], w["bout"], rnd))
+    q = heads(lin(x, "wq", "bq"))
+    k = heads(lin(x, "wk", "bk"))
+    v = heads(lin(x, "wv", "bv"))
+    h = rnd(h + lin(attention(q, k, v, rnd, p_bf16), "wout", "bout"))
     x = layer_norm(h, w["ln2w"], w["ln2b"], g.ln_eps, rnd)
-    x = linear_bias(rnd(gelu_tanh(linear_bias(x, w["w1"], w["b1"], rnd))), w["w2"], w["b2"], rnd)
+    x = lin(rnd(gelu_tanh(lin(x, "w1", "b1"))), "w2", "b2")
     return rnd(h + x)
 
 
-def vision_tower(pixels: torch.Tensor, layers: list[dict], heads: dict, g: SiglipGeometry, rnd: Callable = _bf) -> torch.Tensor:
+def vision_tower(pixels: torch.Tensor, layers: list[dict], heads: dict, g: SiglipGeometry, rnd: Callable = _bf,
+                 p_bf16: bool = False, acc64: bool = False) -> torch.Tensor:
     """SigLIP last hidden state after post_layernorm ``[N, 256, width]``."""
     h = embeddings(pixels, heads, g, rnd)
     for w in layers:
-        h = encoder_layer(w, g, h, rnd)
+        h = encoder_layer(w, g, h, rnd, p_bf16, acc64)
     return layer_norm(h, heads["post_w"], heads["post_b"], g.ln_eps, rnd)
 
 
 def image_features(pixels: torch.Tensor, layers: list[dict], heads: dict, g: SiglipGeometry, out_scale: float = 1.0,
-                   rnd: Callable = _bf) -> torch.Tensor:
+                   rnd: Callable = _bf, p_bf16: bool = False, acc64: bool = False) -> torch.Tensor:
     """``get_image_features``: projector(vision_tower(pixels)) * out_scale -> ``[N, 256, proj_dim]``."""
-    f = linear_bias(vision_tower(pixels, layers, heads, g, rnd), heads["proj_w"], heads["proj_b"], rnd)
+    f = linear_bias(vision_tower(pixels, layers, heads, g, rnd, p_bf16, acc64), heads["proj_w"], heads["proj_b"], rnd, acc64)
     return f if out_scale == 1.0 else rnd(f * out_scale)
 
 

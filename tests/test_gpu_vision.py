@@ -3,11 +3,14 @@
 
 Tolerance, as for the denoise path (bf16 on the GPU, fp32 with bf16 rounding points in the
 oracle): the image embeddings have cosine similarity >= 0.9999 with the oracle's and max-abs
-error <= 2e-2 of the oracle tensor's range, per image.  Through all 27 layers the bf16 rounding
-noise alone takes the cosine below 0.9999: the oracle against itself with fp64-accumulated GEMMs
-(every rounding point unchanged) reaches 0.99989 on the full-depth case, and with P rounded to
-bf16 before P.V (flash attention's order) 0.99988.  The full-depth bar is therefore cos >= 0.9998
-(the max-abs bar is unchanged).
+error <= 2e-2 of the oracle tensor's range, per image (depth 2).  At depth 27 the bf16 outputs of
+27 layers amplify summation-order differences: the oracle against itself with fp64 instead of
+fp32 GEMM accumulation (every rounding point kept) is already at 1 - cos ~ 1.1e-4.  The full-depth
+case is therefore held to a bar relative to that noise floor, measured in the test: against the
+oracle with the kernel's attention rounding point (P rounded to bf16 before P.V,
+``p_bf16=True``), 1 - cos <= 1.5 x the oracle's own summation-precision distance, plus
+cos >= 0.9998 and the max-abs bar; against the math-path rounding point (normalised fp32 P) cos
+>= 0.9998.
 """
 
 import math
@@ -124,9 +127,26 @@ def test_vision_full_depth_three_images():
     torch.cuda.synchronize()
     ctx.close()
     del _keep
+    # the kernel rounds the unnormalised probabilities to bf16 before P.V (flash attention's
+    # rounding point).  Against the oracle with that rounding point, the engine must be as close as
+    # the oracle is to itself when only its GEMM summation precision changes (fp32 -> fp64, every
+    # rounding point kept): 27 layers of bf16 outputs amplify summation-order differences to
+    # ~1e-4 in 1 - cos, the same size as the engine's distance (measured on MI355X: 1.16e-4 for
+    # the engine, 1.1e-4 for the oracle against itself), so the bar is 1.5x that noise floor
+    ref_flash = SO.image_features(px, layers, heads, G, p_bf16=True)
+    ref_flash64 = SO.image_features(px, layers, heads, G, p_bf16=True, acc64=True)
+    for i in range(3):
+        cos = lambda a, b: torch.nn.functional.cosine_similarity(a.double().flatten(), b.double().flatten(), dim=0).item()  # noqa: E731
+        floor = 1.0 - cos(ref_flash[i], ref_flash64[i])
+        dist = 1.0 - cos(ref_flash[i], got[i].float().cpu())
+        print(f"depth 27 image {i}: engine 1-cos {dist:.3e}, oracle summation-precision floor {floor:.3e}", flush=True)
+        assert dist <= 1.5 * floor, f"image {i}: engine distance {dist} > 1.5 x the oracle's own noise floor {floor}"
+        _close(ref_flash[i], got[i].float(), f"depth 27 image {i} (oracle with bf16 P)", COS_MIN_FULL_DEPTH)
+    # against the math path's rounding point (normalised fp32 P) the two rounding orders differ on
+    # top of the bf16 noise of 27 layers: the relaxed bar
     ref = SO.image_features(px, layers, heads, G)
     for i in range(3):
-        _close(ref[i], got[i].float(), f"depth 27 image {i}", COS_MIN_FULL_DEPTH)
+        _close(ref[i], got[i].float(), f"depth 27 image {i} (oracle with fp32 P)", COS_MIN_FULL_DEPTH)
 
 
 def test_images_and_prompt_to_actions_matches_oracle_chain(weights2):

@@ -74,3 +74,27 @@ def test_bf16_rounding_points():
     assert cos > 0.9999
     half = S.image_features(px, layers, heads, G, out_scale=0.5)
     assert torch.equal(half, f * 0.5)  # scaling by a power of two is exact in bf16
+
+
+def test_attention_flash_rounding_point():
+    """p_bf16: P rounded to bf16 before P.V, normalised once.  Uniform scores make every
+    unnormalised probability exactly 1, so both rounding points give the plain mean of V; for
+    random scores the two differ by bf16 rounding of P only, and both match SDPA in fp32."""
+    g = torch.Generator().manual_seed(3)
+    n, h, s, d = 2, 3, 40, 72
+    v = torch.randn(n, h, s, d, generator=g)
+    q0 = torch.zeros(n, h, s, d)
+    k = torch.randn(n, h, s, d, generator=g)
+    ident = lambda t: t  # noqa: E731  (no output rounding: compare the raw products)
+    a = S.attention(q0, k, v, ident, p_bf16=True)
+    b = S.attention(q0, k, v, ident, p_bf16=False)
+    mean_v = v.mean(dim=2, keepdim=True).expand(n, h, s, d).transpose(1, 2).reshape(n, s, h * d)
+    torch.testing.assert_close(a, mean_v, rtol=0, atol=1e-6)
+    torch.testing.assert_close(b, mean_v, rtol=0, atol=1e-6)
+    q = torch.randn(n, h, s, d, generator=g)
+    a = S.attention(q, k, v, ident, p_bf16=True)
+    b = S.attention(q, k, v, ident, p_bf16=False)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(n, s, h * d)
+    torch.testing.assert_close(b, ref, rtol=0, atol=1e-5)
+    err = (a - ref).abs().max().item()
+    assert 0 < err < 2e-2  # bf16 rounding of P (8 significant bits) and nothing else
