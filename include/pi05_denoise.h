@@ -208,6 +208,26 @@ int pi05_launches_per_step(const pi05_ctx* ctx);
  * traces); it lets a benchmark time one kernel with events. */
 int pi05_bench_kernel(pi05_ctx* ctx, int kernel_id, int layer, int iters, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving or RL weight-sync loops): the adaRMS modulation table that
+ * pi05_refresh_weights builds (and pi05_get_adarms_table returns), computed without a context
+ * straight from caller-owned fp32 weights -- the time MLP tin_w [W, W], tin_b [W], tout_w [W, W],
+ * tout_b [W] and the 2*depth+1 norm dense layers (host arrays dense_w / dense_b of device
+ * pointers to [3W, W] / [3W], in the table's norm order: input_layernorm and
+ * post_attention_layernorm of each layer, then the final norm) -- into table_out
+ * [num_steps][2*depth+1][3W] fp32 (device).  Replaces nothing: it is the table-building part of
+ * pi05_refresh_weights (engine.py:578-599) as a stand-alone call.
+ * It allocates nothing: its scratch (time embedding + two time-MLP activations, 384 KiB) is a
+ * static device array of the library, one per GPU, kept until the process ends; num_steps above
+ * 32 is rejected with PI05_E_INVALID.  Every call on one GPU shares that GPU's scratch (each call
+ * rewrites all of it before reading it): calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  Enqueued on `stream`; dims supplies depth,
+ * num_steps and the time periods. */
+int pi05_adarms_table_noalloc(const pi05_dims* dims, const float* tin_w, const float* tin_b,
+                              const float* tout_w, const float* tout_b,
+                              const float* const* dense_w, const float* const* dense_b,
+                              float* table_out, void* stream);
+
 /* ---- host-only helpers (no GPU needed; what the context computes on the host) ---- */
 
 /* Euler schedule linspace(1, 1/N, N) ++ [0] in fp32, evaluated as the reference's device

@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -632,7 +633,82 @@ int ensure_graph(pi05_ctx* c, bool with_trace) {
 
 }  // namespace
 
+// ---- scratch of pi05_adarms_table_noalloc -----------------------------------------------------
+// The time embedding and the two time-MLP activations of up to kMaxSteps steps live in a
+// file-scope device array (one copy per GPU, held until the process ends), so that entry point
+// allocates nothing.  Host code never passes `scratch` itself to a kernel (in host code the name
+// stands for a host-side shadow, not a device address): the device address is looked up once
+// per device with hipGetSymbolAddress, with that device current, and kept in g_scratch_dev.
+constexpr size_t kNoallocScratchFloats = 3 * (size_t)kMaxSteps * kWidth;  // temb | cond1 | cond: 384 KiB
+static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+constexpr int kMaxNoallocDevices = 64;
+float* g_scratch_dev[kMaxNoallocDevices] = {};
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device (looked up on the first call per device).
+hipError_t noalloc_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxNoallocDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return hipSuccess;
+}
+
 extern "C" {
+
+int pi05_adarms_table_noalloc(const pi05_dims* dims, const float* tin_w, const float* tin_b, const float* tout_w,
+                              const float* tout_b, const float* const* dense_w, const float* const* dense_b, float* table_out,
+                              void* stream) {
+  std::string msg;
+  if (!check_dims_msg(dims, &msg)) {
+    g_last_error = msg;
+    return PI05_E_INVALID;
+  }
+  if (dims->num_steps > kMaxSteps) {
+    g_last_error = "num_steps exceeds the no-alloc scratch maximum";
+    return PI05_E_INVALID;
+  }
+  if (!tin_w || !tin_b || !tout_w || !tout_b || !dense_w || !dense_b || !table_out) {
+    g_last_error = "a pointer argument is NULL";
+    return PI05_E_INVALID;
+  }
+  if (!aligned16(tin_w) || !aligned16(tout_w) || !aligned16(table_out)) {
+    g_last_error = "tin_w / tout_w / table_out must be 16-byte aligned";
+    return PI05_E_INVALID;
+  }
+  const int n_norms = 2 * dims->depth + 1;
+  for (int n = 0; n < n_norms; ++n) {
+    if (!dense_w[n] || !dense_b[n] || !aligned16(dense_w[n])) {
+      g_last_error = "dense_w[n] / dense_b[n] must be non-NULL, dense_w[n] 16-byte aligned";
+      return PI05_E_INVALID;
+    }
+  }
+  float* sp = nullptr;
+  hipError_t e = noalloc_scratch(&sp);
+  if (e != hipSuccess) {
+    g_last_error = std::string("no-alloc scratch lookup failed: ") + hipGetErrorString(e);
+    return PI05_E_HIP;
+  }
+  const size_t per = (size_t)kMaxSteps * kWidth;
+  const AdarmsTableArgs ta{tin_w, tin_b, tout_w, tout_b, dense_w, dense_b, n_norms, dims->num_steps, dims->time_min_period,
+                           dims->time_max_period, sp, sp + per, sp + 2 * per, table_out};
+  e = launch_adarms_table(ta, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    g_last_error = std::string("no-alloc table kernels: ") + hipGetErrorString(e);
+    return PI05_E_HIP;
+  }
+  return PI05_OK;
+}
+
 
 int pi05_abi_version(void) { return PI05_ABI_VERSION; }
 
@@ -737,12 +813,6 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
     std::vector<float> invf(kHalfDim);
     rope_inv_freq(dims->rope_theta, invf.data());
     ae = hipMemcpy(c->inv_freq, invf.data(), p.invf, hipMemcpyHostToDevice);
-  }
-  if (ae == hipSuccess) {
-    std::vector<float> temb((size_t)dims->num_steps * kWidth);
-    for (int s = 0; s < dims->num_steps; ++s)
-      sinusoid(c->ts[s], kWidth, dims->time_min_period, dims->time_max_period, &temb[(size_t)s * kWidth]);
-    ae = hipMemcpy(c->temb, temb.data(), p.temb, hipMemcpyHostToDevice);
   }
   if (ae != hipSuccess) {
     g_last_error = std::string("context allocation failed: ") + hipGetErrorString(ae);
@@ -850,26 +920,22 @@ int pi05_refresh_weights(pi05_ctx* c, void* stream) {
   HIPCHK(c, hipMemcpyAsync(heads_in_b(c), hb.in_b, (size_t)kWidth * 4, hipMemcpyDeviceToDevice, st));
   HIPCHK(c, hipMemcpyAsync(heads_out_b(c), hb.out_b, (size_t)kActDim * 4, hipMemcpyDeviceToDevice, st));
   // adaRMS modulation table (engine.py:578-599): cond = silu(W2 silu(W1 temb + b1) + b2),
-  // table[s][n] = dense_n(cond[s]).
+  // table[s][n] = dense_n(cond[s]); the same kernels as pi05_adarms_table_noalloc
   const int S = c->d.num_steps;
-  GemvArgs g1{hb.tin_w, hb.tin_b, c->temb, c->cond1, kWidth, kWidth, S, kWidth, 0, 1};
-  HIPCHK(c, launch_gemv_rows(g1, st));
-  GemvArgs g2{hb.tout_w, hb.tout_b, c->cond1, c->cond, kWidth, kWidth, S, kWidth, 0, 1};
-  HIPCHK(c, launch_gemv_rows(g2, st));
+  std::vector<const float*> dw(p.n_norms), db(p.n_norms);
   for (int n = 0; n < p.n_norms; ++n) {
-    const float* w;
-    const float* b;
     if (n == p.n_norms - 1) {
-      w = hb.norm_w;
-      b = hb.norm_b;
+      dw[n] = hb.norm_w;
+      db[n] = hb.norm_b;
     } else {
       const LayerBind& lb = c->layers[n / 2];
-      w = (n & 1) ? lb.ln2_w : lb.ln1_w;
-      b = (n & 1) ? lb.ln2_b : lb.ln1_b;
+      dw[n] = (n & 1) ? lb.ln2_w : lb.ln1_w;
+      db[n] = (n & 1) ? lb.ln2_b : lb.ln1_b;
     }
-    GemvArgs gd{w, b, c->cond, c->table, kModW, kWidth, S, p.n_norms * kModW, n * kModW, 0};
-    HIPCHK(c, launch_gemv_rows(gd, st));
   }
+  const AdarmsTableArgs ta{hb.tin_w, hb.tin_b, hb.tout_w, hb.tout_b, dw.data(), db.data(), p.n_norms, S,
+                           c->d.time_min_period, c->d.time_max_period, c->temb, c->cond1, c->cond, c->table};
+  HIPCHK(c, launch_adarms_table(ta, st));
   HIPCHK(c, launch_scale_plus_one(c->table, c->table_s1, S * p.n_norms, st));
   ShiftBiasArgs sb{c->wpack, c->table, c->bias, c->d.depth, S};
   HIPCHK(c, launch_shift_bias(sb, st));

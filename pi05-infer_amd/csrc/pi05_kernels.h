@@ -179,6 +179,30 @@ hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);
 hipError_t launch_prime_tables(const PrimeTablesArgs& a, int batch, hipStream_t st);
 hipError_t launch_export_invariants(const ExportInvariantsArgs& a, hipStream_t st);
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st);
+// temb[s][0:W/2] = sin(2 pi t_s / period_i), temb[s][W/2:W] = cos(...) in float64, rounded to fp32,
+// periods min_p * (max_p / min_p)^frac_i over the float64 device linspace(0, 1, W/2)
+// (pi0_pytorch.py:29-46), t_s the Euler schedule of num_steps steps (engine.py:411-429) computed
+// on the device with the host's fp32 operations (bit-identical to euler_schedule on the host).
+hipError_t launch_time_embedding(int num_steps, float* temb, double min_p, double max_p, hipStream_t st);
+
+// The adaRMS modulation table (engine.py:578-599) from the time MLP and the 2*depth+1 norm dense
+// layers: temb -> cond1 = silu(W1 temb + b1) -> cond = silu(W2 cond1 + b2) -> table[s][n] =
+// dense_n(cond[s]).  temb / cond1 / cond: caller-provided scratch of num_steps * W floats each.
+struct AdarmsTableArgs {
+  const float* tin_w;
+  const float* tin_b;
+  const float* tout_w;
+  const float* tout_b;
+  const float* const* dense_w;  // host array of n_norms device pointers [3W, W]
+  const float* const* dense_b;  // host array of n_norms device pointers [3W]
+  int n_norms, num_steps;
+  double min_period, max_period;
+  float* temb;
+  float* cond1;
+  float* cond;
+  float* table;  // [num_steps][n_norms][3W]
+};
+hipError_t launch_adarms_table(const AdarmsTableArgs& a, hipStream_t st);
 // out[r] = in[r] with 1 + scale in place of scale, for rows of [3W] modulation (scale | shift | gate)
 hipError_t launch_scale_plus_one(const float* in, float* out, int rows, hipStream_t st);
 hipError_t launch_step_io(const StepIoArgs& a, hipStream_t st);

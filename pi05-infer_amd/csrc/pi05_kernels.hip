@@ -726,6 +726,52 @@ hipError_t launch_export_invariants(const ExportInvariantsArgs& a, hipStream_t s
   return hipGetLastError();
 }
 
+// Euler timestep s of num_steps: linspace(1, 1/N, N) ++ [0] in fp32 as the elementwise GPU
+// linspace evaluates it (engine.py:411-429), with the same correctly rounded fp32 operations as
+// the host's euler_schedule.
+__device__ float euler_timestep(int n, int s) {
+  if (s >= n) return 0.f;
+  if (n == 1) return 1.f;
+  const float start = 1.0f, end = (float)(1.0 / (double)n);
+  const float step = __fdiv_rn(__fsub_rn(end, start), (float)(n - 1));
+  return s < n / 2 ? __fadd_rn(start, __fmul_rn(step, (float)s)) : __fsub_rn(end, __fmul_rn(step, (float)(n - s - 1)));
+}
+
+// One thread per (step, frequency): the linspace element in the GPU kernel's two-sided form,
+// the period, then sin and cos of the float64 argument, each rounded to fp32 once.
+__global__ void time_embedding_kernel(int S, float* __restrict__ temb, double min_p, double max_p) {
+  constexpr int half = kWidth / 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * half) return;
+  const int s = i / half, f = i % half;
+  const double step = 1.0 / (double)(half - 1);
+  const double frac = f < half / 2 ? step * (double)f : 1.0 - step * (double)(half - f - 1);
+  const double period = min_p * pow(max_p / min_p, frac);
+  const double arg = (1.0 / period * 2.0 * M_PI) * (double)euler_timestep(S, s);
+  temb[(size_t)s * kWidth + f] = (float)sin(arg);
+  temb[(size_t)s * kWidth + half + f] = (float)cos(arg);
+}
+
+hipError_t launch_time_embedding(int num_steps, float* temb, double min_p, double max_p, hipStream_t st) {
+  const int n = num_steps * (kWidth / 2);
+  time_embedding_kernel<<<(n + 255) / 256, 256, 0, st>>>(num_steps, temb, min_p, max_p);
+  return hipGetLastError();
+}
+
+hipError_t launch_adarms_table(const AdarmsTableArgs& a, hipStream_t st) {
+  hipError_t e = launch_time_embedding(a.num_steps, a.temb, a.min_period, a.max_period, st);
+  if (e != hipSuccess) return e;
+  const GemvArgs g1{a.tin_w, a.tin_b, a.temb, a.cond1, kWidth, kWidth, a.num_steps, kWidth, 0, 1};
+  if ((e = launch_gemv_rows(g1, st)) != hipSuccess) return e;
+  const GemvArgs g2{a.tout_w, a.tout_b, a.cond1, a.cond, kWidth, kWidth, a.num_steps, kWidth, 0, 1};
+  if ((e = launch_gemv_rows(g2, st)) != hipSuccess) return e;
+  for (int n = 0; n < a.n_norms; ++n) {
+    const GemvArgs gd{a.dense_w[n], a.dense_b[n], a.cond, a.table, kModW, kWidth, a.num_steps, a.n_norms * kModW, n * kModW, 0};
+    if ((e = launch_gemv_rows(gd, st)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_gemv_rows(const GemvArgs& a, hipStream_t st) {
   gemv_rows_kernel<<<(a.rows + 3) / 4, 256, 0, st>>>(a);
   return hipGetLastError();

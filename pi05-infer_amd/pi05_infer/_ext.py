@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "pi05_get_schedule",
     "pi05_launches_per_step",
     "pi05_bench_kernel",
+    "pi05_adarms_table_noalloc",
     "pi05_euler_schedule",
     "pi05_time_embedding",
     "pi05_rope_inv_freq",
@@ -178,6 +179,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_get_schedule": (i32, [vp]),
         "pi05_launches_per_step": (i32, [vp]),
         "pi05_bench_kernel": (i32, [vp, i32, i32, i32, vp]),
+        "pi05_adarms_table_noalloc": (i32, [dims_p, vp, vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp, vp]),
         "pi05_euler_schedule": (i32, [i32, vp]),
         "pi05_time_embedding": (i32, [dims_p, ctypes.c_float, vp]),
         "pi05_rope_inv_freq": (i32, [dims_p, vp]),
@@ -241,6 +243,27 @@ def check_dims(dims: Pi05Dims) -> None:
 
 def device_bytes(dims: Pi05Dims) -> int:
     return int(load_library().pi05_ctx_device_bytes(ctypes.byref(dims)))
+
+
+def adarms_table_noalloc(dims: Pi05Dims, tin_w, tin_b, tout_w, tout_b, dense_w: Sequence[torch.Tensor],
+                         dense_b: Sequence[torch.Tensor], out: torch.Tensor, stream=None) -> torch.Tensor:
+    """pi05_adarms_table_noalloc: the modulation table from caller-owned fp32 device tensors into
+    ``out`` ``[num_steps, 2*depth+1, 3W]`` fp32, with no device allocation by the library."""
+    lib = load_library()
+    n = 2 * dims.depth + 1
+    if len(dense_w) != n or len(dense_b) != n:
+        raise ValueError(f"need {n} dense weights and biases")
+    dev = out.device
+    f32 = torch.float32
+    if tuple(out.shape) != (dims.num_steps, n, 3 * dims.width):
+        raise ValueError("out shape mismatch")
+    wp = (ctypes.c_void_p * n)(*[_ptr(t, f32, "dense_w", dev) for t in dense_w])
+    bp = (ctypes.c_void_p * n)(*[_ptr(t, f32, "dense_b", dev) for t in dense_b])
+    rc = lib.pi05_adarms_table_noalloc(ctypes.byref(dims), _ptr(tin_w, f32, "tin_w", dev), _ptr(tin_b, f32, "tin_b", dev),
+                                       _ptr(tout_w, f32, "tout_w", dev), _ptr(tout_b, f32, "tout_b", dev), wp, bp,
+                                       _ptr(out, f32, "out", dev), _stream_ptr(stream))
+    _check(lib, rc, None)
+    return out
 
 
 def euler_schedule(num_steps: int) -> torch.Tensor:
