@@ -1,5 +1,10 @@
-"""Build libpi05_denoise.so for gfx950 with hipcc (in-tree, next to the Python package), and the
-C-ABI benchmark driver ``denoise_bench`` linked against it.
+"""Build the gfx950 libraries with hipcc (in-tree, next to the Python package) and the C-ABI
+benchmark driver ``denoise_bench``.
+
+* ``libpi05_denoise.so``: the denoise engine (include/pi05_denoise.h), hand-written kernels only;
+* ``libpi05_prefix.so``: the prefix prefill and the vision tower (include/pi05_prefill.h,
+  include/pi05_siglip.h), whose plain GEMMs run on hipBLASLt -- the only library that links it, so
+  a denoise-only process never loads hipBLASLt.
 
     python pi05-infer_amd/build_lib.py [--verbose]
 """
@@ -15,8 +20,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
-SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip", "pi05_prefill.hip", "pi05_siglip.hip"]
-LIBS = ["-lhipblaslt"]  # the plain GEMMs of the prefill and the vision tower
+SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_engine.hip"]
+PREFIX_OUT = os.path.join(HERE, "pi05_infer", "libpi05_prefix.so")
+PREFIX_SOURCES = ["pi05_prefill.hip", "pi05_siglip.hip"]
+PREFIX_LIBS = ["-lhipblaslt"]  # the plain GEMMs of the prefill and the vision tower
 BENCH_SRC = "denoise_bench.hip"
 BENCH_OUT = os.path.join(HERE, "pi05_infer", "denoise_bench")
 
@@ -50,9 +57,12 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], *LIBS, "-o",
+    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES], "-o",
           OUT + ".tmp"], verbose)
     os.replace(OUT + ".tmp", OUT)
+    _run([hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in PREFIX_SOURCES], *PREFIX_LIBS,
+          "-o", PREFIX_OUT + ".tmp"], verbose)
+    os.replace(PREFIX_OUT + ".tmp", PREFIX_OUT)
     bench_flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
     _run([hipcc(), *bench_flags, f"-I{INCLUDE}", os.path.join(CSRC, BENCH_SRC), f"-L{os.path.dirname(OUT)}", "-lpi05_denoise",
           "-Wl,-rpath,$ORIGIN", "-o", BENCH_OUT + ".tmp"], verbose)

@@ -1,8 +1,9 @@
-"""ctypes binding of ``libpi05_denoise.so`` (the C ABIs in ``include/pi05_denoise.h``,
-``include/pi05_prefill.h`` and ``include/pi05_siglip.h``).
+"""ctypes bindings of ``libpi05_denoise.so`` (the C ABI in ``include/pi05_denoise.h``) and
+``libpi05_prefix.so`` (``include/pi05_prefill.h`` and ``include/pi05_siglip.h``, loaded on first
+use, so a denoise-only process never loads hipBLASLt).
 
-The shared library is built in-tree next to this file (``build_lib.py``).  There is no fallback:
-if the library is missing or fails to load, every entry point raises.
+The shared libraries are built in-tree next to this file (``build_lib.py``).  There is no
+fallback: if a library is missing or fails to load, every entry point of it raises.
 """
 
 from __future__ import annotations
@@ -15,6 +16,8 @@ import torch
 
 LIB_NAME = "libpi05_denoise.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+PREFIX_LIB_NAME = "libpi05_prefix.so"
+PREFIX_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), PREFIX_LIB_NAME)
 ABI_VERSION = 1
 
 PI05_OK = 0
@@ -140,6 +143,7 @@ class Pi05VisionDims(ctypes.Structure):
 
 
 _lib: Optional[ctypes.CDLL] = None
+_prefix_lib: Optional[ctypes.CDLL] = None
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -155,8 +159,6 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib = ctypes.CDLL(path)
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     dims_p = ctypes.POINTER(Pi05Dims)
-    pdims_p = ctypes.POINTER(Pi05PrefixDims)
-    vdims_p = ctypes.POINTER(Pi05VisionDims)
     sig = {
         "pi05_abi_version": (i32, []),
         "pi05_default_dims": (None, [dims_p]),
@@ -183,6 +185,32 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_euler_schedule": (i32, [i32, vp]),
         "pi05_time_embedding": (i32, [dims_p, ctypes.c_float, vp]),
         "pi05_rope_inv_freq": (i32, [dims_p, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.pi05_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_NAME} ABI {lib.pi05_abi_version()} != expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def load_prefix_library(path: str = PREFIX_LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and type the prefill / vision library; raises if it is absent."""
+    global _prefix_lib
+    if _prefix_lib is not None:
+        return _prefix_lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{PREFIX_LIB_NAME} not found at {path}; build it first (python pi05-infer_amd/build_lib.py). "
+            "There is no fallback implementation."
+        )
+    lib = ctypes.CDLL(path)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    pdims_p = ctypes.POINTER(Pi05PrefixDims)
+    vdims_p = ctypes.POINTER(Pi05VisionDims)
+    sig = {
         "pi05_prefix_default_dims": (None, [pdims_p]),
         "pi05_prefix_check_dims": (i32, [pdims_p]),
         "pi05_prefix_device_bytes": (ctypes.c_size_t, [pdims_p]),
@@ -208,9 +236,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.pi05_abi_version() != ABI_VERSION:
-        raise RuntimeError(f"{LIB_NAME} ABI {lib.pi05_abi_version()} != expected {ABI_VERSION}")
-    _lib = lib
+    _prefix_lib = lib
     return lib
 
 
@@ -460,26 +486,26 @@ def _check_prefix(lib: ctypes.CDLL, rc: int, ctx: Optional[int]) -> None:
 
 
 def prefix_default_dims() -> Pi05PrefixDims:
-    lib = load_library()
+    lib = load_prefix_library()
     d = Pi05PrefixDims()
     lib.pi05_prefix_default_dims(ctypes.byref(d))
     return d
 
 
 def prefix_check_dims(dims: Pi05PrefixDims) -> None:
-    lib = load_library()
+    lib = load_prefix_library()
     _check_prefix(lib, lib.pi05_prefix_check_dims(ctypes.byref(dims)), None)
 
 
 def prefix_device_bytes(dims: Pi05PrefixDims) -> int:
-    return int(load_library().pi05_prefix_device_bytes(ctypes.byref(dims)))
+    return int(load_prefix_library().pi05_prefix_device_bytes(ctypes.byref(dims)))
 
 
 class PrefixContext:
     """One prefix-LM prefill context: a (batch, prefix_len) signature on the current device."""
 
     def __init__(self, dims: Pi05PrefixDims, device: torch.device):
-        self.lib = load_library()
+        self.lib = load_prefix_library()
         self.dims = dims
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:
@@ -566,26 +592,26 @@ def _check_vision(lib: ctypes.CDLL, rc: int, ctx: Optional[int]) -> None:
 
 
 def vision_default_dims() -> Pi05VisionDims:
-    lib = load_library()
+    lib = load_prefix_library()
     d = Pi05VisionDims()
     lib.pi05_vision_default_dims(ctypes.byref(d))
     return d
 
 
 def vision_check_dims(dims: Pi05VisionDims) -> None:
-    lib = load_library()
+    lib = load_prefix_library()
     _check_vision(lib, lib.pi05_vision_check_dims(ctypes.byref(dims)), None)
 
 
 def vision_device_bytes(dims: Pi05VisionDims) -> int:
-    return int(load_library().pi05_vision_device_bytes(ctypes.byref(dims)))
+    return int(load_prefix_library().pi05_vision_device_bytes(ctypes.byref(dims)))
 
 
 class VisionContext:
     """One SigLIP + projector context: an image count on the current device."""
 
     def __init__(self, dims: Pi05VisionDims, device: torch.device):
-        self.lib = load_library()
+        self.lib = load_prefix_library()
         self.dims = dims
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:

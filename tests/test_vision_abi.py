@@ -18,7 +18,7 @@ HEADER = os.path.join(ROOT, "include", "pi05_siglip.h")
 
 @pytest.fixture(scope="module")
 def lib():
-    return _ext.load_library()
+    return _ext.load_prefix_library()
 
 
 def header_functions():
@@ -31,7 +31,7 @@ def test_header_and_binding_agree():
 
 
 def test_library_exports_every_declared_symbol(lib):
-    out = subprocess.run(["nm", "-D", "--defined-only", _ext.LIB_PATH], capture_output=True, text=True).stdout
+    out = subprocess.run(["nm", "-D", "--defined-only", _ext.PREFIX_LIB_PATH], capture_output=True, text=True).stdout
     exported = set(re.findall(r"\bT (pi05_\w+)", out))
     for name in header_functions():
         assert hasattr(lib, name) and name in exported, name
