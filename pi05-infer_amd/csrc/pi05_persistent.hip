@@ -636,6 +636,15 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(norm_w_tile<kModeQkv>(a, l, 1) + 31 * 512 + lane * 8));
     if (rope_thread) load_rope(0);
   }
+  // the item's shift . W^T columns (static within the launch), by wave 1 ahead of the polls and
+  // straight into LDS: the work area is free (every wave passed the previous phase's last
+  // barrier) and the wait's barrier orders the stores before their readers
+  if (tid >= 64 && tid < 96) {
+    const int c = tid - 64;
+    const int col = MODE == kModeQkv ? (c < 16 ? tile0 * 16 + c : (rotated ? tile0 + 8 : tile0 + 1) * 16 + c - 16)
+                                     : (c < 16 ? kQkvCols + tile0 * 16 + c : kQkvCols + kMlp + tile0 * 16 + c - 16);
+    s_bias[c] = bias[col];
+  }
   PHASE_TS(s, l, PH, 1);
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
@@ -643,12 +652,6 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     if (!wait_flags(a, dep, ndep, s_flag)) return false;
   }
   PHASE_TS(s, l, PH, 2);
-  // the item's shift . W^T columns (static within the launch; loaded here, not ahead of the polls)
-  if (tid < 32) {
-    const int col = MODE == kModeQkv ? (tid < 16 ? tile0 * 16 + tid : (rotated ? tile0 + 8 : tile0 + 1) * 16 + tid - 16)
-                                     : (tid < 16 ? kQkvCols + tile0 * 16 + tid : kQkvCols + kMlp + tile0 * 16 + tid - 16);
-    s_bias[tid] = bias[col];
-  }
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
   for (int b = 0; b < a.batch; ++b) {
     const int m0 = b * kRowsPerSample;
