@@ -164,6 +164,30 @@ Plan make_plan(const pi05_dims& d) {
   return p;
 }
 
+// The persistent kernel addresses each per-(step, layer) slice through a buffer resource whose
+// byte offset is a 32-bit VGPR (signed in its bounds arithmetic): the largest such window of a
+// plan must stay below 2^31 bytes.  The windows, as the kernel builds them: the A operands of the
+// norm GEMMs (g / gmid rows) and of down_proj (the GeGLU rows), the query and K/V-tail stores, the
+// attention split partials and their (m, l) pairs, the down K-quarter partials, the row
+// statistics, and one phase instance's replicated flags.
+size_t max_offset_window(const Plan& p, const pi05_dims& d) {
+  const size_t R = p.R;
+  const size_t w[] = {
+      R * kWidth * 2,                                         // g, gmid, h slices
+      R * kMlp * 2,                                           // act slice
+      R * kQRowsPerTok * kHeadDim * 2,                        // q slice
+      (size_t)d.batch * 64 * kHeadDim * 2,                    // K/V tail slice
+      (size_t)p.nsplit_p * p.nbp * 16 * kHeadDim * 4,         // attention split partials
+      (size_t)p.nsplit_p * p.nbp * 32 * 4,                    // their (m, l) pairs
+      (size_t)4 * (kWidth / 16) * R * 16 * 4,                 // down K-quarter partials
+      (size_t)kRowSlots * R * 4,                              // row statistics slice
+      (size_t)kFlagCopies * p.fstride * 4,                    // one phase instance's flags
+  };
+  size_t m = 0;
+  for (size_t v : w) m = std::max(m, v);
+  return m;
+}
+
 bool check_dims_msg(const pi05_dims* d, std::string* msg) {
   char buf[256];
   if (!d) {
@@ -194,6 +218,11 @@ bool check_dims_msg(const pi05_dims* d, std::string* msg) {
   REQ(std::isfinite(d->time_min_period) && d->time_min_period > 0.0 && std::isfinite(d->time_max_period) &&
           d->time_max_period > d->time_min_period,
       "time periods must satisfy 0 < min_period < max_period");
+  {
+    const size_t win = max_offset_window(make_plan(*d), *d);
+    REQ(win < ((size_t)1 << 31), "batch %d x prefix_len %d needs a %zu-byte slice, beyond the kernel's 32-bit offsets", d->batch,
+        d->prefix_len, win);
+  }
 #undef REQ
   return true;
 }

@@ -107,6 +107,23 @@ def test_device_bytes_covers_weights_and_cache(lib):
     assert _ext.device_bytes(d8) > got
 
 
+def test_largest_dims_fit_the_kernel_32bit_offsets(lib):
+    """pi05_check_dims rejects dims whose largest per-(step, layer) slice reaches 2^31 bytes (the
+    persistent kernel's buffer offsets are 32-bit).  At the largest accepted dims (64 samples,
+    16384 prefix tokens) the largest window is the attention split partials: 16 key splits x
+    64 * 25 two-token row blocks x 16 rows x 256 fp32 = 400 MiB; the GeGLU rows are 64 * 64 rows x
+    4096 bf16 = 32 MiB."""
+    d = _ext.default_dims()
+    d.batch, d.prefix_len, d.num_steps = 64, 16384, 32
+    _ext.check_dims(d)
+    assert 16 * 64 * 25 * 16 * 256 * 4 == 400 * 2**20 < 2**31
+    # the whole plan at those dims exceeds one GPU's 288 GB: creating it fails with a HIP
+    # out-of-memory error, not in the kernel
+    assert _ext.device_bytes(d) > 288e9
+    d.num_steps = 10
+    assert _ext.device_bytes(d) < 288e9
+
+
 def test_null_handles_and_pointers_are_invalid(lib):
     vp = ctypes.c_void_p
     assert lib.pi05_bind_layer(None, 0, *([None] * 11)) == -1
