@@ -137,6 +137,21 @@ __device__ __forceinline__ bool copy_wave() { return threadIdx.x >= kCompThreads
 // before it in program order stays before it, so its completion is what the wait observes.
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier that orders LDS only: each wave's LDS operations complete, then s_barrier; the
+// empty asm statements keep the compiler from moving memory operations across it.  Unlike
+// __syncthreads() it carries no workgroup-scope fence, whose release half makes every wave with a
+// vector load in flight wait for it (vmcnt(0)) before the barrier -- and a wave's vector memory
+// operations complete in issue order, so that wait also covers the copy wave's whole direct-to-LDS
+// burst, the poller's second poll and its earlier flag stores.  Uses that need global memory or
+// a direct-to-LDS copy complete wait for it explicitly before the barrier (publish, the phase
+// tops that consume copied weights, the query fragments of the attention splits).
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt not waited for
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Operand blocks are loaded with the compiler's own buffer loads (so it counts them) and fenced
 // with a scheduling barrier after the last one: the scheduler may not sink a load next to its
 // use, so a whole block is in flight at once and each MFMA waits only for its own fragments.
@@ -231,17 +246,19 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
     }
     if (lane == 0) *s_flag = ok;
   }
-  __syncthreads();
+  wg_barrier();
   const bool ok = *s_flag != 0;
-  __syncthreads();
+  wg_barrier();
   return ok;
 }
 
-// The compute waves' stores for this item are complete -> wave 0 sets the item's flag in every
-// replica.  Every thread of the workgroup calls it (it holds a barrier).
-__device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsigned epoch) {
-  if (!copy_wave()) wait_stores();
-  __syncthreads();
+// The stores of this item are complete (the compute waves', and the copy wave's when
+// `copy_stores`: it waits only then, since its stores complete behind its direct-to-LDS copies)
+// -> wave 0 sets the item's flag in every replica.  Every thread of the workgroup calls it (it
+// holds a barrier).
+__device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsigned epoch, bool copy_stores = false) {
+  if (!copy_wave() || copy_stores) wait_stores();
+  wg_barrier();
   if (threadIdx.x < kFlagCopies) st_u32(flag + (size_t)threadIdx.x * a.fstride, epoch);
 }
 
@@ -250,7 +267,7 @@ __device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsig
 // (an intra-XCD hand-off: 0.69 us against ~1 us through the memory side, measured on MI355X).
 __device__ __forceinline__ void publish_local(const MegaArgs& a, unsigned* flag, unsigned epoch) {
   if (!copy_wave()) wait_stores();
-  __syncthreads();
+  wg_barrier();
   if (threadIdx.x == 0) {
     const brsrc r = make_rsrc(uniform_ptr(flag + (size_t)(blockIdx.x % kFlagCopies) * a.fstride), 4);
     __builtin_amdgcn_raw_buffer_store_b32(epoch, r, 0, 0, 0);
@@ -1006,7 +1023,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       }
     }
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 5);
-    publish(a, fsplit + bp * a.nsplit_pad + split, a.epoch);
+    publish(a, fsplit + bp * a.nsplit_pad + split, a.epoch, true);  // the copy wave stored d-tiles 12..15
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
     __syncthreads();  // the LDS tiles are reused by the next item
   }
