@@ -130,6 +130,15 @@ Plan make_plan(const pi05_dims& d) {
   const int nkb = p.s_pre / 32 + 2;
   p.nsplit_p = (nkb + 3) / 4;
   if (p.nsplit_p > kMaxAttnSplits) p.nsplit_p = kMaxAttnSplits;
+  {
+    // large batches: when the split items would take more than 4 passes of the 256 workgroups,
+    // use just enough splits to fill them once -- each split item has a fixed cost (query load,
+    // wave merge, partial store, publish) that more keys per item amortize (B = 8, P = 968:
+    // 2 splits, 25.9 ms/predict against 27.1 with 9; at B <= 2 and at P = 3272 fewer splits are
+    // slower, so the rule leaves them alone)
+    const int nbp = d.batch * (kHorizon / 2), fill = (256 + nbp - 1) / nbp;
+    if (nbp * p.nsplit_p > 4 * 256 && p.nsplit_p > fill) p.nsplit_p = fill;
+  }
   p.nsplit_pad = (p.nsplit_p + 3) / 4 * 4;
   p.R = 64 * d.batch;
   p.nbp = d.batch * (kHorizon / 2);

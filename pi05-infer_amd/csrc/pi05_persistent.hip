@@ -221,8 +221,10 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
     const int lane = threadIdx.x;
     const unsigned ep = a.epoch;
     int ok = 1;
-    // two coherent (sc1) 16-byte polls in flight, issued back to back (measured: sleeping between
-    // polls costs ~0.1 us per wait): a completion is seen one load latency after it lands
+    // one coherent (sc1) 16-byte poll in flight at a time: measured on MI355X, keeping a second
+    // poll in flight (staggered by half a round trip) makes the whole predict ~4% slower -- poll
+    // traffic on the flag lines delays the flag stores it waits for.  The compiler barrier keeps
+    // every poll a fresh load.
     const brsrc rf = make_rsrc(f, (size_t)a.fstride * 4);
     for (int base = 0; base < n && ok; base += 256) {
       const int i0 = base + lane * 4;
@@ -230,18 +232,15 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
       auto done = [&](u32x4 v) {
         return i0 >= n || (v[0] == ep && (i0 + 1 >= n || v[1] == ep) && (i0 + 2 >= n || v[2] == ep) && (i0 + 3 >= n || v[3] == ep));
       };
-      u32x4 va = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
-      for (int spins = 0;; spins += 2) {
-        u32x4 vb = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
-        if (__all(done(va))) break;
-        va = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
-        if (__all(done(vb))) break;
-        if (spins > a.spin_limit || ((spins & 63) == 62 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
+      for (int spins = 0;; ++spins) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
+        if (__all(done(v))) break;
+        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
           if (lane == 0) record_error(a);
           ok = 0;
           break;
         }
-        asm volatile("" ::: "memory");  // every poll is a fresh load
+        asm volatile("" ::: "memory");
       }
     }
     if (lane == 0) *s_flag = ok;
