@@ -76,13 +76,21 @@ __device__ __forceinline__ void load_kv_block(KvBlock& blk, const u16* kc, const
   blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + 16 + g * 4);
 }
 
-__device__ __forceinline__ void attend_block(const KvBlock& blk, const bf16x8 (&qf)[8], float& m_run, float& l_run, f32x4 (&oacc)[16]) {
+// One 32-key block of the online-softmax MQA attention for a 16-row query m-tile (2 tokens x 8
+// heads sharing the KV head).  S^T = K Q^T on MFMA (two 16-key tiles), scores bf16(q.k) * 1/16
+// (exact in bf16) with masked keys at -inf (modeling_gemma.py:265-268), the running max / sum
+// update, P rounded to bf16 before P.V, and O^T = V^T P^T accumulated per 16-dim tile; the V
+// fragments' key order (vkey) makes P^T exactly the S^T accumulator each lane holds.  qfrag(ds)
+// returns the query fragment of d-step ds (from registers or from LDS, as the caller keeps it).
+template <class QF>
+__device__ __forceinline__ void attend_block_q(const KvBlock& blk, QF qfrag, float& m_run, float& l_run, f32x4 (&oacc)[16]) {
   f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int ds = 0; ds < 8; ++ds) {
+    const bf16x8 qf = qfrag(ds);
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) sacc[t] = mfma16x16x32(blk.k[t * 8 + ds], qf[ds], sacc[t]);
-  // scores: bf16(q.k) * 1/16 (exact in bf16); masked keys -> -inf (modeling_gemma.py:265-268)
+    for (int t = 0; t < 2; ++t) sacc[t] = mfma16x16x32(blk.k[t * 8 + ds], qf, sacc[t]);
+  }
   float s[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -119,6 +127,11 @@ __device__ __forceinline__ void attend_block(const KvBlock& blk, const bf16x8 (&
     oacc[dt] *= alpha;
     oacc[dt] = mfma16x16x32(blk.v[dt], pfrag, oacc[dt]);
   }
+}
+
+// The same with the query fragments in registers.
+__device__ __forceinline__ void attend_block(const KvBlock& blk, const bf16x8 (&qf)[8], float& m_run, float& l_run, f32x4 (&oacc)[16]) {
+  attend_block_q(blk, [&](int ds) { return qf[ds]; }, m_run, l_run, oacc);
 }
 
 }  // namespace pi05

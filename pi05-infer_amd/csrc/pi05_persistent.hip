@@ -820,50 +820,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
 // One 32-key block with the query fragments read from LDS (sq: 8 fragments, 1 KiB each).
 __device__ __forceinline__ void attend_block_lds(const KvBlock& blk, const u16* sq, int lane, float& m_run, float& l_run,
                                                  f32x4 (&oacc)[16]) {
-  f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-  for (int ds = 0; ds < 8; ++ds) {
-    const bf16x8 qf = *reinterpret_cast<const bf16x8*>(sq + ds * 512 + lane * 8);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) sacc[t] = mfma16x16x32(blk.k[t * 8 + ds], qf, sacc[t]);
-  }
-  // scores: bf16(q.k) * 1/16 (exact in bf16); masked keys -> -inf (modeling_gemma.py:265-268)
-  float s[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s[i] = ((blk.valid0 >> (8 * i)) & 0xff) ? round_bf(sacc[0][i]) * 0.0625f : -INFINITY;
-    s[4 + i] = ((blk.valid1 >> (8 * i)) & 0xff) ? round_bf(sacc[1][i]) * 0.0625f : -INFINITY;
-  }
-  float bm = s[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
-  const float m_new = fmaxf(m_run, bm);
-  float alpha = 1.f;
-  float e[8];
-  if (m_new == -INFINITY) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = 0.f;
-  } else {
-    alpha = __expf(m_run - m_new);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = __expf(s[i] - m_new);
-  }
-  float esum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) esum += e[i];
-  l_run = l_run * alpha + esum;
-  m_run = m_new;
-  u16x8 pf;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) pf[i] = f2bf(e[i]);
-  const bf16x8 pfrag = as_bf16x8(pf);
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt) {
-    oacc[dt] *= alpha;
-    oacc[dt] = mfma16x16x32(blk.v[dt], pfrag, oacc[dt]);
-  }
+  attend_block_q(blk, [&](int ds) { return *reinterpret_cast<const bf16x8*>(sq + ds * 512 + lane * 8); }, m_run, l_run, oacc);
 }
 
 __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
