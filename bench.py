@@ -399,6 +399,34 @@ def algorithmic_bytes_per_predict(depth: int, batch: int, prefix_len: int, steps
     return steps * (weights + kv + mod + heads + x)
 
 
+def algorithmic_flops_per_predict(depth: int, batch: int, prefix_len: int, steps: int) -> int:
+    """FLOPs of one predict: per step the expert GEMMs over the 50 action rows of each sample, the
+    MQA attention (8 heads of 256 over prefix + action keys: Q.K^T and P.V) and the fp32 action
+    in/out projections."""
+    W, H, D, I, A, a = 1024, 8, 256, 4096, 50, 32
+    rows = A * batch
+    per_layer = (H + 2) * D * W + W * H * D + 2 * I * W + W * I
+    gemm = 2 * rows * per_layer * depth
+    attn = 4 * H * rows * D * (prefix_len + A) * depth
+    heads = 2 * rows * a * W * 2
+    return steps * (gemm + attn + heads)
+
+
+def roofline_entry(schedule, mfma_bound, gbs, nbytes, tflops, flops, launch_us, traffic) -> dict:
+    """The bench line's roofline: HBM at B = 1 (60-81 FLOP/B), MFMA where the arithmetic intensity
+    passes the ridge (B = 8: 400 FLOP/B); the other side is reported beside it."""
+    hbm = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes_per_launch": nbytes}
+    mfma = {"achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops}
+    main, other = (mfma, ("hbm", hbm)) if mfma_bound else (hbm, ("mfma", mfma))
+    out = {"kernel": "denoise_loop_kernel (whole predict, one launch)" if schedule == "persistent"
+           else "whole predict (one hipGraph replay)", "bound": "mfma" if mfma_bound else "hbm"}
+    out.update(main)
+    out.update({"traffic": traffic, "avg_launch_us": round(launch_us, 2), other[0]: other[1]})
+    return out
+
+
 def host_threads() -> int:
     """CPU threads for the CPU baseline: the cores this process may run on (its affinity set, which
     is the host's CPU share where the scheduler restricts it), capped by OMP_NUM_THREADS when set."""
@@ -511,6 +539,10 @@ def main() -> int:
     pred_bytes = algorithmic_bytes_per_predict(g.depth, B, P, steps)
     launch_us = ms_per_predict * 1e3
     pred_gbs = pred_bytes / (launch_us * 1e-6) / 1e9
+    # the MFMA side of the roofline (the bound at B = 8: 400 FLOP/B against a ridge of ~315)
+    pred_flops = algorithmic_flops_per_predict(g.depth, B, P, steps)
+    pred_tflops = pred_flops / (launch_us * 1e-6) / 1e12
+    mfma_bound = pred_flops / pred_bytes > BF16_PEAK_TFLOPS / HBM_PEAK_GBS * 1e3
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -561,18 +593,7 @@ def main() -> int:
             "schedule": schedule,
             "launches_per_step": ctx.launches_per_step(),
         },
-        "roofline": {
-            "kernel": "denoise_loop_kernel (whole predict, one launch)" if schedule == "persistent"
-                      else "whole predict (one hipGraph replay)",
-            "bound": "hbm",
-            "achieved": round(pred_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(pred_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "avg_launch_us": round(launch_us, 2),
-            "algorithmic_bytes_per_launch": pred_bytes,
-        },
+        "roofline": roofline_entry(schedule, mfma_bound, pred_gbs, pred_bytes, pred_tflops, pred_flops, launch_us, traffic),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -134,23 +134,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y
 // v] (ldq = 2560), or [k | v] (ldq = 512, kv_only).  RoPE in fp32 on the bf16 values with bf16
 // cos/sin of freq = inv_freq[d mod 128] * pos, rounded once (modeling_gemma.py:169-216): q to the
 // attention's A-fragment layout (row = token * 8 + head), k and v to the attention's packed K/V
-// block and to the caller's cache [B, 1, P, D].
+// block and to the caller's cache [B, 1, P, D].  The cos/sin values depend on the position only
+// (a position is in [-1, P): leading pad tokens sit at cumsum - 1 = -1), so rope_table_kernel
+// evaluates them once per context into tab[pos + 1][cos 128 | sin 128] (bf16 bits), and the
+// per-layer kernel only reads them.
 // ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(128) void rope_table_kernel(const float* inv_freq, int P, u16* tab) {
+  const int row = blockIdx.x, d = threadIdx.x, pos = row - 1;
+  if (row > P) return;
+  const float freq = fmul(inv_freq[d], (float)pos);
+  tab[(size_t)row * kHeadDim + d] = f2bf(cosf(freq));
+  tab[(size_t)row * kHeadDim + kHalfDim + d] = f2bf(sinf(freq));
+}
+
 struct RopeKvArgs {
   const u16* qkv;
   int ldq, kv_only, P, s_pad;
   const int* pos;
-  const float* inv_freq;
+  const u16* tab;  // [P + 1][cos 128 | sin 128] bf16 bits, row = position + 1
   u16 *qf, *kf, *vf;   // per sample: q fragments [s_pad*8 rows][256], K / V blocks [s_pad keys][256]
   u16 *kout, *vout;    // caller's cache of this layer
   int64_t kv_bs, kv_rs;
 };
 
-__device__ __forceinline__ void rope4(const u16* src, float pos, const float* inv_freq, int lo, u16 (&olo)[4], u16 (&ohi)[4]) {
+__device__ __forceinline__ void rope4(const u16* src, const u16* cs, int lo, u16 (&olo)[4], u16 (&ohi)[4]) {
+  const u16x4 c4 = *reinterpret_cast<const u16x4*>(cs + lo), s4 = *reinterpret_cast<const u16x4*>(cs + kHalfDim + lo);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float freq = fmul(inv_freq[lo + i], pos);
-    const float c = round_bf(cosf(freq)), s = round_bf(sinf(freq));
+    const float c = bf2f(c4[i]), s = bf2f(s4[i]);
     const float xl = bf2f(src[lo + i]), xh = bf2f(src[kHalfDim + lo + i]);
     olo[i] = f2bf(fsub(fmul(xl, c), fmul(xh, s)));
     ohi[i] = f2bf(fadd(fmul(xh, c), fmul(xl, s)));
@@ -164,14 +175,14 @@ __device__ __forceinline__ void store4(u16* dst, const u16 (&v)[4]) {
 __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   const int row = blockIdx.x, b = row / a.P, p = row % a.P, t = threadIdx.x;
   const u16* src = a.qkv + (size_t)row * a.ldq;
-  const float pos = (float)a.pos[(size_t)b * a.s_pad + p];
+  const u16* cs = a.tab + (size_t)(a.pos[(size_t)b * a.s_pad + p] + 1) * kHeadDim;
   const u16* ksrc = src + (a.kv_only ? 0 : kPHD);
   const u16* vsrc = ksrc + kHeadDim;
   if (!a.kv_only) {
     // q: thread t -> head t/32, dims 4(t%32) .. +3 and their partners + 128
     const int head = t >> 5, lo = (t & 31) * 4;
     u16 olo[4], ohi[4];
-    rope4(src + head * kHeadDim, pos, a.inv_freq, lo, olo, ohi);
+    rope4(src + head * kHeadDim, cs, lo, olo, ohi);
     u16* qb = a.qf + (size_t)b * a.s_pad * kHeads * kHeadDim;
     const int qrow = p * kHeads + head;
     store4(qb + afrag_index(qrow, lo, kHeadDim / 32), olo);
@@ -181,7 +192,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
   if (t < 32) {
     const int lo = t * 4;
     u16 olo[4], ohi[4];
-    rope4(ksrc, pos, a.inv_freq, lo, olo, ohi);
+    rope4(ksrc, cs, lo, olo, ohi);
     u16* kb = a.kf + (size_t)b * a.s_pad * kHeadDim;
     store4(kb + kfrag_index(p, lo), olo);
     store4(kb + kfrag_index(p, lo + kHalfDim), ohi);
@@ -377,9 +388,9 @@ struct LayerBind {
 // Device layout of one context: sizes in bytes.
 struct PrefixPlan {
   int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0, nsplit = 1;
-  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, err, ws, po, pml, dpart;
+  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, rtab, err, ws, po, pml, dpart;
   size_t total() const {
-    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + err + ws + po + pml + dpart + 16 * 256;
+    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + rtab + err + ws + po + pml + dpart + 17 * 256;
   }
 };
 constexpr size_t kWorkspace = 64ull << 20;
@@ -413,6 +424,7 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   p.pos = rup((size_t)p.B * p.s_pad * 4);
   p.valid = rup((size_t)p.B * p.s_pad);
   p.invf = rup(kHalfDim * 4);
+  p.rtab = rup((size_t)(p.P + 1) * kHeadDim * 2);
   p.err = 256;
   p.ws = kWorkspace;
   const size_t rows = (size_t)p.B * p.n_mt * 16;
@@ -470,6 +482,7 @@ struct pi05_prefix_ctx {
   u16 *w = nullptr, *h = nullptr, *n = nullptr, *y = nullptr, *qkv = nullptr, *attn = nullptr, *gu = nullptr, *act = nullptr;
   u16 *qf = nullptr, *kf = nullptr, *vf = nullptr;
   float *ln = nullptr, *inv_freq = nullptr, *po = nullptr, *pml = nullptr, *dpart = nullptr;
+  u16* rope_tab = nullptr;  // [P + 1][cos | sin] bf16, row = position + 1
   bool down_split = false;  // down_proj as kDownSplits fp32 split-K GEMMs reduced in the residual norm
   bool o_split = false;     // o_proj likewise
   int* pos = nullptr;
@@ -583,6 +596,7 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   c->pos = reinterpret_cast<int*>(take(p.pos));
   c->valid = reinterpret_cast<uint8_t*>(take(p.valid));
   c->inv_freq = reinterpret_cast<float*>(take(p.invf));
+  c->rope_tab = reinterpret_cast<u16*>(take(p.rtab));
   c->err_flag = reinterpret_cast<unsigned*>(take(p.err));
   c->ws = take(p.ws);
   c->po = reinterpret_cast<float*>(take(p.po));
@@ -594,6 +608,11 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   float invf[kHalfDim];
   prefix_inv_freq(dims->rope_theta, invf);
   if (e == hipSuccess) e = hipMemcpy(c->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    rope_table_kernel<<<p.P + 1, kHalfDim>>>(c->inv_freq, p.P, c->rope_tab);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+  }
   if (e != hipSuccess) {
     hipFree(c->base);
     delete c;
@@ -732,7 +751,7 @@ int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* p
     const u16* w = c->w + (size_t)l * kPLayerElems;
     const float* ln = c->ln + (size_t)l * 2 * kPW;
     const bool kv_only = c->d.skip_last_layer && l == p.L - 1;
-    RopeKvArgs ra{c->qkv, kv_only ? kPKvN : kPQkvN, kv_only ? 1 : 0, p.P, p.s_pad, c->pos, c->inv_freq,
+    RopeKvArgs ra{c->qkv, kv_only ? kPKvN : kPQkvN, kv_only ? 1 : 0, p.P, p.s_pad, c->pos, c->rope_tab,
                   c->qf, c->kf, c->vf, static_cast<u16*>(k_layers[l]), static_cast<u16*>(v_layers[l]), kv_batch_stride, kv_row_stride};
     int rc = kv_only ? gemm(c, c->g_kv, w + kPOffQkv + (size_t)kPHD * kPW, c->n, c->qkv, st) : gemm(c, c->g_qkv, w + kPOffQkv, c->n, c->qkv, st);
     if (rc != PI05_OK) return rc;
