@@ -90,6 +90,15 @@ def bench_e2e(args) -> int:
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     assert out["actions"].shape == (B, 50, 32) and bool(torch.isfinite(out["actions"]).all())
+    # host time to enqueue one predict (the call returns before the GPU is done): where it nears
+    # the GPU time, the host's kernel submissions are what paces back-to-back predicts
+    issue = []
+    for _ in range(5):
+        t = time.perf_counter()
+        model.sample_actions(obs, x1)
+        issue.append((time.perf_counter() - t) * 1e3)
+        torch.cuda.synchronize()
+    issue_ms = statistics.median(issue)
 
     # the same predict phase by phase (each phase timed alone, same clock, same inputs)
     imgs, img_masks = list(images.values()), list(masks.values())
@@ -109,7 +118,8 @@ def bench_e2e(args) -> int:
     kv_obs = Observation([k for k, _ in kv], [v for _, v in kv], pads)
     den_ms, _ = timed(lambda: model.sample_actions(kv_obs, x1))
     phases = {"vision_ms": round(vis_ms, 3), "embed_prefix_ms (vision + token embedding + concat)": round(emb_ms, 3),
-              "prefill_ms": round(pre_ms, 3), "denoise_ms (prime + 10 steps)": round(den_ms, 3)}
+              "prefill_ms": round(pre_ms, 3), "denoise_ms (prime + 10 steps)": round(den_ms, 3),
+              "host_issue_ms (one predict enqueued, GPU idle before)": round(issue_ms, 3)}
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -77,10 +77,19 @@ int pi05_prefix_refresh_weights(pi05_prefix_ctx* ctx, void* stream);
 
 /* Language-token embedding of embed_prefix: out[i] = bf16(table[ids[i]] * sqrt(width)) for
  * n_tokens int32 ids (pi0_pytorch.py:225-228).  table [vocab, W] bf16, out [n_tokens, W] bf16.
- * Ids outside [0, vocab) are rejected on the device: the row is zero-filled and the call reports
- * PI05_E_INVALID after synchronising `stream`. */
+ * Enqueues only.  Ids outside [0, vocab) are caught on the device: their rows are zero-filled
+ * and the call's tag goes to a pinned host word; the error is reported as PI05_E_INVALID once,
+ * by the next pi05_prefix_embed_tokens on the context (which then enqueues nothing) or by
+ * pi05_prefix_status.  (The reference's embedding lookup fails asynchronously too, with a
+ * device-side assert.) */
 int pi05_prefix_embed_tokens(pi05_prefix_ctx* ctx, const int32_t* ids, int64_t n_tokens, const void* table,
                              int64_t vocab, void* out, void* stream);
+
+/* Waits for `stream` and reports a token id outside [0, vocab) met by an earlier
+ * pi05_prefix_embed_tokens call on this context that has not been reported yet (PI05_E_INVALID,
+ * once).  No counterpart in the reference (its lookup asserts on the device); call it where the
+ * embeddings must be known good. */
+int pi05_prefix_status(pi05_prefix_ctx* ctx, void* stream);
 
 /* The prefill: embeds [B, P, W] bf16 (SigLIP image embeddings followed by the scaled language
  * embeddings, embed_prefix, pi0_pytorch.py:190-255) and prefix_pad [B, P] uint8/bool (1 = valid)

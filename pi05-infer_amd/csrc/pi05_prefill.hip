@@ -364,11 +364,14 @@ __global__ __launch_bounds__(256) void geglu_kernel(const u16* gu, u16* act, siz
 
 // out[i] = bf16(table[ids[i]] * sqrt(2048)); an id outside [0, vocab) zero-fills its row and
 // sets *err.
-__global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u16* table, int64_t vocab, u16* out, unsigned* err) {
+// A row whose id is outside [0, vocab) is written as zeros and the call's tag goes to a pinned
+// host word (system scope), which the host reads without synchronising.
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* ids, const u16* table, int64_t vocab, u16* out,
+                                                    unsigned* host_bad, unsigned tag) {
   const int64_t i = blockIdx.x;
   const int32_t id = ids[i];
   const bool ok = id >= 0 && id < vocab;
-  if (!ok && threadIdx.x == 0) *err = 1u;
+  if (!ok && threadIdx.x == 0) __hip_atomic_store(host_bad, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   const size_t d = (size_t)threadIdx.x * 8;
   u16x8 o = {0, 0, 0, 0, 0, 0, 0, 0};
   if (ok) {
@@ -388,9 +391,9 @@ struct LayerBind {
 // Device layout of one context: sizes in bytes.
 struct PrefixPlan {
   int L = 0, B = 0, P = 0, M = 0, s_pad = 0, n_mt = 0, items = 0, nsplit = 1;
-  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, rtab, err, ws, po, pml, dpart;
+  size_t w, ln, h, n, y, qkv, attn, gu, act, qf, kv, pos, valid, invf, rtab, ws, po, pml, dpart;
   size_t total() const {
-    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + rtab + err + ws + po + pml + dpart + 17 * 256;
+    return w + ln + 3 * h + qkv + attn + gu + act + qf + 2 * kv + pos + valid + invf + rtab + ws + po + pml + dpart + 16 * 256;
   }
 };
 constexpr size_t kWorkspace = 64ull << 20;
@@ -425,7 +428,6 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   p.valid = rup((size_t)p.B * p.s_pad);
   p.invf = rup(kHalfDim * 4);
   p.rtab = rup((size_t)(p.P + 1) * kHeadDim * 2);
-  p.err = 256;
   p.ws = kWorkspace;
   const size_t rows = (size_t)p.B * p.n_mt * 16;
   p.po = p.nsplit > 1 ? rup((size_t)p.nsplit * rows * kHeadDim * 4) : 0;
@@ -487,7 +489,8 @@ struct pi05_prefix_ctx {
   bool o_split = false;     // o_proj likewise
   int* pos = nullptr;
   uint8_t* valid = nullptr;
-  unsigned* err_flag = nullptr;
+  unsigned* host_bad = nullptr;  // pinned host word: tag of the last embed call that met a bad token id
+  unsigned embed_tag = 0, reported_tag = 0;
   void* ws = nullptr;
   hipblasLtHandle_t lt = nullptr;
   GemmPlan g_qkv, g_kv, g_o, g_gu, g_d, g_dsk, g_osk;
@@ -597,7 +600,6 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   c->valid = reinterpret_cast<uint8_t*>(take(p.valid));
   c->inv_freq = reinterpret_cast<float*>(take(p.invf));
   c->rope_tab = reinterpret_cast<u16*>(take(p.rtab));
-  c->err_flag = reinterpret_cast<unsigned*>(take(p.err));
   c->ws = take(p.ws);
   c->po = reinterpret_cast<float*>(take(p.po));
   c->pml = reinterpret_cast<float*>(take(p.pml));
@@ -605,6 +607,8 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
   // everything starts zeroed: query rows and keys past P stay zero (finite and masked) for the
   // life of the context, and the GEMM tuning below reads defined values
   e = hipMemset(c->base, 0, p.total());
+  if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&c->host_bad), sizeof(unsigned), hipHostMallocMapped);
+  if (e == hipSuccess) *c->host_bad = 0;
   float invf[kHalfDim];
   prefix_inv_freq(dims->rope_theta, invf);
   if (e == hipSuccess) e = hipMemcpy(c->inv_freq, invf, sizeof(invf), hipMemcpyHostToDevice);
@@ -614,6 +618,7 @@ int pi05_prefix_create(const pi05_prefix_dims* dims, pi05_prefix_ctx** out) {
     if (e == hipSuccess) e = hipDeviceSynchronize();
   }
   if (e != hipSuccess) {
+    if (c->host_bad) (void)hipHostFree(c->host_bad);
     hipFree(c->base);
     delete c;
     return fail(nullptr, PI05_E_HIP, std::string("prefix context initialisation failed: ") + hipGetErrorString(e));
@@ -663,6 +668,11 @@ int pi05_prefix_destroy(pi05_prefix_ctx* c) {
   free_plan(&c->g_dsk);
   free_plan(&c->g_osk);
   if (c->lt) hipblasLtDestroy(c->lt);
+  // an embed kernel still in flight may write the pinned word
+  if (c->host_bad) {
+    (void)hipDeviceSynchronize();
+    (void)hipHostFree(c->host_bad);
+  }
   if (c->base) hipFree(c->base);
   delete c;
   return PI05_OK;
@@ -707,6 +717,16 @@ int pi05_prefix_refresh_weights(pi05_prefix_ctx* c, void* stream) {
   return PI05_OK;
 }
 
+// A bad token id of an earlier embed call that has not been reported yet: report it (once).
+static int pending_bad_ids(pi05_prefix_ctx* c) {
+  const unsigned seen = __atomic_load_n(c->host_bad, __ATOMIC_ACQUIRE);
+  if (seen > c->reported_tag) {
+    c->reported_tag = seen;
+    return fail(c, PI05_E_INVALID, "a token id of an earlier pi05_prefix_embed_tokens call was outside [0, vocab) (its row was written as zeros)");
+  }
+  return PI05_OK;
+}
+
 int pi05_prefix_embed_tokens(pi05_prefix_ctx* c, const int32_t* ids, int64_t n_tokens, const void* table, int64_t vocab,
                              void* out, void* stream) {
   if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
@@ -714,17 +734,21 @@ int pi05_prefix_embed_tokens(pi05_prefix_ctx* c, const int32_t* ids, int64_t n_t
   if (n_tokens < 1 || n_tokens > (1 << 24) || vocab < 1) return fail(c, PI05_E_INVALID, "n_tokens must be in [1, 2^24] and vocab >= 1");
   if (reinterpret_cast<uintptr_t>(table) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
     return fail(c, PI05_E_INVALID, "table and out must be 16-byte aligned");
+  const int rc = pending_bad_ids(c);
+  if (rc != PI05_OK) return rc;  // enqueues nothing
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = hipMemsetAsync(c->err_flag, 0, 4, st);
+  embed_kernel<<<(unsigned)n_tokens, 256, 0, st>>>(ids, static_cast<const u16*>(table), vocab, static_cast<u16*>(out), c->host_bad,
+                                                   ++c->embed_tag);
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(c, "embed", e);
-  embed_kernel<<<(unsigned)n_tokens, 256, 0, st>>>(ids, static_cast<const u16*>(table), vocab, static_cast<u16*>(out), c->err_flag);
-  unsigned flag = 0;
-  e = hipGetLastError();
-  if (e == hipSuccess) e = hipMemcpyAsync(&flag, c->err_flag, 4, hipMemcpyDeviceToHost, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  if (e != hipSuccess) return hip_fail(c, "embed", e);
-  if (flag) return fail(c, PI05_E_INVALID, "a token id is outside [0, vocab)");
   return PI05_OK;
+}
+
+int pi05_prefix_status(pi05_prefix_ctx* c, void* stream) {
+  if (!c) return fail(nullptr, PI05_E_INVALID, "ctx is NULL");
+  const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(c, "status", e);
+  return pending_bad_ids(c);
 }
 
 int pi05_prefix_forward(pi05_prefix_ctx* c, const void* embeds, const uint8_t* prefix_pad, void* const* k_layers,

@@ -94,16 +94,21 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
 #pragma unroll
   for (int j = 0; j < 9; ++j) h[2 * j] = bf2f((u16)(xv[j] & 0xffff)), h[2 * j + 1] = bf2f((u16)(xv[j] >> 16));
   if (ys) {
-    float2 acc[9];
+    // every split's partial row is loaded before the first sum (the splits are summed in order, as
+    // before): a loop that waited for each split's loads in turn paid one memory round trip per split
+    float2 acc[9], a[kVMaxSplits - 1][9];
 #pragma unroll
     for (int j = 0; j < 9; ++j) acc[j] = *reinterpret_cast<const float2*>(ys + ro + 2 * (lane + 64 * j));
-    for (int sp = 1; sp < nsplit; ++sp) {
-      float2 a[9];
 #pragma unroll
-      for (int j = 0; j < 9; ++j) a[j] = *reinterpret_cast<const float2*>(ys + (size_t)sp * split_stride + ro + 2 * (lane + 64 * j));
+    for (int sp = 1; sp < kVMaxSplits; ++sp)
+      if (sp < nsplit)
 #pragma unroll
-      for (int j = 0; j < 9; ++j) acc[j].x += a[j].x, acc[j].y += a[j].y;
-    }
+        for (int j = 0; j < 9; ++j) a[sp - 1][j] = *reinterpret_cast<const float2*>(ys + (size_t)sp * split_stride + ro + 2 * (lane + 64 * j));
+#pragma unroll
+    for (int sp = 1; sp < kVMaxSplits; ++sp)
+      if (sp < nsplit)
+#pragma unroll
+        for (int j = 0; j < 9; ++j) acc[j].x += a[sp - 1][j].x, acc[j].y += a[sp - 1][j].y;
 #pragma unroll
     for (int j = 0; j < 9; ++j) {
       const float2 bb = *reinterpret_cast<const float2*>(ybias + 2 * (lane + 64 * j));
@@ -492,7 +497,8 @@ int pi05_vision_create(const pi05_vision_dims* dims, pi05_vision_ctx** out) {
   fc1o.ld_c = kVIp;
   GemmOpts fc2o = bias;
   fc2o.ld_k = kVIp;
-  const int splits[2] = {4, 8};
+  constexpr int splits[2] = {4, 8};
+  static_assert(splits[0] <= kVMaxSplits && splits[1] <= kVMaxSplits, "layernorm_kernel reduces at most kVMaxSplits slices");
   bool ok = lt_ok(hipblasLtCreate(&c->lt)) && make_plan(c->lt, M, kVW, kVPD, kVWorkspace, &c->g_patch, &perr, f32) &&
             make_plan(c->lt, M, kVQkvN, kVW, kVWorkspace, &c->g_qkv, &perr, bias) && make_plan(c->lt, M, kVW, kVW, kVWorkspace, &c->g_o, &perr, bias) &&
             make_plan(c->lt, M, kVI, kVW, kVWorkspace, &c->g_fc1, &perr, fc1o) && make_plan(c->lt, M, kVW, kVIp, kVWorkspace, &c->g_fc2, &perr, fc2o) &&

@@ -64,6 +64,7 @@ PREFIX_EXPORTED_SYMBOLS = (
     "pi05_prefix_bind_layer",
     "pi05_prefix_refresh_weights",
     "pi05_prefix_embed_tokens",
+    "pi05_prefix_status",
     "pi05_prefix_forward",
 )
 
@@ -220,6 +221,7 @@ def load_prefix_library(path: str = PREFIX_LIB_PATH) -> ctypes.CDLL:
         "pi05_prefix_bind_layer": (i32, [vp, i32] + [vp] * 9),
         "pi05_prefix_refresh_weights": (i32, [vp, vp]),
         "pi05_prefix_embed_tokens": (i32, [vp, vp, i64, vp, i64, vp, vp]),
+        "pi05_prefix_status": (i32, [vp, vp]),
         "pi05_prefix_forward": (i32, [vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(vp), i64, i64, vp]),
         "pi05_vision_default_dims": (None, [vdims_p]),
         "pi05_vision_check_dims": (i32, [vdims_p]),
@@ -532,13 +534,22 @@ class PrefixContext:
         self._call(self.lib.pi05_prefix_refresh_weights(self.handle, _stream_ptr(stream)))
 
     def embed_tokens(self, ids: torch.Tensor, table: torch.Tensor, stream=None) -> torch.Tensor:
-        """``bf16(table[ids] * sqrt(W))`` for int32/int64 ids of any shape -> ``[*ids.shape, W]``."""
+        """``bf16(table[ids] * sqrt(W))`` for int32/int64 ids of any shape -> ``[*ids.shape, W]``.
+        Enqueues only: device ids outside ``[0, vocab)`` give zero rows and are reported by the
+        next call or by ``status()``; host ids are checked here, before the copy."""
+        if ids.device.type == "cpu" and ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= table.shape[0]):
+            raise Pi05Error(-1, "a token id is outside [0, vocab)")
         ids32 = ids.to(device=self.device, dtype=torch.int32).contiguous()
         tp = _ptr(table, torch.bfloat16, "table", self.device)
         out = torch.empty((*ids.shape, self.dims.width), dtype=torch.bfloat16, device=self.device)
         self._call(self.lib.pi05_prefix_embed_tokens(self.handle, ids32.data_ptr(), ids32.numel(), tp, table.shape[0],
                                                      out.data_ptr(), _stream_ptr(stream)))
         return out
+
+    def status(self, stream=None) -> None:
+        """Wait for the stream; raise if an earlier ``embed_tokens`` met a token id outside
+        ``[0, vocab)`` that has not been reported yet."""
+        self._call(self.lib.pi05_prefix_status(self.handle, _stream_ptr(stream)))
 
     def forward(self, embeds: torch.Tensor, prefix_pad: torch.Tensor, k_layers: Sequence[torch.Tensor],
                 v_layers: Sequence[torch.Tensor], stream=None) -> None:

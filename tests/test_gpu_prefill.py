@@ -127,8 +127,27 @@ def test_embed_tokens_exact_and_rejects_bad_ids():
     assert torch.equal(got.float().cpu(), ref)
     bad = ids.clone()
     bad[1, 4] = 1000
+    tb = table.to(torch.bfloat16).cuda()
+    # host ids are checked before the copy
     with pytest.raises(_ext.Pi05Error):
-        ctx.embed_tokens(bad.cuda(), table.to(torch.bfloat16).cuda())
+        ctx.embed_tokens(bad, tb)
+    # device ids: the call only enqueues; the bad row is zero and status() reports it, once
+    out = ctx.embed_tokens(bad.cuda(), tb)
+    with pytest.raises(_ext.Pi05Error):
+        ctx.status()
+    ctx.status()
+    assert torch.equal(out[1, 4].float().cpu(), torch.zeros(G.width))
+    keep = torch.ones(2, 13, dtype=torch.bool)
+    keep[1, 4] = False
+    assert torch.equal(out.float().cpu()[keep], ref[keep])
+    # or the next call reports it (and enqueues nothing); the call after that runs
+    ctx.embed_tokens(bad.cuda(), tb)
+    torch.cuda.synchronize()
+    with pytest.raises(_ext.Pi05Error):
+        ctx.embed_tokens(ids.cuda(), tb)
+    got = ctx.embed_tokens(ids.cuda(), tb)
+    ctx.status()
+    assert torch.equal(got.float().cpu(), ref)
 
 
 def test_prefill_then_denoise_matches_oracle_chain(layers3):
