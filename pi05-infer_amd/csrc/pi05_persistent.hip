@@ -199,6 +199,9 @@ constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sa
 // tile for its finisher (quarter 0)
 constexpr int kPartFlags = 256;
 constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-tile of a sample, tile)
+#ifndef PI05_GU_PAIRS
+#define PI05_GU_PAIRS 1
+#endif
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
@@ -321,10 +324,18 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 // weights of item blockIdx.x -> region A.  A qkv item's tile 1 is copied without its last
 // fragment (k-step 31), which the wave owning that k-step loads into registers: both qkv tiles
 // then fit one 63-copy burst.
+// gate_up items.  B = 1: workgroup w computes tile pair w (gate tile w, up tile w) for the one
+// sample.  B > 1: workgroup w computes tile pairs 2g and 2g + 1, g = w mod 128, for half of the
+// samples (w / 128): each activation row it reads then serves four tiles instead of two, so an
+// XCD's workgroups read half as many activation bytes (the phase is bound by that L2 traffic).
+// Region A holds pair 2g; the compute waves hold pair 2g + 1 in registers.
+__device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
+  return a.batch > 1 ? 2 * ((int)blockIdx.x % (kGuItems / 2)) : (int)blockIdx.x;
+}
 template <int MODE>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = MODE == kModeQkv ? qkv_item() % kQkvPairs : (int)blockIdx.x;  // qkv: the tile pair
+  const int p = MODE == kModeQkv ? qkv_item() % kQkvPairs : gu_pair0(a);  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -806,6 +817,138 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
 }
 
 // =============================================================================================
+// gate_up at B > 1: two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from registers) for the
+// samples [b0, b1) of half w / 128 (see gu_pair0).  Per sample the three compute waves split K
+// (11 | 11 | 10 k-steps) over four m-tiles and four tiles; the pairs are then reduced and written
+// in turn with the same epilogue as phase_norm_gemm<kModeGateUp>.  The flag of item w covers both
+// pairs and the half's samples.
+// =============================================================================================
+__device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 4;
+  const int L = a.depth, R = a.R;
+  const int item = (int)blockIdx.x;
+  PHASE_TS(s, l, kPhGu, 0);
+  // copy wave: pair p0's weights (region A) and everything issued before them have landed
+  if (copy_wave()) wait_vmcnt<0>();
+  const int half = item / (kGuItems / 2), p0 = gu_pair0(a), p1 = p0 + 1;
+  const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  if (item >= kGuItems) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const bool comp = tid < kCompThreads;
+  const int r16 = lane & 15;
+  const int ks0 = wave * KSW;  // this wave's k-steps [ks0, ks0 + KSW) (wave 2: the last one past K)
+  const size_t slw = (size_t)s * L + l;
+  const u16* gin = a.gmid + slw * R * kWidth;
+  const float* ssin = a.ssmid + slw * kTiles * R;
+  const float* bias = a.bias + slw * kBiasCols;
+  float* s_rstd = smem + kLdsWork;  // [64] (sample rows)
+  float* s_bias = s_rstd + 64;      // [64] shift . W^T: gate p0, up p0, gate p1, up p1 (16 each)
+  float* s_rs = s_bias + 64;        // [3][64]
+  float* red = s_rs + 192;          // [3 waves][4 m-tiles][2 tiles][64 lanes][4] (one pair at a time)
+  float* T = red + kCompWaves * MT * 2 * 256;  // [64][TS]
+  // pair p1's weight fragments of this wave's k-steps (gate, up): waves 1 and 2 ahead of the
+  // polls, wave 0 (which polls) after them
+  const u16* wl = a.wpack + (size_t)l * kLayerElems;
+  bf16x8 w1[2][KSW];
+  auto load_w1 = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) {
+        const int ks = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;  // the surplus step multiplies zeros
+        w1[t][s2] = *reinterpret_cast<const bf16x8*>(wl + (t == 0 ? kOffGate : kOffUp) + ((size_t)p1 * KSTEPS + ks) * 512 + lane * 8);
+      }
+  };
+  if (wave == 1 || wave == 2) load_w1();
+  if (tid >= 64 && tid < 128) {
+    const int c = tid - 64, pr = c >> 5, gu = (c >> 4) & 1, n = c & 15;
+    s_bias[c] = bias[kQkvCols + gu * kMlp + (p0 + pr) * 16 + n];
+  }
+  PHASE_TS(s, l, kPhGu, 1);
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  PHASE_TS(s, l, kPhGu, 2);
+  if (wave == 0) load_w1();
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
+  for (int b = b0; b < b1; ++b) {
+    const int m0 = b * kRowsPerSample;
+    f32x4 acc[MT][NT];
+    if (comp) {
+      const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
+      const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
+      float st[22];
+#pragma unroll
+      for (int t = 0; t < 22; ++t) {
+        const int tile = 22 * wave + t;
+        buf_f32(st[t], rsrc_s, tile < kTiles ? ((tile * R + m0 + lane) * 4) : kOob);
+      }
+      bf16x8 hr[MT][KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bool ok = r16 < kHorizon - mt * 16 && ks0 + s2 < KSTEPS;
+          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+        }
+      sched_fence();
+      float v = 0.f;
+#pragma unroll
+      for (int t = 0; t < 22; ++t) v += st[t];
+      s_rs[wave * 64 + lane] = v;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
+        if (t >= 2) return w1[t - 2][s2];
+        const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
+        return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
+      });
+    }
+    __syncthreads();  // the row sums are in LDS
+    if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      if (comp) {
+        f32x4 accp[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) accp[mt][0] = acc[mt][2 * pr], accp[mt][1] = acc[mt][2 * pr + 1];
+        store_wave_partials<MT, 2>(red, accp, wave, lane);
+      }
+      __syncthreads();
+      reduce_to_tile<MT, 2, TS>(red, T);
+      __syncthreads();
+      // GeGLU (rlinf_fused_denoise.py:166-173) of pair p0 + pr; chunk = (row, half of 16 columns)
+      if (tid < 2 * kHorizon) {
+        const int row = tid >> 1, hf = tid & 1;
+        const float rstd = s_rstd[row];
+        float tg[8], tu[8], bgv[8], buv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          tg[q] = T[row * TS + hf * 8 + q];
+          tu[q] = T[row * TS + 16 + hf * 8 + q];
+          bgv[q] = s_bias[32 * pr + hf * 8 + q];
+          buv[q] = s_bias[32 * pr + 16 + hf * 8 + q];
+        }
+        sched_fence();
+        u16 o8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float gt = round_bf(__builtin_fmaf(rstd, tg[q], bgv[q]));
+          const float up = __builtin_fmaf(rstd, tu[q], buv[q]);
+          o8[q] = f2bf(fmul(gelu_tanh(gt), up));
+        }
+        st_bf16x8(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + row, (p0 + pr) * 16 + hf * 8, kMlp / 32), o8);
+      }
+      __syncthreads();  // red and T are reused
+    }
+  }
+  PHASE_TS(s, l, kPhGu, 5);
+  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch);
+  PHASE_TS(s, l, kPhGu, 6);
+  return true;
+}
+
+// =============================================================================================
 // attention, two stages.
 // Splits: item = (row block bp of 2 tokens x 8 heads of one sample, key split c); compute wave w
 // attends 32-key blocks kb_lo + w, kb_lo + w + 3, ... (online softmax).  Each wave's first block,
@@ -1211,8 +1354,14 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
   const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
   PHASE_TS(s, l, PH, 1);
   {
-    // the gate_up items of this quarter's 1024 activation columns
-    if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)) return false;
+    // the gate_up items of this quarter's 1024 activation columns: pairs 64 ksp .. 64 ksp + 63,
+    // i.e. items 64 ksp .. at B = 1 and, at B > 1, items 32 ksp .. of both sample halves
+    const unsigned* fgu = flag_base(a, s, l, kPhGu);
+    if (a.batch > 1 && PI05_GU_PAIRS) {
+      if (!wait_flags(a, fgu + ksp * 32, 32, s_flag) || !wait_flags(a, fgu + kGuItems / 2 + ksp * 32, 32, s_flag)) return false;
+    } else if (!wait_flags(a, fgu + ksp * 64, 64, s_flag)) {
+      return false;
+    }
   }
   PHASE_TS(s, l, PH, 2);
   // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
@@ -1348,6 +1497,7 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 // the kernel
 // =============================================================================================
 static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
+static_assert(64 + 64 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "gate_up pairs working area");
 static_assert(kCompWaves * 4 * 256 + 64 * 17 + 128 <= kWorkFloats, "residual working area");
 static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
@@ -1364,7 +1514,8 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
       ok = phase_norm_gemm<kModeQkv>(a, s, l, smem, &s_flag) && phase_attn(a, s, l, smem, &s_flag) &&
-           phase_oproj(a, s, l, smem, &s_flag) && phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag) &&
+           phase_oproj(a, s, l, smem, &s_flag) &&
+           (a.batch > 1 && PI05_GU_PAIRS ? phase_gateup_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag)) &&
            phase_down(a, s, l, smem, &s_flag);
     }
   }

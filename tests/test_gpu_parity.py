@@ -119,6 +119,16 @@ def test_c3_batch8(full_weights):
     model.close()
 
 
+def test_batch5_batch_paths(full_weights):
+    """B=5: the batch paths at an odd batch -- attention with the batch-aware key-split count (3
+    splits: 125 row blocks x 9 would take more than four passes of the grid) and gate_up's
+    two-pair items over sample halves of 3 and 2."""
+    print("case B=5: depth 4, B=5, P=968, 3 steps", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, depth=4, B=5, steps=3)
+    _check("B=5", ref, got, 3)
+    model.close()
+
+
 def test_ragged_prefix_padding(full_weights):
     print("case ragged: depth 4, B=3, P=300, padded tails", flush=True)
 
