@@ -202,6 +202,9 @@ constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-til
 #ifndef PI05_GU_PAIRS
 #define PI05_GU_PAIRS 1
 #endif
+#ifndef PI05_DOWN_PAIRS
+#define PI05_DOWN_PAIRS 1
+#endif
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
@@ -355,12 +358,29 @@ __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
 }
 
 // down_proj weights of item blockIdx.x = (tile, K quarter) -> region B.
+// down_proj items.  B = 1: workgroup w = (tile w mod 64, K quarter w / 64).  B > 1: workgroup w =
+// (tiles 2g and 2g + 1 with g = u mod 32, K quarter u / 32, u = w mod 128) for half w / 128 of the
+// samples -- half the activation bytes per XCD, as for gate_up.  Either way the quarters of a
+// tile (group) run on one XCD (w mod 8 is the same for all four).  Region B holds the first tile's
+// quarter; at B > 1 the compute waves hold the second one in registers.
+__device__ __forceinline__ void down_item(const MegaArgs& a, int* nt0, int* ksp) {
+  const int w = (int)blockIdx.x;
+  if (a.batch > 1 && PI05_DOWN_PAIRS) {
+    const int u = w % (kTiles * kKSplit / 2);
+    *nt0 = 2 * (u % (kTiles / 2));
+    *ksp = u / (kTiles / 2);
+  } else {
+    *nt0 = w % kTiles;
+    *ksp = w / kTiles;
+  }
+}
 template <int KSTEPS>
 __device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
   constexpr int KQ = KSTEPS / kKSplit;
   const int item = blockIdx.x;
   if (!copy_wave() || item >= kTiles * kKSplit) return;
-  const int nt = item % kTiles, ksp = item / kTiles;
+  int nt, ksp;
+  down_item(a, &nt, &ksp);
   const u16* tile = a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)nt * KSTEPS * 512 + (size_t)ksp * KQ * 512;
   lds_burst<KQ>(smem + kLdsB, tile);
 }
@@ -1494,11 +1514,171 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 }
 
 // =============================================================================================
+// down_proj at B > 1: two tiles (nt0 = 2g from region B, nt1 = 2g + 1 from registers) and one K
+// quarter for the samples [b0, b1) of half h (see down_item).  Quarters 1..3 store their partials
+// of both tiles and flag them for the group's finisher (quarter 0, same XCD), which adds the four
+// quarters in order and applies the gated residual to both tiles, as phase_down does for one.  The
+// finisher's flag (index g + 32 h) covers both tiles and the half's samples.
+// =============================================================================================
+__device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kMlp / 32;
+  constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 33;
+  constexpr int PH = kPhDown, NG = kTiles / 2;
+  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  const int item = (int)blockIdx.x;
+  PHASE_TS(s, l, PH, 0);
+  // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
+  {
+    int ln;
+    if (next_layer(a, s, l, &ln)) {
+      copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
+      copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
+    }
+  }
+  if (item >= kTiles * kKSplit) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const bool comp = tid < kCompThreads;
+  int nt0, ksp;
+  down_item(a, &nt0, &ksp);
+  const int grp = nt0 / 2, half = item / (kTiles * kKSplit / 2);
+  const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  const int kw0 = wave * KSW;  // this wave's k-steps in the quarter: [kw0, kw0 + KSW) clipped to KQ
+  const size_t slw = (size_t)s * L + l;
+  const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
+  // the second tile's quarter: waves 1 and 2 ahead of the polls, wave 0 after them
+  const u16* wl = a.wpack + (size_t)l * kLayerElems + kOffDown;
+  bf16x8 w1[KSW];
+  auto load_w1 = [&]() {
+#pragma unroll
+    for (int s2 = 0; s2 < KSW; ++s2) {
+      const int kc = kw0 + s2 < KQ ? kw0 + s2 : KQ - 1;  // the surplus step multiplies zeros
+      w1[s2] = *reinterpret_cast<const bf16x8*>(wl + ((size_t)(nt0 + 1) * KSTEPS + ksp * KQ + kc) * 512 + lane * 8);
+    }
+  };
+  if (wave == 1 || wave == 2) load_w1();
+  PHASE_TS(s, l, PH, 1);
+  // the gate_up items of this quarter's activation columns for this half's samples
+  if (!wait_flags(a, flag_base(a, s, l, kPhGu) + half * (kGuItems / 2) + ksp * 32, 32, s_flag)) return false;
+  PHASE_TS(s, l, PH, 2);
+  if (wave == 0) load_w1();
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // the first tile's K-quarter fragments
+  const u16* act = a.act + slw * (size_t)R * kMlp;
+  float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;  // [quarter][tile][row][16]
+  float* red = smem + kLdsWork;
+  float* T = red + kCompWaves * 4 * 2 * 256;  // [64][TS]: the two tiles side by side
+  const int r16 = lane & 15;
+  const brsrc rsrc_a = make_rsrc(act, (size_t)R * KSTEPS * 32 * 2);
+  for (int b = b0; b < b1; ++b) {
+    if (comp) {
+      bf16x8 af[4][KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const bool ok = r16 < kHorizon - mt * 16 && kw0 + s2 < KQ;
+          buf_frag(af[mt][s2], rsrc_a, ok ? (int)((afrag_offset(b * 4 + mt, ksp * KQ + kw0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+        }
+      sched_fence();
+      f32x4 acc[4][2];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mfma_steps<KSW, 2, 0, 4>(acc, af, [&](int t, int s2) {
+        if (t == 1) return w1[s2];
+        const int kc = kw0 + s2 < KQ ? kw0 + s2 : KQ - 1;
+        return *reinterpret_cast<const bf16x8*>(lw + (size_t)kc * 512 + lane * 8);
+      });
+      store_wave_partials<4, 2>(red, acc, wave, lane);
+    }
+    __syncthreads();
+    reduce_to_tile<4, 2, TS>(red, T);
+    __syncthreads();
+    // partials [quarter][tile][row][16] of both tiles (the finisher's own too: it reloads them);
+    // compute waves only, whose stores publish_local waits for
+    for (int e = tid; comp && e < 512; e += kCompThreads) {
+      const int t = e >> 8, row = (e >> 2) & 63, q4 = e & 3;
+      const float* tr = T + row * TS + t * 16 + 4 * q4;
+      st_l2_16(dpart, (uint32_t)(((((size_t)ksp * kTiles + nt0 + t) * R + b * kRowsPerSample + row) * 16 + 4 * q4) * 4),
+               u32x4{__float_as_uint(tr[0]), __float_as_uint(tr[1]), __float_as_uint(tr[2]), __float_as_uint(tr[3])});
+    }
+    __syncthreads();  // T is reused by the next sample
+  }
+  PHASE_TS(s, l, PH, 5);
+  unsigned* fl = flag_base(a, s, l, PH);
+  unsigned* fpart = fl + kPartFlags + 4 * (grp + NG * half);
+  if (ksp != 0) {
+    // this quarter's partials are in this XCD's L2: flag them for the group's finisher
+    publish_local(a, fpart + (ksp - 1), a.epoch);
+    return true;
+  }
+  // ---- the finisher (quarter 0): thread t -> tile t / 128, row t % 64, columns ((t / 64) % 2) * 8 .. +7
+  if (comp) wait_stores();  // its own partials, reloaded below
+  if (!wait_flags(a, fpart, kKSplit - 1, s_flag)) return false;
+  PHASE_TS(s, l, PH, 7);
+  {
+    const int ft = tid >> 7, frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;
+    const int col = (nt0 + ft) * 16;
+    const u16* hres = a.hmid + slw * (size_t)R * kWidth;
+    u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
+    u16* gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
+    float* rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
+    float gate[8], s1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      gate[i] = round_bf(gmod[i]);
+      if (next_g) s1[i] = smod[i];
+    }
+    float* s_ss = T;  // [2 tiles][2 halves][64 rows]
+    for (int b = b0; b < b1; ++b) {
+      const int r = b * kRowsPerSample + frow;
+      float ss = 0.f;
+      if (frow < kHorizon) {
+        float pv[kKSplit][8];
+#pragma unroll
+        for (int q = 0; q < kKSplit; ++q) {
+          const float* pp = dpart + (((size_t)q * kTiles + nt0 + ft) * R + r) * 16 + fc0;
+          const float4 v0 = *reinterpret_cast<const float4*>(pp), v1 = *reinterpret_cast<const float4*>(pp + 4);
+          pv[q][0] = v0.x, pv[q][1] = v0.y, pv[q][2] = v0.z, pv[q][3] = v0.w;
+          pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
+        }
+        const u16x8 hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
+        u16 hn[8], gn[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float y = ((pv[0][i] + pv[1][i]) + pv[2][i]) + pv[3][i];
+          const float prod = round_bf(fmul(round_bf(y), gate[i]));
+          hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
+          const float hf = bf2f(hn[i]);
+          gn[i] = f2bf(fmul(hf, s1[i]));
+          ss += hf * hf;
+        }
+        st_bf16x8(hout, afrag_index(r, col + fc0, kWidth / 32), hn);
+        if (next_g) st_bf16x8(gout, afrag_index(r, col + fc0, kWidth / 32), gn);
+      }
+      s_ss[(ft * 2 + (fc0 >> 3)) * 64 + frow] = ss;
+      __syncthreads();
+      // tile-major statistics: each tile's sums of the sample's 64 rows (one 256-byte run per tile)
+      if (tid < 128) {
+        const int t = tid >> 6, rw = tid & 63;
+        st_f32(rout + (size_t)(nt0 + t) * R + b * kRowsPerSample + rw, s_ss[(t * 2) * 64 + rw] + s_ss[(t * 2 + 1) * 64 + rw]);
+      }
+      __syncthreads();  // s_ss is reused by the next sample
+    }
+  }
+  PHASE_TS(s, l, PH, 8);
+  publish(a, fl + grp + NG * half, a.epoch, true);  // the copy wave stored rows too
+  PHASE_TS(s, l, PH, 9);
+  return true;
+}
+
+// =============================================================================================
 // the kernel
 // =============================================================================================
 static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
 static_assert(64 + 64 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "gate_up pairs working area");
 static_assert(kCompWaves * 4 * 256 + 64 * 17 + 128 <= kWorkFloats, "residual working area");
+static_assert(kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "down_proj pairs working area");
 static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
 
@@ -1516,7 +1696,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
       ok = phase_norm_gemm<kModeQkv>(a, s, l, smem, &s_flag) && phase_attn(a, s, l, smem, &s_flag) &&
            phase_oproj(a, s, l, smem, &s_flag) &&
            (a.batch > 1 && PI05_GU_PAIRS ? phase_gateup_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag)) &&
-           phase_down(a, s, l, smem, &s_flag);
+           (a.batch > 1 && PI05_DOWN_PAIRS ? phase_down_pairs(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
