@@ -358,20 +358,21 @@ __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
 }
 
 // down_proj weights of item blockIdx.x = (tile, K quarter) -> region B.
-// down_proj items.  B = 1: workgroup w = (tile w mod 64, K quarter w / 64).  B > 1: workgroup w =
-// (tiles 2g and 2g + 1 with g = u mod 32, K quarter u / 32, u = w mod 128) for half w / 128 of the
-// samples -- half the activation bytes per XCD, as for gate_up.  Either way the quarters of a
-// tile (group) run on one XCD (w mod 8 is the same for all four).  Region B holds the first tile's
-// quarter; at B > 1 the compute waves hold the second one in registers.
-__device__ __forceinline__ void down_item(const MegaArgs& a, int* nt0, int* ksp) {
+// down_proj items.  B = 1: workgroup w = (tile w mod 64, K quarter w / 64).  B > 1: workgroup
+// w = 64 q + 32 h + g computes tiles 2g and 2g + 1 over K quarter q for half h of the samples --
+// half the activation bytes per XCD, as for gate_up.  Either way the quarters of a tile (group)
+// run on one XCD (w mod 8 is the same for all four) and poll one flag replica (w mod 32), and the
+// finishers (quarter 0) are workgroups 0..63, which hold no qkv item.  Region B holds the first
+// tile's quarter; at B > 1 the compute waves hold the second one in registers.
+__device__ __forceinline__ void down_item(const MegaArgs& a, int* nt0, int* ksp, int* half = nullptr) {
   const int w = (int)blockIdx.x;
+  *ksp = w / kTiles;
   if (a.batch > 1 && PI05_DOWN_PAIRS) {
-    const int u = w % (kTiles * kKSplit / 2);
-    *nt0 = 2 * (u % (kTiles / 2));
-    *ksp = u / (kTiles / 2);
+    *nt0 = 2 * (w % (kTiles / 2));
+    if (half) *half = (w / (kTiles / 2)) % 2;
   } else {
     *nt0 = w % kTiles;
-    *ksp = w / kTiles;
+    if (half) *half = 0;
   }
 }
 template <int KSTEPS>
@@ -1515,7 +1516,7 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 
 // =============================================================================================
 // down_proj at B > 1: two tiles (nt0 = 2g from region B, nt1 = 2g + 1 from registers) and one K
-// quarter for the samples [b0, b1) of half h (see down_item).  Quarters 1..3 store their partials
+// quarter for the samples [b0, b1) of half h (workgroup 64 q + 32 h + g, see down_item).  Quarters 1..3 store their partials
 // of both tiles and flag them for the group's finisher (quarter 0, same XCD), which adds the four
 // quarters in order and applies the gated residual to both tiles, as phase_down does for one.  The
 // finisher's flag (index g + 32 h) covers both tiles and the half's samples.
@@ -1538,9 +1539,9 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   if (item >= kTiles * kKSplit) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const bool comp = tid < kCompThreads;
-  int nt0, ksp;
-  down_item(a, &nt0, &ksp);
-  const int grp = nt0 / 2, half = item / (kTiles * kKSplit / 2);
+  int nt0, ksp, half;
+  down_item(a, &nt0, &ksp, &half);
+  const int grp = nt0 / 2;
   const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
   const int kw0 = wave * KSW;  // this wave's k-steps in the quarter: [kw0, kw0 + KSW) clipped to KQ
   const size_t slw = (size_t)s * L + l;
