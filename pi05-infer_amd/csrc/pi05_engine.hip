@@ -138,6 +138,8 @@ Plan make_plan(const pi05_dims& d) {
     // slower, so the rule leaves them alone)
     const int nbp = d.batch * (kHorizon / 2), fill = (256 + nbp - 1) / nbp;
     if (nbp * p.nsplit_p > 4 * 256 && p.nsplit_p > fill) p.nsplit_p = fill;
+    // batches of kAttnGroupMinBatch and more: grouped items (4 row blocks each), one pass of the grid
+    if (d.batch >= kAttnGroupMinBatch) p.nsplit_p = attn_group_splits(d.batch, nkb);
   }
   p.nsplit_pad = (p.nsplit_p + 3) / 4 * 4;
   p.R = 64 * d.batch;

@@ -87,6 +87,18 @@ struct GemmArgs {
 };
 
 constexpr int kMaxAttnSplits = 16;
+// Persistent attention at batches of at least kAttnGroupMinBatch: items of kAttnGroup two-token
+// row blocks of one sample, one per wave, sharing each K/V block through LDS; the key splits
+// then fill the 256 workgroups once (attn_group_splits).
+constexpr int kAttnGroupMinBatch = 4;
+constexpr int kAttnGroup = 4;
+constexpr int kAttnGroupsPerSample = (50 / 2 + kAttnGroup - 1) / kAttnGroup;  // 7 groups of the 25 row blocks
+inline int attn_group_splits(int batch, int nkb) {
+  int n = 256 / (batch * kAttnGroupsPerSample);
+  if (n > kMaxAttnSplits) n = kMaxAttnSplits;
+  if (n > nkb) n = nkb;
+  return n < 1 ? 1 : n;
+}
 
 struct AttnArgs {
   const u16* q;        // [rows, D] (rows = M * H)

@@ -987,6 +987,140 @@ __device__ __forceinline__ void attend_block_lds(const KvBlock& blk, const u16* 
   attend_block_q(blk, [&](int ds) { return *reinterpret_cast<const bf16x8*>(sq + ds * 512 + lane * 8); }, m_run, l_run, oacc);
 }
 
+#ifndef PI05_ATTN_GROUP
+#define PI05_ATTN_GROUP 1
+#endif
+__device__ __forceinline__ bool attn_grouped(const MegaArgs& a) { return PI05_ATTN_GROUP && a.batch >= kAttnGroupMinBatch; }
+
+typedef uint32_t u32x4_lds __attribute__((ext_vector_type(4)));
+// One 16-byte LDS read issued as inline asm (ds_read_b128 at byte address addr); the caller waits
+// for it with lds_reads_done.  The grouped attention reads its staged K/V blocks this way because
+// the compiler cannot tell the two stage buffers apart and would otherwise wait for the next
+// block's direct-to-LDS loads (vmcnt(0)) before reading the current one.
+__device__ __forceinline__ u32x4_lds lds_read16(uint32_t addr) {
+  u32x4_lds r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+// s_waitcnt lgkmcnt(0), then the N fragments `f` as in/out operands, so nothing that uses them
+// is scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void lds_reads_done(u32x4_lds (&f)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(f[i]));
+}
+
+// Grouped split items (batches of kAttnGroupMinBatch and more): item n = (sample n mod B, group
+// grp of kAttnGroup two-token row blocks, key split c); wave j (the copy wave included) attends row
+// block kAttnGroup * grp + j over the split's whole key range.  Every 32-key K/V block is staged
+// once in LDS for the four waves (double-buffered direct-to-LDS loads, 8 of its 32 fragments per
+// wave; buffers: the upper half of region A, free during attention, and the working area), so an
+// item reads each block from L2 once for 64 query rows instead of once per 16: at B = 8 the
+// splits' K/V delivery drops from 200 MiB to 56 MiB per layer.  Each wave stores its row block's
+// partial exactly as a split item does after its wave merge, so the merges are unchanged.  With
+// 256 workgroups, item n runs on workgroup n: sample n mod B on XCD n mod 8, so at B = 8 all of a
+// sample's items share the XCD whose L2 holds that sample's K/V.
+__device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit, B = a.batch;
+  const int n_items = B * kAttnGroupsPerSample * nsplit;
+  const int tid = phase_tid(), lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r16 = lane & 15;
+  const size_t slw = (size_t)s * L + l;
+  const int nkb_pre = a.s_pre >> 5, nkb = nkb_pre + 2;
+  float* apart = a.apart + slw * (size_t)nsplit * nbp * 16 * kHeadDim;
+  float* apart_ml = a.apart_ml + slw * (size_t)nsplit * nbp * 32;
+  unsigned* fsplit = flag_base(a, s, l, kPhSplit);
+  u16* const buf0 = reinterpret_cast<u16*>(smem + kLdsA1);
+  u16* const buf1 = reinterpret_cast<u16*>(smem + kLdsWork);
+  const u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int b = item % B, rr = item / B, grp = rr % kAttnGroupsPerSample, split = rr / kAttnGroupsPerSample;
+    const int pair = grp * kAttnGroup + wave;
+    const bool has_rows = pair < kPairs;
+    const int bp = b * kPairs + pair;
+    const int kb_lo = split * nkb / nsplit, kb_hi = (split + 1) * nkb / nsplit;
+    const u16* kpre = a.kpre + ((size_t)l * B + b) * a.s_pre * kHeadDim;
+    const u16* vpre = a.vpre + ((size_t)l * B + b) * a.s_pre * kHeadDim;
+    const u16* ksf = a.ksuf + (slw * B + b) * 64 * kHeadDim;
+    const u16* vsf = a.vsuf + (slw * B + b) * 64 * kHeadDim;
+    const uint8_t* valid = a.valid + (size_t)b * (a.s_pre + 64);
+    // this wave's 8 of block kb's 32 fragments [K 0..15 | V 0..15] -> LDS buffer `dst`: waves 0, 1
+    // the K halves, waves 2, 3 the V halves
+    const u16* ksrc = wave < 2 ? kpre : vpre;
+    const u16* ssrc = wave < 2 ? ksf : vsf;
+    auto stage = [&](int kb, u16* dst) __attribute__((always_inline)) {
+      const bool pre = kb < nkb_pre;
+      const u16* src = (pre ? ksrc : ssrc) + (size_t)(pre ? kb : kb - nkb_pre) * 16 * 512 + (size_t)(wave & 1) * 8 * 512;
+      const brsrc r = make_rsrc(uniform_ptr(src), 8 * 1024);
+      u16* d = dst + wave * 8 * 512;
+#pragma unroll
+      for (int f = 0; f < 8; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, lane * 16, f * 1024, 0, 0);
+    };
+    // the row block's query fragments (registers), then the first two blocks
+    bf16x8 qf[8];
+    const int rbq = b * (kRowsPerSample / 2) + (has_rows ? pair : 0);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(qs + afrag_offset(rbq, ds, kHeadDim / 32) + lane * 8);
+    stage(kb_lo, buf0);
+    if (kb_lo + 1 < kb_hi) stage(kb_lo + 1, buf1);
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 oacc[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
+    for (int kb = kb_lo; kb < kb_hi; ++kb) {
+      const int bi = (kb - kb_lo) & 1;
+      // this wave's loads of block kb have landed (block kb + 1's 8 may still be in flight), then
+      // every wave's (the barrier)
+      if (kb + 1 < kb_hi) wait_vmcnt<8>();
+      else wait_vmcnt<0>();
+      wg_barrier();
+      u32x4_lds fr[32];
+      const uint32_t base = (uint32_t)reinterpret_cast<uintptr_t>(bi ? buf1 : buf0) + (uint32_t)lane * 16;
+#pragma unroll
+      for (int f = 0; f < 32; ++f) fr[f] = lds_read16(base + f * 1024);
+      KvBlock blk;
+      blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
+      blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
+      lds_reads_done(fr);
+      wg_barrier();  // every wave has read buffer bi: block kb + 2 may replace it
+      if (kb + 2 < kb_hi) stage(kb + 2, bi ? buf1 : buf0);
+#pragma unroll
+      for (int f = 0; f < 16; ++f) {
+        blk.k[f] = __builtin_bit_cast(bf16x8, fr[f]);
+        blk.v[f] = __builtin_bit_cast(bf16x8, fr[16 + f]);
+      }
+      if (has_rows) attend_block_q(blk, [&](int ds) { return qf[ds]; }, m_run, l_run, oacc);
+    }
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 4);
+    // this row block's partial: O (unnormalised, relative to m_run), running max and sum; fp32
+    // [16 rows][D], row r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
+    if (has_rows) {
+      float* part = apart + ((size_t)split * nbp + bp) * 16 * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) st_f32x4(part, (size_t)r16 * kHeadDim + g * 4 + dt * 16, float4{oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]});
+      if (g == 0) {
+        st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + r16, m_run);
+        st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + 16 + r16, l_run);
+      }
+    }
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 5);
+    // the item's flags (one per row block), every replica; every wave stored rows
+    wait_stores();
+    wg_barrier();
+    if (tid < kAttnGroup * kFlagCopies) {
+      const int j = tid / kFlagCopies, rep = tid % kFlagCopies, pj = grp * kAttnGroup + j;
+      if (pj < kPairs) st_u32(fsplit + (size_t)(b * kPairs + pj) * a.nsplit_pad + split + (size_t)rep * a.fstride, a.epoch);
+    }
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
+  }
+  return true;
+}
+
 __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
   const int n_items = nbp * nsplit;
@@ -1010,7 +1144,16 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   float* s_l = s_m + 64;                       // [4][16]
   PHASE_TS(s, l, kPhSplit, 0);
   bool waited = false, burst = false;
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  if (attn_grouped(a)) {
+    // gate_up(l) tile 0, fragments 0..15 -> region A's lower half, ahead of the polls
+    copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
+    burst = true;
+    PHASE_TS(s, l, kPhSplit, 1);
+    if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
+    PHASE_TS(s, l, kPhSplit, 2);
+    if (!attn_group_items(a, s, l, smem, s_flag)) return false;
+  }
+  for (int item = attn_grouped(a) ? n_items : (int)blockIdx.x; item < n_items; item += gridDim.x) {
     const int bp = item % nbp, split = item / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
     const int rbq = b * (kRowsPerSample / 2) + pair;  // query-row m-tile (16 rows = 2 tokens x 8 heads)
