@@ -843,7 +843,7 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   int coop = 0, per_cu = 0;
   if (ae == hipSuccess) ae = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
   if (ae == hipSuccess)
-    ae = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0);
+    ae = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(c->d.batch), denoise_loop_threads(), 0);
   // one workgroup per CU; the weight phases have 256 items, one per workgroup
   c->grid = prop.multiProcessorCount;
   c->schedule = (coop && per_cu >= 1 && c->grid >= 256) ? PI05_SCHEDULE_PERSISTENT : PI05_SCHEDULE_GRAPH;
@@ -1157,7 +1157,7 @@ int pi05_set_schedule(pi05_ctx* c, int schedule) {
   if (schedule == PI05_SCHEDULE_PERSISTENT) {
     int coop = 0, per_cu = 0;
     HIPCHK(c, hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device));
-    HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(), denoise_loop_threads(), 0));
+    HIPCHK(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, denoise_loop_kernel_ptr(c->d.batch), denoise_loop_threads(), 0));
     if (!coop || per_cu < 1 || c->grid < 256)
       return c->fail(PI05_E_NODEVICE, "device cannot run the persistent schedule (cooperative launch of 256 workgroups)");
   }

@@ -184,7 +184,7 @@ struct ShiftBiasArgs {
 hipError_t launch_shift_bias(const ShiftBiasArgs& a, hipStream_t st);
 hipError_t launch_denoise_loop(const MegaArgs& a, int grid, hipStream_t st);
 int denoise_loop_threads();
-const void* denoise_loop_kernel_ptr();
+const void* denoise_loop_kernel_ptr(int batch);  // the instance launch_denoise_loop uses for `batch`
 
 hipError_t launch_pack_weight(const void* src, u16* dst, int N, int K, hipStream_t st);
 hipError_t launch_prime_kv(const PrimeKvArgs& a, int depth, hipStream_t st);

@@ -32,6 +32,13 @@
 #include "pi05_blocks.h"
 #include "pi05_kernels.h"
 
+// This file is compiled twice: as itself (instance 0: the one-sample kernel and the host-side
+// entry points) and through pi05_persistent_batched.hip (instance 1: the kernel for batches), so
+// that neither kernel's code generation depends on the other's.
+#ifndef PI05_PERSISTENT_INSTANCE
+#define PI05_PERSISTENT_INSTANCE 0
+#endif
+
 namespace pi05 {
 
 // Phase timestamps for profiling builds (-DPI05_PHASE_TIMESTAMPS): thread 0 of every workgroup
@@ -205,6 +212,18 @@ constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-til
 #ifndef PI05_DOWN_PAIRS
 #define PI05_DOWN_PAIRS 1
 #endif
+#ifndef PI05_ATTN_GROUP
+#define PI05_ATTN_GROUP 1
+#endif
+// Batches of kAttnGroupMinBatch and more: grouped attention items (attn_group_items), which stage
+// K/V blocks in region B as well, so down(l)'s weights are copied to B at gate_up(l) instead of
+// at qkv(l).
+// G: the kernel instance for batches (denoise_loop_kernel<true>); the one-sample instance does not
+// contain the grouped path at all.
+template <bool G>
+__device__ __forceinline__ bool attn_grouped(const MegaArgs& a) {
+  return G && PI05_ATTN_GROUP && PI05_GU_PAIRS && PI05_DOWN_PAIRS && a.batch >= kAttnGroupMinBatch;
+}
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
@@ -614,7 +633,7 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
 // A operand g (or gmid) straight from the producer; rstd from the tile sums of squares; the
 // epilogue computes y = bf16(rstd * acc + shift . W^T) and then RoPE (qkv) or GeGLU (gate_up).
 // =============================================================================================
-template <int MODE>
+template <int MODE, bool G>
 __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32, TS = 33;
   // m-tiles per item: qkv items are one half of a sample's rows (m-tiles 2h, 2h+1), gate_up all four
@@ -634,7 +653,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   if (copy_wave()) {
     wait_vmcnt<0>();
     if constexpr (MODE == kModeQkv) {
-      copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
+      if (!attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
     }
   }
   if (!has_item) return true;
@@ -844,13 +863,18 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
 // in turn with the same epilogue as phase_norm_gemm<kModeGateUp>.  The flag of item w covers both
 // pairs and the half's samples.
 // =============================================================================================
+template <bool G>
 __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 4;
   const int L = a.depth, R = a.R;
   const int item = (int)blockIdx.x;
   PHASE_TS(s, l, kPhGu, 0);
-  // copy wave: pair p0's weights (region A) and everything issued before them have landed
-  if (copy_wave()) wait_vmcnt<0>();
+  // copy wave: pair p0's weights (region A) and everything issued before them have landed; with
+  // grouped attention (which used region B) down(l)'s weights go to B now
+  if (copy_wave()) {
+    wait_vmcnt<0>();
+    if (attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
+  }
   const int half = item / (kGuItems / 2), p0 = gu_pair0(a), p1 = p0 + 1;
   const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
   if (item >= kGuItems) return true;
@@ -987,10 +1011,6 @@ __device__ __forceinline__ void attend_block_lds(const KvBlock& blk, const u16* 
   attend_block_q(blk, [&](int ds) { return *reinterpret_cast<const bf16x8*>(sq + ds * 512 + lane * 8); }, m_run, l_run, oacc);
 }
 
-#ifndef PI05_ATTN_GROUP
-#define PI05_ATTN_GROUP 1
-#endif
-__device__ __forceinline__ bool attn_grouped(const MegaArgs& a) { return PI05_ATTN_GROUP && a.batch >= kAttnGroupMinBatch; }
 
 typedef uint32_t u32x4_lds __attribute__((ext_vector_type(4)));
 // One 16-byte LDS read issued as inline asm (ds_read_b128 at byte address addr); the caller waits
@@ -1005,22 +1025,51 @@ __device__ __forceinline__ u32x4_lds lds_read16(uint32_t addr) {
 // s_waitcnt lgkmcnt(0), then the N fragments `f` as in/out operands, so nothing that uses them
 // is scheduled before the wait.
 template <int N>
-__device__ __forceinline__ void lds_reads_done(u32x4_lds (&f)[N]) {
+__device__ __forceinline__ void lds_reads_done(u32x4_lds (&f)[N], uint32_t& w0, uint32_t& w1) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(f[i]));
+  asm volatile("" : "+v"(w0), "+v"(w1));
+}
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
 }
 
 // Grouped split items (batches of kAttnGroupMinBatch and more): item n = (sample n mod B, group
 // grp of kAttnGroup two-token row blocks, key split c); wave j (the copy wave included) attends row
 // block kAttnGroup * grp + j over the split's whole key range.  Every 32-key K/V block is staged
-// once in LDS for the four waves (double-buffered direct-to-LDS loads, 8 of its 32 fragments per
-// wave; buffers: the upper half of region A, free during attention, and the working area), so an
-// item reads each block from L2 once for 64 query rows instead of once per 16: at B = 8 the
-// splits' K/V delivery drops from 200 MiB to 56 MiB per layer.  Each wave stores its row block's
-// partial exactly as a split item does after its wave merge, so the merges are unchanged.  With
-// 256 workgroups, item n runs on workgroup n: sample n mod B on XCD n mod 8, so at B = 8 all of a
-// sample's items share the XCD whose L2 holds that sample's K/V.
+// once in LDS for the four waves (direct-to-LDS loads, 8 of its 32 fragments per wave, and its 32
+// key-valid bytes by wave 0) in a ring of three buffers -- the upper half of region A (free during
+// attention), the working area and region B (down_proj's weights are copied there at gate_up
+// instead) -- two blocks ahead of the one being attended.  An item thus reads each block from L2
+// once for 64 query rows instead of once per 16 (at B = 8 the splits' K/V delivery drops from 200
+// MiB to 56 MiB per layer).  Everything the block loop waits for is staged through LDS and read
+// with inline ds_reads: a global load waited for there would, loads completing in order, also wait
+// for the later blocks' copies.  Each wave stores its row block's partial exactly as a split item
+// does after its wave merge, so the merges are unchanged.  With 256 workgroups, item n runs on
+// workgroup n: sample n mod B on XCD n mod 8 (at B = 8 all of a sample's items share the XCD whose
+// L2 holds that sample's K/V).
+constexpr int kAttnRing = 3;
+// This wave's share of one K/V block's staging (see attn_group_items): fragments 8 (wave & 1) .. +7
+// of the block's K (waves 0, 1) or V (waves 2, 3) -> dst + wave * 8 KiB, and for wave 0 the
+// block's 32 key-valid bytes -> vdst.
+__device__ __forceinline__ void attn_stage(const u16* pre_src, const u16* suf_src, const uint8_t* valid, int nkb_pre, int kb,
+                                           u16* dst, float* vdst, int wave, int lane) {
+  const bool pre = kb < nkb_pre;
+  const u16* src = (pre ? pre_src : suf_src) + (size_t)(pre ? kb : kb - nkb_pre) * 16 * 512 + (size_t)(wave & 1) * 8 * 512;
+  const brsrc r = make_rsrc(uniform_ptr(src), 8 * 1024);
+  u16* d = dst + wave * 8 * 512;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, lane * 16, f * 1024, 0, 0);
+  if (wave == 0) {
+    const brsrc rv = make_rsrc(uniform_ptr(valid + kb * 32), 32);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, vdst, 4, lane * 4, 0, 0, 0);
+  }
+}
+constexpr int kVringFloats = 64;  // per ring slot: 32 valid bytes (+ the zeros of the out-of-range lanes)
+static_assert(8192 + kAttnRing * kVringFloats <= kWorkFloats, "grouped attention: K/V buffer and valid ring in the working area");
 __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit, B = a.batch;
   const int n_items = B * kAttnGroupsPerSample * nsplit;
@@ -1034,6 +1083,8 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
   unsigned* fsplit = flag_base(a, s, l, kPhSplit);
   u16* const buf0 = reinterpret_cast<u16*>(smem + kLdsA1);
   u16* const buf1 = reinterpret_cast<u16*>(smem + kLdsWork);
+  u16* const buf2 = reinterpret_cast<u16*>(smem + kLdsB);
+  float* const vring = smem + kLdsWork + 8192;
   const u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int b = item % B, rr = item / B, grp = rr % kAttnGroupsPerSample, split = rr / kAttnGroupsPerSample;
@@ -1046,52 +1097,56 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     const u16* ksf = a.ksuf + (slw * B + b) * 64 * kHeadDim;
     const u16* vsf = a.vsuf + (slw * B + b) * 64 * kHeadDim;
     const uint8_t* valid = a.valid + (size_t)b * (a.s_pre + 64);
-    // this wave's 8 of block kb's 32 fragments [K 0..15 | V 0..15] -> LDS buffer `dst`: waves 0, 1
-    // the K halves, waves 2, 3 the V halves
+    // this wave's 8 of block kb's 32 fragments [K 0..15 | V 0..15] -> ring slot `slot` (waves 0, 1:
+    // the K halves, waves 2, 3: the V halves); wave 0 also the block's 32 key-valid bytes
     const u16* ksrc = wave < 2 ? kpre : vpre;
     const u16* ssrc = wave < 2 ? ksf : vsf;
-    auto stage = [&](int kb, u16* dst) __attribute__((always_inline)) {
-      const bool pre = kb < nkb_pre;
-      const u16* src = (pre ? ksrc : ssrc) + (size_t)(pre ? kb : kb - nkb_pre) * 16 * 512 + (size_t)(wave & 1) * 8 * 512;
-      const brsrc r = make_rsrc(uniform_ptr(src), 8 * 1024);
-      u16* d = dst + wave * 8 * 512;
-#pragma unroll
-      for (int f = 0; f < 8; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, lane * 16, f * 1024, 0, 0);
-    };
-    // the row block's query fragments (registers), then the first two blocks
+    // the row block's query fragments (registers), then the first blocks
     bf16x8 qf[8];
     const int rbq = b * (kRowsPerSample / 2) + (has_rows ? pair : 0);
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(qs + afrag_offset(rbq, ds, kHeadDim / 32) + lane * 8);
-    stage(kb_lo, buf0);
-    if (kb_lo + 1 < kb_hi) stage(kb_lo + 1, buf1);
+    attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo, buf0, vring, wave, lane);
+    if (kb_lo + 1 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 1, buf1, vring + kVringFloats, wave, lane);
+    if (kb_lo + 2 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 2, buf2, vring + 2 * kVringFloats, wave, lane);
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 oacc[16];
 #pragma unroll
     for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
-      const int bi = (kb - kb_lo) & 1;
-      // this wave's loads of block kb have landed (block kb + 1's 8 may still be in flight), then
-      // every wave's (the barrier)
-      if (kb + 1 < kb_hi) wait_vmcnt<8>();
-      else wait_vmcnt<0>();
+      const int slot = (kb - kb_lo) % kAttnRing;
+      // this wave's loads of block kb have landed (up to two later blocks' may still be in flight:
+      // 9 loads each for wave 0, 8 for the others), then every wave's (the barrier)
+      const int after = kb_hi - 1 - kb < kAttnRing - 1 ? kb_hi - 1 - kb : kAttnRing - 1;
+      if (wave == 0) {
+        if (after >= 2) wait_vmcnt<18>();
+        else if (after == 1) wait_vmcnt<9>();
+        else wait_vmcnt<0>();
+      } else {
+        if (after >= 2) wait_vmcnt<16>();
+        else if (after == 1) wait_vmcnt<8>();
+        else wait_vmcnt<0>();
+      }
       wg_barrier();
       u32x4_lds fr[32];
-      const uint32_t base = (uint32_t)reinterpret_cast<uintptr_t>(bi ? buf1 : buf0) + (uint32_t)lane * 16;
+      const uint32_t base = (uint32_t)reinterpret_cast<uintptr_t>(slot == 0 ? buf0 : slot == 1 ? buf1 : buf2) + (uint32_t)lane * 16;
 #pragma unroll
       for (int f = 0; f < 32; ++f) fr[f] = lds_read16(base + f * 1024);
+      const uint32_t vbase = (uint32_t)reinterpret_cast<uintptr_t>(vring + slot * kVringFloats) + (uint32_t)g * 4;
+      uint32_t v0 = lds_read4(vbase), v1 = lds_read4(vbase + 16);
+      lds_reads_done(fr, v0, v1);
+      wg_barrier();  // every wave has read slot `slot`: block kb + 3 may replace it
+      if (kb + kAttnRing < kb_hi)
+        attn_stage(ksrc, ssrc, valid, nkb_pre, kb + kAttnRing, slot == 0 ? buf0 : slot == 1 ? buf1 : buf2, vring + slot * kVringFloats, wave, lane);
       KvBlock blk;
-      blk.valid0 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + g * 4);
-      blk.valid1 = *reinterpret_cast<const uint32_t*>(valid + kb * 32 + 16 + g * 4);
-      lds_reads_done(fr);
-      wg_barrier();  // every wave has read buffer bi: block kb + 2 may replace it
-      if (kb + 2 < kb_hi) stage(kb + 2, bi ? buf1 : buf0);
 #pragma unroll
       for (int f = 0; f < 16; ++f) {
         blk.k[f] = __builtin_bit_cast(bf16x8, fr[f]);
         blk.v[f] = __builtin_bit_cast(bf16x8, fr[16 + f]);
       }
+      blk.valid0 = v0;
+      blk.valid1 = v1;
       if (has_rows) attend_block_q(blk, [&](int ds) { return qf[ds]; }, m_run, l_run, oacc);
     }
     l_run += __shfl_xor(l_run, 16);
@@ -1121,6 +1176,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
   return true;
 }
 
+template <bool G>
 __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
   const int n_items = nbp * nsplit;
@@ -1144,7 +1200,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   float* s_l = s_m + 64;                       // [4][16]
   PHASE_TS(s, l, kPhSplit, 0);
   bool waited = false, burst = false;
-  if (attn_grouped(a)) {
+  if (attn_grouped<G>(a)) {
     // gate_up(l) tile 0, fragments 0..15 -> region A's lower half, ahead of the polls
     copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
     burst = true;
@@ -1153,7 +1209,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     PHASE_TS(s, l, kPhSplit, 2);
     if (!attn_group_items(a, s, l, smem, s_flag)) return false;
   }
-  for (int item = attn_grouped(a) ? n_items : (int)blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = attn_grouped<G>(a) ? n_items : (int)blockIdx.x; item < n_items; item += gridDim.x) {
     const int bp = item % nbp, split = item / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
     const int rbq = b * (kRowsPerSample / 2) + pair;  // query-row m-tile (16 rows = 2 tokens x 8 heads)
@@ -1664,6 +1720,7 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 // quarters in order and applies the gated residual to both tiles, as phase_down does for one.  The
 // finisher's flag (index g + 32 h) covers both tiles and the half's samples.
 // =============================================================================================
+template <bool G>
 __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   constexpr int KSTEPS = kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 33;
@@ -1671,6 +1728,9 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = (int)blockIdx.x;
   PHASE_TS(s, l, PH, 0);
+  // copy wave: with grouped attention this layer's down_proj weights were copied to region B at
+  // gate_up; they have landed (read after the polls' barrier)
+  if (attn_grouped<G>(a) && copy_wave()) wait_vmcnt<0>();
   // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
   {
     int ln;
@@ -1826,6 +1886,15 @@ static_assert(kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "down_proj pair
 static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
 
+// Two instances: MULTI = false for one sample, where the batch is the constant 1, so none of the
+// batched phases' code (pair items, grouped attention) is compiled into it -- carrying that code
+// costs the single-sample schedule 3.5 % through register allocation -- and MULTI = true for
+// batches of two and more.
+// Two instances of the kernel: G = false for one sample, G = true for batches (always the pair
+// items), which alone contains the grouped attention.  Each is compiled in a translation unit of
+// its own: inlined into one module, the batched code changed the one-sample kernel's register
+// allocation (measured +2-3.5 % per C1 predict).
+template <bool G>
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   __shared__ __align__(16) float smem[kLdsFloats];
   __shared__ int s_flag;
@@ -1837,24 +1906,32 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
     ok = phase_io(a, s, smem, &s_flag);
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
-      ok = phase_norm_gemm<kModeQkv>(a, s, l, smem, &s_flag) && phase_attn(a, s, l, smem, &s_flag) &&
+      ok = phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag) && phase_attn<G>(a, s, l, smem, &s_flag) &&
            phase_oproj(a, s, l, smem, &s_flag) &&
-           (a.batch > 1 && PI05_GU_PAIRS ? phase_gateup_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeGateUp>(a, s, l, smem, &s_flag)) &&
-           (a.batch > 1 && PI05_DOWN_PAIRS ? phase_down_pairs(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
+           ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
+                                                : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag)) &&
+           ((G || a.batch > 1) && PI05_DOWN_PAIRS ? phase_down_pairs<G>(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
   wait_vmcnt<0>();
 }
 
+#if PI05_PERSISTENT_INSTANCE == 1
+const void* denoise_loop_kernel_batched() { return reinterpret_cast<const void*>(denoise_loop_kernel<true>); }
+#else
+const void* denoise_loop_kernel_batched();  // instance 1
+
+const void* denoise_loop_kernel_ptr(int batch) {
+  return batch > 1 ? denoise_loop_kernel_batched() : reinterpret_cast<const void*>(denoise_loop_kernel<false>);
+}
+
 hipError_t launch_denoise_loop(const MegaArgs& a, int grid, hipStream_t st) {
   void* args[] = {const_cast<MegaArgs*>(&a)};
-  return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(denoise_loop_kernel), dim3(grid), dim3(kThreads), args, 0, st);
+  return hipLaunchCooperativeKernel(denoise_loop_kernel_ptr(a.batch), dim3(grid), dim3(kThreads), args, 0, st);
 }
 
 int denoise_loop_threads() { return kThreads; }
-
-const void* denoise_loop_kernel_ptr() { return reinterpret_cast<const void*>(denoise_loop_kernel); }
 
 // =============================================================================================
 // shift . W^T table (built by pi05_refresh_weights): one wave per (layer, output column), lane
@@ -1907,16 +1984,35 @@ hipError_t launch_shift_bias(const ShiftBiasArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+#endif  // PI05_PERSISTENT_INSTANCE
+
 }  // namespace pi05
 
 #ifdef PI05_PHASE_TIMESTAMPS
-// Copy the phase timestamps of the last launch to the host (profiling builds only).
-extern "C" int pi05_debug_phase_timestamps(unsigned long long* host) {
+// Phase timestamps of the last launch to the host / zeroed before the launch to be recorded
+// (profiling builds only).  Each instance has its own array; the one that did not run holds zeros.
+#if PI05_PERSISTENT_INSTANCE == 1
+int pi05_phase_ts_copy_batched(unsigned long long* host) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(pi05::pi05_phase_ts), sizeof(pi05::pi05_phase_ts), 0, hipMemcpyDeviceToHost);
 }
-// Zero the phase timestamps (before the launch to be recorded).
+int pi05_phase_ts_clear_batched(const unsigned long long* zeros) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(pi05::pi05_phase_ts), 0, hipMemcpyHostToDevice);
+}
+#else
+int pi05_phase_ts_copy_batched(unsigned long long* host);
+int pi05_phase_ts_clear_batched(const unsigned long long* zeros);
+extern "C" int pi05_debug_phase_timestamps(unsigned long long* host) {
+  constexpr size_t n = sizeof(pi05::pi05_phase_ts) / sizeof(unsigned long long);
+  static unsigned long long other[n];
+  int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(pi05::pi05_phase_ts), sizeof(pi05::pi05_phase_ts), 0, hipMemcpyDeviceToHost);
+  if (rc == 0) rc = pi05_phase_ts_copy_batched(other);
+  for (size_t i = 0; rc == 0 && i < n; ++i) host[i] += other[i];
+  return rc;
+}
 extern "C" int pi05_debug_phase_timestamps_clear(void) {
   static unsigned long long zeros[sizeof(pi05::pi05_phase_ts) / sizeof(unsigned long long)];
-  return (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+  int rc = (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+  return rc == 0 ? pi05_phase_ts_clear_batched(zeros) : rc;
 }
+#endif
 #endif
