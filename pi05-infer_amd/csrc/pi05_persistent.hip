@@ -354,10 +354,18 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 __device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
   return a.batch > 1 ? 2 * ((int)blockIdx.x % (kGuItems / 2)) : (int)blockIdx.x;
 }
-template <int MODE>
+// qkv items.  B = 1: item i = qkv_item() computes tile pair i mod 80 over row half i / 80 of the
+// sample.  In the batched kernel instance (G): item i computes tile pairs 2 (i mod 40) and
+// 2 (i mod 40) + 1 over row half (i / 40) mod 2 for sample half i / 80, as gate_up's pair items
+// do; region A holds the first pair.
+template <bool G>
+__device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
+  return G && a.batch > 1 ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item() % kQkvPairs;
+}
+template <int MODE, bool G = false>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = MODE == kModeQkv ? qkv_item() % kQkvPairs : gu_pair0(a);  // qkv: the tile pair
+  const int p = MODE == kModeQkv ? qkv_pair0<G>(a) : gu_pair0(a);  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -369,11 +377,11 @@ __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int 
     return wl + (which == 0 ? kOffGate : kOffUp) + (size_t)p * KSTEPS * 512;
   }
 }
-template <int MODE, int F0, int N>
+template <int MODE, int F0, int N, bool G = false>
 __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
   if (!copy_wave()) return;
   if (MODE == kModeQkv ? (unsigned)qkv_item() >= (unsigned)kQkvItems : blockIdx.x >= kGuItems) return;
-  lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE>(a, l, which) + F0 * 512);
+  lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE, G>(a, l, which) + F0 * 512);
 }
 
 // down_proj weights of item blockIdx.x = (tile, K quarter) -> region B.
@@ -990,6 +998,193 @@ __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem,
   PHASE_TS(s, l, kPhGu, 5);
   publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch);
   PHASE_TS(s, l, kPhGu, 6);
+  return true;
+}
+
+// =============================================================================================
+// qkv in the batched kernel instance: two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from
+// registers) over row half mh for the samples [b0, b1) of sample half sh (see qkv_pair0), as
+// gate_up's pair items do; both pairs are RoPE pairs (g < 36) or both v pairs.  The epilogue per
+// pair is phase_norm_gemm's: bf16(rstd * acc + shift . W^T), then RoPE into the query rows or the
+// action-key block, or the permuted V fragments.
+// =============================================================================================
+__device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 2;
+  const int L = a.depth, R = a.R;
+  const int item = qkv_item();
+  PHASE_TS(s, l, kPhQkv, 0);
+  // copy wave: this phase's weights (region A) and everything issued before them have landed;
+  // down(l) -> B here unless grouped attention stages K/V there (then at gate_up)
+  if (copy_wave()) {
+    wait_vmcnt<0>();
+    if (!attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
+  }
+  if (item < 0 || item >= kQkvItems) return true;
+  const int grp = item % (kQkvPairs / 2), mh = (item / (kQkvPairs / 2)) % 2, sh = item / kQkvPairs;
+  const int p0 = 2 * grp;
+  const bool rotated = p0 < 72;
+  const int rb = 32 * mh, nrow = MT * 16 < kHorizon - rb ? MT * 16 : kHorizon - rb;
+  const int bh = (a.batch + 1) / 2, b0 = sh * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const bool comp = tid < kCompThreads;
+  const int r16 = lane & 15;
+  const int ks0 = wave * KSW;
+  const size_t slw = (size_t)s * L + l;
+  const u16* gin = a.g + slw * R * kWidth;
+  const float* ssin = a.ss + ((size_t)s * (L + 1) + l) * kTiles * R;
+  const float* bias = a.bias + slw * kBiasCols;
+  // the pair's two tiles: RoPE pairs (head, d-tile dt) -> tiles head*16 + dt and + 8; v pairs ->
+  // consecutive v tiles
+  auto tile_of = [&](int p, int which) {
+    const int t0 = p < 72 ? (p >> 3) * 16 + (p & 7) : 144 + 2 * (p - 72);
+    return which == 0 ? t0 : (p < 72 ? t0 + 8 : t0 + 1);
+  };
+  float* s_rstd = smem + kLdsWork;  // [32] (item rows)
+  float* s_bias = s_rstd + 64;      // [64] shift . W^T: pair p0 (tile 0, tile 1), pair p1 (tile 0, tile 1)
+  float* s_rs = s_bias + 64;        // [3][64]
+  float* red = s_rs + 192;          // [3 waves][MT][2][64 lanes][4] (one pair at a time)
+  float* T = red + kCompWaves * MT * 2 * 256;  // [32][TS]
+  // pair p1's weight fragments of this wave's k-steps (both tiles): waves 1 and 2 ahead of the
+  // polls, wave 0 after them; wave 2's fragment of p0's tile 1 at k-step 31 (not in LDS)
+  const u16* wq = a.wpack + (size_t)l * kLayerElems + kOffQkv;
+  bf16x8 w1[2][KSW];
+  auto load_w1 = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) {
+        const int ks = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;  // the surplus step multiplies zeros
+        w1[t][s2] = *reinterpret_cast<const bf16x8*>(wq + ((size_t)tile_of(p0 + 1, t) * KSTEPS + ks) * 512 + lane * 8);
+      }
+  };
+  bf16x8 w31 = {};
+  if (wave == 1 || wave == 2) load_w1();
+  if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(wq + ((size_t)tile_of(p0, 1) * KSTEPS + 31) * 512 + lane * 8));
+  if (tid >= 64 && tid < 128) {
+    const int c = tid - 64, pr = c >> 5, t = (c >> 4) & 1, n = c & 15;
+    s_bias[c] = bias[tile_of(p0 + pr, t) * 16 + n];
+  }
+  PHASE_TS(s, l, kPhQkv, 1);
+  {
+    const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
+    const int ndep = l == 0 ? a.batch * kHorizon : kTiles;
+    if (!wait_flags(a, dep, ndep, s_flag)) return false;
+  }
+  PHASE_TS(s, l, kPhQkv, 2);
+  if (wave == 0) load_w1();
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
+  const int et = tid - 64;  // RoPE epilogue thread: item row et/2, half et%2
+  const bool rope_thread = rotated && et >= 0 && et < 2 * nrow;
+  for (int b = b0; b < b1; ++b) {
+    const int m0 = b * kRowsPerSample;
+    f32x4 acc[MT][NT];
+    if (comp) {
+      const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
+      const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
+      float st[22];
+#pragma unroll
+      for (int t = 0; t < 22; ++t) {
+        const int tile = 22 * wave + t;
+        buf_f32(st[t], rsrc_s, tile < kTiles && lane < 16 * MT ? ((tile * R + m0 + rb + lane) * 4) : kOob);
+      }
+      bf16x8 hr[MT][KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bool ok = r16 < nrow - mt * 16 && ks0 + s2 < KSTEPS;
+          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + 2 * mh + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+        }
+      sched_fence();
+      float v = 0.f;
+#pragma unroll
+      for (int t = 0; t < 22; ++t) v += st[t];
+      s_rs[wave * 64 + lane] = v;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
+        if (t >= 2) return w1[t - 2][s2];
+        const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
+        if (t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
+        return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
+      });
+    }
+    __syncthreads();  // the row sums are in LDS
+    if (tid < 16 * MT) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      if (comp) {
+        f32x4 accp[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) accp[mt][0] = acc[mt][2 * pr], accp[mt][1] = acc[mt][2 * pr + 1];
+        store_wave_partials<MT, 2>(red, accp, wave, lane);
+      }
+      __syncthreads();
+      reduce_to_tile<MT, 2, TS>(red, T);
+      __syncthreads();
+      const int p = p0 + pr, tile0 = tile_of(p, 0);
+      if (rotated) {
+        // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
+        if (rope_thread) {
+          const int head = p >> 3, dt = p & 7;
+          const int row = et >> 1, half = et & 1;
+          const size_t cr = (size_t)(b * kHorizon + rb + row) * kHeadDim + dt * 16 + half * 8;
+          const u16x8 cs_lo = *reinterpret_cast<const u16x8*>(a.cos_tab + cr), sn_lo = *reinterpret_cast<const u16x8*>(a.sin_tab + cr);
+          const u16x8 cs_hi = *reinterpret_cast<const u16x8*>(a.cos_tab + cr + kHalfDim), sn_hi = *reinterpret_cast<const u16x8*>(a.sin_tab + cr + kHalfDim);
+          const float rstd = s_rstd[row];
+          float tl[8], th[8], bl[8], bhh[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            tl[q] = T[row * TS + half * 8 + q];
+            th[q] = T[row * TS + 16 + half * 8 + q];
+            bl[q] = s_bias[32 * pr + half * 8 + q];
+            bhh[q] = s_bias[32 * pr + 16 + half * 8 + q];
+          }
+          sched_fence();
+          u16 olo[8], ohi[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float x_lo = round_bf(__builtin_fmaf(rstd, tl[q], bl[q]));
+            const float x_hi = round_bf(__builtin_fmaf(rstd, th[q], bhh[q]));
+            olo[q] = f2bf(fsub(fmul(x_lo, bf2f(cs_lo[q])), fmul(x_hi, bf2f(sn_lo[q]))));
+            ohi[q] = f2bf(fadd(fmul(x_hi, bf2f(cs_hi[q])), fmul(x_lo, bf2f(sn_hi[q]))));
+          }
+          const int d = dt * 16 + half * 8;
+          if (head < kHeads) {
+            u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
+            const int qrow = (m0 + rb + row) * kQRowsPerTok + head;
+            st_bf16x8(qs, afrag_index(qrow, d, kHeadDim / 32), olo);
+            st_bf16x8(qs, afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
+          } else {
+            u16* kc = a.ksuf + (slw * a.batch + b) * 64 * kHeadDim;
+            st_bf16x8(kc, kfrag_index(rb + row, d), olo);
+            st_bf16x8(kc, kfrag_index(rb + row, d + kHalfDim), ohi);
+          }
+        }
+      } else if (comp) {
+        // v: chunk -> (dim dcol of the tile pair, key group (kb, g) of the permuted V fragment);
+        // this item's rows are the keys of 32-key block kb = mh
+        for (int ci = tid; ci < 128; ci += kCompThreads) {
+          const int dcol = ci & 31, kb = mh, gg = ci >> 5;
+          u16 v8[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int key = vkey(kb, gg, q);
+            v8[q] = key < kHorizon ? f2bf(__builtin_fmaf(s_rstd[key - rb], T[(key - rb) * TS + dcol], s_bias[32 * pr + dcol])) : (u16)0;
+          }
+          const int dv = (tile0 - 144) * 16 + dcol;
+          u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
+          st_bf16x8(vc, ((size_t)kb * 16 + (dv >> 4)) * 512 + (size_t)(gg * 16 + (dv & 15)) * 8, v8);
+        }
+      }
+      __syncthreads();  // red and T are reused
+    }
+  }
+  PHASE_TS(s, l, kPhQkv, 5);
+  publish(a, flag_base(a, s, l, kPhQkv) + item, a.epoch);
+  PHASE_TS(s, l, kPhQkv, 6);
   return true;
 }
 
@@ -1735,8 +1930,8 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   {
     int ln;
     if (next_layer(a, s, l, &ln)) {
-      copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
-      copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
+      copy_norm_w<kModeQkv, 0, 32, G>(a, ln, 0, smem);
+      copy_norm_w<kModeQkv, 0, 31, G>(a, ln, 1, smem);
     }
   }
   if (item >= kTiles * kKSplit) return true;
@@ -1881,6 +2076,7 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
 // =============================================================================================
 static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
 static_assert(64 + 64 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "gate_up pairs working area");
+static_assert(64 + 64 + 192 + kCompWaves * 2 * 2 * 256 + 32 * 33 <= kWorkFloats, "qkv pairs working area");
 static_assert(kCompWaves * 4 * 256 + 64 * 17 + 128 <= kWorkFloats, "residual working area");
 static_assert(kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "down_proj pairs working area");
 static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
@@ -1899,14 +2095,15 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   __shared__ __align__(16) float smem[kLdsFloats];
   __shared__ int s_flag;
   // the copy wave: step 0, layer 0 qkv and o_proj weights
-  copy_norm_w<kModeQkv, 0, 32>(a, 0, 0, smem);
-  copy_norm_w<kModeQkv, 0, 31>(a, 0, 1, smem);
+  copy_norm_w<kModeQkv, 0, 32, G>(a, 0, 0, smem);
+  copy_norm_w<kModeQkv, 0, 31, G>(a, 0, 1, smem);
   bool ok = true;
   for (int s = 0; s <= a.steps && ok; ++s) {
     ok = phase_io(a, s, smem, &s_flag);
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
-      ok = phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag) && phase_attn<G>(a, s, l, smem, &s_flag) &&
+      ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
+           phase_attn<G>(a, s, l, smem, &s_flag) &&
            phase_oproj(a, s, l, smem, &s_flag) &&
            ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
                                                 : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag)) &&
