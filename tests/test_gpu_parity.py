@@ -120,9 +120,9 @@ def test_c3_batch8(full_weights):
 
 
 def test_batch5_batch_paths(full_weights):
-    """B=5: the batch paths at an odd batch -- attention with the batch-aware key-split count (3
-    splits: 125 row blocks x 9 would take more than four passes of the grid) and gate_up's
-    two-pair items over sample halves of 3 and 2."""
+    """B=5: the batched kernel at an odd batch -- grouped attention items (4 row blocks of a sample
+    sharing each K/V block; 7 key splits) and the qkv / gate_up / down_proj pair items over sample
+    halves of 3 and 2."""
     print("case B=5: depth 4, B=5, P=968, 3 steps", flush=True)
     model, _, _, _, ref, got = _run_case(full_weights, depth=4, B=5, steps=3)
     _check("B=5", ref, got, 3)
@@ -139,6 +139,22 @@ def test_ragged_prefix_padding(full_weights):
 
     model, _, _, _, ref, got = _run_case(full_weights, depth=4, P=300, B=3, steps=3, pad_fn=pad_fn)
     _check("ragged", ref, got, 3)
+    model.close()
+
+
+def test_ragged_grouped_attention(full_weights):
+    """B=4 (grouped attention: each 32-key block and its key-valid bytes staged through LDS) with
+    padded tails, an interior hole and a sample whose valid keys end inside a block."""
+    print("case ragged grouped: depth 3, B=4, P=300, padded tails and a hole", flush=True)
+
+    def pad_fn(pad):
+        pad[0, 281:] = False
+        pad[1, 40:77] = False
+        pad[2, 130:] = False
+        pad[3, 0:3] = False
+
+    model, _, _, _, ref, got = _run_case(full_weights, depth=3, P=300, B=4, steps=2, pad_fn=pad_fn)
+    _check("ragged grouped", ref, got, 2)
     model.close()
 
 
