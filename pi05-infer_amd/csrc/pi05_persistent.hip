@@ -483,6 +483,7 @@ __device__ __forceinline__ float sum32(const float (&v)[32]) {
 // =============================================================================================
 constexpr int kOutParts = 6;
 constexpr int kOutRun = 172;
+template <bool G>
 __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
   const int L = a.depth, NN = 2 * L + 1, R = a.R, NC = a.batch * kHorizon;
   const int tid = phase_tid();
@@ -524,7 +525,7 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
       if (tid < 128) load_mod();
     }
     if (has_prev && !waited) {
-      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), kTiles, s_flag)) return false;
+      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), G ? kKSplit * kTiles : kTiles, s_flag)) return false;
       waited = true;
     }
     if (has_prev && tid < 64) {
@@ -1067,7 +1068,7 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
   PHASE_TS(s, l, kPhQkv, 1);
   {
     const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
-    const int ndep = l == 0 ? a.batch * kHorizon : kTiles;
+    const int ndep = l == 0 ? a.batch * kHorizon : kKSplit * kTiles;  // down_proj_pairs: one flag per (group, quarter)
     if (!wait_flags(a, dep, ndep, s_flag)) return false;
   }
   PHASE_TS(s, l, kPhQkv, 2);
@@ -1910,10 +1911,12 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 
 // =============================================================================================
 // down_proj at B > 1: two tiles (nt0 = 2g from region B, nt1 = 2g + 1 from registers) and one K
-// quarter for the samples [b0, b1) of half h (workgroup 64 q + 32 h + g, see down_item).  Quarters 1..3 store their partials
-// of both tiles and flag them for the group's finisher (quarter 0, same XCD), which adds the four
-// quarters in order and applies the gated residual to both tiles, as phase_down does for one.  The
-// finisher's flag (index g + 32 h) covers both tiles and the half's samples.
+// quarter for the samples [b0, b1) of half h (workgroup 64 q + 32 h + g, see down_item).  Every
+// quarter stores its partials of both tiles and flags them for the group (the four quarters run on
+// one XCD); then quarter q finishes samples b0 + q, b0 + q + 4, ... of the half: it adds the four
+// quarters in order and applies the gated residual to both tiles, as phase_down does for one.  Its
+// flag (index 4 (g + 32 h) + q) covers both tiles and those samples, so the next phase waits for
+// 256 flags.
 // =============================================================================================
 template <bool G>
 __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
@@ -1991,7 +1994,7 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
     __syncthreads();
     reduce_to_tile<4, 2, TS>(red, T);
     __syncthreads();
-    // partials [quarter][tile][row][16] of both tiles (the finisher's own too: it reloads them);
+    // partials [quarter][tile][row][16] of both tiles (every quarter's: the finishers reload them);
     // compute waves only, whose stores publish_local waits for
     for (int e = tid; comp && e < 512; e += kCompThreads) {
       const int t = e >> 8, row = (e >> 2) & 63, q4 = e & 3;
@@ -2004,14 +2007,10 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   PHASE_TS(s, l, PH, 5);
   unsigned* fl = flag_base(a, s, l, PH);
   unsigned* fpart = fl + kPartFlags + 4 * (grp + NG * half);
-  if (ksp != 0) {
-    // this quarter's partials are in this XCD's L2: flag them for the group's finisher
-    publish_local(a, fpart + (ksp - 1), a.epoch);
-    return true;
-  }
-  // ---- the finisher (quarter 0): thread t -> tile t / 128, row t % 64, columns ((t / 64) % 2) * 8 .. +7
-  if (comp) wait_stores();  // its own partials, reloaded below
-  if (!wait_flags(a, fpart, kKSplit - 1, s_flag)) return false;
+  // this quarter's partials are in this XCD's L2: flag them for the group (all four quarters run on
+  // this XCD), then wait for the other three; quarter q finishes samples b0 + q, b0 + q + 4, ...
+  publish_local(a, fpart + ksp, a.epoch);
+  if (!wait_flags(a, fpart, kKSplit, s_flag)) return false;
   PHASE_TS(s, l, PH, 7);
   {
     const int ft = tid >> 7, frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;
@@ -2029,7 +2028,7 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
       if (next_g) s1[i] = smod[i];
     }
     float* s_ss = T;  // [2 tiles][2 halves][64 rows]
-    for (int b = b0; b < b1; ++b) {
+    for (int b = b0 + ksp; b < b1; b += kKSplit) {
       const int r = b * kRowsPerSample + frow;
       float ss = 0.f;
       if (frow < kHorizon) {
@@ -2066,7 +2065,7 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
     }
   }
   PHASE_TS(s, l, PH, 8);
-  publish(a, fl + grp + NG * half, a.epoch, true);  // the copy wave stored rows too
+  publish(a, fl + (grp + NG * half) * kKSplit + ksp, a.epoch, true);  // the copy wave stored rows too
   PHASE_TS(s, l, PH, 9);
   return true;
 }
@@ -2099,7 +2098,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   copy_norm_w<kModeQkv, 0, 31, G>(a, 0, 1, smem);
   bool ok = true;
   for (int s = 0; s <= a.steps && ok; ++s) {
-    ok = phase_io(a, s, smem, &s_flag);
+    ok = phase_io<G>(a, s, smem, &s_flag);
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
       ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
