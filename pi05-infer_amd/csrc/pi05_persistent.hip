@@ -1372,6 +1372,79 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
   return true;
 }
 
+// Merges after the grouped split items: one role per row block (all four head pairs), so the 200
+// row blocks at B = 8 take one pass of the grid instead of the 800 (row block, head pair) roles'
+// three.  Thread t combines row t / 16 of the row block (16 rows: 2 tokens x 8 heads), dims
+// (t % 16) * 16 .. +15, over the splits in the same order and arithmetic as the merges below, and
+// stores them straight into o_proj's A operand; then the row block's four merge flags.
+__device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) {
+  const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
+  const size_t slw = (size_t)s * L + l;
+  const float* apart = a.apart + slw * (size_t)nsplit * nbp * 16 * kHeadDim;
+  const float* apart_ml = a.apart_ml + slw * (size_t)nsplit * nbp * 32;
+  const unsigned* fsplit = flag_base(a, s, l, kPhSplit);
+  unsigned* fmerge = flag_base(a, s, l, kPhMerge);
+  u16* os = a.o + slw * (size_t)R * (kHeads * kHeadDim);
+  const int tid = phase_tid(), rr = tid >> 4, d0 = (tid & 15) * 16;
+  const brsrc rml = make_rsrc(apart_ml, (size_t)nsplit * nbp * 32 * 4);
+  const brsrc rpo = make_rsrc(apart, (size_t)nsplit * nbp * 16 * kHeadDim * 4);
+  for (int bp = blockIdx.x; bp < nbp; bp += gridDim.x) {
+    const int b = bp / kPairs, pair = bp % kPairs;
+    if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
+    float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
+#pragma unroll
+    for (int c = 0; c < kMaxAttnSplits; ++c) {
+      const int mo = (c * nbp + bp) * 32 + rr;
+      buf_f32(mc[c], rml, c < nsplit ? mo * 4 : kOob);
+      buf_f32(lc[c], rml, c < nsplit ? (mo + 16) * 4 : kOob);
+    }
+    float Mb = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kMaxAttnSplits; ++c) Mb = fmaxf(Mb, c < nsplit ? mc[c] : -INFINITY);
+    float Lb = 0.f;
+    f32x4 ob[4] = {};
+    for (int c0 = 0; c0 < nsplit; c0 += 4) {
+      f32x4 oc[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bool ok = c0 + c < nsplit;
+          oc[c][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rpo, ok ? (int)((((size_t)((c0 + c) * nbp + bp) * 16 + rr) * kHeadDim + d0 + 4 * q) * 4) : kOob, 0, 0));
+        }
+      sched_fence();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c0 + c >= nsplit) break;
+        float m = mc[0], lcv = lc[0];
+#pragma unroll
+        for (int k = 1; k < kMaxAttnSplits; ++k)
+          if (k == c0 + c) m = mc[k], lcv = lc[k];
+        const float wc = m == -INFINITY ? 0.f : __expf(m - Mb);
+        Lb += lcv * wc;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ob[q] += oc[c][q] * wc;
+      }
+    }
+    const float inv = 1.0f / Lb;
+    const int token = rr >> 3, head = rr & 7;
+    const int r = b * kRowsPerSample + 2 * pair + token;
+#pragma unroll
+    for (int h8 = 0; h8 < 2; ++h8) {
+      u16 v8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v8[i] = f2bf(ob[2 * h8 + i / 4][i % 4] * inv);
+      st_bf16x8(os, afrag_index(r, head * kHeadDim + d0 + 8 * h8, kHeads * kHeadDim / 32), v8);
+    }
+    // the row block's four (row block, head pair) flags, every replica
+    wait_stores();
+    wg_barrier();
+    if (tid < kHeadPairs * kFlagCopies) st_u32(fmerge + 4 * bp + tid / kFlagCopies + (size_t)(tid % kFlagCopies) * a.fstride, a.epoch);
+  }
+  return true;
+}
+
 template <bool G>
 __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
@@ -1547,6 +1620,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   if (!burst) copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
   copy_norm_w<kModeGateUp, 16, 16>(a, l, 0, smem);
   copy_norm_w<kModeGateUp, 0, 32>(a, l, 1, smem);
+  if (attn_grouped<G>(a)) return attn_group_merges(a, s, l, s_flag);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
   // on work of its own.  All four waves merge (the copy wave has nothing in flight by now): thread
