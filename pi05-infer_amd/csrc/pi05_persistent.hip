@@ -319,7 +319,10 @@ constexpr int kLdsB = kLdsA + 16384;
 constexpr int kLdsWork = kLdsB + 8192;
 constexpr int kWorkFloats = 8736;
 constexpr int kLdsFloats = kLdsWork + kWorkFloats;
-static_assert(kLdsFloats * 4 <= 160 * 1024, "LDS budget of a gfx950 workgroup");
+// the batched kernel instance's working area (its gate_up reduces four waves' partials)
+constexpr int kWorkFloatsBatched = 10752;
+constexpr int kLdsFloatsBatched = kLdsWork + kWorkFloatsBatched;
+static_assert(kLdsFloats * 4 <= 160 * 1024 && kLdsFloatsBatched * 4 <= 160 * 1024, "LDS budget of a gfx950 workgroup");
 constexpr int kLdsA1 = kLdsA + 8192;  // upper half of A (tile 1); during attention: wave O slots
 
 // A burst of N contiguous 1 KiB fragments (N <= 63, a compile-time count) from src to LDS dst by
@@ -451,6 +454,28 @@ __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
     f32x4 v = r[0][t];
 #pragma unroll
     for (int w = 1; w < kCompWaves; ++w) v += r[w][t];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) T[(mt * 16 + (ln >> 4) * 4 + i) * TS + t * 16 + (ln & 15)] = v[i];
+  }
+}
+
+// The same over NW waves' partials (red[wave][mt][t][lane], NW * MT * NT fragments).
+template <int NW, int MT, int NT, int TS>
+__device__ __forceinline__ void reduce_to_tile_n(const float* red, float* T) {
+  const int tid = threadIdx.x;
+  const int mt = tid >> 6, ln = tid & 63;
+  if (mt >= MT) return;
+  f32x4 r[NW][NT];
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) r[w][t] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * MT + mt) * NT + t) * 64 + ln) * 4);
+  sched_fence();
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    f32x4 v = r[0][t];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += r[w][t];
 #pragma unroll
     for (int i = 0; i < 4; ++i) T[(mt * 16 + (ln >> 4) * 4 + i) * TS + t * 16 + (ln & 15)] = v[i];
   }
@@ -1188,6 +1213,125 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
   PHASE_TS(s, l, kPhQkv, 6);
   return true;
 }
+
+// =============================================================================================
+// gate_up in the batched kernel instance: phase_gateup_pairs' items, with the copy wave as a fourth
+// compute wave (its down_proj copy is issued before o_proj instead): K splits 8 k-steps per wave, so
+// a sample's 48 loads per wave stay under the 63 a wave may have in flight and each wave runs 128
+// MFMAs per sample instead of 176; the four partials are added in wave order.
+// =============================================================================================
+__device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int NW = 4, NT = 4, KSW = 8, KSTEPS = kWidth / 32, TS = 33, MT = 4, TPW = kTiles / NW;
+  const int L = a.depth, R = a.R;
+  const int item = (int)blockIdx.x;
+  PHASE_TS(s, l, kPhGu, 0);
+  // copy wave: pair p0's weights (region A) and everything issued before them have landed
+  if (copy_wave()) wait_vmcnt<0>();
+  const int half = item / (kGuItems / 2), p0 = gu_pair0(a), p1 = p0 + 1;
+  const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  if (item >= kGuItems) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int ks0 = wave * KSW;
+  const size_t slw = (size_t)s * L + l;
+  const u16* gin = a.gmid + slw * R * kWidth;
+  const float* ssin = a.ssmid + slw * kTiles * R;
+  const float* bias = a.bias + slw * kBiasCols;
+  float* s_rstd = smem + kLdsWork;  // [64] (sample rows)
+  float* s_bias = s_rstd + 64;      // [64] shift . W^T: gate p0, up p0, gate p1, up p1 (16 each)
+  float* s_rs = s_bias + 64;        // [4][64]
+  float* red = s_rs + 256;          // [4 waves][4 m-tiles][2 tiles][64 lanes][4] (one pair at a time)
+  float* T = red + NW * MT * 2 * 256;  // [64][TS]
+  const u16* wl = a.wpack + (size_t)l * kLayerElems;
+  bf16x8 w1[2][KSW];
+  auto load_w1 = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2)
+        w1[t][s2] = *reinterpret_cast<const bf16x8*>(wl + (t == 0 ? kOffGate : kOffUp) + ((size_t)p1 * KSTEPS + ks0 + s2) * 512 + lane * 8);
+  };
+  if (wave != 0) load_w1();
+  if (tid >= 64 && tid < 128) {
+    const int c = tid - 64, pr = c >> 5, gu = (c >> 4) & 1, n = c & 15;
+    s_bias[c] = bias[kQkvCols + gu * kMlp + (p0 + pr) * 16 + n];
+  }
+  PHASE_TS(s, l, kPhGu, 1);
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  PHASE_TS(s, l, kPhGu, 2);
+  if (wave == 0) load_w1();
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
+  for (int b = b0; b < b1; ++b) {
+    const int m0 = b * kRowsPerSample;
+    f32x4 acc[MT][NT];
+    {
+      const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
+      const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
+      float st[TPW];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) buf_f32(st[t], rsrc_s, ((TPW * wave + t) * R + m0 + lane) * 4);
+      bf16x8 hr[MT][KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          buf_frag(hr[mt][s2], rsrc_g, r16 < kHorizon - mt * 16 ? (int)((afrag_offset(b * 4 + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+      sched_fence();
+      float v = 0.f;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) v += st[t];
+      s_rs[wave * 64 + lane] = v;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
+        if (t >= 2) return w1[t - 2][s2];
+        return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ks0 + s2) * 512 + lane * 8);
+      });
+    }
+    __syncthreads();  // the row sums are in LDS
+    if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd((((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) + s_rs[192 + tid]) * (1.0f / kWidth), a.eps));
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      f32x4 accp[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) accp[mt][0] = acc[mt][2 * pr], accp[mt][1] = acc[mt][2 * pr + 1];
+      store_wave_partials<MT, 2>(red, accp, wave, lane);
+      __syncthreads();
+      reduce_to_tile_n<NW, MT, 2, TS>(red, T);
+      __syncthreads();
+      // GeGLU (rlinf_fused_denoise.py:166-173) of pair p0 + pr; chunk = (row, half of 16 columns)
+      if (tid < 2 * kHorizon) {
+        const int row = tid >> 1, hf = tid & 1;
+        const float rstd = s_rstd[row];
+        float tg[8], tu[8], bgv[8], buv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          tg[q] = T[row * TS + hf * 8 + q];
+          tu[q] = T[row * TS + 16 + hf * 8 + q];
+          bgv[q] = s_bias[32 * pr + hf * 8 + q];
+          buv[q] = s_bias[32 * pr + 16 + hf * 8 + q];
+        }
+        sched_fence();
+        u16 o8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float gt = round_bf(__builtin_fmaf(rstd, tg[q], bgv[q]));
+          const float up = __builtin_fmaf(rstd, tu[q], buv[q]);
+          o8[q] = f2bf(fmul(gelu_tanh(gt), up));
+        }
+        st_bf16x8(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + row, (p0 + pr) * 16 + hf * 8, kMlp / 32), o8);
+      }
+      __syncthreads();  // red and T are reused
+    }
+  }
+  PHASE_TS(s, l, kPhGu, 5);
+  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch);
+  PHASE_TS(s, l, kPhGu, 6);
+  return true;
+}
+static_assert(64 + 64 + 256 + 4 * 4 * 2 * 256 + 64 * 33 <= kWorkFloatsBatched, "batched gate_up working area");
 
 // =============================================================================================
 // attention, two stages.
@@ -2165,7 +2309,7 @@ static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "
 // allocation (measured +2-3.5 % per C1 predict).
 template <bool G>
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
-  __shared__ __align__(16) float smem[kLdsFloats];
+  __shared__ __align__(16) float smem[G ? kLdsFloatsBatched : kLdsFloats];
   __shared__ int s_flag;
   // the copy wave: step 0, layer 0 qkv and o_proj weights
   copy_norm_w<kModeQkv, 0, 32, G>(a, 0, 0, smem);
@@ -2177,9 +2321,11 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
     for (int l = 0; l < a.depth && ok; ++l) {
       ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
            phase_attn<G>(a, s, l, smem, &s_flag) &&
+           (!G || !attn_grouped<G>(a) || (copy_residual_w<kMlp / 32>(a, l, smem), true)) &&  // grouped: down(l) -> B
            phase_oproj(a, s, l, smem, &s_flag) &&
-           ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
-                                                : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag)) &&
+           (G ? phase_gateup_pairs4(a, s, l, smem, &s_flag)
+              : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
+                                                     : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
            ((G || a.batch > 1) && PI05_DOWN_PAIRS ? phase_down_pairs<G>(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
     }
   }
