@@ -276,6 +276,43 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
   return ok;
 }
 
+// The same for cnt runs of n flags each, run r starting stride words after run r - 1 (f and the
+// stride 16-byte aligned): one poll covers the runs of every sample an item serves, where a wait
+// per sample would cost a memory round trip each.
+__device__ bool wait_flag_runs(const MegaArgs& a, const unsigned* f, int n, int stride, int cnt, int* s_flag) {
+  f += (size_t)(blockIdx.x % kFlagCopies) * a.fstride;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const unsigned ep = a.epoch;
+    const int cpr = (n + 3) >> 2, nch = cpr * cnt;  // 4-word chunks per run, in all
+    int ok = 1;
+    const brsrc rf = make_rsrc(f, (size_t)a.fstride * 4);
+    for (int base = 0; base < nch && ok; base += 64) {
+      const int c = base + lane, run = c / cpr, j = (c - run * cpr) * 4;
+      const bool act = c < nch;
+      const int off = act ? (run * stride + j) * 4 : kOob;
+      auto done = [&](u32x4 v) {
+        return !act || (v[0] == ep && (j + 1 >= n || v[1] == ep) && (j + 2 >= n || v[2] == ep) && (j + 3 >= n || v[3] == ep));
+      };
+      for (int spins = 0;; ++spins) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
+        if (__all(done(v))) break;
+        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
+          if (lane == 0) record_error(a);
+          ok = 0;
+          break;
+        }
+        asm volatile("" ::: "memory");
+      }
+    }
+    if (lane == 0) *s_flag = ok;
+  }
+  wg_barrier();
+  const bool ok = *s_flag != 0;
+  wg_barrier();
+  return ok;
+}
+
 // The stores of this item are complete (the compute waves', and the copy wave's when
 // `copy_stores`: it waits only then, since its stores complete behind its direct-to-LDS copies)
 // -> wave 0 sets the item's flag in every replica.  Every thread of the workgroup calls it (it
@@ -1951,6 +1988,132 @@ __device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s
   return true;
 }
 
+// o_proj of the batched instance: one wait for every sample's merges (which finish in one pass of
+// the grid), then two wave pairs, (1, 2) and (0, 3), each holding the tile's weights in K halves
+// (wave 1 / 0: k-steps 0..31, wave 2 / 3: 32..63), take samples 2i and 2i + 1 of iteration i side
+// by side.  Per sample the arithmetic is phase_oproj's (same accumulation chains, K halves added in
+// order, same epilogue); epilogue threads: lanes 0..31 of wave 1 (pair 0) and of wave 0 (pair 1).
+// With grouped attention the copy wave issues down(l)'s weights into region B after its own weight
+// loads and before the polls.  Measured on MI355X against one sample at a time on waves 1 and 2
+// with a wait per sample: B=8 17.9 -> 17.1 ms, B=3 11.5 -> 11.4, B=2 7.88 -> 7.79 per predict.
+// =============================================================================================
+__device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / 2, TS = 17;
+  constexpr int NCH = 4;
+  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  const int item = blockIdx.x;
+  PHASE_TS(s, l, kPhO, 0);
+  const bool grouped = attn_grouped<true>(a);
+  if (item >= kOItems) {
+    if (grouped) copy_residual_w<kMlp / 32>(a, l, smem);
+    return true;
+  }
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int pr = (wave == 1 || wave == 2) ? 0 : 1;  // wave pair
+  const int kh = (wave == 2 || wave == 3) ? 1 : 0;  // K half
+  const int nt = item % kTiles, mq = item / kTiles;
+  const int col = nt * 16, ks0 = kh * KSW, r16 = lane & 15;
+  const int nrow = kHorizon - 16 * mq < 16 ? kHorizon - 16 * mq : 16;
+  const int np = (nrow + 1) / 2;
+  const size_t slw = (size_t)s * L + l;
+  bf16x8 wf[KSW];
+  {
+    const brsrc rw = make_rsrc(a.wpack + (size_t)l * kLayerElems + kOffO + (size_t)nt * KSTEPS * 512, (size_t)KSTEPS * 1024);
+#pragma unroll
+    for (int s2 = 0; s2 < KSW; ++s2) buf_frag(wf[s2], rw, ((ks0 + s2) * 512 + lane * 8) * 2);
+  }
+  if (grouped) copy_residual_w<kMlp / 32>(a, l, smem);  // copy wave: down(l) -> B (after attention's use of B)
+  const bool ep_thread = (wave == 1 || wave == 0) && lane < 32;
+  const int erow = lane >> 1, ec0 = (lane & 1) * 8;
+  const u16* hres = a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
+  float4 g4[2] = {}, s14[2] = {};
+  if (ep_thread) {
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + ec0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + ec0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
+      s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
+    }
+  }
+  PHASE_TS(s, l, kPhO, 1);
+  const u16* act = a.o + slw * (size_t)R * (KSTEPS * 32);
+  u16* hout = a.hmid + slw * (size_t)R * kWidth;
+  u16* gout = a.gmid + slw * (size_t)R * kWidth;
+  float* rout = a.ssmid + slw * kTiles * R;
+  float* red = smem + kLdsWork;     // [pair][K half][64 lanes][4]
+  float* T = red + 4 * 256;         // [pair][16][TS]
+  float* s_ss = T + 2 * 16 * TS;    // [pair][2 column halves][16 rows]
+  float* Tp = T + pr * 16 * TS;
+  const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
+                         round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
+  const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
+  // merge flags 4 * bp + hp: sample b's run for this m-tile starts at 4 (25 b + 8 mq)
+  if (!wait_flag_runs(a, flag_base(a, s, l, kPhMerge) + 4 * 8 * mq, 4 * np, 4 * kPairs, a.batch, s_flag)) return false;
+  PHASE_TS(s, l, kPhO, 2);
+  for (int i = 0; 2 * i < a.batch; ++i) {
+    const int b = 2 * i + pr;
+    const bool has = b < a.batch;
+    const int m = 4 * b + mq;  // m-tile of the activations
+    const int r = 16 * m + erow;
+    u16x8 hold = {};
+    if (ep_thread && has && erow < nrow) hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + ec0, kWidth / 32));
+    {
+      const brsrc ra = make_rsrc(act, (size_t)R * KSTEPS * 64);
+      bf16x8 af[KSW];
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) {
+        const bool ok = has && r16 < nrow;
+        buf_frag(af[s2], ra, ok ? (int)((afrag_offset(m, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+      }
+      sched_fence();
+      f32x4 acc[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) acc[s2 % NCH] = mfma16x16x32(af[s2], wf[s2], acc[s2 % NCH]);
+      *reinterpret_cast<f32x4*>(red + (((size_t)pr * 2 + kh) * 64 + lane) * 4) = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    if (i == 0) PHASE_TS(s, l, kPhO, 4);
+    wg_barrier();
+    // each pair's two K halves in order, scattered row-major into its T (wave p: pair p)
+    if (tid < 128) {
+      const int pp = tid >> 6;
+      const float* rp = red + (size_t)pp * 2 * 256;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(rp + (size_t)lane * 4) + *reinterpret_cast<const f32x4*>(rp + (size_t)(64 + lane) * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) T[(size_t)pp * 16 * TS + ((lane >> 4) * 4 + j) * TS + (lane & 15)] = v[j];
+    }
+    wg_barrier();
+    float ss = 0.f;
+    if (ep_thread && has && erow < nrow) {
+      u16 hn[8], gn[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float prod = round_bf(fmul(round_bf(Tp[erow * TS + ec0 + j]), gate[j]));
+        hn[j] = f2bf(fadd(bf2f(hold[j]), prod));
+        const float hf = bf2f(hn[j]);
+        gn[j] = f2bf(fmul(hf, s1[j]));
+        ss += hf * hf;
+      }
+      st_bf16x8(hout, afrag_index(r, col + ec0, kWidth / 32), hn);
+      st_bf16x8(gout, afrag_index(r, col + ec0, kWidth / 32), gn);
+    }
+    if (ep_thread) s_ss[pr * 32 + (lane & 1) * 16 + erow] = ss;
+    wg_barrier();
+    // tile-major statistics of both samples: the tile's sums of the m-tile's 16 rows (padded rows: zero)
+    if (tid < 32) {
+      const int pp = tid >> 4, rr = tid & 15, bb = 2 * i + pp;
+      if (bb < a.batch) st_f32(rout + (size_t)nt * R + 16 * (4 * bb + mq) + rr, s_ss[pp * 32 + rr] + s_ss[pp * 32 + 16 + rr]);
+    }
+    wg_barrier();  // red, T and s_ss are reused by the next iteration
+  }
+  PHASE_TS(s, l, kPhO, 5);
+  publish(a, flag_base(a, s, l, kPhO) + item, a.epoch);
+  PHASE_TS(s, l, kPhO, 6);
+  return true;
+}
+
 // =============================================================================================
 // down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves split the quarter.
 // Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on the same XCD) keeps
@@ -2321,8 +2484,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
     for (int l = 0; l < a.depth && ok; ++l) {
       ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
            phase_attn<G>(a, s, l, smem, &s_flag) &&
-           (!G || !attn_grouped<G>(a) || (copy_residual_w<kMlp / 32>(a, l, smem), true)) &&  // grouped: down(l) -> B
-           phase_oproj(a, s, l, smem, &s_flag) &&
+           (G ? phase_oproj_pairs(a, s, l, smem, &s_flag) : phase_oproj(a, s, l, smem, &s_flag)) &&
            (G ? phase_gateup_pairs4(a, s, l, smem, &s_flag)
               : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
                                                      : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
