@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "pi05_infer", "libpi05_denoise.so")
-SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_persistent_batched.hip", "pi05_engine.hip"]
+SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_persistent_batched.hip", "pi05_persistent_grouped.hip", "pi05_engine.hip"]
 PREFIX_OUT = os.path.join(HERE, "pi05_infer", "libpi05_prefix.so")
 PREFIX_SOURCES = ["pi05_prefill.hip", "pi05_siglip.hip"]
 PREFIX_LIBS = ["-lhipblaslt"]  # the plain GEMMs of the prefill and the vision tower

@@ -91,6 +91,9 @@ constexpr int kMaxAttnSplits = 16;
 // row blocks of one sample, one per wave, sharing each K/V block through LDS; the key splits
 // then fill the 256 workgroups once (attn_group_splits).
 constexpr int kAttnGroupMinBatch = 4;
+// Batches from which the persistent kernel's gate_up items split rows over waves instead of K
+// (each wave one sample over the whole K; kernel instance 2).
+constexpr int kRowSplitMinBatch = 3;
 constexpr int kAttnGroup = 4;
 constexpr int kAttnGroupsPerSample = (50 / 2 + kAttnGroup - 1) / kAttnGroup;  // 7 groups of the 25 row blocks
 inline int attn_group_splits(int batch, int nkb) {

@@ -32,12 +32,15 @@
 #include "pi05_blocks.h"
 #include "pi05_kernels.h"
 
-// This file is compiled twice: as itself (instance 0: the one-sample kernel and the host-side
-// entry points) and through pi05_persistent_batched.hip (instance 1: the kernel for batches), so
-// that neither kernel's code generation depends on the other's.
+// This file is compiled three times: as itself (instance 0: the one-sample kernel and the
+// host-side entry points), through pi05_persistent_batched.hip (instance 1: the kernel for batches
+// of 2) and through pi05_persistent_grouped.hip (instance 2: batches of kRowSplitMinBatch and more,
+// with the row-split gate_up and, from kAttnGroupMinBatch on, the grouped attention), so that no
+// kernel's code generation depends on another's paths.
 #ifndef PI05_PERSISTENT_INSTANCE
 #define PI05_PERSISTENT_INSTANCE 0
 #endif
+#define PI05_INSTANCE_GROUPED (PI05_PERSISTENT_INSTANCE == 2)
 
 namespace pi05 {
 
@@ -99,6 +102,11 @@ __device__ __forceinline__ T* uniform_ptr(T* p) {
 // vector store, and publish() waits for it.
 __device__ __forceinline__ void st_wt16(const void* base, uint32_t off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, make_rsrc(uniform_ptr(base), 0x7fffffff), off, 0, 16);
+}
+// The same for 8 bytes (offset 8-byte aligned).
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_wt8(const void* base, uint32_t off, uint32_t lo, uint32_t hi) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, make_rsrc(uniform_ptr(base), 0x7fffffff), off, 0, 16);
 }
 // The same as a plain (L2 write-back) store, for data whose reader runs on the same XCD: it is
 // complete once the XCD's L2 holds it, and that reader's sc1 loads see the dirty line.
@@ -215,14 +223,12 @@ constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-til
 #ifndef PI05_ATTN_GROUP
 #define PI05_ATTN_GROUP 1
 #endif
-// Batches of kAttnGroupMinBatch and more: grouped attention items (attn_group_items), which stage
-// K/V blocks in region B as well, so down(l)'s weights are copied to B at gate_up(l) instead of
-// at qkv(l).
-// G: the kernel instance for batches (denoise_loop_kernel<true>); the one-sample instance does not
-// contain the grouped path at all.
+// Batches of kAttnGroupMinBatch and more (in kernel instance 2): grouped attention items
+// (attn_group_items), which stage K/V blocks in region B as well, so down(l)'s weights are copied
+// to B before o_proj(l) instead of at qkv(l).  G: a batched instance.
 template <bool G>
 __device__ __forceinline__ bool attn_grouped(const MegaArgs& a) {
-  return G && PI05_ATTN_GROUP && PI05_GU_PAIRS && PI05_DOWN_PAIRS && a.batch >= kAttnGroupMinBatch;
+  return G && PI05_INSTANCE_GROUPED && PI05_ATTN_GROUP && PI05_GU_PAIRS && PI05_DOWN_PAIRS && a.batch >= kAttnGroupMinBatch;
 }
 __device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
@@ -391,6 +397,12 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 // samples (w / 128): each activation row it reads then serves four tiles instead of two, so an
 // XCD's workgroups read half as many activation bytes (the phase is bound by that L2 traffic).
 // Region A holds pair 2g; the compute waves hold pair 2g + 1 in registers.
+// The gate_up of kernel instance 2 (phase_gateup_msplit, batches of kRowSplitMinBatch and more):
+// item w = pair w.
+template <bool G>
+__device__ __forceinline__ bool gu_msplit(const MegaArgs&) {
+  return G && PI05_INSTANCE_GROUPED;
+}
 __device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
   return a.batch > 1 ? 2 * ((int)blockIdx.x % (kGuItems / 2)) : (int)blockIdx.x;
 }
@@ -405,7 +417,7 @@ __device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
 template <int MODE, bool G = false>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = MODE == kModeQkv ? qkv_pair0<G>(a) : gu_pair0(a);  // qkv: the tile pair
+  const int p = MODE == kModeQkv ? qkv_pair0<G>(a) : (gu_msplit<G>(a) ? (int)blockIdx.x : gu_pair0(a));  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -1371,6 +1383,125 @@ __device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem
 static_assert(64 + 64 + 256 + 4 * 4 * 2 * 256 + 64 * 33 <= kWorkFloatsBatched, "batched gate_up working area");
 
 // =============================================================================================
+// gate_up of the batched kernel instance, split by rows: item w = gate|up tile pair w for every
+// sample; region A holds its two tiles (gate, up: 32 k-steps each).  Wave j takes samples j,
+// j + 4, ...: for each, all four m-tiles over the whole K, so no partial sum crosses waves and the
+// waves never wait for each other.  The A fragments stream from L2 in chunks of 4 k-steps, two
+// chunks ahead of the MFMAs (into the next sample's first chunks at the end of a sample); the
+// products are formed as W.A^T, so a lane ends with 4 consecutive columns of one row and its
+// GeGLU and 8-byte stores need nothing from other lanes.  Lane r (= row r of the sample) sums its
+// row's 64 tile sums of squares in four groups of 16, loaded during the first four chunks.
+// =============================================================================================
+constexpr int kGuCk = 4;                     // k-steps per A chunk
+constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
+// chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
+__device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane) {
+  const int r16 = lane & 15;
+#pragma unroll
+  for (int s2 = 0; s2 < kGuCk; ++s2)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const bool ok = ok_b && r16 < kHorizon - mt * 16;
+      buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, c * kGuCk + s2, kWidth / 32) + lane * 8) * 2) : kOob);
+    }
+}
+__device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4], const bf16x8 (&A)[4][kGuCk], const u16* lw, int c,
+                                              int lane) {
+  constexpr int KSTEPS = kWidth / 32;
+#pragma unroll
+  for (int s2 = 0; s2 < kGuCk; ++s2) {
+    const int ks = c * kGuCk + s2;
+    const bf16x8 wg = *reinterpret_cast<const bf16x8*>(lw + (size_t)ks * 512 + lane * 8);
+    const bf16x8 wu = *reinterpret_cast<const bf16x8*>(lw + ((size_t)KSTEPS + ks) * 512 + lane * 8);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      accg[mt] = mfma16x16x32(wg, A[mt][s2], accg[mt]);
+      accu[mt] = mfma16x16x32(wu, A[mt][s2], accu[mt]);
+    }
+  }
+}
+__device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  const int L = a.depth, R = a.R;
+  const int item = (int)blockIdx.x;
+  PHASE_TS(s, l, kPhGu, 0);
+  // copy wave: the pair's weights (region A) and everything issued before them have landed
+  if (copy_wave()) wait_vmcnt<0>();
+  if (item >= kGuItems) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const size_t slw = (size_t)s * L + l;
+  const float* bias = a.bias + slw * kBiasCols;
+  // shift . W^T of this lane's columns 4g .. 4g+3 of the gate and up tiles
+  float bgv[4], buv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bgv[i] = bias[kQkvCols + item * 16 + 4 * g + i];
+    buv[i] = bias[kQkvCols + kMlp + item * 16 + 4 * g + i];
+  }
+  PHASE_TS(s, l, kPhGu, 1);
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  PHASE_TS(s, l, kPhGu, 2);
+  const brsrc rg = make_rsrc(a.gmid + slw * R * kWidth, (size_t)R * kWidth * 2);
+  const brsrc rs = make_rsrc(a.ssmid + slw * kTiles * R, (size_t)kTiles * R * 4);
+  u16* act = a.act + slw * (size_t)R * kMlp;
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);
+  bf16x8 A[4][4][kGuCk];  // [ring slot = chunk mod 4][m-tile][k-step]
+  gu_load_chunk(A[0], rg, wave, wave < a.batch, 0, lane);
+  gu_load_chunk(A[1], rg, wave, wave < a.batch, 1, lane);
+  sched_fence();
+  for (int b = wave; b < a.batch; b += 4) {
+    const int bn = b + 4;
+    const bool ok_n = bn < a.batch;
+    f32x4 accg[4], accu[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) accg[mt] = accu[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float st[4][16];
+    float ssq[4];
+#pragma unroll
+    for (int c = 0; c < kGuChunks; ++c) {
+      // two chunks ahead: this sample's, then the next sample's first two
+      if (c + 2 < kGuChunks) gu_load_chunk(A[(c + 2) % 4], rg, b, true, c + 2, lane);
+      else gu_load_chunk(A[(c + 2) % 4], rg, bn, ok_n, c + 2 - kGuChunks, lane);
+      if (c < 4) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) buf_f32(st[c][t], rs, (((16 * c + t) * R) + b * kRowsPerSample + lane) * 4);
+      }
+      sched_fence();
+      gu_mfma_chunk(accg, accu, A[c % 4], lw, c, lane);
+      if (c >= 1 && c <= 4) {
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) v += st[c - 1][t];
+        ssq[c - 1] = v;
+      }
+    }
+    // lane r's row r: rstd of adaRMSNorm (the same grouping as the one-sample phases)
+    const float rstd_lane = 1.0f / sqrtf(fadd((((ssq[0] + ssq[1]) + ssq[2]) + ssq[3]) * (1.0f / kWidth), a.eps));
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int row = mt * 16 + r16;
+      const float rstd = __shfl(rstd_lane, row);
+      if (row < kHorizon) {
+        u16 o4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // GeGLU (rlinf_fused_denoise.py:166-173)
+          const float gt = round_bf(__builtin_fmaf(rstd, accg[mt][i], bgv[i]));
+          const float up = __builtin_fmaf(rstd, accu[mt][i], buv[i]);
+          o4[i] = f2bf(fmul(gelu_tanh(gt), up));
+        }
+        st_wt8(act, (uint32_t)(afrag_index(b * kRowsPerSample + row, item * 16 + 4 * g, kMlp / 32) * 2),
+               (uint32_t)o4[0] | ((uint32_t)o4[1] << 16), (uint32_t)o4[2] | ((uint32_t)o4[3] << 16));
+      }
+    }
+  }
+  PHASE_TS(s, l, kPhGu, 5);
+  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch, true);  // every wave stored rows
+  PHASE_TS(s, l, kPhGu, 6);
+  return true;
+}
+
+// =============================================================================================
 // attention, two stages.
 // Splits: item = (row block bp of 2 tokens x 8 heads of one sample, key split c); compute wave w
 // attends 32-key blocks kb_lo + w, kb_lo + w + 3, ... (online softmax).  Each wave's first block,
@@ -1652,7 +1783,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   bool waited = false, burst = false;
   if (attn_grouped<G>(a)) {
     // gate_up(l) tile 0, fragments 0..15 -> region A's lower half, ahead of the polls
-    copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
+    copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
     burst = true;
     PHASE_TS(s, l, kPhSplit, 1);
     if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
@@ -1688,7 +1819,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     KvBlock blk;
     if (pre) load(blk, kb0);
     if (!burst) {
-      copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
+      copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
       burst = true;
     }
     PHASE_TS(s, l, kPhSplit, 1);
@@ -1798,9 +1929,9 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   }
   // the rest of gate_up(l) -> region A, whose upper half the split items no longer use (the
   // workgroups without a split item: all of it), ahead of the merge polls
-  if (!burst) copy_norm_w<kModeGateUp, 0, 16>(a, l, 0, smem);
-  copy_norm_w<kModeGateUp, 16, 16>(a, l, 0, smem);
-  copy_norm_w<kModeGateUp, 0, 32>(a, l, 1, smem);
+  if (!burst) copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
+  copy_norm_w<kModeGateUp, 16, 16, G>(a, l, 0, smem);
+  copy_norm_w<kModeGateUp, 0, 32, G>(a, l, 1, smem);
   if (attn_grouped<G>(a)) return attn_group_merges(a, s, l, s_flag);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
@@ -2341,7 +2472,10 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   if (wave == 1 || wave == 2) load_w1();
   PHASE_TS(s, l, PH, 1);
   // the gate_up items of this quarter's activation columns for this half's samples
-  if (!wait_flags(a, flag_base(a, s, l, kPhGu) + half * (kGuItems / 2) + ksp * 32, 32, s_flag)) return false;
+  // (phase_gateup_msplit: item w computes pair w for every sample)
+  if (!(gu_msplit<G>(a) ? wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)
+          : wait_flags(a, flag_base(a, s, l, kPhGu) + half * (kGuItems / 2) + ksp * 32, 32, s_flag)))
+    return false;
   PHASE_TS(s, l, PH, 2);
   if (wave == 0) load_w1();
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // the first tile's K-quarter fragments
@@ -2466,11 +2600,13 @@ static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "
 // batched phases' code (pair items, grouped attention) is compiled into it -- carrying that code
 // costs the single-sample schedule 3.5 % through register allocation -- and MULTI = true for
 // batches of two and more.
-// Two instances of the kernel: G = false for one sample, G = true for batches (always the pair
-// items), which alone contains the grouped attention.  Each is compiled in a translation unit of
-// its own: inlined into one module, the batched code changed the one-sample kernel's register
-// allocation (measured +2-3.5 % per C1 predict).
-template <bool G>
+// Three instances of the kernel: G = false for one sample, G = true for batches (always the pair
+// items); I = the instance number (0, 1, 2), instance 2 (batches of kRowSplitMinBatch and more)
+// alone containing the row-split gate_up and the grouped attention.  Each is compiled in a
+// translation unit of its own: inlined into one module, the batched code changed the one-sample
+// kernel's register allocation (measured +2-3.5 % per C1 predict), and the batch paths each
+// other's (+1-1.5 %).
+template <bool G, int I>
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
   __shared__ __align__(16) float smem[G ? kLdsFloatsBatched : kLdsFloats];
   __shared__ int s_flag;
@@ -2485,7 +2621,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
       ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
            phase_attn<G>(a, s, l, smem, &s_flag) &&
            (G ? phase_oproj_pairs(a, s, l, smem, &s_flag) : phase_oproj(a, s, l, smem, &s_flag)) &&
-           (G ? phase_gateup_pairs4(a, s, l, smem, &s_flag)
+           (G ? (gu_msplit<G>(a) ? phase_gateup_msplit(a, s, l, smem, &s_flag) : phase_gateup_pairs4(a, s, l, smem, &s_flag))
               : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
                                                      : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
            ((G || a.batch > 1) && PI05_DOWN_PAIRS ? phase_down_pairs<G>(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
@@ -2496,12 +2632,17 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
 }
 
 #if PI05_PERSISTENT_INSTANCE == 1
-const void* denoise_loop_kernel_batched() { return reinterpret_cast<const void*>(denoise_loop_kernel<true>); }
+const void* denoise_loop_kernel_batched() { return reinterpret_cast<const void*>(denoise_loop_kernel<true, 1>); }
+#elif PI05_PERSISTENT_INSTANCE == 2
+const void* denoise_loop_kernel_grouped() { return reinterpret_cast<const void*>(denoise_loop_kernel<true, 2>); }
 #else
 const void* denoise_loop_kernel_batched();  // instance 1
+const void* denoise_loop_kernel_grouped();  // instance 2
 
 const void* denoise_loop_kernel_ptr(int batch) {
-  return batch > 1 ? denoise_loop_kernel_batched() : reinterpret_cast<const void*>(denoise_loop_kernel<false>);
+  return batch >= kRowSplitMinBatch ? denoise_loop_kernel_grouped()
+         : batch > 1                 ? denoise_loop_kernel_batched()
+                                     : reinterpret_cast<const void*>(denoise_loop_kernel<false, 0>);
 }
 
 hipError_t launch_denoise_loop(const MegaArgs& a, int grid, hipStream_t st) {
@@ -2576,21 +2717,33 @@ int pi05_phase_ts_copy_batched(unsigned long long* host) {
 int pi05_phase_ts_clear_batched(const unsigned long long* zeros) {
   return (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(pi05::pi05_phase_ts), 0, hipMemcpyHostToDevice);
 }
+#elif PI05_PERSISTENT_INSTANCE == 2
+int pi05_phase_ts_copy_grouped(unsigned long long* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(pi05::pi05_phase_ts), sizeof(pi05::pi05_phase_ts), 0, hipMemcpyDeviceToHost);
+}
+int pi05_phase_ts_clear_grouped(const unsigned long long* zeros) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(pi05::pi05_phase_ts), 0, hipMemcpyHostToDevice);
+}
 #else
 int pi05_phase_ts_copy_batched(unsigned long long* host);
 int pi05_phase_ts_clear_batched(const unsigned long long* zeros);
+int pi05_phase_ts_copy_grouped(unsigned long long* host);
+int pi05_phase_ts_clear_grouped(const unsigned long long* zeros);
 extern "C" int pi05_debug_phase_timestamps(unsigned long long* host) {
   constexpr size_t n = sizeof(pi05::pi05_phase_ts) / sizeof(unsigned long long);
   static unsigned long long other[n];
   int rc = (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(pi05::pi05_phase_ts), sizeof(pi05::pi05_phase_ts), 0, hipMemcpyDeviceToHost);
-  if (rc == 0) rc = pi05_phase_ts_copy_batched(other);
-  for (size_t i = 0; rc == 0 && i < n; ++i) host[i] += other[i];
+  for (int inst = 1; inst <= 2 && rc == 0; ++inst) {
+    rc = inst == 1 ? pi05_phase_ts_copy_batched(other) : pi05_phase_ts_copy_grouped(other);
+    for (size_t i = 0; rc == 0 && i < n; ++i) host[i] += other[i];
+  }
   return rc;
 }
 extern "C" int pi05_debug_phase_timestamps_clear(void) {
   static unsigned long long zeros[sizeof(pi05::pi05_phase_ts) / sizeof(unsigned long long)];
   int rc = (int)hipMemcpyToSymbol(HIP_SYMBOL(pi05::pi05_phase_ts), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
-  return rc == 0 ? pi05_phase_ts_clear_batched(zeros) : rc;
+  if (rc == 0) rc = pi05_phase_ts_clear_batched(zeros);
+  return rc == 0 ? pi05_phase_ts_clear_grouped(zeros) : rc;
 }
 #endif
 #endif

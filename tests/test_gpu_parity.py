@@ -119,10 +119,20 @@ def test_c3_batch8(full_weights):
     model.close()
 
 
+def test_batch2_pair_items(full_weights):
+    """B=2: the two-sample kernel instance -- one 32-key block per wave in the attention splits and
+    the qkv / gate_up / down_proj pair items over sample halves of 1 (gate_up's K split over the four
+    waves)."""
+    print("case B=2: depth 3, B=2, P=200, 2 steps", flush=True)
+    model, _, _, _, ref, got = _run_case(full_weights, depth=3, P=200, B=2, steps=2)
+    _check("B=2", ref, got, 2)
+    model.close()
+
+
 def test_batch5_batch_paths(full_weights):
     """B=5: the batched kernel at an odd batch -- grouped attention items (4 row blocks of a sample
-    sharing each K/V block; 7 key splits) and the qkv / gate_up / down_proj pair items over sample
-    halves of 3 and 2."""
+    sharing each K/V block; 7 key splits), gate_up split by rows (waves 0..3 take samples 0..3, wave
+    0 also sample 4) and the qkv / down_proj pair items over sample halves of 3 and 2."""
     print("case B=5: depth 4, B=5, P=968, 3 steps", flush=True)
     model, _, _, _, ref, got = _run_case(full_weights, depth=4, B=5, steps=3)
     _check("B=5", ref, got, 3)
@@ -130,6 +140,8 @@ def test_batch5_batch_paths(full_weights):
 
 
 def test_ragged_prefix_padding(full_weights):
+    """B=3: the attention split items (not grouped) with the row-split gate_up (three waves one
+    sample each, the fourth idle)."""
     print("case ragged: depth 4, B=3, P=300, padded tails", flush=True)
 
     def pad_fn(pad):
