@@ -397,6 +397,15 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 // samples (w / 128): each activation row it reads then serves four tiles instead of two, so an
 // XCD's workgroups read half as many activation bytes (the phase is bound by that L2 traffic).
 // Region A holds pair 2g; the compute waves hold pair 2g + 1 in registers.
+#ifndef PI05_QKV_MSPLIT
+#define PI05_QKV_MSPLIT 1
+#endif
+// The qkv of kernel instance 2 (phase_qkv_msplit): item i = tile pair i mod 80 for sample half
+// i / 80.
+template <bool G>
+__device__ __forceinline__ constexpr bool qkv_msplit() {
+  return G && PI05_INSTANCE_GROUPED && PI05_QKV_MSPLIT;
+}
 // The gate_up of kernel instance 2 (phase_gateup_msplit, batches of kRowSplitMinBatch and more):
 // item w = pair w.
 template <bool G>
@@ -412,7 +421,7 @@ __device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
 // do; region A holds the first pair.
 template <bool G>
 __device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
-  return G && a.batch > 1 ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item() % kQkvPairs;
+  return G && a.batch > 1 && !qkv_msplit<G>() ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item() % kQkvPairs;
 }
 template <int MODE, bool G = false>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
@@ -1263,6 +1272,194 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
   return true;
 }
 
+// Row-split GEMM phases (kernel instance 2): A chunks of kGuCk k-steps x 4 m-tiles.
+constexpr int kGuCk = 4;                     // k-steps per A chunk
+constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
+#ifndef PI05_GU_AHEAD
+#define PI05_GU_AHEAD 2
+#endif
+constexpr int kGuAhead = PI05_GU_AHEAD;  // chunks in flight ahead of the MFMAs (ring of 4)
+static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
+// chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
+__device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane) {
+  const int r16 = lane & 15;
+#pragma unroll
+  for (int s2 = 0; s2 < kGuCk; ++s2)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const bool ok = ok_b && r16 < kHorizon - mt * 16;
+      buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, c * kGuCk + s2, kWidth / 32) + lane * 8) * 2) : kOob);
+    }
+}
+// the products of chunk c with the two weight tiles in region A (lw: tile 0, then tile 1, 32
+// fragments each); LAST1: tile 1's last k-step comes from the register w1_last instead
+template <bool LAST1 = false>
+__device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4], const bf16x8 (&A)[4][kGuCk], const u16* lw, int c,
+                                              int lane, bf16x8 w1_last = {}) {
+  constexpr int KSTEPS = kWidth / 32;
+#pragma unroll
+  for (int s2 = 0; s2 < kGuCk; ++s2) {
+    const int ks = c * kGuCk + s2;
+    const bf16x8 wg = *reinterpret_cast<const bf16x8*>(lw + (size_t)ks * 512 + lane * 8);
+    const bf16x8 wu = LAST1 && s2 == kGuCk - 1 && c == kGuChunks - 1
+                          ? w1_last
+                          : *reinterpret_cast<const bf16x8*>(lw + ((size_t)KSTEPS + ks) * 512 + lane * 8);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      accg[mt] = mfma16x16x32(wg, A[mt][s2], accg[mt]);
+      accu[mt] = mfma16x16x32(wu, A[mt][s2], accu[mt]);
+    }
+  }
+}
+
+// =============================================================================================
+// qkv of kernel instance 2, split by rows as phase_gateup_msplit: item i = tile pair i mod 80 (a
+// RoPE pair of q or k tiles, or two consecutive v tiles) for sample half i / 80; region A holds
+// the pair's two tiles except the second one's last k-step (the 63-copy burst leaves it out),
+// which every wave loads into a register.  Wave j takes sample j of the half (j + 4, ... past 8
+// samples): all four m-tiles over the whole K, A streamed two chunks ahead.  As W.A^T, a lane
+// ends with columns 4g .. 4g+3 of both tiles for one row, so the RoPE rotation (which pairs
+// column d of the first tile with column d of the second) and the 8-byte q / k stores are
+// lane-local; v rows go through a per-wave LDS tile into the permuted V fragment layout.
+// =============================================================================================
+__device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kWidth / 32;
+  const int L = a.depth, R = a.R;
+  const int item = qkv_item();
+  PHASE_TS(s, l, kPhQkv, 0);
+  // copy wave: this phase's weights (region A) and everything issued before them have landed;
+  // down(l) -> B here unless grouped attention stages K/V there (then before o_proj)
+  if (copy_wave()) {
+    wait_vmcnt<0>();
+    if (!attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
+  }
+  if (item < 0 || item >= kQkvItems) return true;
+  const int p = item % kQkvPairs, sh = item / kQkvPairs;
+  const bool rotated = p < 72;
+  const int bh = (a.batch + 1) / 2, b0 = sh * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const size_t slw = (size_t)s * L + l;
+  const int t0 = rotated ? (p >> 3) * 16 + (p & 7) : 144 + 2 * (p - 72);
+  const int t1 = rotated ? t0 + 8 : t0 + 1;
+  const u16* wq = a.wpack + (size_t)l * kLayerElems + kOffQkv;
+  const bf16x8 w1_last = load_frag(wq + ((size_t)t1 * KSTEPS + KSTEPS - 1) * 512 + lane * 8);
+  // shift . W^T of this lane's columns 4g .. 4g+3 of both tiles
+  const float* bias = a.bias + slw * kBiasCols;
+  float bv0[4], bv1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bv0[i] = bias[t0 * 16 + 4 * g + i];
+    bv1[i] = bias[t1 * 16 + 4 * g + i];
+  }
+  PHASE_TS(s, l, kPhQkv, 1);
+  {
+    const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
+    const int ndep = l == 0 ? a.batch * kHorizon : kKSplit * kTiles;  // down_proj_pairs: one flag per (group, quarter)
+    if (!wait_flags(a, dep, ndep, s_flag)) return false;
+  }
+  PHASE_TS(s, l, kPhQkv, 2);
+  const brsrc rg = make_rsrc(a.g + slw * R * kWidth, (size_t)R * kWidth * 2);
+  const brsrc rs = make_rsrc(a.ss + ((size_t)s * (L + 1) + l) * kTiles * R, (size_t)kTiles * R * 4);
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);
+  u16* s_v = reinterpret_cast<u16*>(smem + kLdsWork) + wave * 64 * 32;  // v items: [64 keys][32 dims]
+  bf16x8 A[4][4][kGuCk];  // [ring slot = chunk mod 4][m-tile][k-step]
+  const int bf = b0 + wave;
+#pragma unroll
+  for (int c = 0; c < kGuAhead; ++c) gu_load_chunk(A[c], rg, bf, bf < b1, c, lane);
+  sched_fence();
+  for (int b = bf; b < b1; b += 4) {
+    const int bn = b + 4;
+    const bool ok_n = bn < b1;
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc0[mt] = acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float st[4][16];
+    float ssq[4];
+#pragma unroll
+    for (int c = 0; c < kGuChunks; ++c) {
+      if (c + kGuAhead < kGuChunks) gu_load_chunk(A[(c + kGuAhead) % 4], rg, b, true, c + kGuAhead, lane);
+      else gu_load_chunk(A[(c + kGuAhead) % 4], rg, bn, ok_n, c + kGuAhead - kGuChunks, lane);
+      if (c < 4) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) buf_f32(st[c][t], rs, (((16 * c + t) * R) + b * kRowsPerSample + lane) * 4);
+      }
+      sched_fence();
+      gu_mfma_chunk<true>(acc0, acc1, A[c % 4], lw, c, lane, w1_last);
+      if (c >= 1 && c <= 4) {
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) v += st[c - 1][t];
+        ssq[c - 1] = v;
+      }
+    }
+    const float rstd_lane = 1.0f / sqrtf(fadd((((ssq[0] + ssq[1]) + ssq[2]) + ssq[3]) * (1.0f / kWidth), a.eps));
+    if (rotated) {
+      // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
+      const int head = p >> 3, dt = p & 7, d = dt * 16 + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = mt * 16 + r16;
+        const float rstd = __shfl(rstd_lane, row);
+        if (row < kHorizon) {
+          const size_t cr = (size_t)(b * kHorizon + row) * kHeadDim + d;
+          const u16x4 cs_lo = *reinterpret_cast<const u16x4*>(a.cos_tab + cr), sn_lo = *reinterpret_cast<const u16x4*>(a.sin_tab + cr);
+          const u16x4 cs_hi = *reinterpret_cast<const u16x4*>(a.cos_tab + cr + kHalfDim), sn_hi = *reinterpret_cast<const u16x4*>(a.sin_tab + cr + kHalfDim);
+          u16 olo[4], ohi[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x_lo = round_bf(__builtin_fmaf(rstd, acc0[mt][i], bv0[i]));
+            const float x_hi = round_bf(__builtin_fmaf(rstd, acc1[mt][i], bv1[i]));
+            olo[i] = f2bf(fsub(fmul(x_lo, bf2f(cs_lo[i])), fmul(x_hi, bf2f(sn_lo[i]))));
+            ohi[i] = f2bf(fadd(fmul(x_hi, bf2f(cs_hi[i])), fmul(x_lo, bf2f(sn_hi[i]))));
+          }
+          const uint32_t lo0 = (uint32_t)olo[0] | ((uint32_t)olo[1] << 16), lo1 = (uint32_t)olo[2] | ((uint32_t)olo[3] << 16);
+          const uint32_t hi0 = (uint32_t)ohi[0] | ((uint32_t)ohi[1] << 16), hi1 = (uint32_t)ohi[2] | ((uint32_t)ohi[3] << 16);
+          if (head < kHeads) {
+            u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
+            const int qrow = (b * kRowsPerSample + row) * kQRowsPerTok + head;
+            st_wt8(qs, (uint32_t)(afrag_index(qrow, d, kHeadDim / 32) * 2), lo0, lo1);
+            st_wt8(qs, (uint32_t)(afrag_index(qrow, d + kHalfDim, kHeadDim / 32) * 2), hi0, hi1);
+          } else {
+            u16* kc = a.ksuf + (slw * a.batch + b) * 64 * kHeadDim;
+            st_wt8(kc, (uint32_t)(kfrag_index(row, d) * 2), lo0, lo1);
+            st_wt8(kc, (uint32_t)(kfrag_index(row, d + kHalfDim) * 2), hi0, hi1);
+          }
+        }
+      }
+    } else {
+      // v: the wave's rows into its LDS tile (keys past the horizon as zeros), then chunk ci of
+      // the 256 (block kb, key group gg, dim dcol) -> 8 keys of one dim of the permuted fragment
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = mt * 16 + r16;
+        const float rstd = __shfl(rstd_lane, row);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s_v[row * 32 + 4 * g + i] = row < kHorizon ? f2bf(__builtin_fmaf(rstd, acc0[mt][i], bv0[i])) : (u16)0;
+          s_v[row * 32 + 16 + 4 * g + i] = row < kHorizon ? f2bf(__builtin_fmaf(rstd, acc1[mt][i], bv1[i])) : (u16)0;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS writes are done
+      u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int ci = lane + 64 * k, dcol = ci & 31, kb = ci >> 7, gg = (ci >> 5) & 3;
+        u16 v8[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v8[q] = s_v[vkey(kb, gg, q) * 32 + dcol];
+        const int dv = (t0 - 144) * 16 + dcol;
+        st_bf16x8(vc, ((size_t)kb * 16 + (dv >> 4)) * 512 + (size_t)(gg * 16 + (dv & 15)) * 8, v8);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile's reads are done before the next sample's writes
+    }
+  }
+  PHASE_TS(s, l, kPhQkv, 5);
+  publish(a, flag_base(a, s, l, kPhQkv) + item, a.epoch, true);  // every wave stored rows
+  PHASE_TS(s, l, kPhQkv, 6);
+  return true;
+}
+
 // =============================================================================================
 // gate_up in the batched kernel instance: phase_gateup_pairs' items, with the copy wave as a fourth
 // compute wave (its down_proj copy is issued before o_proj instead): K splits 8 k-steps per wave, so
@@ -1392,34 +1589,6 @@ static_assert(64 + 64 + 256 + 4 * 4 * 2 * 256 + 64 * 33 <= kWorkFloatsBatched, "
 // GeGLU and 8-byte stores need nothing from other lanes.  Lane r (= row r of the sample) sums its
 // row's 64 tile sums of squares in four groups of 16, loaded during the first four chunks.
 // =============================================================================================
-constexpr int kGuCk = 4;                     // k-steps per A chunk
-constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
-// chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
-__device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane) {
-  const int r16 = lane & 15;
-#pragma unroll
-  for (int s2 = 0; s2 < kGuCk; ++s2)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const bool ok = ok_b && r16 < kHorizon - mt * 16;
-      buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, c * kGuCk + s2, kWidth / 32) + lane * 8) * 2) : kOob);
-    }
-}
-__device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4], const bf16x8 (&A)[4][kGuCk], const u16* lw, int c,
-                                              int lane) {
-  constexpr int KSTEPS = kWidth / 32;
-#pragma unroll
-  for (int s2 = 0; s2 < kGuCk; ++s2) {
-    const int ks = c * kGuCk + s2;
-    const bf16x8 wg = *reinterpret_cast<const bf16x8*>(lw + (size_t)ks * 512 + lane * 8);
-    const bf16x8 wu = *reinterpret_cast<const bf16x8*>(lw + ((size_t)KSTEPS + ks) * 512 + lane * 8);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      accg[mt] = mfma16x16x32(wg, A[mt][s2], accg[mt]);
-      accu[mt] = mfma16x16x32(wu, A[mt][s2], accu[mt]);
-    }
-  }
-}
 __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   const int L = a.depth, R = a.R;
   const int item = (int)blockIdx.x;
@@ -1446,8 +1615,8 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
   u16* act = a.act + slw * (size_t)R * kMlp;
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);
   bf16x8 A[4][4][kGuCk];  // [ring slot = chunk mod 4][m-tile][k-step]
-  gu_load_chunk(A[0], rg, wave, wave < a.batch, 0, lane);
-  gu_load_chunk(A[1], rg, wave, wave < a.batch, 1, lane);
+#pragma unroll
+  for (int c = 0; c < kGuAhead; ++c) gu_load_chunk(A[c], rg, wave, wave < a.batch, c, lane);
   sched_fence();
   for (int b = wave; b < a.batch; b += 4) {
     const int bn = b + 4;
@@ -1459,9 +1628,9 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
     float ssq[4];
 #pragma unroll
     for (int c = 0; c < kGuChunks; ++c) {
-      // two chunks ahead: this sample's, then the next sample's first two
-      if (c + 2 < kGuChunks) gu_load_chunk(A[(c + 2) % 4], rg, b, true, c + 2, lane);
-      else gu_load_chunk(A[(c + 2) % 4], rg, bn, ok_n, c + 2 - kGuChunks, lane);
+      // kGuAhead chunks ahead: this sample's, then the next sample's first ones
+      if (c + kGuAhead < kGuChunks) gu_load_chunk(A[(c + kGuAhead) % 4], rg, b, true, c + kGuAhead, lane);
+      else gu_load_chunk(A[(c + kGuAhead) % 4], rg, bn, ok_n, c + kGuAhead - kGuChunks, lane);
       if (c < 4) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) buf_f32(st[c][t], rs, (((16 * c + t) * R) + b * kRowsPerSample + lane) * 4);
@@ -2618,7 +2787,9 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
     ok = phase_io<G>(a, s, smem, &s_flag);
     if (!ok || s == a.steps) break;
     for (int l = 0; l < a.depth && ok; ++l) {
-      ok = (G ? phase_qkv_pairs(a, s, l, smem, &s_flag) : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
+      ok = (qkv_msplit<G>() ? phase_qkv_msplit(a, s, l, smem, &s_flag)
+            : G             ? phase_qkv_pairs(a, s, l, smem, &s_flag)
+                            : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
            phase_attn<G>(a, s, l, smem, &s_flag) &&
            (G ? phase_oproj_pairs(a, s, l, smem, &s_flag) : phase_oproj(a, s, l, smem, &s_flag)) &&
            (G ? (gu_msplit<G>(a) ? phase_gateup_msplit(a, s, l, smem, &s_flag) : phase_gateup_pairs4(a, s, l, smem, &s_flag))
