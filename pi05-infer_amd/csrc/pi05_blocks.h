@@ -55,6 +55,28 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return fmul(t3, fadd(t11, 1.0f));
 }
 
+// max / sum of x and its value in lane l ^ 16 (rows of 16 lanes swapped pairwise) or l ^ 32
+// (wave halves swapped), on the gfx950 permlane swaps: VALU only, where a __shfl_xor is an LDS
+// crossbar operation whose lgkmcnt wait would also wait for every LDS read in flight.  The swap
+// of two copies of x leaves x in one result and the partner's value in the other (which one
+// depends on the lane), so max and sum are order-free and equal to the shuffle's.
+__device__ __forceinline__ float lane_max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lane_max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lane_sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float lane_sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // One 32-key block of K/V fragments (prefetched as a unit) and its key-valid bytes.
 struct KvBlock {
   bf16x8 k[16];
@@ -100,8 +122,7 @@ __device__ __forceinline__ void attend_block_q(const KvBlock& blk, QF qfrag, flo
   float bm = s[0];
 #pragma unroll
   for (int i = 1; i < 8; ++i) bm = fmaxf(bm, s[i]);
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  bm = lane_max_xor32(lane_max_xor16(bm));
   const float m_new = fmaxf(m_run, bm);
   float alpha = 1.f;
   float e[8];
