@@ -400,6 +400,9 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 #ifndef PI05_QKV_MSPLIT
 #define PI05_QKV_MSPLIT 1
 #endif
+#ifndef PI05_DOWN_MSPLIT
+#define PI05_DOWN_MSPLIT 1
+#endif
 // The qkv of kernel instance 2 (phase_qkv_msplit): item i = tile pair i mod 80 for sample half
 // i / 80.
 template <bool G>
@@ -472,6 +475,17 @@ __device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
   down_item(a, &nt, &ksp);
   const u16* tile = a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)nt * KSTEPS * 512 + (size_t)ksp * KQ * 512;
   lds_burst<KQ>(smem + kLdsB, tile);
+}
+
+// Kernel instance 2: down_proj's second tile (nt0 + 1) of the item's K quarter -> the working
+// area's first kDownW1Floats floats (phase_down_msplit reads it after tile nt0's quarter in B).
+constexpr int kDownW1Floats = 8192;
+__device__ void copy_down_w1(const MegaArgs& a, int l, float* smem) {
+  constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
+  if (!copy_wave() || (int)blockIdx.x >= kTiles * kKSplit) return;
+  int nt, ksp;
+  down_item(a, &nt, &ksp);
+  lds_burst<KQ>(smem + kLdsWork, a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)(nt + 1) * KSTEPS * 512 + (size_t)ksp * KQ * 512);
 }
 
 // The layer after (s, l): (s, l + 1), or (s + 1, 0) after the last layer; false past the loop.
@@ -1281,14 +1295,16 @@ constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
 constexpr int kGuAhead = PI05_GU_AHEAD;  // chunks in flight ahead of the MFMAs (ring of 4)
 static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
 // chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
-__device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane) {
+// (NKS: k-steps of the activation rows; KS0: the first k-step of chunk 0)
+template <int NKS = kWidth / 32>
+__device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane, int ks0 = 0) {
   const int r16 = lane & 15;
 #pragma unroll
   for (int s2 = 0; s2 < kGuCk; ++s2)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const bool ok = ok_b && r16 < kHorizon - mt * 16;
-      buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, c * kGuCk + s2, kWidth / 32) + lane * 8) * 2) : kOob);
+      buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, ks0 + c * kGuCk + s2, NKS) + lane * 8) * 2) : kOob);
     }
 }
 // the products of chunk c with the two weight tiles in region A (lw: tile 0, then tile 1, 32
@@ -1593,8 +1609,10 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
   const int L = a.depth, R = a.R;
   const int item = (int)blockIdx.x;
   PHASE_TS(s, l, kPhGu, 0);
-  // copy wave: the pair's weights (region A) and everything issued before them have landed
+  // copy wave: the pair's weights (region A) and everything issued before them have landed; then
+  // down_proj's second tile into the working area (free from here to down_proj)
   if (copy_wave()) wait_vmcnt<0>();
+  if (PI05_DOWN_MSPLIT) copy_down_w1(a, l, smem);
   if (item >= kGuItems) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
@@ -2590,6 +2608,69 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
   return true;
 }
 
+// The finishing of phase_down_msplit (the same steps as phase_down_pairs' own): quarter ksp of the
+// group finishes samples b0 + ksp, b0 + ksp + 4, ... of the half: it adds the four quarters'
+// partials in order and applies the gated residual to both tiles (h, g of the next layer's first
+// norm, the tiles' row sums of squares).  s_ss: 256 floats of LDS.
+__device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int l, float* s_ss, int nt0, int ksp, int b0, int b1, bool next_g,
+                                                  int NN) {
+  const int L = a.depth, R = a.R;
+  const int tid = phase_tid();
+  const size_t slw = (size_t)s * L + l;
+  const float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;
+  {
+    const int ft = tid >> 7, frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;
+    const int col = (nt0 + ft) * 16;
+    const u16* hres = a.hmid + slw * (size_t)R * kWidth;
+    u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
+    u16* gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
+    float* rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
+    const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
+    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
+    float gate[8], s1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      gate[i] = round_bf(gmod[i]);
+      if (next_g) s1[i] = smod[i];
+    }
+    for (int b = b0 + ksp; b < b1; b += kKSplit) {
+      const int r = b * kRowsPerSample + frow;
+      float ss = 0.f;
+      if (frow < kHorizon) {
+        float pv[kKSplit][8];
+#pragma unroll
+        for (int q = 0; q < kKSplit; ++q) {
+          const float* pp = dpart + (((size_t)q * kTiles + nt0 + ft) * R + r) * 16 + fc0;
+          const float4 v0 = *reinterpret_cast<const float4*>(pp), v1 = *reinterpret_cast<const float4*>(pp + 4);
+          pv[q][0] = v0.x, pv[q][1] = v0.y, pv[q][2] = v0.z, pv[q][3] = v0.w;
+          pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
+        }
+        const u16x8 hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
+        u16 hn[8], gn[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float y = ((pv[0][i] + pv[1][i]) + pv[2][i]) + pv[3][i];
+          const float prod = round_bf(fmul(round_bf(y), gate[i]));
+          hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
+          const float hf = bf2f(hn[i]);
+          gn[i] = f2bf(fmul(hf, s1[i]));
+          ss += hf * hf;
+        }
+        st_bf16x8(hout, afrag_index(r, col + fc0, kWidth / 32), hn);
+        if (next_g) st_bf16x8(gout, afrag_index(r, col + fc0, kWidth / 32), gn);
+      }
+      s_ss[(ft * 2 + (fc0 >> 3)) * 64 + frow] = ss;
+      __syncthreads();
+      // tile-major statistics: each tile's sums of the sample's 64 rows (one 256-byte run per tile)
+      if (tid < 128) {
+        const int t = tid >> 6, rw = tid & 63;
+        st_f32(rout + (size_t)(nt0 + t) * R + b * kRowsPerSample + rw, s_ss[(t * 2) * 64 + rw] + s_ss[(t * 2 + 1) * 64 + rw]);
+      }
+      __syncthreads();  // s_ss is reused by the next sample
+    }
+  }
+}
+
 // =============================================================================================
 // down_proj at B > 1: two tiles (nt0 = 2g from region B, nt1 = 2g + 1 from registers) and one K
 // quarter for the samples [b0, b1) of half h (workgroup 64 q + 32 h + g, see down_item).  Every
@@ -2755,6 +2836,90 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
 }
 
 // =============================================================================================
+// down_proj of kernel instance 2, split by rows: the items of phase_down_pairs (tiles nt0, nt0 + 1,
+// K quarter q, sample half h); the first tile's quarter in region B, the second's in the working
+// area (copied there at gate_up), so wave j takes sample j of the half over the quarter's whole K
+// with both tiles, as phase_gateup_msplit, and stores its partials straight from the accumulators
+// (a lane: columns 4g .. 4g+3 of one row).  The finishers are phase_down_pairs'.
+// =============================================================================================
+__device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
+  constexpr int PH = kPhDown, NG = kTiles / 2;
+  static_assert(KQ == kGuChunks * kGuCk, "a K quarter is one row-split pass");
+  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  const int item = (int)blockIdx.x;
+  PHASE_TS(s, l, PH, 0);
+  // copy wave: this layer's down_proj weights (region B, the working area) have landed (read after
+  // the polls' barrier); then, ahead of the polls, the next layer's qkv tiles
+  if (copy_wave()) wait_vmcnt<0>();
+  {
+    int ln;
+    if (next_layer(a, s, l, &ln)) {
+      copy_norm_w<kModeQkv, 0, 32, true>(a, ln, 0, smem);
+      copy_norm_w<kModeQkv, 0, 31, true>(a, ln, 1, smem);
+    }
+  }
+  if (item >= kTiles * kKSplit) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  int nt0, ksp, half;
+  down_item(a, &nt0, &ksp, &half);
+  const int grp = nt0 / 2;
+  const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  const size_t slw = (size_t)s * L + l;
+  const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
+  PHASE_TS(s, l, PH, 1);
+  if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)) return false;  // gate_up items 64 q ..
+  PHASE_TS(s, l, PH, 2);
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // tile nt0's quarter, then nt0 + 1's
+  const brsrc rg = make_rsrc(a.act + slw * (size_t)R * kMlp, (size_t)R * kMlp * 2);
+  float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;  // [quarter][tile][row][16]
+  bf16x8 A[4][4][kGuCk];
+  const int bf = b0 + wave;
+#pragma unroll
+  for (int c = 0; c < kGuAhead; ++c) gu_load_chunk<KSTEPS>(A[c], rg, bf, bf < b1, c, lane, ksp * KQ);
+  sched_fence();
+  for (int b = bf; b < b1; b += 4) {
+    const int bn = b + 4;
+    const bool ok_n = bn < b1;
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc0[mt] = acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kGuChunks; ++c) {
+      if (c + kGuAhead < kGuChunks) gu_load_chunk<KSTEPS>(A[(c + kGuAhead) % 4], rg, b, true, c + kGuAhead, lane, ksp * KQ);
+      else gu_load_chunk<KSTEPS>(A[(c + kGuAhead) % 4], rg, bn, ok_n, c + kGuAhead - kGuChunks, lane, ksp * KQ);
+      sched_fence();
+      gu_mfma_chunk(acc0, acc1, A[c % 4], lw, c, lane);
+    }
+    // partials of both tiles (into this XCD's L2, where the group's finishers read them)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int row = mt * 16 + r16;
+      if (row < kHorizon) {
+        const size_t r = (size_t)b * kRowsPerSample + row;
+        st_l2_16(dpart, (uint32_t)(((((size_t)ksp * kTiles + nt0) * R + r) * 16 + 4 * g) * 4),
+                 u32x4{__float_as_uint(acc0[mt][0]), __float_as_uint(acc0[mt][1]), __float_as_uint(acc0[mt][2]), __float_as_uint(acc0[mt][3])});
+        st_l2_16(dpart, (uint32_t)(((((size_t)ksp * kTiles + nt0 + 1) * R + r) * 16 + 4 * g) * 4),
+                 u32x4{__float_as_uint(acc1[mt][0]), __float_as_uint(acc1[mt][1]), __float_as_uint(acc1[mt][2]), __float_as_uint(acc1[mt][3])});
+      }
+    }
+  }
+  PHASE_TS(s, l, PH, 5);
+  unsigned* fl = flag_base(a, s, l, PH);
+  unsigned* fpart = fl + kPartFlags + 4 * (grp + NG * half);
+  if (copy_wave()) wait_stores();  // publish_local waits for the compute waves' stores only
+  publish_local(a, fpart + ksp, a.epoch);
+  if (!wait_flags(a, fpart, kKSplit, s_flag)) return false;
+  PHASE_TS(s, l, PH, 7);
+  down_pairs_finish(a, s, l, smem + kLdsWork + kDownW1Floats, nt0, ksp, b0, b1, next_g, NN);
+  PHASE_TS(s, l, PH, 8);
+  publish(a, fl + (grp + NG * half) * kKSplit + ksp, a.epoch, true);  // every wave stored rows
+  PHASE_TS(s, l, PH, 9);
+  return true;
+}
+
+// =============================================================================================
 // the kernel
 // =============================================================================================
 static_assert(64 + 32 + 192 + kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "norm GEMM working area");
@@ -2764,6 +2929,7 @@ static_assert(kCompWaves * 4 * 256 + 64 * 17 + 128 <= kWorkFloats, "residual wor
 static_assert(kCompWaves * 4 * 2 * 256 + 64 * 33 <= kWorkFloats, "down_proj pairs working area");
 static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
+static_assert(kDownW1Floats + 256 <= kWorkFloatsBatched, "row-split down_proj: second tile + finisher sums");
 
 // Two instances: MULTI = false for one sample, where the batch is the constant 1, so none of the
 // batched phases' code (pair items, grouped attention) is compiled into it -- carrying that code
@@ -2795,7 +2961,9 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
            (G ? (gu_msplit<G>(a) ? phase_gateup_msplit(a, s, l, smem, &s_flag) : phase_gateup_pairs4(a, s, l, smem, &s_flag))
               : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
                                                      : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
-           ((G || a.batch > 1) && PI05_DOWN_PAIRS ? phase_down_pairs<G>(a, s, l, smem, &s_flag) : phase_down(a, s, l, smem, &s_flag));
+           (G && PI05_INSTANCE_GROUPED && PI05_DOWN_MSPLIT ? phase_down_msplit(a, s, l, smem, &s_flag)
+            : (G || a.batch > 1) && PI05_DOWN_PAIRS       ? phase_down_pairs<G>(a, s, l, smem, &s_flag)
+                                                          : phase_down(a, s, l, smem, &s_flag));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
