@@ -1295,17 +1295,42 @@ constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
 constexpr int kGuAhead = PI05_GU_AHEAD;  // chunks in flight ahead of the MFMAs (ring of 4)
 static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
 // chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
-// (NKS: k-steps of the activation rows; KS0: the first k-step of chunk 0)
+// (NKS: k-steps of the activation rows; KS0: the first k-step of chunk 0.)  M-tiles 0..2 take one
+// load per k-step; m-tile 3 holds 2 rows (48, 49), so one load brings the whole chunk's: lane
+// 16 kc + 2 s2 + r gets row 48 + r, k-step s2, k-range kc -> A[3][0], which gu_mfma_chunk spreads
+// to the fragment lanes (16 kc + r) with a row shift per k-step.  The fragments' other lanes of
+// m-tile 3 then hold other rows' data: they are rows 50..63, whose products no phase stores.
+static_assert(kHorizon == 3 * 16 + 2, "m-tile 3 holds rows 48 and 49");
 template <int NKS = kWidth / 32>
 __device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, int b, bool ok_b, int c, int lane, int ks0 = 0) {
   const int r16 = lane & 15;
 #pragma unroll
   for (int s2 = 0; s2 < kGuCk; ++s2)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < 3; ++mt) {
       const bool ok = ok_b && r16 < kHorizon - mt * 16;
       buf_frag(A[mt][s2], rg, ok ? (int)((afrag_offset(b * 4 + mt, ks0 + c * kGuCk + s2, NKS) + lane * 8) * 2) : kOob);
     }
+  const int s2 = r16 >> 1, r = r16 & 1, kc = lane >> 4;
+  const bool ok = ok_b && r16 < 2 * kGuCk;
+  buf_frag(A[3][0], rg, ok ? (int)((afrag_offset(b * 4 + 3, ks0 + c * kGuCk + s2, NKS) + (16 * kc + r) * 8) * 2) : kOob);
+}
+// v moved up by N lanes within each row of 16 (DPP row_shl: lane i takes lane i + N of its row)
+template <int N>
+__device__ __forceinline__ bf16x8 frag_row_shl(bf16x8 v) {
+  if constexpr (N == 0) {
+    return v;
+  } else {
+    const u32x4 x = __builtin_bit_cast(u32x4, v);
+    u32x4 y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x[i], 0x100 + N, 0xf, 0xf, false);
+    return __builtin_bit_cast(bf16x8, y);
+  }
+}
+template <int S2>
+__device__ __forceinline__ bf16x8 mtile3_frag(const bf16x8 (&A)[4][kGuCk]) {
+  return frag_row_shl<2 * S2>(A[3][0]);
 }
 // the products of chunk c with the two weight tiles in region A (lw: tile 0, then tile 1, 32
 // fragments each); LAST1: tile 1's last k-step comes from the register w1_last instead
@@ -1320,10 +1345,12 @@ __device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4]
     const bf16x8 wu = LAST1 && s2 == kGuCk - 1 && c == kGuChunks - 1
                           ? w1_last
                           : *reinterpret_cast<const bf16x8*>(lw + ((size_t)KSTEPS + ks) * 512 + lane * 8);
+    const bf16x8 a3 = s2 == 0 ? mtile3_frag<0>(A) : s2 == 1 ? mtile3_frag<1>(A) : s2 == 2 ? mtile3_frag<2>(A) : mtile3_frag<3>(A);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      accg[mt] = mfma16x16x32(wg, A[mt][s2], accg[mt]);
-      accu[mt] = mfma16x16x32(wu, A[mt][s2], accu[mt]);
+      const bf16x8 am = mt < 3 ? A[mt][s2] : a3;
+      accg[mt] = mfma16x16x32(wg, am, accg[mt]);
+      accu[mt] = mfma16x16x32(wu, am, accu[mt]);
     }
   }
 }
