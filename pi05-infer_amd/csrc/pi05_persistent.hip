@@ -1315,6 +1315,26 @@ __device__ __forceinline__ void gu_load_chunk(bf16x8 (&A)[4][kGuCk], brsrc rg, i
   const bool ok = ok_b && r16 < 2 * kGuCk;
   buf_frag(A[3][0], rg, ok ? (int)((afrag_offset(b * 4 + 3, ks0 + c * kGuCk + s2, NKS) + (16 * kc + r) * 8) * 2) : kOob);
 }
+// Row statistics of the row-split phases, 16-byte loads: lane (j = lane % 16, q = lane / 16)
+// loads the tile sums of squares of rows 4j .. 4j+3 for tile 16 q + t (t = 0 .. 15, in order);
+// row_rstd adds the four tile groups across lanes and returns lane r's row rstd.
+__device__ __forceinline__ float4 row_stats4(brsrc rs, int R, int b, int t, int lane) {
+  const int j = lane & 15, q = lane >> 4;
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((16 * q + t) * R + b * kRowsPerSample + 4 * j) * 4, 0, 0));
+}
+__device__ __forceinline__ float row_rstd(float4 s, int lane, float eps) {
+  float r4[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r4[i] = 1.0f / sqrtf(fadd(lane_sum_xor32(lane_sum_xor16(r4[i])) * (1.0f / kWidth), eps));
+  // row `lane` is component lane % 4 of lane lane / 4
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v = __shfl(r4[i], lane >> 2);
+    r = (lane & 3) == i ? v : r;
+  }
+  return r;
+}
 // v moved up by N lanes within each row of 16 (DPP row_shl: lane i takes lane i + N of its row)
 template <int N>
 __device__ __forceinline__ bf16x8 frag_row_shl(bf16x8 v) {
@@ -1417,26 +1437,24 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
     f32x4 acc0[4], acc1[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc0[mt] = acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float st[4][16];
-    float ssq[4];
+    float4 st[4][4];
+    float4 ss4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kGuChunks; ++c) {
       if (c + kGuAhead < kGuChunks) gu_load_chunk(A[(c + kGuAhead) % 4], rg, b, true, c + kGuAhead, lane);
       else gu_load_chunk(A[(c + kGuAhead) % 4], rg, bn, ok_n, c + kGuAhead - kGuChunks, lane);
       if (c < 4) {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) buf_f32(st[c][t], rs, (((16 * c + t) * R) + b * kRowsPerSample + lane) * 4);
+        for (int t = 0; t < 4; ++t) st[c][t] = row_stats4(rs, R, b, 4 * c + t, lane);
       }
       sched_fence();
       gu_mfma_chunk<true>(acc0, acc1, A[c % 4], lw, c, lane, w1_last);
       if (c >= 1 && c <= 4) {
-        float v = 0.f;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v += st[c - 1][t];
-        ssq[c - 1] = v;
+        for (int t = 0; t < 4; ++t) ss4 += st[c - 1][t];
       }
     }
-    const float rstd_lane = 1.0f / sqrtf(fadd((((ssq[0] + ssq[1]) + ssq[2]) + ssq[3]) * (1.0f / kWidth), a.eps));
+    const float rstd_lane = row_rstd(ss4, lane, a.eps);
     if (rotated) {
       // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
       const int head = p >> 3, dt = p & 7, d = dt * 16 + 4 * g;
@@ -1669,8 +1687,8 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
     f32x4 accg[4], accu[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) accg[mt] = accu[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float st[4][16];
-    float ssq[4];
+    float4 st[4][4];
+    float4 ss4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kGuChunks; ++c) {
       // kGuAhead chunks ahead: this sample's, then the next sample's first ones
@@ -1678,19 +1696,17 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
       else gu_load_chunk(A[(c + kGuAhead) % 4], rg, bn, ok_n, c + kGuAhead - kGuChunks, lane);
       if (c < 4) {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) buf_f32(st[c][t], rs, (((16 * c + t) * R) + b * kRowsPerSample + lane) * 4);
+        for (int t = 0; t < 4; ++t) st[c][t] = row_stats4(rs, R, b, 4 * c + t, lane);
       }
       sched_fence();
       gu_mfma_chunk(accg, accu, A[c % 4], lw, c, lane);
       if (c >= 1 && c <= 4) {
-        float v = 0.f;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) v += st[c - 1][t];
-        ssq[c - 1] = v;
+        for (int t = 0; t < 4; ++t) ss4 += st[c - 1][t];
       }
     }
     // lane r's row r: rstd of adaRMSNorm (the same grouping as the one-sample phases)
-    const float rstd_lane = 1.0f / sqrtf(fadd((((ssq[0] + ssq[1]) + ssq[2]) + ssq[3]) * (1.0f / kWidth), a.eps));
+    const float rstd_lane = row_rstd(ss4, lane, a.eps);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int row = mt * 16 + r16;
