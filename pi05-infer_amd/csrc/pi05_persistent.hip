@@ -2974,13 +2974,9 @@ static_assert(2048 + 2 * 3072 + 128 <= kWorkFloats, "attention working area");
 static_assert(kWidth + 2 * kActDim + 4 + kCompThreads + kWidth <= kWorkFloats, "step boundary working area");
 static_assert(kDownW1Floats + 256 <= kWorkFloatsBatched, "row-split down_proj: second tile + finisher sums");
 
-// Two instances: MULTI = false for one sample, where the batch is the constant 1, so none of the
-// batched phases' code (pair items, grouped attention) is compiled into it -- carrying that code
-// costs the single-sample schedule 3.5 % through register allocation -- and MULTI = true for
-// batches of two and more.
-// Three instances of the kernel: G = false for one sample, G = true for batches (always the pair
-// items); I = the instance number (0, 1, 2), instance 2 (batches of kRowSplitMinBatch and more)
-// alone containing the row-split gate_up and the grouped attention.  Each is compiled in a
+// Three instances of the kernel: G = false for one sample, G = true for batches; I = the instance
+// number (0, 1, 2), instance 2 (batches of kRowSplitMinBatch and more) alone containing the
+// row-split qkv / gate_up / down_proj phases and the grouped attention.  Each is compiled in a
 // translation unit of its own: inlined into one module, the batched code changed the one-sample
 // kernel's register allocation (measured +2-3.5 % per C1 predict), and the batch paths each
 // other's (+1-1.5 %).
