@@ -409,6 +409,17 @@ template <bool G>
 __device__ __forceinline__ constexpr bool qkv_msplit() {
   return G && PI05_INSTANCE_GROUPED && PI05_QKV_MSPLIT;
 }
+// phase_qkv_msplit's items: tile pair i mod 80 for sample third i / 80, on workgroups 16..255
+constexpr int kQkvItemsRS = 3 * kQkvPairs;
+constexpr int kQkvWg0RS = 256 - kQkvItemsRS;
+template <bool G>
+__device__ __forceinline__ constexpr int n_qkv_items() {
+  return qkv_msplit<G>() ? kQkvItemsRS : kQkvItems;
+}
+template <bool G>
+__device__ __forceinline__ int qkv_item_of() {
+  return qkv_msplit<G>() ? (int)blockIdx.x - kQkvWg0RS : qkv_item();
+}
 // The gate_up of kernel instance 2 (phase_gateup_msplit, batches of kRowSplitMinBatch and more):
 // item w = pair w.
 template <bool G>
@@ -424,7 +435,7 @@ __device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
 // do; region A holds the first pair.
 template <bool G>
 __device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
-  return G && a.batch > 1 && !qkv_msplit<G>() ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item() % kQkvPairs;
+  return G && a.batch > 1 && !qkv_msplit<G>() ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item_of<G>() % kQkvPairs;
 }
 template <int MODE, bool G = false>
 __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
@@ -444,7 +455,7 @@ __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int 
 template <int MODE, int F0, int N, bool G = false>
 __device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
   if (!copy_wave()) return;
-  if (MODE == kModeQkv ? (unsigned)qkv_item() >= (unsigned)kQkvItems : blockIdx.x >= kGuItems) return;
+  if (MODE == kModeQkv ? (unsigned)qkv_item_of<G>() >= (unsigned)n_qkv_items<G>() : blockIdx.x >= kGuItems) return;
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE, G>(a, l, which) + F0 * 512);
 }
 
@@ -1377,9 +1388,10 @@ __device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4]
 
 // =============================================================================================
 // qkv of kernel instance 2, split by rows as phase_gateup_msplit: item i = tile pair i mod 80 (a
-// RoPE pair of q or k tiles, or two consecutive v tiles) for sample half i / 80; region A holds
+// RoPE pair of q or k tiles, or two consecutive v tiles) for sample third i / 80 (240 items on
+// workgroups 16..255); region A holds
 // the pair's two tiles except the second one's last k-step (the 63-copy burst leaves it out),
-// which every wave loads into a register.  Wave j takes sample j of the half (j + 4, ... past 8
+// which every wave loads into a register.  Wave j takes sample j of the third (j + 4, ... past 12
 // samples): all four m-tiles over the whole K, A streamed two chunks ahead.  As W.A^T, a lane
 // ends with columns 4g .. 4g+3 of both tiles for one row, so the RoPE rotation (which pairs
 // column d of the first tile with column d of the second) and the 8-byte q / k stores are
@@ -1388,7 +1400,7 @@ __device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4]
 __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
   constexpr int KSTEPS = kWidth / 32;
   const int L = a.depth, R = a.R;
-  const int item = qkv_item();
+  const int item = qkv_item_of<true>();
   PHASE_TS(s, l, kPhQkv, 0);
   // copy wave: this phase's weights (region A) and everything issued before them have landed;
   // down(l) -> B here unless grouped attention stages K/V there (then before o_proj)
@@ -1396,10 +1408,10 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
     wait_vmcnt<0>();
     if (!attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
   }
-  if (item < 0 || item >= kQkvItems) return true;
-  const int p = item % kQkvPairs, sh = item / kQkvPairs;
+  if (item < 0 || item >= kQkvItemsRS) return true;
+  const int p = item % kQkvPairs, sg = item / kQkvPairs;
   const bool rotated = p < 72;
-  const int bh = (a.batch + 1) / 2, b0 = sh * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
+  const int bt = (a.batch + 2) / 3, b0 = sg * bt, b1 = b0 + bt < a.batch ? b0 + bt : a.batch;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const size_t slw = (size_t)s * L + l;
@@ -2016,7 +2028,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
     burst = true;
     PHASE_TS(s, l, kPhSplit, 1);
-    if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
+    if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), s_flag)) return false;
     PHASE_TS(s, l, kPhSplit, 2);
     if (!attn_group_items(a, s, l, smem, s_flag)) return false;
   }
@@ -2054,7 +2066,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     }
     PHASE_TS(s, l, kPhSplit, 1);
     if (!waited) {
-      if (!wait_flags(a, flag_base(a, s, l, kPhQkv), kQkvItems, s_flag)) return false;
+      if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), s_flag)) return false;
       waited = true;
     }
     PHASE_TS(s, l, kPhSplit, 2);
