@@ -39,6 +39,7 @@ constexpr size_t kPOffO = kPOffQkv + (size_t)kPQkvN * kPW;
 constexpr size_t kPOffGu = kPOffO + (size_t)kPW * kPHD;
 constexpr size_t kPOffD = kPOffGu + (size_t)kPGuN * kPW;
 constexpr size_t kPLayerElems = kPOffD + (size_t)kPW * kPI;
+constexpr int kDownSplits = 4;  // down_proj / o_proj split-K candidates: 4 slices of K
 constexpr int kAttnMtPerWg = 8;  // attention m-tiles (16 query rows: 2 tokens x 8 heads) per workgroup
 // s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt not waited for (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14])
@@ -84,19 +85,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y
                                                       const float* ys = nullptr, int nsplit = 0, size_t split_stride = 0) {
   const size_t off = (size_t)blockIdx.x * kPW + threadIdx.x * 8;
   __shared__ float s_part[4];
+  // every load is issued before the first use: the norm weight, the row and every split's
+  // partial (a loop that waited for each split in turn paid one memory round trip per split)
+  const float4 w0 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8);
+  const float4 w1 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8 + 4);
   const u16x8 xv = *reinterpret_cast<const u16x8*>(x + off);
   float h[8];
   if (ys) {
-    float acc[8];
-    {
-      const float4 a0 = *reinterpret_cast<const float4*>(ys + off), a1 = *reinterpret_cast<const float4*>(ys + off + 4);
-      acc[0] = a0.x, acc[1] = a0.y, acc[2] = a0.z, acc[3] = a0.w, acc[4] = a1.x, acc[5] = a1.y, acc[6] = a1.z, acc[7] = a1.w;
-    }
-    for (int sp = 1; sp < nsplit; ++sp) {
-      const float* q = ys + (size_t)sp * split_stride + off;
-      const float4 a0 = *reinterpret_cast<const float4*>(q), a1 = *reinterpret_cast<const float4*>(q + 4);
-      acc[0] += a0.x, acc[1] += a0.y, acc[2] += a0.z, acc[3] += a0.w, acc[4] += a1.x, acc[5] += a1.y, acc[6] += a1.z, acc[7] += a1.w;
-    }
+    float4 a[kDownSplits][2];
+#pragma unroll
+    for (int sp = 0; sp < kDownSplits; ++sp)
+      if (sp < nsplit) {
+        const float* q = ys + (size_t)sp * split_stride + off;
+        a[sp][0] = *reinterpret_cast<const float4*>(q), a[sp][1] = *reinterpret_cast<const float4*>(q + 4);
+      }
+    float acc[8] = {a[0][0].x, a[0][0].y, a[0][0].z, a[0][0].w, a[0][1].x, a[0][1].y, a[0][1].z, a[0][1].w};
+#pragma unroll
+    for (int sp = 1; sp < kDownSplits; ++sp)
+      if (sp < nsplit) {
+        acc[0] += a[sp][0].x, acc[1] += a[sp][0].y, acc[2] += a[sp][0].z, acc[3] += a[sp][0].w;
+        acc[4] += a[sp][1].x, acc[5] += a[sp][1].y, acc[6] += a[sp][1].z, acc[7] += a[sp][1].w;
+      }
 #pragma unroll
     for (int i = 0; i < 8; ++i) h[i] = round_bf(fadd(bf2f(xv[i]), round_bf(acc[i])));
   } else if (y) {
@@ -116,8 +125,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const u16* x, const u16* y
   __syncthreads();
   const float var = ((s_part[0] + s_part[1]) + (s_part[2] + s_part[3])) * (1.0f / kPW);
   const float rs = 1.0f / sqrtf(var + eps);
-  const float4 w0 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8);
-  const float4 w1 = *reinterpret_cast<const float4*>(w + threadIdx.x * 8 + 4);
   const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
   u16x8 hv, nv;
 #pragma unroll
@@ -397,7 +404,6 @@ struct PrefixPlan {
   }
 };
 constexpr size_t kWorkspace = 64ull << 20;
-constexpr int kDownSplits = 4;  // down_proj split-K candidate: 4 slices of K = 4096
 
 size_t rup(size_t x) { return (x + 255) / 256 * 256; }
 

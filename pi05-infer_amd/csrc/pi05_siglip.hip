@@ -86,7 +86,13 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= rows) return;
   const size_t ro = (size_t)row * kVW;
-  // every load of the row is issued before the first use
+  // every load of the row is issued before the first use, the norm's weight and bias included
+  float2 wv[9], bv[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    wv[j] = *reinterpret_cast<const float2*>(w + 2 * (lane + 64 * j));
+    bv[j] = *reinterpret_cast<const float2*>(b + 2 * (lane + 64 * j));
+  }
   uint32_t xv[9];
 #pragma unroll
   for (int j = 0; j < 9; ++j) xv[j] = *reinterpret_cast<const uint32_t*>(x + ro + 2 * (lane + 64 * j));
@@ -96,9 +102,12 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
   if (ys) {
     // every split's partial row is loaded before the first sum (the splits are summed in order, as
     // before): a loop that waited for each split's loads in turn paid one memory round trip per split
-    float2 acc[9], a[kVMaxSplits - 1][9];
+    float2 acc[9], a[kVMaxSplits - 1][9], yb[9];
 #pragma unroll
-    for (int j = 0; j < 9; ++j) acc[j] = *reinterpret_cast<const float2*>(ys + ro + 2 * (lane + 64 * j));
+    for (int j = 0; j < 9; ++j) {
+      acc[j] = *reinterpret_cast<const float2*>(ys + ro + 2 * (lane + 64 * j));
+      yb[j] = *reinterpret_cast<const float2*>(ybias + 2 * (lane + 64 * j));
+    }
 #pragma unroll
     for (int sp = 1; sp < kVMaxSplits; ++sp)
       if (sp < nsplit)
@@ -111,9 +120,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
         for (int j = 0; j < 9; ++j) acc[j].x += a[sp - 1][j].x, acc[j].y += a[sp - 1][j].y;
 #pragma unroll
     for (int j = 0; j < 9; ++j) {
-      const float2 bb = *reinterpret_cast<const float2*>(ybias + 2 * (lane + 64 * j));
-      h[2 * j] = round_bf(fadd(h[2 * j], round_bf(fadd(acc[j].x, bb.x))));
-      h[2 * j + 1] = round_bf(fadd(h[2 * j + 1], round_bf(fadd(acc[j].y, bb.y))));
+      h[2 * j] = round_bf(fadd(h[2 * j], round_bf(fadd(acc[j].x, yb[j].x))));
+      h[2 * j + 1] = round_bf(fadd(h[2 * j + 1], round_bf(fadd(acc[j].y, yb[j].y))));
     }
   } else if (y) {
     uint32_t yv[9];
@@ -141,9 +149,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const u16* x, const u16*
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
     const int e = 2 * (lane + 64 * j);
-    const float2 wv = *reinterpret_cast<const float2*>(w + e), bv = *reinterpret_cast<const float2*>(b + e);
-    const u16 n0 = f2bf(fadd(fmul(fmul(fsub(h[2 * j], mean), rstd), wv.x), bv.x));
-    const u16 n1 = f2bf(fadd(fmul(fmul(fsub(h[2 * j + 1], mean), rstd), wv.y), bv.y));
+    const u16 n0 = f2bf(fadd(fmul(fmul(fsub(h[2 * j], mean), rstd), wv[j].x), bv[j].x));
+    const u16 n1 = f2bf(fadd(fmul(fmul(fsub(h[2 * j + 1], mean), rstd), wv[j].y), bv[j].y));
     *reinterpret_cast<uint32_t*>(n_out + ro + e) = (uint32_t)n0 | ((uint32_t)n1 << 16);
     if (write_h) *reinterpret_cast<uint32_t*>(h_out + ro + e) = (uint32_t)f2bf(h[2 * j]) | ((uint32_t)f2bf(h[2 * j + 1]) << 16);
   }
