@@ -238,7 +238,8 @@ struct AttnArgs {
   int B, P, s_pad, n_mt, items, nsplit;
 };
 
-constexpr int kAttnMaxBlocks = 65536 / 32;  // key blocks of the longest prefix (batch * prefix_len <= 65536)
+constexpr int kAttnMaxBlocks = 65536 / 32;
+constexpr int kAttnMaxSplits = 8;  // the split count's cap (prefill_plan)  // key blocks of the longest prefix (batch * prefix_len <= 65536)
 
 __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) u16 s_kv[2][32][512];
@@ -333,19 +334,32 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* po, const 
   const int b = blockIdx.x / P, token = blockIdx.x % P, t = threadIdx.x;
   const int head = t >> 5, d0 = (t & 31) * 8;
   const size_t rows = (size_t)n_mt * 16, row = (size_t)token * kHeads + head;
+  // every split's (max, sum) and partial row are loaded before the first use (a loop that waited
+  // for each split's loads in turn paid one memory round trip per split); splits combined in order
+  float2 ml[kAttnMaxSplits];
+  float4 v0[kAttnMaxSplits], v1[kAttnMaxSplits];
+#pragma unroll
+  for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+    if (sp < nsplit) {
+      const size_t r = ((size_t)sp * B + b) * rows + row;
+      ml[sp] = *reinterpret_cast<const float2*>(pml + r * 2);
+      v0[sp] = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0);
+      v1[sp] = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0 + 4);
+    }
   float M = -INFINITY;
-  for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, pml[(((size_t)sp * B + b) * rows + row) * 2]);
+#pragma unroll
+  for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+    if (sp < nsplit) M = fmaxf(M, ml[sp].x);
   float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const size_t r = ((size_t)sp * B + b) * rows + row;
-    const float ms = pml[r * 2];
-    const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-    L += pml[r * 2 + 1] * w;
-    const float4 v0 = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0);
-    const float4 v1 = *reinterpret_cast<const float4*>(po + r * kHeadDim + d0 + 4);
-    o[0] += v0.x * w, o[1] += v0.y * w, o[2] += v0.z * w, o[3] += v0.w * w;
-    o[4] += v1.x * w, o[5] += v1.y * w, o[6] += v1.z * w, o[7] += v1.w * w;
-  }
+#pragma unroll
+  for (int sp = 0; sp < kAttnMaxSplits; ++sp)
+    if (sp < nsplit) {
+      const float ms = ml[sp].x;
+      const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+      L += ml[sp].y * w;
+      o[0] += v0[sp].x * w, o[1] += v0[sp].y * w, o[2] += v0[sp].z * w, o[3] += v0[sp].w * w;
+      o[4] += v1[sp].x * w, o[5] += v1[sp].y * w, o[6] += v1[sp].z * w, o[7] += v1[sp].w * w;
+    }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   u16x8 r8;
 #pragma unroll
@@ -417,7 +431,7 @@ PrefixPlan plan_of(const pi05_prefix_dims& d) {
   // workgroup per CU), at most 8 and at most one per key block
   const int nkb = p.s_pad / 32;
   p.nsplit = 256 / (p.B * p.items);
-  if (p.nsplit > 8) p.nsplit = 8;
+  if (p.nsplit > kAttnMaxSplits) p.nsplit = kAttnMaxSplits;
   if (p.nsplit > nkb) p.nsplit = nkb;
   if (p.nsplit < 1) p.nsplit = 1;
   const size_t M = p.M;
