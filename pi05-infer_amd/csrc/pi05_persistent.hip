@@ -1438,6 +1438,9 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
   const brsrc rs = make_rsrc(a.ss + ((size_t)s * (L + 1) + l) * kTiles * R, (size_t)kTiles * R * 4);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);
   u16* s_v = reinterpret_cast<u16*>(smem + kLdsWork) + wave * 64 * 32;  // v items: [64 keys][32 dims]
+  const int rope_d = (p & 7) * 16 + 4 * g;  // RoPE items: the lane's first column of the low tile
+  const brsrc rcos = make_rsrc(a.cos_tab, (size_t)a.batch * kHorizon * kHeadDim * 2);
+  const brsrc rsin = make_rsrc(a.sin_tab, (size_t)a.batch * kHorizon * kHeadDim * 2);
   bf16x8 A[4][4][kGuCk];  // [ring slot = chunk mod 4][m-tile][k-step]
   const int bf = b0 + wave;
 #pragma unroll
@@ -1451,6 +1454,7 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
     for (int mt = 0; mt < 4; ++mt) acc0[mt] = acc1[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float4 st[4][4];
     float4 ss4 = {0.f, 0.f, 0.f, 0.f};
+    u32x2 cst[4][4];  // RoPE: [m-tile][cos lo, sin lo, cos hi, sin hi] of the lane's row, columns d .. d+3
 #pragma unroll
     for (int c = 0; c < kGuChunks; ++c) {
       if (c + kGuAhead < kGuChunks) gu_load_chunk(A[(c + kGuAhead) % 4], rg, b, true, c + kGuAhead, lane);
@@ -1458,6 +1462,20 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
       if (c < 4) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) st[c][t] = row_stats4(rs, R, b, 4 * c + t, lane);
+      }
+      if (c == 4 && rotated) {
+        // the epilogue's cos / sin, loaded here so that their latency hides behind the MFMAs
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int row = mt * 16 + r16;
+          const bool ok = row < kHorizon;
+          const int lo = ok ? (int)(((size_t)(b * kHorizon + row) * kHeadDim + rope_d) * 2) : kOob;
+          const int hi = ok ? lo + kHalfDim * 2 : kOob;
+          cst[mt][0] = __builtin_amdgcn_raw_buffer_load_b64(rcos, lo, 0, 0);
+          cst[mt][1] = __builtin_amdgcn_raw_buffer_load_b64(rsin, lo, 0, 0);
+          cst[mt][2] = __builtin_amdgcn_raw_buffer_load_b64(rcos, hi, 0, 0);
+          cst[mt][3] = __builtin_amdgcn_raw_buffer_load_b64(rsin, hi, 0, 0);
+        }
       }
       sched_fence();
       gu_mfma_chunk<true>(acc0, acc1, A[c % 4], lw, c, lane, w1_last);
@@ -1469,15 +1487,14 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
     const float rstd_lane = row_rstd(ss4, lane, a.eps);
     if (rotated) {
       // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
-      const int head = p >> 3, dt = p & 7, d = dt * 16 + 4 * g;
+      const int head = p >> 3, d = rope_d;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int row = mt * 16 + r16;
         const float rstd = __shfl(rstd_lane, row);
         if (row < kHorizon) {
-          const size_t cr = (size_t)(b * kHorizon + row) * kHeadDim + d;
-          const u16x4 cs_lo = *reinterpret_cast<const u16x4*>(a.cos_tab + cr), sn_lo = *reinterpret_cast<const u16x4*>(a.sin_tab + cr);
-          const u16x4 cs_hi = *reinterpret_cast<const u16x4*>(a.cos_tab + cr + kHalfDim), sn_hi = *reinterpret_cast<const u16x4*>(a.sin_tab + cr + kHalfDim);
+          const u16x4 cs_lo = __builtin_bit_cast(u16x4, cst[mt][0]), sn_lo = __builtin_bit_cast(u16x4, cst[mt][1]);
+          const u16x4 cs_hi = __builtin_bit_cast(u16x4, cst[mt][2]), sn_hi = __builtin_bit_cast(u16x4, cst[mt][3]);
           u16 olo[4], ohi[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
