@@ -139,6 +139,22 @@ def test_batch5_batch_paths(full_weights):
     model.close()
 
 
+def test_batch16_multi_pass_items(full_weights):
+    """B=16: every per-workgroup loop of the batched kernel runs more than once -- gate_up rows four
+    samples per wave, qkv thirds of six samples (two per wave for two waves), down_proj halves of
+    eight (two per wave), o_proj's wave pairs eight iterations, the grouped attention two key
+    splits -- with a ragged prefix."""
+    print("case B=16: depth 2, B=16, P=100, 2 steps", flush=True)
+
+    def pad_fn(pad):
+        pad[3, 90:] = False
+        pad[11, 0:7] = False
+
+    model, _, _, _, ref, got = _run_case(full_weights, depth=2, P=100, B=16, steps=2, pad_fn=pad_fn, schedules=("persistent",))
+    _check("B=16", ref, got, 2)
+    model.close()
+
+
 def test_ragged_prefix_padding(full_weights):
     """B=3: the attention split items (not grouped) with the row-split gate_up (three waves one
     sample each, the fourth idle)."""
