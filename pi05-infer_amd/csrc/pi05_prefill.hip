@@ -223,9 +223,10 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(RopeKvArgs a) {
 // m-tiles of one sample in 8 waves, wave w owns m-tile w (query fragments in registers; one m-tile
 // per wave keeps a wave under 256 registers, so two waves share each SIMD and one wave's softmax
 // overlaps the other's MFMAs).  Key blocks of 32 (16 KiB of K + 16 KiB of V fragments) are staged
-// into LDS with direct-to-LDS loads, double buffered, and every wave runs the online-softmax block
-// update of the denoise attention (attend_block) on its m-tile.  Masked keys are skipped; a query row with no valid key
-// (a padded token) is written as zeros.  With nsplit > 1 the key blocks are split over nsplit
+// into LDS with direct-to-LDS loads two blocks at a time (one barrier per two blocks), double
+// buffered, and every wave runs the online-softmax block update of the denoise attention
+// (attend_block) on its m-tile.  Masked keys are skipped; a query row with no valid key (a padded
+// token) is written as zeros.  With nsplit > 1 the key blocks are split over nsplit
 // workgroups per m-tile group (so that short prefixes still fill the GPU), which store their
 // unnormalised fp32 O and running (max, sum) per row for attn_merge_kernel.
 // ---------------------------------------------------------------------------------------------
@@ -242,7 +243,7 @@ constexpr int kAttnMaxBlocks = 65536 / 32;
 constexpr int kAttnMaxSplits = 8;  // the split count's cap (prefill_plan)  // key blocks of the longest prefix (batch * prefix_len <= 65536)
 
 __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
-  __shared__ __align__(16) u16 s_kv[2][32][512];
+  __shared__ __align__(16) u16 s_kv[2][64][512];  // two stages of two 32-key blocks
   __shared__ uint32_t s_bits[kAttnMaxBlocks];  // bit j of word i: key 32 (kb_lo + i) + j is valid
   const int split = blockIdx.x % a.nsplit, bi = blockIdx.x / a.nsplit;
   const int b = bi / a.items, item = bi % a.items;
@@ -269,37 +270,49 @@ __global__ __launch_bounds__(512, 1) void prefix_attn_kernel(AttnArgs a) {
   bf16x8 qf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) qf[ds] = mt < a.n_mt ? load_frag(qb + afrag_offset(mt, ds, kHeadDim / 32) + lane * 8) : zero_frag();
-  // wave w copies fragments 4w .. 4w+3 of a block (K fragments 0..15, then V fragments)
-  auto stage = [&](int kb, int buf) {
+  // stage j = blocks kb_lo + 2j and + 1; wave w copies fragments 4w .. 4w+3 of each (K fragments
+  // 0..15, then V fragments): one barrier per two blocks
+  auto stage = [&](int j, int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = wu * 4 + i;
-      const u16* src = f < 16 ? kb0 + ((size_t)2 * kb * 8 + f) * 512 : vb0 + ((size_t)kb * 16 + (f - 16)) * 512;
-      __builtin_amdgcn_global_load_lds(const_cast<u16*>(src) + lane * 8, &s_kv[buf][f][0], 16, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+      const int kb = kb_lo + 2 * j + h;
+      if (kb < kb_hi) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int f = wu * 4 + i;
+          const u16* src = f < 16 ? kb0 + ((size_t)2 * kb * 8 + f) * 512 : vb0 + ((size_t)kb * 16 + (f - 16)) * 512;
+          __builtin_amdgcn_global_load_lds(const_cast<u16*>(src) + lane * 8, &s_kv[buf][32 * h + f][0], 16, 0, 0);
+        }
+      }
     }
   };
-  stage(kb_lo, kb_lo & 1);
+  stage(0, 0);
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 oacc[16];
 #pragma unroll
   for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = kb_lo; kb < kb_hi; ++kb) {
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of block kb have landed
-    __syncthreads();  // every wave's copies of block kb have landed; buffer (kb+1)&1 is no longer read
-    if (kb + 1 < kb_hi) stage(kb + 1, (kb + 1) & 1);
-    const int buf = kb & 1;
-    KvBlock blk;
+  for (int j = 0; kb_lo + 2 * j < kb_hi; ++j) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's copies of stage j have landed
+    __syncthreads();  // every wave's copies of stage j have landed; buffer (j+1)&1 is no longer read
+    if (kb_lo + 2 * (j + 1) < kb_hi) stage(j + 1, (j + 1) & 1);
+    const int buf = j & 1;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      blk.k[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][i][lane * 8]);
-      blk.v[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][16 + i][lane * 8]);
+    for (int h = 0; h < 2; ++h) {
+      const int kb = kb_lo + 2 * j + h;
+      if (kb >= kb_hi) break;
+      KvBlock blk;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        blk.k[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][32 * h + i][lane * 8]);
+        blk.v[i] = *reinterpret_cast<const bf16x8*>(&s_kv[buf][32 * h + 16 + i][lane * 8]);
+      }
+      // attend_block's key-valid bytes: keys 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3
+      const uint32_t bits = s_bits[kb - kb_lo];
+      const uint32_t lo = (bits >> (4 * g)) & 15u, hi = (bits >> (16 + 4 * g)) & 15u;
+      blk.valid0 = (lo & 1u) | ((lo & 2u) << 7) | ((lo & 4u) << 14) | ((lo & 8u) << 21);
+      blk.valid1 = (hi & 1u) | ((hi & 2u) << 7) | ((hi & 4u) << 14) | ((hi & 8u) << 21);
+      if (mt < a.n_mt) attend_block(blk, qf, m_run, l_run, oacc);
     }
-    // attend_block's key-valid bytes: keys 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3
-    const uint32_t bits = s_bits[kb - kb_lo];
-    const uint32_t lo = (bits >> (4 * g)) & 15u, hi = (bits >> (16 + 4 * g)) & 15u;
-    blk.valid0 = (lo & 1u) | ((lo & 2u) << 7) | ((lo & 4u) << 14) | ((lo & 8u) << 21);
-    blk.valid1 = (hi & 1u) | ((hi & 2u) << 7) | ((hi & 4u) << 14) | ((hi & 8u) << 21);
-    if (mt < a.n_mt) attend_block(blk, qf, m_run, l_run, oacc);
   }
   // O = acc / l: lane (row r16 = token 2 mt + r16/8, head r16 % 8) holds dims 16 dt + 4 g .. +3
   if (mt >= a.n_mt) return;  // after the last barrier
