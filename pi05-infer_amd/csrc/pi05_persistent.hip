@@ -430,9 +430,9 @@ __device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
   return a.batch > 1 ? 2 * ((int)blockIdx.x % (kGuItems / 2)) : (int)blockIdx.x;
 }
 // qkv items.  B = 1: item i = qkv_item() computes tile pair i mod 80 over row half i / 80 of the
-// sample.  In the batched kernel instance (G): item i computes tile pairs 2 (i mod 40) and
-// 2 (i mod 40) + 1 over row half (i / 40) mod 2 for sample half i / 80, as gate_up's pair items
-// do; region A holds the first pair.
+// sample.  B = 2 (kernel instance 1): item i computes tile pairs 2 (i mod 40) and 2 (i mod 40) + 1
+// over row half (i / 40) mod 2 for sample half i / 80, as gate_up's pair items do; region A holds
+// the first pair.  Kernel instance 2: item i = tile pair i mod 80 for sample third i / 80.
 template <bool G>
 __device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
   return G && a.batch > 1 && !qkv_msplit<G>() ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item_of<G>() % kQkvPairs;
@@ -1111,7 +1111,7 @@ __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem,
 }
 
 // =============================================================================================
-// qkv in the batched kernel instance: two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from
+// qkv at B = 2 (kernel instance 1): two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from
 // registers) over row half mh for the samples [b0, b1) of sample half sh (see qkv_pair0), as
 // gate_up's pair items do; both pairs are RoPE pairs (g < 36) or both v pairs.  The epilogue per
 // pair is phase_norm_gemm's: bf16(rstd * acc + shift . W^T), then RoPE into the query rows or the
@@ -1551,7 +1551,7 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
 }
 
 // =============================================================================================
-// gate_up in the batched kernel instance: phase_gateup_pairs' items, with the copy wave as a fourth
+// gate_up at B = 2 (kernel instance 1): phase_gateup_pairs' items, with the copy wave as a fourth
 // compute wave (its down_proj copy is issued before o_proj instead): K splits 8 k-steps per wave, so
 // a sample's 48 loads per wave stay under the 63 a wave may have in flight and each wave runs 128
 // MFMAs per sample instead of 176; the four partials are added in wave order.
@@ -1670,7 +1670,7 @@ __device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem
 static_assert(64 + 64 + 256 + 4 * 4 * 2 * 256 + 64 * 33 <= kWorkFloatsBatched, "batched gate_up working area");
 
 // =============================================================================================
-// gate_up of the batched kernel instance, split by rows: item w = gate|up tile pair w for every
+// gate_up of kernel instance 2 (B >= 3), split by rows: item w = gate|up tile pair w for every
 // sample; region A holds its two tiles (gate, up: 32 k-steps each).  Wave j takes samples j,
 // j + 4, ...: for each, all four m-tiles over the whole K, so no partial sum crosses waves and the
 // waves never wait for each other.  The A fragments stream from L2 in chunks of 4 k-steps, two
@@ -2378,7 +2378,7 @@ __device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s
   return true;
 }
 
-// o_proj of the batched instance: one wait for every sample's merges (which finish in one pass of
+// o_proj of both batch instances: one wait for every sample's merges (which finish in one pass of
 // the grid), then two wave pairs, (1, 2) and (0, 3), each holding the tile's weights in K halves
 // (wave 1 / 0: k-steps 0..31, wave 2 / 3: 32..63), take samples 2i and 2i + 1 of iteration i side
 // by side.  Per sample the arithmetic is phase_oproj's (same accumulation chains, K halves added in
