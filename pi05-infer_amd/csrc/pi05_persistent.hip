@@ -1962,12 +1962,16 @@ __device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) 
   for (int bp = blockIdx.x; bp < nbp; bp += gridDim.x) {
     const int b = bp / kPairs, pair = bp % kPairs;
     if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
+    // only the splits there are: masked loads would still take an issue slot each
     float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
 #pragma unroll
     for (int c = 0; c < kMaxAttnSplits; ++c) {
-      const int mo = (c * nbp + bp) * 32 + rr;
-      buf_f32(mc[c], rml, c < nsplit ? mo * 4 : kOob);
-      buf_f32(lc[c], rml, c < nsplit ? (mo + 16) * 4 : kOob);
+      mc[c] = -INFINITY, lc[c] = 0.f;
+      if (c < nsplit) {
+        const int mo = (c * nbp + bp) * 32 + rr;
+        buf_f32(mc[c], rml, mo * 4);
+        buf_f32(lc[c], rml, (mo + 16) * 4);
+      }
     }
     float Mb = -INFINITY;
 #pragma unroll
@@ -2684,8 +2688,33 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
 // group finishes samples b0 + ksp, b0 + ksp + 4, ... of the half: it adds the four quarters'
 // partials in order and applies the gated residual to both tiles (h, g of the next layer's first
 // norm, the tiles' row sums of squares).  s_ss: 256 floats of LDS.
+// The finisher thread's static operands (gate, 1 + scale of its 8 columns) and the residual rows of
+// its first sample, loaded before the quarter flags' wait (they depend on nothing this phase makes).
+struct DownFinishPre {
+  float gate[8], s1[8];
+  u16x8 hold0;
+};
+__device__ __forceinline__ void down_finish_prefetch(const MegaArgs& a, int s, int l, int nt0, int ksp, int b0, int b1, bool next_g, int NN,
+                                                     DownFinishPre& pre) {
+  const int L = a.depth, R = a.R;
+  const int tid = phase_tid();
+  const int ft = tid >> 7, frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;
+  const int col = (nt0 + ft) * 16;
+  const size_t slw = (size_t)s * L + l;
+  const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
+  const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pre.gate[i] = gmod[i];
+    pre.s1[i] = next_g ? smod[i] : 0.f;
+  }
+  pre.hold0 = u16x8{0, 0, 0, 0, 0, 0, 0, 0};
+  const int b = b0 + ksp;
+  if (b < b1 && frow < kHorizon)
+    pre.hold0 = *reinterpret_cast<const u16x8*>(a.hmid + slw * (size_t)R * kWidth + afrag_index(b * kRowsPerSample + frow, col + fc0, kWidth / 32));
+}
 __device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int l, float* s_ss, int nt0, int ksp, int b0, int b1, bool next_g,
-                                                  int NN) {
+                                                  const DownFinishPre& pre) {
   const int L = a.depth, R = a.R;
   const int tid = phase_tid();
   const size_t slw = (size_t)s * L + l;
@@ -2697,13 +2726,11 @@ __device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int 
     u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
     u16* gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
     float* rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
-    const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
-    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
-    float gate[8], s1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float gate[8], s1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      gate[i] = round_bf(gmod[i]);
-      if (next_g) s1[i] = smod[i];
+      gate[i] = round_bf(pre.gate[i]);
+      s1[i] = pre.s1[i];
     }
     for (int b = b0 + ksp; b < b1; b += kKSplit) {
       const int r = b * kRowsPerSample + frow;
@@ -2717,7 +2744,7 @@ __device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int 
           pv[q][0] = v0.x, pv[q][1] = v0.y, pv[q][2] = v0.z, pv[q][3] = v0.w;
           pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
         }
-        const u16x8 hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
+        const u16x8 hold = b == b0 + ksp ? pre.hold0 : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
         u16 hn[8], gn[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -2945,6 +2972,9 @@ __device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, 
   PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // tile nt0's quarter, then nt0 + 1's
   const brsrc rg = make_rsrc(a.act + slw * (size_t)R * kMlp, (size_t)R * kMlp * 2);
+  // the finisher's operands (the residual rows are o_proj's, which the gate_up flags imply)
+  DownFinishPre fpre;
+  down_finish_prefetch(a, s, l, nt0, ksp, b0, b1, next_g, NN, fpre);
   float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;  // [quarter][tile][row][16]
   bf16x8 A[4][4][kGuCk];
   const int bf = b0 + wave;
@@ -2984,7 +3014,7 @@ __device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, 
   publish_local(a, fpart + ksp, a.epoch);
   if (!wait_flags(a, fpart, kKSplit, s_flag)) return false;
   PHASE_TS(s, l, PH, 7);
-  down_pairs_finish(a, s, l, smem + kLdsWork + kDownW1Floats, nt0, ksp, b0, b1, next_g, NN);
+  down_pairs_finish(a, s, l, smem + kLdsWork + kDownW1Floats, nt0, ksp, b0, b1, next_g, fpre);
   PHASE_TS(s, l, PH, 8);
   publish(a, fl + (grp + NG * half) * kKSplit + ksp, a.epoch, true);  // every wave stored rows
   PHASE_TS(s, l, PH, 9);
