@@ -1875,7 +1875,6 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(qs + afrag_offset(rbq, ds, kHeadDim / 32) + lane * 8);
     attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo, buf0, vring, wave, lane);
     if (kb_lo + 1 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 1, buf1, vring + kVringFloats, wave, lane);
-    if (kb_lo + 2 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 2, buf2, vring + 2 * kVringFloats, wave, lane);
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 oacc[16];
 #pragma unroll
@@ -1883,19 +1882,20 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
       const int slot = (kb - kb_lo) % kAttnRing;
-      // this wave's loads of block kb have landed (up to two later blocks' may still be in flight:
-      // 9 loads each for wave 0, 8 for the others), then every wave's (the barrier)
-      const int after = kb_hi - 1 - kb < kAttnRing - 1 ? kb_hi - 1 - kb : kAttnRing - 1;
-      if (wave == 0) {
-        if (after >= 2) wait_vmcnt<18>();
-        else if (after == 1) wait_vmcnt<9>();
-        else wait_vmcnt<0>();
+      // this wave's loads of block kb have landed (block kb + 1's may still be in flight: 9 loads
+      // for wave 0, 8 for the others), then every wave's (the barrier), which also means every wave
+      // has read block kb - 1's slot: block kb + 2 replaces it
+      if (kb + 1 < kb_hi) {
+        if (wave == 0) wait_vmcnt<9>();
+        else wait_vmcnt<8>();
       } else {
-        if (after >= 2) wait_vmcnt<16>();
-        else if (after == 1) wait_vmcnt<8>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<0>();
       }
       wg_barrier();
+      if (kb + 2 < kb_hi) {
+        const int sn = (kb + 2 - kb_lo) % kAttnRing;
+        attn_stage(ksrc, ssrc, valid, nkb_pre, kb + 2, sn == 0 ? buf0 : sn == 1 ? buf1 : buf2, vring + sn * kVringFloats, wave, lane);
+      }
       u32x4_lds fr[32];
       const uint32_t base = (uint32_t)reinterpret_cast<uintptr_t>(slot == 0 ? buf0 : slot == 1 ? buf1 : buf2) + (uint32_t)lane * 16;
 #pragma unroll
@@ -1903,9 +1903,6 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
       const uint32_t vbase = (uint32_t)reinterpret_cast<uintptr_t>(vring + slot * kVringFloats) + (uint32_t)g * 4;
       uint32_t v0 = lds_read4(vbase), v1 = lds_read4(vbase + 16);
       lds_reads_done(fr, v0, v1);
-      wg_barrier();  // every wave has read slot `slot`: block kb + 3 may replace it
-      if (kb + kAttnRing < kb_hi)
-        attn_stage(ksrc, ssrc, valid, nkb_pre, kb + kAttnRing, slot == 0 ? buf0 : slot == 1 ? buf1 : buf2, vring + slot * kVringFloats, wave, lane);
       KvBlock blk;
 #pragma unroll
       for (int f = 0; f < 16; ++f) {
