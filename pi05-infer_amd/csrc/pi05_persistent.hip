@@ -403,6 +403,9 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 #ifndef PI05_DOWN_MSPLIT
 #define PI05_DOWN_MSPLIT 1
 #endif
+#ifndef PI05_OPROJ_MSPLIT
+#define PI05_OPROJ_MSPLIT 1
+#endif
 // The qkv of kernel instance 2 (phase_qkv_msplit): item i = tile pair i mod 80 for sample half
 // i / 80.
 template <bool G>
@@ -2506,6 +2509,132 @@ __device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, 
 }
 
 // =============================================================================================
+// o_proj of kernel instance 2, split by rows.  KS = 2 (batches above 4): item i = (16-column tile
+// nt = i mod 64, sample pair j = i / 64), wave (p, h) = (wave & 1, wave >> 1) takes sample 2j + p
+// over K half h and finishes m-tiles 2h, 2h + 1.  KS = 4 (batches up to 4, so that every
+// workgroup has an item): item i = (nt, sample j), wave h takes K quarter h and finishes m-tile
+// h.  Items past the grid loop.  A wave's weight fragments are in registers (loaded before the
+// polls); all four m-tiles of its sample's attention output stream two chunks ahead as in
+// phase_gateup_msplit.  The K parts of a sample meet in LDS and are added in K order; the gated
+// residual after attention then runs lane-local on columns 4g .. 4g+3 of one row
+// (modeling_gemma.py:231-249, 503): h = bf16(h + bf16(bf16(y) * gate)), g = bf16(h * (1 + scale))
+// of the pre-MLP norm, and the tile's row sums of squares (the four column groups added across
+// lanes; padded rows: zero).  An item waits only for its samples' merges.  Every workgroup
+// publishes one flag, after its items.
+// =============================================================================================
+template <int KS>
+__device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+  constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / KS, NCH = KSW / kGuCk;
+  constexpr int SPI = 4 / KS, MPW = 4 / KS;  // samples per item, m-tiles finished per wave
+  static_assert(KS == 2 || KS == 4, "K halves or quarters");
+  static_assert(4 * 4 * 64 * 4 <= kWorkFloatsBatched, "row-split o_proj: K-part exchange in the working area");
+  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  PHASE_TS(s, l, kPhO, 0);
+  copy_residual_w<kMlp / 32>(a, l, smem);  // copy wave: down(l) -> B (after attention's use of B)
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int pr = KS == 2 ? (wave & 1) : 0, kh = KS == 2 ? (wave >> 1) : wave;
+  const int n_items = kTiles * ((a.batch + SPI - 1) / SPI);
+  const size_t slw = (size_t)s * L + l;
+  const brsrc rg = make_rsrc(a.o + slw * (size_t)R * (KSTEPS * 32), (size_t)R * KSTEPS * 64);
+  const u16* hres = a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
+  u16* hout = a.hmid + slw * (size_t)R * kWidth;
+  u16* gout = a.gmid + slw * (size_t)R * kWidth;
+  float* rout = a.ssmid + slw * kTiles * R;
+  float* xch = smem + kLdsWork;  // [sample p][from K part h][m-tile][64 lanes][4]
+  auto pick = [](const f32x4 (&v)[4], int mt) { return mt == 0 ? v[0] : mt == 1 ? v[1] : mt == 2 ? v[2] : v[3]; };
+  for (int item = (int)blockIdx.x; item < n_items; item += gridDim.x) {
+    const int nt = item % kTiles, j = item / kTiles;
+    const int col = nt * 16, b = SPI * j + pr;
+    const bool has = b < a.batch;
+    bf16x8 wf[KSW];
+    {
+      const brsrc rw = make_rsrc(a.wpack + (size_t)l * kLayerElems + kOffO + (size_t)nt * KSTEPS * 512, (size_t)KSTEPS * 1024);
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) buf_frag(wf[s2], rw, ((kh * KSW + s2) * 512 + lane * 8) * 2);
+    }
+    // gate (rounded to bf16) and 1 + scale of columns col + 4g .. col + 4g + 3
+    const float4 g4 = *reinterpret_cast<const float4*>(a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + 4 * g);
+    const float4 s14 = *reinterpret_cast<const float4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + 4 * g);
+    const float gate[4] = {round_bf(g4.x), round_bf(g4.y), round_bf(g4.z), round_bf(g4.w)};
+    const float s1[4] = {s14.x, s14.y, s14.z, s14.w};
+    PHASE_TS(s, l, kPhO, 1);
+    // the merges of the item's row blocks: 4 flags per row block, kPairs row blocks per sample
+    const int nb = a.batch - SPI * j < SPI ? a.batch - SPI * j : SPI;
+    if (!wait_flags(a, flag_base(a, s, l, kPhMerge) + 4 * kPairs * SPI * j, 4 * kPairs * nb, s_flag)) return false;
+    PHASE_TS(s, l, kPhO, 2);
+    // residual rows of the m-tiles this wave finishes (rows 16 mt + r16, columns col + 4g ..)
+    uint2 hold[MPW] = {};
+#pragma unroll
+    for (int q = 0; q < MPW; ++q) {
+      const int row = 16 * (MPW * kh + q) + r16;
+      if (has && row < kHorizon)
+        hold[q] = *reinterpret_cast<const uint2*>(hres + afrag_index(b * kRowsPerSample + row, col + 4 * g, kWidth / 32));
+    }
+    bf16x8 A[4][4][kGuCk];
+#pragma unroll
+    for (int c = 0; c < kGuAhead; ++c) gu_load_chunk<KSTEPS>(A[c], rg, b, has, c, lane, kh * KSW);
+    sched_fence();
+    f32x4 acc[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c + kGuAhead < NCH) gu_load_chunk<KSTEPS>(A[(c + kGuAhead) % 4], rg, b, has, c + kGuAhead, lane, kh * KSW);
+      sched_fence();
+#pragma unroll
+      for (int s2 = 0; s2 < kGuCk; ++s2) {
+        const bf16x8 a3 = s2 == 0 ? mtile3_frag<0>(A[c % 4]) : s2 == 1 ? mtile3_frag<1>(A[c % 4]) : s2 == 2 ? mtile3_frag<2>(A[c % 4]) : mtile3_frag<3>(A[c % 4]);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma16x16x32(wf[c * kGuCk + s2], mt < 3 ? A[c % 4][mt][s2] : a3, acc[mt]);
+      }
+    }
+    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhO, 4);
+    // the m-tiles other waves finish -> LDS
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      if (mt / MPW != kh) *reinterpret_cast<f32x4*>(xch + ((((size_t)pr * KS + kh) * 4 + mt) * 64 + lane) * 4) = acc[mt];
+    wg_barrier();
+#pragma unroll
+    for (int q = 0; q < MPW; ++q) {
+      const int mt = MPW * kh + q, row = 16 * mt + r16;
+      const f32x4 own = pick(acc, mt);
+      f32x4 y;
+#pragma unroll
+      for (int h = 0; h < KS; ++h) {
+        const f32x4 v = h == kh ? own : *reinterpret_cast<const f32x4*>(xch + ((((size_t)pr * KS + h) * 4 + mt) * 64 + lane) * 4);
+        y = h == 0 ? v : y + v;
+      }
+      const bool live = has && row < kHorizon;
+      const uint32_t hw[2] = {hold[q].x, hold[q].y};
+      u16 hn[4], gn[4];
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u16 hb = (u16)(hw[i >> 1] >> (16 * (i & 1)));
+        const float prod = round_bf(fmul(round_bf(y[i]), gate[i]));
+        hn[i] = f2bf(fadd(bf2f(hb), prod));
+        const float hf = bf2f(hn[i]);
+        gn[i] = f2bf(fmul(hf, s1[i]));
+        ss += hf * hf;
+      }
+      if (live) {
+        const uint32_t off = (uint32_t)(afrag_index(b * kRowsPerSample + row, col + 4 * g, kWidth / 32) * 2);
+        st_wt8(hout, off, (uint32_t)hn[0] | ((uint32_t)hn[1] << 16), (uint32_t)hn[2] | ((uint32_t)hn[3] << 16));
+        st_wt8(gout, off, (uint32_t)gn[0] | ((uint32_t)gn[1] << 16), (uint32_t)gn[2] | ((uint32_t)gn[3] << 16));
+      }
+      ss = lane_sum_xor32(lane_sum_xor16(live ? ss : 0.f));
+      if (has && g == 0) st_f32(rout + (size_t)nt * R + b * kRowsPerSample + row, ss);
+    }
+    wg_barrier();  // xch is reused by the next item
+  }
+  PHASE_TS(s, l, kPhO, 5);
+  if ((int)blockIdx.x < kOItems) publish(a, flag_base(a, s, l, kPhO) + blockIdx.x, a.epoch, true);  // every wave stored rows
+  PHASE_TS(s, l, kPhO, 6);
+  return true;
+}
+
+// =============================================================================================
 // down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves split the quarter.
 // Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on the same XCD) keeps
 // its own, waits for the other three, adds the four in quarter order and applies the gated
@@ -3052,7 +3181,10 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
             : G             ? phase_qkv_pairs(a, s, l, smem, &s_flag)
                             : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
            phase_attn<G>(a, s, l, smem, &s_flag) &&
-           (G ? phase_oproj_pairs(a, s, l, smem, &s_flag) : phase_oproj(a, s, l, smem, &s_flag)) &&
+           (G && PI05_INSTANCE_GROUPED && PI05_OPROJ_MSPLIT ? (a.batch <= 4 ? phase_oproj_msplit<4>(a, s, l, smem, &s_flag)
+                                                                             : phase_oproj_msplit<2>(a, s, l, smem, &s_flag))
+            : G                                             ? phase_oproj_pairs(a, s, l, smem, &s_flag)
+                                                            : phase_oproj(a, s, l, smem, &s_flag)) &&
            (G ? (gu_msplit<G>(a) ? phase_gateup_msplit(a, s, l, smem, &s_flag) : phase_gateup_pairs4(a, s, l, smem, &s_flag))
               : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
                                                      : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
