@@ -1961,7 +1961,9 @@ __device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) 
   const brsrc rpo = make_rsrc(apart, (size_t)nsplit * nbp * 16 * kHeadDim * 4);
   for (int bp = blockIdx.x; bp < nbp; bp += gridDim.x) {
     const int b = bp / kPairs, pair = bp % kPairs;
+    PHASE_TS(s, l, kPhMerge, 1);
     if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
+    PHASE_TS(s, l, kPhMerge, 2);
     // only the splits there are: masked loads would still take an issue slot each
     float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
 #pragma unroll
@@ -2013,9 +2015,12 @@ __device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) 
       st_bf16x8(os, afrag_index(r, head * kHeadDim + d0 + 8 * h8, kHeads * kHeadDim / 32), v8);
     }
     // the row block's four (row block, head pair) flags, every replica
+    PHASE_TS(s, l, kPhMerge, 4);
     wait_stores();
+    PHASE_TS(s, l, kPhMerge, 5);
     wg_barrier();
     if (tid < kHeadPairs * kFlagCopies) st_u32(fmerge + 4 * bp + tid / kFlagCopies + (size_t)(tid % kFlagCopies) * a.fstride, a.epoch);
+    PHASE_TS(s, l, kPhMerge, 6);
   }
   return true;
 }
