@@ -1304,9 +1304,12 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
 constexpr int kGuCk = 4;                     // k-steps per A chunk
 constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
 #ifndef PI05_GU_AHEAD
-#define PI05_GU_AHEAD 2
+#define PI05_GU_AHEAD 1
 #endif
-constexpr int kGuAhead = PI05_GU_AHEAD;  // chunks in flight ahead of the MFMAs (ring of 4)
+// chunks in flight ahead of the MFMAs (ring of 4).  One: measured on MI355X, a second chunk in
+// flight made every row-split phase slower (the vector-memory instruction stream of the CU, not
+// the latency, is what these phases wait on)
+constexpr int kGuAhead = PI05_GU_AHEAD;
 static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
 // chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
 // (NKS: k-steps of the activation rows; KS0: the first k-step of chunk 0.)  M-tiles 0..2 take one
@@ -1395,7 +1398,7 @@ __device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4]
 // workgroups 16..255); region A holds
 // the pair's two tiles except the second one's last k-step (the 63-copy burst leaves it out),
 // which every wave loads into a register.  Wave j takes sample j of the third (j + 4, ... past 12
-// samples): all four m-tiles over the whole K, A streamed two chunks ahead.  As W.A^T, a lane
+// samples): all four m-tiles over the whole K, A streamed one chunk ahead.  As W.A^T, a lane
 // ends with columns 4g .. 4g+3 of both tiles for one row, so the RoPE rotation (which pairs
 // column d of the first tile with column d of the second) and the 8-byte q / k stores are
 // lane-local; v rows go through a per-wave LDS tile into the permuted V fragment layout.
@@ -2519,7 +2522,7 @@ __device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, 
 // over K half h and finishes m-tiles 2h, 2h + 1.  KS = 4 (batches up to 4, so that every
 // workgroup has an item): item i = (nt, sample j), wave h takes K quarter h and finishes m-tile
 // h.  Items past the grid loop.  A wave's weight fragments are in registers (loaded before the
-// polls); all four m-tiles of its sample's attention output stream two chunks ahead as in
+// polls); all four m-tiles of its sample's attention output stream one chunk ahead as in
 // phase_gateup_msplit.  The K parts of a sample meet in LDS and are added in K order; the gated
 // residual after attention then runs lane-local on columns 4g .. 4g+3 of one row
 // (modeling_gemma.py:231-249, 503): h = bf16(h + bf16(bf16(y) * gate)), g = bf16(h * (1 + scale))
