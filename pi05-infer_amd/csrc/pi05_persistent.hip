@@ -1814,9 +1814,11 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
 // grp of kAttnGroup two-token row blocks, key split c); wave j (the copy wave included) attends row
 // block kAttnGroup * grp + j over the split's whole key range.  Every 32-key K/V block is staged
 // once in LDS for the four waves (direct-to-LDS loads, 8 of its 32 fragments per wave, and its 32
-// key-valid bytes by wave 0) in a ring of three buffers -- the upper half of region A (free during
-// attention), the working area and region B (down_proj's weights are copied there at gate_up
-// instead) -- two blocks ahead of the one being attended.  An item thus reads each block from L2
+// key-valid bytes by wave 0) in a ring of kAttnRing buffers -- the upper half of region A (free
+// during attention), the working area and, for a third, region B (down_proj's weights are copied
+// there at o_proj) -- kAttnAhead blocks ahead of the one being attended: one, measured on MI355X
+// (a second block in flight made batches of 8 0.5 % and of 4, 5 1.1 % slower: the fewer vector-memory
+// instructions in flight, the sooner the ones waited for complete).  An item thus reads each block from L2
 // once for 64 query rows instead of once per 16 (at B = 8 the splits' K/V delivery drops from 200
 // MiB to 56 MiB per layer).  Everything the block loop waits for is staged through LDS and read
 // with inline ds_reads: a global load waited for there would, loads completing in order, also wait
@@ -1824,7 +1826,12 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
 // does after its wave merge, so the merges are unchanged.  With 256 workgroups, item n runs on
 // workgroup n: sample n mod B on XCD n mod 8 (at B = 8 all of a sample's items share the XCD whose
 // L2 holds that sample's K/V).
-constexpr int kAttnRing = 3;
+#ifndef PI05_ATTN_AHEAD
+#define PI05_ATTN_AHEAD 1
+#endif
+constexpr int kAttnAhead = PI05_ATTN_AHEAD;  // blocks staged ahead of the one being attended
+constexpr int kAttnRing = kAttnAhead + 1;
+static_assert(kAttnAhead == 1 || kAttnAhead == 2, "ring of two or three buffers");
 // This wave's share of one K/V block's staging (see attn_group_items): fragments 8 (wave & 1) .. +7
 // of the block's K (waves 0, 1) or V (waves 2, 3) -> dst + wave * 8 KiB, and for wave 0 the
 // block's 32 key-valid bytes -> vdst.
@@ -1880,7 +1887,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) qf[ds] = load_frag(qs + afrag_offset(rbq, ds, kHeadDim / 32) + lane * 8);
     attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo, buf0, vring, wave, lane);
-    if (kb_lo + 1 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 1, buf1, vring + kVringFloats, wave, lane);
+    if (kAttnAhead == 2 && kb_lo + 1 < kb_hi) attn_stage(ksrc, ssrc, valid, nkb_pre, kb_lo + 1, buf1, vring + kVringFloats, wave, lane);
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 oacc[16];
 #pragma unroll
@@ -1888,19 +1895,19 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
       const int slot = (kb - kb_lo) % kAttnRing;
-      // this wave's loads of block kb have landed (block kb + 1's may still be in flight: 9 loads
-      // for wave 0, 8 for the others), then every wave's (the barrier), which also means every wave
-      // has read block kb - 1's slot: block kb + 2 replaces it
-      if (kb + 1 < kb_hi) {
+      // this wave's loads of block kb have landed (with two blocks ahead, block kb + 1's may still
+      // be in flight: 9 loads for wave 0, 8 for the others), then every wave's (the barrier), which
+      // also means every wave has read block kb - 1's slot: block kb + kAttnAhead replaces it
+      if (kAttnAhead == 2 && kb + 1 < kb_hi) {
         if (wave == 0) wait_vmcnt<9>();
         else wait_vmcnt<8>();
       } else {
         wait_vmcnt<0>();
       }
       wg_barrier();
-      if (kb + 2 < kb_hi) {
-        const int sn = (kb + 2 - kb_lo) % kAttnRing;
-        attn_stage(ksrc, ssrc, valid, nkb_pre, kb + 2, sn == 0 ? buf0 : sn == 1 ? buf1 : buf2, vring + sn * kVringFloats, wave, lane);
+      if (kb + kAttnAhead < kb_hi) {
+        const int sn = (kb + kAttnAhead - kb_lo) % kAttnRing;
+        attn_stage(ksrc, ssrc, valid, nkb_pre, kb + kAttnAhead, sn == 0 ? buf0 : sn == 1 ? buf1 : buf2, vring + sn * kVringFloats, wave, lane);
       }
       u32x4_lds fr[32];
       const uint32_t base = (uint32_t)reinterpret_cast<uintptr_t>(slot == 0 ? buf0 : slot == 1 ? buf1 : buf2) + (uint32_t)lane * 16;
@@ -3171,7 +3178,7 @@ static_assert(kDownW1Floats + 256 <= kWorkFloatsBatched, "row-split down_proj: s
 // number (0, 1, 2), instance 2 (batches of kRowSplitMinBatch and more) alone containing the
 // row-split qkv / gate_up / down_proj phases and the grouped attention.  Each is compiled in a
 // translation unit of its own: inlined into one module, the batched code changed the one-sample
-// kernel's register allocation (measured +2-3.5 % per C1 predict), and the batch paths each
+// kernel's register allocation (measured +2-3.5 % per one-sample predict), and the batch paths each
 // other's (+1-1.5 %).
 template <bool G, int I>
 __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
