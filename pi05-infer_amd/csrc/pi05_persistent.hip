@@ -2563,11 +2563,14 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
     const int col = nt * 16, b = SPI * j + pr;
     const bool has = b < a.batch;
     bf16x8 wf[KSW];
-    {
+    auto load_w = [&]() {
       const brsrc rw = make_rsrc(a.wpack + (size_t)l * kLayerElems + kOffO + (size_t)nt * KSTEPS * 512, (size_t)KSTEPS * 1024);
 #pragma unroll
       for (int s2 = 0; s2 < KSW; ++s2) buf_frag(wf[s2], rw, ((kh * KSW + s2) * 512 + lane * 8) * 2);
-    }
+    };
+    // the weight fragments: before the polls, except wave 0's (it polls; its polls would queue
+    // behind the workgroup's 128 KiB of weight loads)
+    if (wave != 0) load_w();
     // gate (rounded to bf16) and 1 + scale of columns col + 4g .. col + 4g + 3
     const float4 g4 = *reinterpret_cast<const float4*>(a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + 4 * g);
     const float4 s14 = *reinterpret_cast<const float4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + 4 * g);
@@ -2578,6 +2581,7 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
     const int nb = a.batch - SPI * j < SPI ? a.batch - SPI * j : SPI;
     if (!wait_flags(a, flag_base(a, s, l, kPhMerge) + 4 * kPairs * SPI * j, 4 * kPairs * nb, s_flag)) return false;
     PHASE_TS(s, l, kPhO, 2);
+    if (wave == 0) load_w();
     // residual rows of the m-tiles this wave finishes (rows 16 mt + r16, columns col + 4g ..)
     uint2 hold[MPW] = {};
 #pragma unroll
