@@ -1311,6 +1311,14 @@ constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
 // the latency, is what these phases wait on)
 constexpr int kGuAhead = PI05_GU_AHEAD;
 static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
+// Grouped attention (attn_group_items): 32-key K/V blocks staged this many ahead of the one
+// being attended, in a ring of kAttnRing LDS buffers.
+#ifndef PI05_ATTN_AHEAD
+#define PI05_ATTN_AHEAD 1
+#endif
+constexpr int kAttnAhead = PI05_ATTN_AHEAD;  // blocks staged ahead of the one being attended
+constexpr int kAttnRing = kAttnAhead + 1;
+static_assert(kAttnAhead == 1 || kAttnAhead == 2, "ring of two or three buffers");
 // chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
 // (NKS: k-steps of the activation rows; KS0: the first k-step of chunk 0.)  M-tiles 0..2 take one
 // load per k-step; m-tile 3 holds 2 rows (48, 49), so one load brings the whole chunk's: lane
@@ -1409,10 +1417,11 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
   const int item = qkv_item_of<true>();
   PHASE_TS(s, l, kPhQkv, 0);
   // copy wave: this phase's weights (region A) and everything issued before them have landed;
-  // down(l) -> B here unless grouped attention stages K/V there (then before o_proj)
+  // down(l) -> B here unless grouped attention stages K/V there (a ring of three; then before
+  // o_proj)
   if (copy_wave()) {
     wait_vmcnt<0>();
-    if (!attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
+    if (kAttnRing < 3 || !attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
   }
   if (item < 0 || item >= kQkvItemsRS) return true;
   const int p = item % kQkvPairs, sg = item / kQkvPairs;
@@ -1826,12 +1835,6 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
 // does after its wave merge, so the merges are unchanged.  With 256 workgroups, item n runs on
 // workgroup n: sample n mod B on XCD n mod 8 (at B = 8 all of a sample's items share the XCD whose
 // L2 holds that sample's K/V).
-#ifndef PI05_ATTN_AHEAD
-#define PI05_ATTN_AHEAD 1
-#endif
-constexpr int kAttnAhead = PI05_ATTN_AHEAD;  // blocks staged ahead of the one being attended
-constexpr int kAttnRing = kAttnAhead + 1;
-static_assert(kAttnAhead == 1 || kAttnAhead == 2, "ring of two or three buffers");
 // This wave's share of one K/V block's staging (see attn_group_items): fragments 8 (wave & 1) .. +7
 // of the block's K (waves 0, 1) or V (waves 2, 3) -> dst + wave * 8 KiB, and for wave 0 the
 // block's 32 key-valid bytes -> vdst.
@@ -2545,7 +2548,8 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
   static_assert(4 * 4 * 64 * 4 <= kWorkFloatsBatched, "row-split o_proj: K-part exchange in the working area");
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   PHASE_TS(s, l, kPhO, 0);
-  copy_residual_w<kMlp / 32>(a, l, smem);  // copy wave: down(l) -> B (after attention's use of B)
+  // copy wave: down(l) -> B, when grouped attention's K/V ring used B (else copied at qkv)
+  if (kAttnRing >= 3 && attn_grouped<true>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
   const int pr = KS == 2 ? (wave & 1) : 0, kh = KS == 2 ? (wave >> 1) : wave;
