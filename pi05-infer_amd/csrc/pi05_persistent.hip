@@ -1824,8 +1824,8 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
 // block kAttnGroup * grp + j over the split's whole key range.  Every 32-key K/V block is staged
 // once in LDS for the four waves (direct-to-LDS loads, 8 of its 32 fragments per wave, and its 32
 // key-valid bytes by wave 0) in a ring of kAttnRing buffers -- the upper half of region A (free
-// during attention), the working area and, for a third, region B (down_proj's weights are copied
-// there at o_proj) -- kAttnAhead blocks ahead of the one being attended: one, measured on MI355X
+// during attention), the working area and, for a third, region B (down_proj's weights are then
+// copied there at o_proj, else at qkv) -- kAttnAhead blocks ahead of the one being attended: one, measured on MI355X
 // (a second block in flight made batches of 8 0.5 % and of 4, 5 1.1 % slower: the fewer vector-memory
 // instructions in flight, the sooner the ones waited for complete).  An item thus reads each block from L2
 // once for 64 query rows instead of once per 16 (at B = 8 the splits' K/V delivery drops from 200
