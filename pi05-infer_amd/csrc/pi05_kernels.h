@@ -90,7 +90,7 @@ constexpr int kMaxAttnSplits = 16;
 // Persistent attention at batches of at least kAttnGroupMinBatch: items of kAttnGroup two-token
 // row blocks of one sample, one per wave, sharing each K/V block through LDS; the key splits
 // then fill the 256 workgroups once (attn_group_splits).
-constexpr int kAttnGroupMinBatch = 4;
+constexpr int kAttnGroupMinBatch = 3;
 // Batches from which the persistent kernel's gate_up items split rows over waves instead of K
 // (each wave one sample over the whole K; kernel instance 2).
 constexpr int kRowSplitMinBatch = 3;

@@ -156,8 +156,8 @@ def test_batch16_multi_pass_items(full_weights):
 
 
 def test_ragged_prefix_padding(full_weights):
-    """B=3: the attention split items (not grouped) with the row-split gate_up (three waves one
-    sample each, the fourth idle)."""
+    """B=3: the grouped attention items (12 key splits at this prefix) with the row-split gate_up
+    (three waves one sample each, the fourth idle) and o_proj (one sample per item)."""
     print("case ragged: depth 4, B=3, P=300, padded tails", flush=True)
 
     def pad_fn(pad):
