@@ -461,6 +461,71 @@ def cpu_model() -> str:
     return platform.processor()
 
 
+class GpuState:
+    """Graphics / memory clock (MHz), socket power (W) and temperatures (C) of the benchmark's GPU
+    from amdsmi, sampled while the timed region runs, as the reference's bench records SM clock,
+    memory clock, power and temperature with every run (bench/standalone_infer_bench.py:281-316).
+    amdsmi enumerates every GPU of the host whatever HIP_VISIBLE_DEVICES says, so the handle is
+    resolved by the device's PCI address; on a multi-GPU host where that fails nothing is reported
+    rather than another card's state."""
+
+    def __init__(self, device_index: int):
+        self.samples: list[dict] = []
+        self.error = None
+        self.handle = None
+        try:
+            import amdsmi
+            import torch
+
+            self.smi = amdsmi
+            amdsmi.amdsmi_init()
+            props = torch.cuda.get_device_properties(device_index)
+            bdf = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}"
+            handles = amdsmi.amdsmi_get_processor_handles()
+            for h in handles:
+                if str(amdsmi.amdsmi_get_gpu_device_bdf(h)).lower().startswith(bdf):
+                    self.handle = h
+                    break
+            if self.handle is None and len(handles) == 1:
+                self.handle = handles[0]
+            if self.handle is None:
+                self.error = f"no amdsmi GPU at PCI address {bdf} among {len(handles)}"
+        except Exception as exc:  # diagnostics only
+            self.error = repr(exc)
+
+    def sample(self) -> None:
+        if self.handle is None:
+            return
+        try:
+            m = self.smi.amdsmi_get_gpu_metrics_info(self.handle)
+            pw = m.get("current_socket_power", "N/A")
+            if not isinstance(pw, (int, float)):
+                pw = m.get("average_socket_power", "N/A")
+            self.samples.append({"gfx_clk_mhz": m.get("current_gfxclk", "N/A"), "mem_clk_mhz": m.get("current_uclk", "N/A"),
+                                 "power_w": pw, "hotspot_c": m.get("temperature_hotspot", "N/A"),
+                                 "mem_temp_c": m.get("temperature_mem", "N/A")})
+        except Exception as exc:
+            self.error = repr(exc)
+            self.handle = None
+
+    def summary(self) -> dict:
+        out = {"source": "amdsmi gpu_metrics, sampled during the timed region", "samples": len(self.samples)}
+        if self.error:
+            out["error"] = self.error
+        for key in ("gfx_clk_mhz", "mem_clk_mhz", "power_w", "hotspot_c", "mem_temp_c"):
+            vals = [x[key] for x in self.samples if isinstance(x[key], (int, float)) and x[key] < 0xFFFF]
+            if vals:
+                out[key] = {"median": statistics.median(vals), "min": min(vals), "max": max(vals)}
+        return out
+
+
+def run_sampling(gpu: GpuState, done) -> None:
+    """Sample the GPU state every ~5 ms until done() (the last event of the timed region) holds."""
+    while not done():
+        gpu.sample()
+        time.sleep(0.005)
+
+
 def read_traffic(name: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/)."""
     path = os.path.join(ROOT, "profiles", name)
@@ -527,11 +592,14 @@ def main() -> int:
     # timed region: K predicts back to back on `stream`, the stream every launch goes to, with an
     # event between consecutive predicts (K + 1 events: per-predict times and their distribution)
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    gpu = GpuState(torch.cuda.current_device())
     torch.cuda.synchronize()
     evs[0].record(stream)
     for i in range(args.steps):
         ctx.denoise(xs[args.warmup + i], stream=stream)
         evs[i + 1].record(stream)
+    # the launches are queued: sample clocks, power and temperatures until the last one ends
+    run_sampling(gpu, evs[-1].query)
     torch.cuda.synchronize()
     ctx.status()  # no launch of the timed region timed out
     ms_per_predict = evs[0].elapsed_time(evs[-1]) / args.steps
@@ -605,6 +673,7 @@ def main() -> int:
         },
         "roofline": roofline_entry(schedule, mfma_bound, pred_gbs, pred_bytes, pred_tflops, pred_flops, launch_us, traffic),
         "cpu_baseline": cpu,
+        "gpu_state": gpu.summary(),
     }
     print(json.dumps(out), flush=True)
     # release the context (device memory, pinned error word) before interpreter teardown

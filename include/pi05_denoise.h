@@ -156,11 +156,17 @@ int pi05_get_step_invariants(pi05_ctx* ctx, int64_t* positions_out, uint8_t* key
  * persistent kernel is bounded: a launch whose wait gives up leaves its outputs invalid and is
  * reported asynchronously, as PI05_E_HIP from the next pi05_denoise on this context (which then
  * enqueues nothing) or from pi05_denoise_status.
+ * Graph capture: in the persistent schedule the call may be captured into a hipGraph (e.g. inside
+ * torch.cuda.graph) and the graph replayed any number of times -- the launch carries no
+ * per-call state; the kernel takes its flag epoch from the context's device memory and advances
+ * it itself.  A timed-out replay is reported by the next pi05_denoise or pi05_denoise_status on
+ * the context.  In the graph schedule (itself a hipGraph) a call on a capturing stream returns
+ * PI05_E_STATE.  Replays and calls of one context must not overlap (one stream).
  * Replaces sample_actions' denoise loop (engine.py:389-405) with sample_mean_var_val /
  * get_velocity / the expert forward (engine.py:629-768, modeling_gemma.py:662-794). */
 int pi05_denoise(pi05_ctx* ctx, float* x_inout, float* v_trace, void* stream);
 
-/* Wait for `stream` and report a timed-out persistent launch of this context that has not been
+/* Wait for `stream` and report the timed-out persistent launches of this context that have not been
  * reported yet (PI05_E_HIP), once.  The reference surfaces device-side failures at the next
  * synchronising call in the same way (CUDA/torch asynchronous error semantics); this is that
  * synchronising call for callers that want it per predict. */
@@ -170,6 +176,13 @@ int pi05_denoise_status(pi05_ctx* ctx, void* stream);
  * 2^20).  A small value makes waits give up on purpose, so the timeout path can be exercised;
  * every workgroup still leaves the kernel normally.  No counterpart in the reference. */
 int pi05_debug_set_spin_limit(pi05_ctx* ctx, int polls);
+
+/* Test hook: set the epoch of the last finished persistent launch (the next launch runs as
+ * epoch + 1; the launch that reaches 2^31 zeroes the flags and the next one runs as epoch 1), so
+ * that the wrap-around can be exercised without 2^31 launches.  Synchronises the device;
+ * persistent schedule only (PI05_E_STATE otherwise).  epoch must be below 2^31.  No counterpart
+ * in the reference. */
+int pi05_debug_set_epoch(pi05_ctx* ctx, uint32_t epoch);
 
 /* Drop the captured graph (it is recaptured on the next pi05_denoise).  Mirrors
  * release_cuda_graph (_vendored/base_policy.py:96-102). */
@@ -215,8 +228,8 @@ int pi05_bench_kernel(pi05_ctx* ctx, int kernel_id, int layer, int iters, void* 
  * tout_b [W] and the 2*depth+1 norm dense layers (host arrays dense_w / dense_b of device
  * pointers to [3W, W] / [3W], in the table's norm order: input_layernorm and
  * post_attention_layernorm of each layer, then the final norm) -- into table_out
- * [num_steps][2*depth+1][3W] fp32 (device).  Replaces nothing: it is the table-building part of
- * pi05_refresh_weights (engine.py:578-599) as a stand-alone call.
+ * [num_steps][2*depth+1][3W] fp32 (device).  It replaces no reference interface: it is the
+ * table-building part of pi05_refresh_weights as a stand-alone call.
  * It allocates nothing: its scratch (time embedding + two time-MLP activations, 384 KiB) is a
  * static device array of the library, one per GPU, kept until the process ends; num_steps above
  * 32 is rejected with PI05_E_INVALID.  Every call on one GPU shares that GPU's scratch (each call

@@ -333,9 +333,8 @@ struct pi05_ctx {
   // persistent schedule
   char* pbase = nullptr;  // one allocation, carved by carve_persistent()
   MegaArgs mega{};
-  unsigned epoch = 0;
-  unsigned* host_err = nullptr;  // pinned host word: epoch of the last launch whose wait timed out
-  unsigned reported = 0;         // the last such epoch already reported to the caller
+  unsigned* host_err = nullptr;  // pinned host word: count of launches whose waits timed out
+  unsigned reported = 0;         // the count already reported to the caller
   int spin_limit = kDefaultSpinLimit;
 
   bool weights_ready = false;
@@ -384,7 +383,6 @@ void free_schedule(pi05_ctx* c) {
       *p = nullptr;
     }
   c->mega = MegaArgs{};
-  c->epoch = 0;
   c->primed = false;
 }
 
@@ -429,6 +427,7 @@ void carve_persistent(pi05_ctx* c) {
   a = MegaArgs{};
   a.err = reinterpret_cast<unsigned*>(take(256));
   a.flags = reinterpret_cast<unsigned*>(take(p.p_flags));
+  a.flag_bytes = p.p_flags;
   a.fstride = p.fstride;
   a.depth = d.depth;
   a.steps = d.num_steps;
@@ -492,7 +491,8 @@ hipError_t alloc_schedule(pi05_ctx* c) {
     ALLOC(x, p.x);
     ALLOC(trace, p.trace);
   } else {
-    // zero-filled: flags must start at 0 (epoch 0 never matches a launch)
+    // zero-filled: flags must start at 0 (epoch 0 never matches a launch), and the launch-control
+    // words (last finished epoch, exit count, error word) too
     ALLOC(pbase, p.persistent_bytes() + 64 * 256);
     if (ae == hipSuccess) carve_persistent(c);
     if (ae == hipSuccess) {
@@ -512,16 +512,6 @@ hipError_t alloc_schedule(pi05_ctx* c) {
   }
 #undef ALLOC
   return ae;
-}
-
-// After a launch whose waits timed out: bring the flags and the error word back to zero.
-hipError_t reset_persistent(pi05_ctx* c, hipStream_t st) {
-  const Plan& p = c->plan;
-  hipError_t e = hipMemsetAsync(c->mega.flags, 0, p.p_flags, st);
-  if (e == hipSuccess) e = hipMemsetAsync(c->mega.err, 0, 256, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  c->epoch = 0;
-  return e;
 }
 
 // Kernel ids of one denoise step (pi05_bench_kernel).
@@ -1069,31 +1059,31 @@ int pi05_get_step_invariants(pi05_ctx* c, int64_t* positions_out, uint8_t* key_v
 
 namespace {
 
-// A timeout recorded by a launch of this context that has not been reported yet: the pinned host
-// word holds the epoch of the last launch whose wait timed out (read without waiting: a launch
-// still running is seen by a later call or by pi05_denoise_status).
+// Timeouts recorded by launches of this context that have not been reported yet: the pinned host
+// word counts the launches whose waits timed out (read without waiting: a launch still running is
+// seen by a later call or by pi05_denoise_status).
 int take_pending_error(pi05_ctx* c) {
   if (!c->host_err) return PI05_OK;
-  const unsigned e = __atomic_load_n(c->host_err, __ATOMIC_ACQUIRE);
-  if (e == 0 || e == c->reported) return PI05_OK;
-  c->reported = e;
-  return c->fail(PI05_E_HIP, "denoise launch %u on this context timed out waiting for its inputs; its actions are invalid "
-                 "(nothing was enqueued by the call reporting it)", e);
+  const unsigned n = __atomic_load_n(c->host_err, __ATOMIC_ACQUIRE);
+  if (n == c->reported) return PI05_OK;
+  const unsigned fresh = n - c->reported;
+  c->reported = n;
+  return c->fail(PI05_E_HIP, "%u denoise launch%s on this context timed out waiting for inputs; %s actions are invalid "
+                 "(nothing was enqueued by the call reporting it)", fresh, fresh == 1 ? "" : "es", fresh == 1 ? "its" : "their");
 }
 
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// One cooperative launch of the whole loop.  Nothing launch-specific is baked into the arguments:
+// the kernel takes its epoch from the context's launch-control block and advances it itself, so
+// the launch may be captured into a graph and replayed any number of times.
 int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t st) {
   const int pending = take_pending_error(c);
   if (pending != PI05_OK) return pending;
-  if (c->epoch >= (1u << 31)) {
-    // the epoch never wraps to 0 (the value of untouched flags): restart from zeroed flags
-    HIPCHK(c, reset_persistent(c, st));
-    const int late = take_pending_error(c);
-    *c->host_err = 0;
-    c->reported = 0;
-    if (late != PI05_OK) return late;
-  }
   MegaArgs a = c->mega;
-  a.epoch = ++c->epoch;
   a.spin_limit = c->spin_limit;
   a.x_io = x_inout;
   a.trace = v_trace;
@@ -1117,6 +1107,9 @@ int pi05_denoise(pi05_ctx* c, float* x_inout, float* v_trace, void* stream) {
   if (!c->primed) return c->fail(PI05_E_STATE, "prefix not primed (call pi05_prime_prefix)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (c->schedule == PI05_SCHEDULE_PERSISTENT) return denoise_persistent(c, x_inout, v_trace, st);
+  if (stream_capturing(st))
+    return c->fail(PI05_E_STATE, "the graph schedule runs its loop as a hipGraph of its own and cannot be captured; "
+                   "capture the persistent schedule (the default)");
   const bool with_trace = v_trace != nullptr;
   int rc = ensure_graph(c, with_trace);
   if (rc != PI05_OK) return rc;
@@ -1143,6 +1136,18 @@ int pi05_debug_set_spin_limit(pi05_ctx* c, int polls) {
   }
   if (polls < 0) return c->fail(PI05_E_INVALID, "polls %d < 0", polls);
   c->spin_limit = polls == 0 ? kDefaultSpinLimit : polls;
+  return PI05_OK;
+}
+
+int pi05_debug_set_epoch(pi05_ctx* c, uint32_t epoch) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (epoch >= kEpochWrap) return c->fail(PI05_E_INVALID, "epoch %u must be below 2^31", epoch);
+  if (c->schedule != PI05_SCHEDULE_PERSISTENT) return c->fail(PI05_E_STATE, "the epoch belongs to the persistent schedule");
+  HIPCHK(c, hipDeviceSynchronize());
+  HIPCHK(c, hipMemcpy(c->mega.err + kCtlEpoch, &epoch, sizeof epoch, hipMemcpyHostToDevice));
   return PI05_OK;
 }
 

@@ -133,9 +133,17 @@ constexpr int kFlagCopies = 32;
 // per (step, layer) in `bias`.
 constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gate, then 4096 up
 
+// Launch-control words of a context (one zero-filled 256-byte block, each word on its own 64-byte
+// line): the error word, the epoch of the last launch that finished, and the count of workgroups
+// that have left the running launch.
+constexpr int kCtlErr = 0;
+constexpr int kCtlEpoch = 16;
+constexpr int kCtlExit = 32;
+constexpr unsigned kEpochWrap = 1u << 31;  // a launch with this epoch zeroes the flags; the next runs as epoch 1
+
 struct MegaArgs {
-  unsigned epoch;      // this launch's flag value (1, 2, ...); flags start at 0
-  unsigned* err;       // set to the launch's epoch by a workgroup whose wait timed out
+  unsigned epoch;      // this launch's flag value (1, 2, ...), read from ctl[kCtlEpoch] at kernel entry
+  unsigned* err;       // the launch-control block; err[kCtlErr] = the epoch of a launch whose wait timed out
   int spin_limit;      // polls before a wait gives up (each poll >= ~1 us)
   unsigned* flags;     // per-item completion flags [(steps+1)][depth+1][7 phases][kFlagCopies][fstride]
   int fstride;         // flag words per phase instance and copy (multiple of 256)
@@ -172,7 +180,8 @@ struct MegaArgs {
   float* x;               // [steps][B*50, a] actions after step s (slot 0 unused)
   float* x_io;            // [B*50, a] caller's buffer: noise on entry, actions on exit
   float* trace;           // [steps][B*50, a] caller's velocity buffer (nullable)
-  unsigned* host_err;     // pinned host word, set to the epoch with err (device-visible mapping)
+  unsigned* host_err;     // pinned host word: count of launches whose waits timed out (device-visible mapping)
+  size_t flag_bytes;      // size of `flags` (zeroed by the launch that reaches kEpochWrap)
 };
 
 // bias[s][l][j] = sum_k shift_{s, norm(j)}[k] * W_l[j][k] from the packed weights, for the fused

@@ -69,6 +69,31 @@ __device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 16];
   } while (0)
 #endif
 
+// ---- scalar register pressure ------------------------------------------------------------------
+// The kernel's phases run inside the Euler-step and layer loops, and the compiler hoists out of
+// those loops everything a phase derives from loop-invariant values -- the kernel arguments, the
+// workgroup index -- where it then stays live across every phase and is spilled (the phases
+// together need far more scalar registers than the 102 a wave has).  So every phase reads them
+// afresh: the workgroup index and grid size through an opaque copy, the kernel arguments through
+// a pointer into the kernel-argument segment that the compiler cannot see through (kargs(); the
+// fields are scalar loads, cached).
+__device__ __forceinline__ int wg_id() {
+  int w = (int)blockIdx.x;
+  asm volatile("" : "+v"(w));
+  return __builtin_amdgcn_readfirstlane(w);
+}
+__device__ __forceinline__ int wg_count() {
+  int n = (int)gridDim.x;
+  asm volatile("" : "+v"(n));
+  return __builtin_amdgcn_readfirstlane(n);
+}
+typedef const __attribute__((address_space(4))) MegaArgs KArgs;
+__device__ __forceinline__ KArgs& kargs() {
+  KArgs* p = (KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *p;
+}
+
 constexpr int kCompWaves = 3;
 constexpr int kCompThreads = kCompWaves * 64;
 constexpr int kThreads = kCompThreads + 64;  // + the copy wave
@@ -192,6 +217,15 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[MT][NT], bf16x8 (&af)[MT
   }
 }
 
+// What every phase's waits and publishes need: this launch's epoch (read from the context's
+// launch-control block at kernel entry, by every workgroup, before any flag of this launch can be
+// published; kept in a scalar register) and the workgroup's LDS word through which wave 0 tells
+// the others how a wait ended.
+struct Sync {
+  unsigned epoch;
+  int* flag;
+};
+
 // ---- phases, items and flags ------------------------------------------------------------------
 enum { kPhIo = 0, kPhQkv = 1, kPhSplit = 2, kPhMerge = 3, kPhO = 4, kPhGu = 5, kPhDown = 6, kNumPh = 7 };
 constexpr int kQkvPairs = 80;        // 72 RoPE pairs of q/k tiles + 8 pairs of v tiles
@@ -199,7 +233,7 @@ constexpr int kQkvItems = 2 * kQkvPairs;  // each pair in two items: rows 0..31 
 // qkv item i runs on workgroup kQkvWg0 + i: not on workgroups 0..63, which finish the previous
 // layer's down_proj tiles (the two items of a pair share an XCD: 80 is a multiple of 8)
 constexpr int kQkvWg0 = 64;
-__device__ __forceinline__ int qkv_item() { return (int)blockIdx.x - kQkvWg0; }
+__device__ __forceinline__ int qkv_item() { return wg_id() - kQkvWg0; }
 constexpr int kTiles = kWidth / 16;  // 64 output tiles of o_proj / down_proj
 constexpr int kGuItems = kMlp / 16;  // 256 (gate tile j, up tile j)
 constexpr int kKSplit = 4;           // K quarters of down_proj
@@ -214,43 +248,62 @@ constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sa
 // tile for its finisher (quarter 0)
 constexpr int kPartFlags = 256;
 constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-tile of a sample, tile)
-#ifndef PI05_GU_PAIRS
-#define PI05_GU_PAIRS 1
-#endif
-#ifndef PI05_DOWN_PAIRS
-#define PI05_DOWN_PAIRS 1
-#endif
-#ifndef PI05_ATTN_GROUP
-#define PI05_ATTN_GROUP 1
-#endif
 // Batches of kAttnGroupMinBatch and more (in kernel instance 2): grouped attention items
 // (attn_group_items), which stage K/V blocks in region B as well, so down(l)'s weights are copied
 // to B before o_proj(l) instead of at qkv(l).  G: a batched instance.
 template <bool G>
-__device__ __forceinline__ bool attn_grouped(const MegaArgs& a) {
-  return G && PI05_INSTANCE_GROUPED && PI05_ATTN_GROUP && PI05_GU_PAIRS && PI05_DOWN_PAIRS && a.batch >= kAttnGroupMinBatch;
+__device__ __forceinline__ bool attn_grouped(KArgs& a) {
+  return G && PI05_INSTANCE_GROUPED && a.batch >= kAttnGroupMinBatch;
 }
-__device__ __forceinline__ unsigned* flag_base(const MegaArgs& a, int s, int l, int ph) {
+__device__ __forceinline__ unsigned* flag_base(KArgs& a, int s, int l, int ph) {
   return a.flags + ((size_t)(s * (a.depth + 1) + l) * kNumPh + ph) * kFlagCopies * a.fstride;
 }
 
-// A timed-out wait: the launch's epoch goes to the device error word (which every waiting
-// workgroup of this launch checks, so all of them leave) and to the pinned host word (which the
-// host reads after the launch).  Words of earlier launches hold older epochs, so nothing needs
-// clearing between launches.
-__device__ void record_error(const MegaArgs& a) {
-  st_u32(a.err, a.epoch);
-  __hip_atomic_store(a.host_err, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+// A timed-out wait: the launch's epoch goes to the device error word, which every waiting
+// workgroup of this launch checks, so all of them leave (leave_launch then counts the launch in
+// the host's word).  Words of earlier launches hold older epochs, so nothing needs clearing
+// between launches.
+__device__ void record_error(KArgs& a, unsigned epoch) { st_u32(a.err + kCtlErr, epoch); }
+
+// Every workgroup counts itself out of the launch.  The last one out -- every other workgroup has
+// read this launch's epoch by then, at its entry -- makes this epoch the last finished one and
+// resets the count, so the next launch on the stream (another call, or a replay of a captured
+// graph of this one) runs with a fresh epoch; the host passes none.  A launch whose waits timed out
+// is counted in the pinned host word (one writer: the last workgroup out of a launch).  The launch
+// that reaches kEpochWrap zeroes the flags and the error word first and restarts the epochs at 1.
+__device__ void leave_launch(KArgs& a, Sync sy) {
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *sy.flag = __hip_atomic_fetch_add(a.err + kCtlExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)wg_count() - 1;
+  __syncthreads();
+  if (!*sy.flag) return;
+  unsigned last = sy.epoch;
+  if (threadIdx.x == 0 && ld_u32(a.err + kCtlErr) == sy.epoch) {
+    const unsigned n = __hip_atomic_load(a.host_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.host_err, n + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (sy.epoch >= kEpochWrap) {
+    uint4* f = reinterpret_cast<uint4*>(a.flags);
+    for (size_t i = threadIdx.x; i < a.flag_bytes / 16; i += blockDim.x) f[i] = uint4{0, 0, 0, 0};
+    if (threadIdx.x == 0) st_u32(a.err + kCtlErr, 0);
+    wait_stores();
+    __syncthreads();
+    last = 0;
+  }
+  if (threadIdx.x == 0) {
+    st_u32(a.err + kCtlExit, 0);
+    st_u32(a.err + kCtlEpoch, last);
+  }
 }
 
 // Wave 0 polls until flags f[0..n) all hold this launch's epoch (f 16-byte aligned; the 16-byte
 // loads may read up to 3 words past n, which the allocation covers).  Ends with a workgroup
 // barrier; returns false (uniformly) after a timeout or another workgroup's error.
-__device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_flag) {
-  f += (size_t)(blockIdx.x % kFlagCopies) * a.fstride;
+__device__ bool wait_flags(KArgs& a, const unsigned* f, int n, Sync sy) {
+  f += (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    const unsigned ep = a.epoch;
+    const unsigned ep = sy.epoch;
     int ok = 1;
     // one coherent (sc1) 16-byte poll in flight at a time: measured on MI355X, keeping a second
     // poll in flight (staggered by half a round trip) makes the whole predict ~4% slower -- poll
@@ -266,18 +319,18 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
       for (int spins = 0;; ++spins) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
         if (__all(done(v))) break;
-        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
-          if (lane == 0) record_error(a);
+        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err + kCtlErr)) == sy.epoch)) {
+          if (lane == 0) record_error(a, sy.epoch);
           ok = 0;
           break;
         }
         asm volatile("" ::: "memory");
       }
     }
-    if (lane == 0) *s_flag = ok;
+    if (lane == 0) *sy.flag = ok;
   }
   wg_barrier();
-  const bool ok = *s_flag != 0;
+  const bool ok = *sy.flag != 0;
   wg_barrier();
   return ok;
 }
@@ -285,11 +338,11 @@ __device__ bool wait_flags(const MegaArgs& a, const unsigned* f, int n, int* s_f
 // The same for cnt runs of n flags each, run r starting stride words after run r - 1 (f and the
 // stride 16-byte aligned): one poll covers the runs of every sample an item serves, where a wait
 // per sample would cost a memory round trip each.
-__device__ bool wait_flag_runs(const MegaArgs& a, const unsigned* f, int n, int stride, int cnt, int* s_flag) {
-  f += (size_t)(blockIdx.x % kFlagCopies) * a.fstride;
+__device__ bool wait_flag_runs(KArgs& a, const unsigned* f, int n, int stride, int cnt, Sync sy) {
+  f += (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride;
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
-    const unsigned ep = a.epoch;
+    const unsigned ep = sy.epoch;
     const int cpr = (n + 3) >> 2, nch = cpr * cnt;  // 4-word chunks per run, in all
     int ok = 1;
     const brsrc rf = make_rsrc(f, (size_t)a.fstride * 4);
@@ -303,18 +356,18 @@ __device__ bool wait_flag_runs(const MegaArgs& a, const unsigned* f, int n, int 
       for (int spins = 0;; ++spins) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, off, 0, 16);
         if (__all(done(v))) break;
-        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err)) == a.epoch)) {
-          if (lane == 0) record_error(a);
+        if (spins > a.spin_limit || ((spins & 63) == 63 && __builtin_amdgcn_readfirstlane(ld_u32(a.err + kCtlErr)) == sy.epoch)) {
+          if (lane == 0) record_error(a, sy.epoch);
           ok = 0;
           break;
         }
         asm volatile("" ::: "memory");
       }
     }
-    if (lane == 0) *s_flag = ok;
+    if (lane == 0) *sy.flag = ok;
   }
   wg_barrier();
-  const bool ok = *s_flag != 0;
+  const bool ok = *sy.flag != 0;
   wg_barrier();
   return ok;
 }
@@ -323,7 +376,7 @@ __device__ bool wait_flag_runs(const MegaArgs& a, const unsigned* f, int n, int 
 // `copy_stores`: it waits only then, since its stores complete behind its direct-to-LDS copies)
 // -> wave 0 sets the item's flag in every replica.  Every thread of the workgroup calls it (it
 // holds a barrier).
-__device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsigned epoch, bool copy_stores = false) {
+__device__ __forceinline__ void publish(KArgs& a, unsigned* flag, unsigned epoch, bool copy_stores = false) {
   if (!copy_wave() || copy_stores) wait_stores();
   wg_barrier();
   if (threadIdx.x < kFlagCopies) st_u32(flag + (size_t)threadIdx.x * a.fstride, epoch);
@@ -332,11 +385,11 @@ __device__ __forceinline__ void publish(const MegaArgs& a, unsigned* flag, unsig
 // The same for a flag that only workgroups of this XCD poll, after data stored with st_l2_16:
 // one replica (this workgroup's, which its XCD's consumer polls), stored plain into the XCD's L2
 // (an intra-XCD hand-off: 0.69 us against ~1 us through the memory side, measured on MI355X).
-__device__ __forceinline__ void publish_local(const MegaArgs& a, unsigned* flag, unsigned epoch) {
+__device__ __forceinline__ void publish_local(KArgs& a, unsigned* flag, unsigned epoch) {
   if (!copy_wave()) wait_stores();
   wg_barrier();
   if (threadIdx.x == 0) {
-    const brsrc r = make_rsrc(uniform_ptr(flag + (size_t)(blockIdx.x % kFlagCopies) * a.fstride), 4);
+    const brsrc r = make_rsrc(uniform_ptr(flag + (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride), 4);
     __builtin_amdgcn_raw_buffer_store_b32(epoch, r, 0, 0, 0);
   }
 }
@@ -368,6 +421,15 @@ constexpr int kLdsFloatsBatched = kLdsWork + kWorkFloatsBatched;
 static_assert(kLdsFloats * 4 <= 160 * 1024 && kLdsFloatsBatched * 4 <= 160 * 1024, "LDS budget of a gfx950 workgroup");
 constexpr int kLdsA1 = kLdsA + 8192;  // upper half of A (tile 1); during attention: wave O slots
 
+// An LDS address as an address-space-3 pointer, from the low 32 bits of a generic pointer into
+// LDS (which hold the LDS offset).  Direct-to-LDS loads take their destination in that form;
+// converting a generic pointer with a cast costs a null check per load and keeps 64-bit generic
+// addresses live in scalar registers across the phases.
+typedef __attribute__((address_space(3))) u16 lds_u16;
+__device__ __forceinline__ lds_u16* lds_addr(const void* p) {
+  return (lds_u16*)(uintptr_t)(uint32_t)reinterpret_cast<uintptr_t>(p);
+}
+
 // A burst of N contiguous 1 KiB fragments (N <= 63, a compile-time count) from src to LDS dst by
 // the copy wave: first make room (at most 63 - N copies in flight), then N buffer loads straight
 // into LDS (fragment f of src lands at dst + f KiB).  One VGPR holds the lane offset and the
@@ -383,13 +445,13 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
   wait_vmcnt<63 - N>();
   const brsrc r = make_rsrc(src, (size_t)N * 1024);
   const unsigned vo = (threadIdx.x & 63) * 16;
-  u16* d = reinterpret_cast<u16*>(dst);
+  lds_u16* d = lds_addr(dst);
 #pragma unroll
   for (int f = 0; f < N; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, vo, f * 1024, 0, kAuxNt);
 }
 
 // Fragments [F0, F0 + N) of tile `which` (0 or 1) of the qkv (MODE = kModeQkv) or gate_up
-// weights of item blockIdx.x -> region A.  A qkv item's tile 1 is copied without its last
+// weights of item (unsigned)wg_id() -> region A.  A qkv item's tile 1 is copied without its last
 // fragment (k-step 31), which the wave owning that k-step loads into registers: both qkv tiles
 // then fit one 63-copy burst.
 // gate_up items.  B = 1: workgroup w computes tile pair w (gate tile w, up tile w) for the one
@@ -397,20 +459,11 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
 // samples (w / 128): each activation row it reads then serves four tiles instead of two, so an
 // XCD's workgroups read half as many activation bytes (the phase is bound by that L2 traffic).
 // Region A holds pair 2g; the compute waves hold pair 2g + 1 in registers.
-#ifndef PI05_QKV_MSPLIT
-#define PI05_QKV_MSPLIT 1
-#endif
-#ifndef PI05_DOWN_MSPLIT
-#define PI05_DOWN_MSPLIT 1
-#endif
-#ifndef PI05_OPROJ_MSPLIT
-#define PI05_OPROJ_MSPLIT 1
-#endif
 // The qkv of kernel instance 2 (phase_qkv_msplit): item i = tile pair i mod 80 for sample half
 // i / 80.
 template <bool G>
 __device__ __forceinline__ constexpr bool qkv_msplit() {
-  return G && PI05_INSTANCE_GROUPED && PI05_QKV_MSPLIT;
+  return G && PI05_INSTANCE_GROUPED;
 }
 // phase_qkv_msplit's items: tile pair i mod 80 for sample third i / 80, on workgroups 16..255
 constexpr int kQkvItemsRS = 3 * kQkvPairs;
@@ -421,29 +474,29 @@ __device__ __forceinline__ constexpr int n_qkv_items() {
 }
 template <bool G>
 __device__ __forceinline__ int qkv_item_of() {
-  return qkv_msplit<G>() ? (int)blockIdx.x - kQkvWg0RS : qkv_item();
+  return qkv_msplit<G>() ? wg_id() - kQkvWg0RS : qkv_item();
 }
 // The gate_up of kernel instance 2 (phase_gateup_msplit, batches of kRowSplitMinBatch and more):
 // item w = pair w.
 template <bool G>
-__device__ __forceinline__ bool gu_msplit(const MegaArgs&) {
+__device__ __forceinline__ bool gu_msplit(KArgs&) {
   return G && PI05_INSTANCE_GROUPED;
 }
-__device__ __forceinline__ int gu_pair0(const MegaArgs& a) {
-  return a.batch > 1 ? 2 * ((int)blockIdx.x % (kGuItems / 2)) : (int)blockIdx.x;
+__device__ __forceinline__ int gu_pair0(KArgs& a) {
+  return a.batch > 1 ? 2 * (wg_id() % (kGuItems / 2)) : wg_id();
 }
 // qkv items.  B = 1: item i = qkv_item() computes tile pair i mod 80 over row half i / 80 of the
 // sample.  B = 2 (kernel instance 1): item i computes tile pairs 2 (i mod 40) and 2 (i mod 40) + 1
 // over row half (i / 40) mod 2 for sample half i / 80, as gate_up's pair items do; region A holds
 // the first pair.  Kernel instance 2: item i = tile pair i mod 80 for sample third i / 80.
 template <bool G>
-__device__ __forceinline__ int qkv_pair0(const MegaArgs& a) {
+__device__ __forceinline__ int qkv_pair0(KArgs& a) {
   return G && a.batch > 1 && !qkv_msplit<G>() ? 2 * (qkv_item() % (kQkvPairs / 2)) : qkv_item_of<G>() % kQkvPairs;
 }
 template <int MODE, bool G = false>
-__device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int which) {
+__device__ __forceinline__ const u16* norm_w_tile(KArgs& a, int l, int which) {
   constexpr int KSTEPS = kWidth / 32;
-  const int p = MODE == kModeQkv ? qkv_pair0<G>(a) : (gu_msplit<G>(a) ? (int)blockIdx.x : gu_pair0(a));  // qkv: the tile pair
+  const int p = MODE == kModeQkv ? qkv_pair0<G>(a) : (gu_msplit<G>(a) ? wg_id() : gu_pair0(a));  // qkv: the tile pair
   const u16* wl = a.wpack + (size_t)l * kLayerElems;
   if constexpr (MODE == kModeQkv) {
     const bool rotated = p < 72;
@@ -456,23 +509,23 @@ __device__ __forceinline__ const u16* norm_w_tile(const MegaArgs& a, int l, int 
   }
 }
 template <int MODE, int F0, int N, bool G = false>
-__device__ void copy_norm_w(const MegaArgs& a, int l, int which, float* smem) {
+__device__ void copy_norm_w(KArgs& a, int l, int which, float* smem) {
   if (!copy_wave()) return;
-  if (MODE == kModeQkv ? (unsigned)qkv_item_of<G>() >= (unsigned)n_qkv_items<G>() : blockIdx.x >= kGuItems) return;
+  if (MODE == kModeQkv ? (unsigned)qkv_item_of<G>() >= (unsigned)n_qkv_items<G>() : (unsigned)wg_id() >= kGuItems) return;
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE, G>(a, l, which) + F0 * 512);
 }
 
-// down_proj weights of item blockIdx.x = (tile, K quarter) -> region B.
+// down_proj weights of item (unsigned)wg_id() = (tile, K quarter) -> region B.
 // down_proj items.  B = 1: workgroup w = (tile w mod 64, K quarter w / 64).  B > 1: workgroup
 // w = 64 q + 32 h + g computes tiles 2g and 2g + 1 over K quarter q for half h of the samples --
 // half the activation bytes per XCD, as for gate_up.  Either way the quarters of a tile (group)
 // run on one XCD (w mod 8 is the same for all four) and poll one flag replica (w mod 32), and the
 // finishers (quarter 0) are workgroups 0..63, which hold no qkv item.  Region B holds the first
 // tile's quarter; at B > 1 the compute waves hold the second one in registers.
-__device__ __forceinline__ void down_item(const MegaArgs& a, int* nt0, int* ksp, int* half = nullptr) {
-  const int w = (int)blockIdx.x;
+__device__ __forceinline__ void down_item(KArgs& a, int* nt0, int* ksp, int* half = nullptr) {
+  const int w = wg_id();
   *ksp = w / kTiles;
-  if (a.batch > 1 && PI05_DOWN_PAIRS) {
+  if (a.batch > 1) {
     *nt0 = 2 * (w % (kTiles / 2));
     if (half) *half = (w / (kTiles / 2)) % 2;
   } else {
@@ -481,9 +534,9 @@ __device__ __forceinline__ void down_item(const MegaArgs& a, int* nt0, int* ksp,
   }
 }
 template <int KSTEPS>
-__device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
+__device__ void copy_residual_w(KArgs& a, int l, float* smem) {
   constexpr int KQ = KSTEPS / kKSplit;
-  const int item = blockIdx.x;
+  const int item = (unsigned)wg_id();
   if (!copy_wave() || item >= kTiles * kKSplit) return;
   int nt, ksp;
   down_item(a, &nt, &ksp);
@@ -494,16 +547,16 @@ __device__ void copy_residual_w(const MegaArgs& a, int l, float* smem) {
 // Kernel instance 2: down_proj's second tile (nt0 + 1) of the item's K quarter -> the working
 // area's first kDownW1Floats floats (phase_down_msplit reads it after tile nt0's quarter in B).
 constexpr int kDownW1Floats = 8192;
-__device__ void copy_down_w1(const MegaArgs& a, int l, float* smem) {
+__device__ void copy_down_w1(KArgs& a, int l, float* smem) {
   constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
-  if (!copy_wave() || (int)blockIdx.x >= kTiles * kKSplit) return;
+  if (!copy_wave() || wg_id() >= kTiles * kKSplit) return;
   int nt, ksp;
   down_item(a, &nt, &ksp);
   lds_burst<KQ>(smem + kLdsWork, a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)(nt + 1) * KSTEPS * 512 + (size_t)ksp * KQ * 512);
 }
 
 // The layer after (s, l): (s, l + 1), or (s + 1, 0) after the last layer; false past the loop.
-__device__ __forceinline__ bool next_layer(const MegaArgs& a, int s, int l, int* ln) {
+__device__ __forceinline__ bool next_layer(KArgs& a, int s, int l, int* ln) {
   if (l + 1 < a.depth) {
     *ln = l + 1;
     return true;
@@ -595,7 +648,7 @@ __device__ __forceinline__ float sum32(const float (&v)[32]) {
 constexpr int kOutParts = 6;
 constexpr int kOutRun = 172;
 template <bool G>
-__device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
+__device__ bool phase_io(KArgs& a, int s, float* smem, Sync sy) {
   const int L = a.depth, NN = 2 * L + 1, R = a.R, NC = a.batch * kHorizon;
   const int tid = phase_tid();
   const bool comp = tid < kCompThreads;
@@ -613,7 +666,7 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
   u16* s_g = s_h + kWidth;
   const bool has_prev = s > 0, has_next = s < a.steps;
   bool waited = false;
-  for (int c = blockIdx.x; c < NC; c += gridDim.x) {
+  for (int c = (unsigned)wg_id(); c < NC; c += (unsigned)wg_count()) {
     const int b = c / kHorizon, t = c % kHorizon, r = b * kRowsPerSample + t;
     // ---- loads that do not depend on the previous phase (waves 1 and 2 only: wave 0 polls, so
     // it issues nothing ahead of its polls and loads its share after the wait)
@@ -636,7 +689,7 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
       if (tid < 128) load_mod();
     }
     if (has_prev && !waited) {
-      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), G ? kKSplit * kTiles : kTiles, s_flag)) return false;
+      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), G ? kKSplit * kTiles : kTiles, sy)) return false;
       waited = true;
     }
     if (has_prev && tid < 64) {
@@ -742,7 +795,7 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
         if ((tid & 1) == 0) st_f32(a.ss + (sl * kTiles + (tid >> 1)) * R + r, ss);
       }
     }
-    publish(a, flag_base(a, s, 0, kPhIo) + c, a.epoch);
+    publish(a, flag_base(a, s, 0, kPhIo) + c, sy.epoch);
     __syncthreads();  // the LDS rows are reused by the next item
   }
   return true;
@@ -754,14 +807,14 @@ __device__ bool phase_io(const MegaArgs& a, int s, float* smem, int* s_flag) {
 // epilogue computes y = bf16(rstd * acc + shift . W^T) and then RoPE (qkv) or GeGLU (gate_up).
 // =============================================================================================
 template <int MODE, bool G>
-__device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32, TS = 33;
   // m-tiles per item: qkv items are one half of a sample's rows (m-tiles 2h, 2h+1), gate_up all four
   constexpr int MT = MODE == kModeQkv ? 2 : 4;
   constexpr int PH = MODE == kModeQkv ? kPhQkv : kPhGu;
   const int L = a.depth, R = a.R;
   const int n_items = MODE == kModeQkv ? kQkvItems : kGuItems;
-  const int item = MODE == kModeQkv ? qkv_item() : (int)blockIdx.x;
+  const int item = MODE == kModeQkv ? qkv_item() : wg_id();
   const bool has_item = item >= 0 && item < n_items;
   const int p = MODE == kModeQkv ? item % kQkvPairs : item;  // tile pair (qkv) / item
   const int mh = MODE == kModeQkv ? item / kQkvPairs : 0;    // qkv: half of the rows
@@ -836,7 +889,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
     const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kTiles) : kOItems;
-    if (!wait_flags(a, dep, ndep, s_flag)) return false;
+    if (!wait_flags(a, dep, ndep, sy)) return false;
   }
   PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
@@ -971,7 +1024,7 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
     __syncthreads();  // T and s_rstd are reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
-  publish(a, flag_base(a, s, l, PH) + item, a.epoch);
+  publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
   PHASE_TS(s, l, PH, 6);
   return true;
 }
@@ -984,10 +1037,10 @@ __device__ bool phase_norm_gemm(const MegaArgs& a, int s, int l, float* smem, in
 // pairs and the half's samples.
 // =============================================================================================
 template <bool G>
-__device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_gateup_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 4;
   const int L = a.depth, R = a.R;
-  const int item = (int)blockIdx.x;
+  const int item = wg_id();
   PHASE_TS(s, l, kPhGu, 0);
   // copy wave: pair p0's weights (region A) and everything issued before them have landed; with
   // grouped attention (which used region B) down(l)'s weights go to B now
@@ -1030,7 +1083,7 @@ __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem,
     s_bias[c] = bias[kQkvCols + gu * kMlp + (p0 + pr) * 16 + n];
   }
   PHASE_TS(s, l, kPhGu, 1);
-  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, sy)) return false;
   PHASE_TS(s, l, kPhGu, 2);
   if (wave == 0) load_w1();
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
@@ -1108,7 +1161,7 @@ __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem,
     }
   }
   PHASE_TS(s, l, kPhGu, 5);
-  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch);
+  publish(a, flag_base(a, s, l, kPhGu) + item, sy.epoch);
   PHASE_TS(s, l, kPhGu, 6);
   return true;
 }
@@ -1120,7 +1173,7 @@ __device__ bool phase_gateup_pairs(const MegaArgs& a, int s, int l, float* smem,
 // pair is phase_norm_gemm's: bf16(rstd * acc + shift . W^T), then RoPE into the query rows or the
 // action-key block, or the permuted V fragments.
 // =============================================================================================
-__device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_qkv_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 2;
   const int L = a.depth, R = a.R;
   const int item = qkv_item();
@@ -1180,7 +1233,7 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
   {
     const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
     const int ndep = l == 0 ? a.batch * kHorizon : kKSplit * kTiles;  // down_proj_pairs: one flag per (group, quarter)
-    if (!wait_flags(a, dep, ndep, s_flag)) return false;
+    if (!wait_flags(a, dep, ndep, sy)) return false;
   }
   PHASE_TS(s, l, kPhQkv, 2);
   if (wave == 0) load_w1();
@@ -1295,7 +1348,7 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
     }
   }
   PHASE_TS(s, l, kPhQkv, 5);
-  publish(a, flag_base(a, s, l, kPhQkv) + item, a.epoch);
+  publish(a, flag_base(a, s, l, kPhQkv) + item, sy.epoch);
   PHASE_TS(s, l, kPhQkv, 6);
   return true;
 }
@@ -1303,20 +1356,14 @@ __device__ bool phase_qkv_pairs(const MegaArgs& a, int s, int l, float* smem, in
 // Row-split GEMM phases (kernel instance 2): A chunks of kGuCk k-steps x 4 m-tiles.
 constexpr int kGuCk = 4;                     // k-steps per A chunk
 constexpr int kGuChunks = kWidth / 32 / kGuCk;  // 8 chunks per sample
-#ifndef PI05_GU_AHEAD
-#define PI05_GU_AHEAD 1
-#endif
 // chunks in flight ahead of the MFMAs (ring of 4).  One: measured on MI355X, a second chunk in
 // flight made every row-split phase slower (the vector-memory instruction stream of the CU, not
 // the latency, is what these phases wait on)
-constexpr int kGuAhead = PI05_GU_AHEAD;
+constexpr int kGuAhead = 1;
 static_assert(kGuAhead >= 1 && kGuAhead <= 3, "the ring holds the current chunk and kGuAhead more");
 // Grouped attention (attn_group_items): 32-key K/V blocks staged this many ahead of the one
 // being attended, in a ring of kAttnRing LDS buffers.
-#ifndef PI05_ATTN_AHEAD
-#define PI05_ATTN_AHEAD 1
-#endif
-constexpr int kAttnAhead = PI05_ATTN_AHEAD;  // blocks staged ahead of the one being attended
+constexpr int kAttnAhead = 1;  // blocks staged ahead of the one being attended
 constexpr int kAttnRing = kAttnAhead + 1;
 static_assert(kAttnAhead == 1 || kAttnAhead == 2, "ring of two or three buffers");
 // chunk c of sample b (4 m-tiles x kGuCk k-steps) -> A; padded rows and absent samples read zeros
@@ -1411,7 +1458,7 @@ __device__ __forceinline__ void gu_mfma_chunk(f32x4 (&accg)[4], f32x4 (&accu)[4]
 // column d of the first tile with column d of the second) and the 8-byte q / k stores are
 // lane-local; v rows go through a per-wave LDS tile into the permuted V fragment layout.
 // =============================================================================================
-__device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_qkv_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kWidth / 32;
   const int L = a.depth, R = a.R;
   const int item = qkv_item_of<true>();
@@ -1446,7 +1493,7 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
   {
     const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
     const int ndep = l == 0 ? a.batch * kHorizon : kKSplit * kTiles;  // down_proj_pairs: one flag per (group, quarter)
-    if (!wait_flags(a, dep, ndep, s_flag)) return false;
+    if (!wait_flags(a, dep, ndep, sy)) return false;
   }
   PHASE_TS(s, l, kPhQkv, 2);
   const brsrc rg = make_rsrc(a.g + slw * R * kWidth, (size_t)R * kWidth * 2);
@@ -1560,7 +1607,7 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
     }
   }
   PHASE_TS(s, l, kPhQkv, 5);
-  publish(a, flag_base(a, s, l, kPhQkv) + item, a.epoch, true);  // every wave stored rows
+  publish(a, flag_base(a, s, l, kPhQkv) + item, sy.epoch, true);  // every wave stored rows
   PHASE_TS(s, l, kPhQkv, 6);
   return true;
 }
@@ -1571,10 +1618,10 @@ __device__ bool phase_qkv_msplit(const MegaArgs& a, int s, int l, float* smem, i
 // a sample's 48 loads per wave stay under the 63 a wave may have in flight and each wave runs 128
 // MFMAs per sample instead of 176; the four partials are added in wave order.
 // =============================================================================================
-__device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_gateup_pairs4(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NW = 4, NT = 4, KSW = 8, KSTEPS = kWidth / 32, TS = 33, MT = 4, TPW = kTiles / NW;
   const int L = a.depth, R = a.R;
-  const int item = (int)blockIdx.x;
+  const int item = wg_id();
   PHASE_TS(s, l, kPhGu, 0);
   // copy wave: pair p0's weights (region A) and everything issued before them have landed
   if (copy_wave()) wait_vmcnt<0>();
@@ -1608,7 +1655,7 @@ __device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem
     s_bias[c] = bias[kQkvCols + gu * kMlp + (p0 + pr) * 16 + n];
   }
   PHASE_TS(s, l, kPhGu, 1);
-  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, sy)) return false;
   PHASE_TS(s, l, kPhGu, 2);
   if (wave == 0) load_w1();
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
@@ -1678,7 +1725,7 @@ __device__ bool phase_gateup_pairs4(const MegaArgs& a, int s, int l, float* smem
     }
   }
   PHASE_TS(s, l, kPhGu, 5);
-  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch);
+  publish(a, flag_base(a, s, l, kPhGu) + item, sy.epoch);
   PHASE_TS(s, l, kPhGu, 6);
   return true;
 }
@@ -1694,14 +1741,14 @@ static_assert(64 + 64 + 256 + 4 * 4 * 2 * 256 + 64 * 33 <= kWorkFloatsBatched, "
 // GeGLU and 8-byte stores need nothing from other lanes.  Lane r (= row r of the sample) sums its
 // row's 64 tile sums of squares in four groups of 16, loaded during the first four chunks.
 // =============================================================================================
-__device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_gateup_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
   const int L = a.depth, R = a.R;
-  const int item = (int)blockIdx.x;
+  const int item = wg_id();
   PHASE_TS(s, l, kPhGu, 0);
   // copy wave: the pair's weights (region A) and everything issued before them have landed; then
   // down_proj's second tile into the working area (free from here to down_proj)
   if (copy_wave()) wait_vmcnt<0>();
-  if (PI05_DOWN_MSPLIT) copy_down_w1(a, l, smem);
+  copy_down_w1(a, l, smem);
   if (item >= kGuItems) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
@@ -1715,7 +1762,7 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
     buv[i] = bias[kQkvCols + kMlp + item * 16 + 4 * g + i];
   }
   PHASE_TS(s, l, kPhGu, 1);
-  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, s_flag)) return false;
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, sy)) return false;
   PHASE_TS(s, l, kPhGu, 2);
   const brsrc rg = make_rsrc(a.gmid + slw * R * kWidth, (size_t)R * kWidth * 2);
   const brsrc rs = make_rsrc(a.ssmid + slw * kTiles * R, (size_t)kTiles * R * 4);
@@ -1770,7 +1817,7 @@ __device__ bool phase_gateup_msplit(const MegaArgs& a, int s, int l, float* smem
     }
   }
   PHASE_TS(s, l, kPhGu, 5);
-  publish(a, flag_base(a, s, l, kPhGu) + item, a.epoch, true);  // every wave stored rows
+  publish(a, flag_base(a, s, l, kPhGu) + item, sy.epoch, true);  // every wave stored rows
   PHASE_TS(s, l, kPhGu, 6);
   return true;
 }
@@ -1843,17 +1890,17 @@ __device__ __forceinline__ void attn_stage(const u16* pre_src, const u16* suf_sr
   const bool pre = kb < nkb_pre;
   const u16* src = (pre ? pre_src : suf_src) + (size_t)(pre ? kb : kb - nkb_pre) * 16 * 512 + (size_t)(wave & 1) * 8 * 512;
   const brsrc r = make_rsrc(uniform_ptr(src), 8 * 1024);
-  u16* d = dst + wave * 8 * 512;
+  lds_u16* d = lds_addr(dst + wave * 8 * 512);
 #pragma unroll
   for (int f = 0; f < 8; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, lane * 16, f * 1024, 0, 0);
   if (wave == 0) {
     const brsrc rv = make_rsrc(uniform_ptr(valid + kb * 32), 32);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, vdst, 4, lane * 4, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, lds_addr(vdst), 4, lane * 4, 0, 0, 0);
   }
 }
 constexpr int kVringFloats = 64;  // per ring slot: 32 valid bytes (+ the zeros of the out-of-range lanes)
 static_assert(8192 + kAttnRing * kVringFloats <= kWorkFloats, "grouped attention: K/V buffer and valid ring in the working area");
-__device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool attn_group_items(KArgs& a, int s, int l, float* smem, Sync sy) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit, B = a.batch;
   const int n_items = B * kAttnGroupsPerSample * nsplit;
   const int tid = phase_tid(), lane = tid & 63;
@@ -1869,7 +1916,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
   u16* const buf2 = reinterpret_cast<u16*>(smem + kLdsB);
   float* const vring = smem + kLdsWork + 8192;
   const u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = (unsigned)wg_id(); item < n_items; item += (unsigned)wg_count()) {
     const int b = item % B, rr = item / B, grp = rr % kAttnGroupsPerSample, split = rr / kAttnGroupsPerSample;
     const int pair = grp * kAttnGroup + wave;
     const bool has_rows = pair < kPairs;
@@ -1895,7 +1942,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     f32x4 oacc[16];
 #pragma unroll
     for (int d = 0; d < 16; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 3);
     for (int kb = kb_lo; kb < kb_hi; ++kb) {
       const int slot = (kb - kb_lo) % kAttnRing;
       // this wave's loads of block kb have landed (with two blocks ahead, block kb + 1's may still
@@ -1931,7 +1978,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
     }
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 4);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 4);
     // this row block's partial: O (unnormalised, relative to m_run), running max and sum; fp32
     // [16 rows][D], row r16 = lane % 16 holding dims dt*16 + g*4 .. +3 of d-tile dt
     if (has_rows) {
@@ -1943,15 +1990,15 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
         st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + 16 + r16, l_run);
       }
     }
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 5);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 5);
     // the item's flags (one per row block), every replica; every wave stored rows
     wait_stores();
     wg_barrier();
     if (tid < kAttnGroup * kFlagCopies) {
       const int j = tid / kFlagCopies, rep = tid % kFlagCopies, pj = grp * kAttnGroup + j;
-      if (pj < kPairs) st_u32(fsplit + (size_t)(b * kPairs + pj) * a.nsplit_pad + split + (size_t)rep * a.fstride, a.epoch);
+      if (pj < kPairs) st_u32(fsplit + (size_t)(b * kPairs + pj) * a.nsplit_pad + split + (size_t)rep * a.fstride, sy.epoch);
     }
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 6);
   }
   return true;
 }
@@ -1961,7 +2008,7 @@ __device__ bool attn_group_items(const MegaArgs& a, int s, int l, float* smem, i
 // three.  Thread t combines row t / 16 of the row block (16 rows: 2 tokens x 8 heads), dims
 // (t % 16) * 16 .. +15, over the splits in the same order and arithmetic as the merges below, and
 // stores them straight into o_proj's A operand; then the row block's four merge flags.
-__device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) {
+__device__ bool attn_group_merges(KArgs& a, int s, int l, Sync sy) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
   const size_t slw = (size_t)s * L + l;
   const float* apart = a.apart + slw * (size_t)nsplit * nbp * 16 * kHeadDim;
@@ -1972,10 +2019,10 @@ __device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) 
   const int tid = phase_tid(), rr = tid >> 4, d0 = (tid & 15) * 16;
   const brsrc rml = make_rsrc(apart_ml, (size_t)nsplit * nbp * 32 * 4);
   const brsrc rpo = make_rsrc(apart, (size_t)nsplit * nbp * 16 * kHeadDim * 4);
-  for (int bp = blockIdx.x; bp < nbp; bp += gridDim.x) {
+  for (int bp = (unsigned)wg_id(); bp < nbp; bp += (unsigned)wg_count()) {
     const int b = bp / kPairs, pair = bp % kPairs;
     PHASE_TS(s, l, kPhMerge, 1);
-    if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
+    if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, sy)) return false;
     PHASE_TS(s, l, kPhMerge, 2);
     // only the splits there are: masked loads would still take an issue slot each
     float mc[kMaxAttnSplits], lc[kMaxAttnSplits];
@@ -2032,14 +2079,14 @@ __device__ bool attn_group_merges(const MegaArgs& a, int s, int l, int* s_flag) 
     wait_stores();
     PHASE_TS(s, l, kPhMerge, 5);
     wg_barrier();
-    if (tid < kHeadPairs * kFlagCopies) st_u32(fmerge + 4 * bp + tid / kFlagCopies + (size_t)(tid % kFlagCopies) * a.fstride, a.epoch);
+    if (tid < kHeadPairs * kFlagCopies) st_u32(fmerge + 4 * bp + tid / kFlagCopies + (size_t)(tid % kFlagCopies) * a.fstride, sy.epoch);
     PHASE_TS(s, l, kPhMerge, 6);
   }
   return true;
 }
 
 template <bool G>
-__device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
   const int L = a.depth, R = a.R, nbp = a.nbp, nsplit = a.nsplit;
   const int n_items = nbp * nsplit;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -2067,11 +2114,11 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
     burst = true;
     PHASE_TS(s, l, kPhSplit, 1);
-    if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), s_flag)) return false;
+    if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), sy)) return false;
     PHASE_TS(s, l, kPhSplit, 2);
-    if (!attn_group_items(a, s, l, smem, s_flag)) return false;
+    if (!attn_group_items(a, s, l, smem, sy)) return false;
   }
-  for (int item = attn_grouped<G>(a) ? n_items : (int)blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = attn_grouped<G>(a) ? n_items : wg_id(); item < n_items; item += (unsigned)wg_count()) {
     const int bp = item % nbp, split = item / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
     const int rbq = b * (kRowsPerSample / 2) + pair;  // query-row m-tile (16 rows = 2 tokens x 8 heads)
@@ -2105,7 +2152,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     }
     PHASE_TS(s, l, kPhSplit, 1);
     if (!waited) {
-      if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), s_flag)) return false;
+      if (!wait_flags(a, flag_base(a, s, l, kPhQkv), n_qkv_items<G>(), sy)) return false;
       waited = true;
     }
     PHASE_TS(s, l, kPhSplit, 2);
@@ -2115,8 +2162,8 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     if (comp) {
       const int wu = __builtin_amdgcn_readfirstlane(wave);  // LDS addresses of direct-to-LDS loads are wave-uniform
       for (int f = wu; f < 8; f += kCompWaves)
-        __builtin_amdgcn_global_load_lds(const_cast<u16*>(qs + afrag_offset(rbq, f, kHeadDim / 32)) + lane * 8, s_q + (size_t)f * 512, 16,
-                                         0, 0);
+        __builtin_amdgcn_global_load_lds(const_cast<u16*>(qs + afrag_offset(rbq, f, kHeadDim / 32)) + lane * 8, lds_addr(s_q + (size_t)f * 512),
+                                         16, 0, 0);
       if (has_block && !pre) load(blk, kb0);
       wait_vmcnt<0>();  // the query fragments have landed in LDS (and this wave's block)
     }
@@ -2135,7 +2182,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
     }
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
-    if (item == (int)blockIdx.x) {
+    if (item == wg_id()) {
       PHASE_TS(s, l, kPhSplit, 4);
       PHASE_TS_W(1, s, l, kPhSplit, 7);
       PHASE_TS_W(2, s, l, kPhSplit, 8);
@@ -2160,7 +2207,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       }
     }
     __syncthreads();
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 3);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 3);
     {
       float mw[4], Mx = -INFINITY, Lx = 0.f, ww[4];
 #pragma unroll
@@ -2203,9 +2250,9 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
         st_f32(apart_ml + ((size_t)split * nbp + bp) * 32 + 16 + r16, Lx);
       }
     }
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 5);
-    publish(a, fsplit + bp * a.nsplit_pad + split, a.epoch, true);  // the copy wave stored d-tiles 12..15
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhSplit, 6);
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 5);
+    publish(a, fsplit + bp * a.nsplit_pad + split, sy.epoch, true);  // the copy wave stored d-tiles 12..15
+    if (item == wg_id()) PHASE_TS(s, l, kPhSplit, 6);
     __syncthreads();  // the LDS tiles are reused by the next item
   }
   // the rest of gate_up(l) -> region A, whose upper half the split items no longer use (the
@@ -2213,7 +2260,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   if (!burst) copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
   copy_norm_w<kModeGateUp, 16, 16, G>(a, l, 0, smem);
   copy_norm_w<kModeGateUp, 0, 32, G>(a, l, 1, smem);
-  if (attn_grouped<G>(a)) return attn_group_merges(a, s, l, s_flag);
+  if (attn_grouped<G>(a)) return attn_group_merges(a, s, l, sy);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
   // (bp, hp) when hp < nsplit.  Every split item was finished above, so no workgroup waits here
   // on work of its own.  All four waves merge (the copy wave has nothing in flight by now): thread
@@ -2221,11 +2268,11 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
   // loads every split's (max, sum, O) at once.
   bool first_merge = true;
   u16* s_ob = reinterpret_cast<u16*>(smem + kLdsWork);  // [4 rows][D] bf16
-  for (int role = blockIdx.x; role < kHeadPairs * nbp; role += gridDim.x) {
+  for (int role = (unsigned)wg_id(); role < kHeadPairs * nbp; role += (unsigned)wg_count()) {
     const int bp = role % nbp, hp = role / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
     if (first_merge) PHASE_TS(s, l, kPhMerge, 1);
-    if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, s_flag)) return false;
+    if (!wait_flags(a, fsplit + bp * a.nsplit_pad, nsplit, sy)) return false;
     if (first_merge) PHASE_TS(s, l, kPhMerge, 2);
     {
       const int jr = tid >> 6, rr = 2 * hp + (jr & 1) + 8 * (jr >> 1);
@@ -2271,7 +2318,7 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
       for (int q = 0; q < 8; ++q) v8[q] = s_ob[j * kHeadDim + d + q];
       st_bf16x8(os, afrag_index(r, head * kHeadDim + d, kHeads * kHeadDim / 32), v8);
     }
-    publish(a, fmerge + 4 * bp + hp, a.epoch);
+    publish(a, fmerge + 4 * bp + hp, sy.epoch);
     if (first_merge) PHASE_TS(s, l, kPhMerge, 6);
     first_merge = false;
     __syncthreads();  // s_ob is reused by the next role
@@ -2288,14 +2335,14 @@ __device__ bool phase_attn(const MegaArgs& a, int s, int l, float* smem, int* s_
 // chains, add the waves in LDS, then h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249,
 // 503), g = bf16(h * (1 + scale)) of the pre-MLP norm and the tile's row sums of squares.
 // =============================================================================================
-__device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   // waves 1 and 2 hold the tile's weights (K halves) and do the MFMA; wave 0 only polls, so
   // nothing it issued before its polls (a wave's vector memory operations complete in issue
   // order) delays seeing the merges; wave 1 also runs the residual epilogue
   constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / 2, TS = 17;
   constexpr int NCH = 4;  // independent accumulation chains per wave
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
-  const int item = blockIdx.x;
+  const int item = (unsigned)wg_id();
   PHASE_TS(s, l, kPhO, 0);
   if (item >= kOItems) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -2342,7 +2389,7 @@ __device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s
   for (int b = 0; b < a.batch; ++b) {
     const int m = 4 * b + mq;  // m-tile of the activations
     // merge flags 4 * bp + hp: the m-tile's row blocks bp = 25 b + 8 mq .. are one contiguous run
-    if (!wait_flags(a, fmerge + 4 * (b * kPairs + 8 * mq), 4 * np, s_flag)) return false;
+    if (!wait_flags(a, fmerge + 4 * (b * kPairs + 8 * mq), 4 * np, sy)) return false;
     if (b == 0) PHASE_TS(s, l, kPhO, 2);
     // the residual rows: the merges waited for imply every earlier phase of the layer, so the
     // previous layer's down_proj has written them (this workgroup may have had no qkv item)
@@ -2395,7 +2442,7 @@ __device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s
     __syncthreads();  // red, T and s_ss are reused by the next sample
   }
   PHASE_TS(s, l, kPhO, 5);
-  publish(a, flag_base(a, s, l, kPhO) + item, a.epoch);
+  publish(a, flag_base(a, s, l, kPhO) + item, sy.epoch);
   PHASE_TS(s, l, kPhO, 6);
   return true;
 }
@@ -2409,11 +2456,11 @@ __device__ bool phase_oproj(const MegaArgs& a, int s, int l, float* smem, int* s
 // loads and before the polls.  Measured on MI355X against one sample at a time on waves 1 and 2
 // with a wait per sample: B=8 17.9 -> 17.1 ms, B=3 11.5 -> 11.4, B=2 7.88 -> 7.79 per predict.
 // =============================================================================================
-__device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_oproj_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / 2, TS = 17;
   constexpr int NCH = 4;
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
-  const int item = blockIdx.x;
+  const int item = (unsigned)wg_id();
   PHASE_TS(s, l, kPhO, 0);
   const bool grouped = attn_grouped<true>(a);
   if (item >= kOItems) {
@@ -2461,7 +2508,7 @@ __device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, 
                          round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
   const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
   // merge flags 4 * bp + hp: sample b's run for this m-tile starts at 4 (25 b + 8 mq)
-  if (!wait_flag_runs(a, flag_base(a, s, l, kPhMerge) + 4 * 8 * mq, 4 * np, 4 * kPairs, a.batch, s_flag)) return false;
+  if (!wait_flag_runs(a, flag_base(a, s, l, kPhMerge) + 4 * 8 * mq, 4 * np, 4 * kPairs, a.batch, sy)) return false;
   PHASE_TS(s, l, kPhO, 2);
   for (int i = 0; 2 * i < a.batch; ++i) {
     const int b = 2 * i + pr;
@@ -2521,7 +2568,7 @@ __device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, 
     wg_barrier();  // red, T and s_ss are reused by the next iteration
   }
   PHASE_TS(s, l, kPhO, 5);
-  publish(a, flag_base(a, s, l, kPhO) + item, a.epoch);
+  publish(a, flag_base(a, s, l, kPhO) + item, sy.epoch);
   PHASE_TS(s, l, kPhO, 6);
   return true;
 }
@@ -2541,7 +2588,7 @@ __device__ bool phase_oproj_pairs(const MegaArgs& a, int s, int l, float* smem, 
 // publishes one flag, after its items.
 // =============================================================================================
 template <int KS>
-__device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_oproj_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / KS, NCH = KSW / kGuCk;
   constexpr int SPI = 4 / KS, MPW = 4 / KS;  // samples per item, m-tiles finished per wave
   static_assert(KS == 2 || KS == 4, "K halves or quarters");
@@ -2562,7 +2609,7 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
   float* rout = a.ssmid + slw * kTiles * R;
   float* xch = smem + kLdsWork;  // [sample p][from K part h][m-tile][64 lanes][4]
   auto pick = [](const f32x4 (&v)[4], int mt) { return mt == 0 ? v[0] : mt == 1 ? v[1] : mt == 2 ? v[2] : v[3]; };
-  for (int item = (int)blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = wg_id(); item < n_items; item += (unsigned)wg_count()) {
     const int nt = item % kTiles, j = item / kTiles;
     const int col = nt * 16, b = SPI * j + pr;
     const bool has = b < a.batch;
@@ -2583,7 +2630,7 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
     PHASE_TS(s, l, kPhO, 1);
     // the merges of the item's row blocks: 4 flags per row block, kPairs row blocks per sample
     const int nb = a.batch - SPI * j < SPI ? a.batch - SPI * j : SPI;
-    if (!wait_flags(a, flag_base(a, s, l, kPhMerge) + 4 * kPairs * SPI * j, 4 * kPairs * nb, s_flag)) return false;
+    if (!wait_flags(a, flag_base(a, s, l, kPhMerge) + 4 * kPairs * SPI * j, 4 * kPairs * nb, sy)) return false;
     PHASE_TS(s, l, kPhO, 2);
     if (wave == 0) load_w();
     // residual rows of the m-tiles this wave finishes (rows 16 mt + r16, columns col + 4g ..)
@@ -2612,7 +2659,7 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
         for (int mt = 0; mt < 4; ++mt) acc[mt] = mfma16x16x32(wf[c * kGuCk + s2], mt < 3 ? A[c % 4][mt][s2] : a3, acc[mt]);
       }
     }
-    if (item == (int)blockIdx.x) PHASE_TS(s, l, kPhO, 4);
+    if (item == wg_id()) PHASE_TS(s, l, kPhO, 4);
     // the m-tiles other waves finish -> LDS
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
@@ -2652,7 +2699,7 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
     wg_barrier();  // xch is reused by the next item
   }
   PHASE_TS(s, l, kPhO, 5);
-  if ((int)blockIdx.x < kOItems) publish(a, flag_base(a, s, l, kPhO) + blockIdx.x, a.epoch, true);  // every wave stored rows
+  if (wg_id() < kOItems) publish(a, flag_base(a, s, l, kPhO) + (unsigned)wg_id(), sy.epoch, true);  // every wave stored rows
   PHASE_TS(s, l, kPhO, 6);
   return true;
 }
@@ -2666,12 +2713,12 @@ __device__ bool phase_oproj_msplit(const MegaArgs& a, int s, int l, float* smem,
 // sums of squares.  (Without the K split, 128 k-steps of weights and a 16-row A block per item
 // measured slower: the loads queue behind each other in the workgroup.)
 // =============================================================================================
-__device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 17;
   constexpr int PH = kPhDown;
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
-  const int item = blockIdx.x;
+  const int item = (unsigned)wg_id();
   PHASE_TS(s, l, PH, 0);
   // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
   {
@@ -2697,9 +2744,9 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
     // the gate_up items of this quarter's 1024 activation columns: pairs 64 ksp .. 64 ksp + 63,
     // i.e. items 64 ksp .. at B = 1 and, at B > 1, items 32 ksp .. of both sample halves
     const unsigned* fgu = flag_base(a, s, l, kPhGu);
-    if (a.batch > 1 && PI05_GU_PAIRS) {
-      if (!wait_flags(a, fgu + ksp * 32, 32, s_flag) || !wait_flags(a, fgu + kGuItems / 2 + ksp * 32, 32, s_flag)) return false;
-    } else if (!wait_flags(a, fgu + ksp * 64, 64, s_flag)) {
+    if (a.batch > 1) {
+      if (!wait_flags(a, fgu + ksp * 32, 32, sy) || !wait_flags(a, fgu + kGuItems / 2 + ksp * 32, 32, sy)) return false;
+    } else if (!wait_flags(a, fgu + ksp * 64, 64, sy)) {
       return false;
     }
   }
@@ -2772,14 +2819,14 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
   unsigned* fl = flag_base(a, s, l, PH);
   if (ksp != 0) {
     // this quarter's partial is stored: flag it for the tile's finisher (quarter 0, same XCD)
-    publish_local(a, fl + kPartFlags + 4 * nt + (ksp - 1), a.epoch);
+    publish_local(a, fl + kPartFlags + 4 * nt + (ksp - 1), sy.epoch);
     return true;
   }
   // ---- the finisher (quarter 0): its own partial stays in LDS at B = 1; it waits for the other
   // three, adds the four in quarter order and writes the tile.  Waves 0 and 1: lane = row,
   // columns half*8 .. +7.
   if (!own_lds && comp) wait_stores();  // its own partials, reloaded below
-  if (!wait_flags(a, fl + kPartFlags + 4 * nt, kKSplit - 1, s_flag)) return false;
+  if (!wait_flags(a, fl + kPartFlags + 4 * nt, kKSplit - 1, sy)) return false;
   PHASE_TS(s, l, PH, 7);
   {
     u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
@@ -2828,7 +2875,7 @@ __device__ bool phase_down(const MegaArgs& a, int s, int l, float* smem, int* s_
     }
   }
   PHASE_TS(s, l, PH, 8);
-  publish(a, flag_base(a, s, l, PH) + nt, a.epoch);
+  publish(a, flag_base(a, s, l, PH) + nt, sy.epoch);
   PHASE_TS(s, l, PH, 9);
   return true;
 }
@@ -2843,7 +2890,7 @@ struct DownFinishPre {
   float gate[8], s1[8];
   u16x8 hold0;
 };
-__device__ __forceinline__ void down_finish_prefetch(const MegaArgs& a, int s, int l, int nt0, int ksp, int b0, int b1, bool next_g, int NN,
+__device__ __forceinline__ void down_finish_prefetch(KArgs& a, int s, int l, int nt0, int ksp, int b0, int b1, bool next_g, int NN,
                                                      DownFinishPre& pre) {
   const int L = a.depth, R = a.R;
   const int tid = phase_tid();
@@ -2862,7 +2909,7 @@ __device__ __forceinline__ void down_finish_prefetch(const MegaArgs& a, int s, i
   if (b < b1 && frow < kHorizon)
     pre.hold0 = *reinterpret_cast<const u16x8*>(a.hmid + slw * (size_t)R * kWidth + afrag_index(b * kRowsPerSample + frow, col + fc0, kWidth / 32));
 }
-__device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int l, float* s_ss, int nt0, int ksp, int b0, int b1, bool next_g,
+__device__ __forceinline__ void down_pairs_finish(KArgs& a, int s, int l, float* s_ss, int nt0, int ksp, int b0, int b1, bool next_g,
                                                   const DownFinishPre& pre) {
   const int L = a.depth, R = a.R;
   const int tid = phase_tid();
@@ -2929,12 +2976,12 @@ __device__ __forceinline__ void down_pairs_finish(const MegaArgs& a, int s, int 
 // 256 flags.
 // =============================================================================================
 template <bool G>
-__device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_down_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kMlp / 32;
   constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 33;
   constexpr int PH = kPhDown, NG = kTiles / 2;
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
-  const int item = (int)blockIdx.x;
+  const int item = wg_id();
   PHASE_TS(s, l, PH, 0);
   // copy wave: with grouped attention this layer's down_proj weights were copied to region B at
   // gate_up; they have landed (read after the polls' barrier)
@@ -2971,8 +3018,8 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   PHASE_TS(s, l, PH, 1);
   // the gate_up items of this quarter's activation columns for this half's samples
   // (phase_gateup_msplit: item w computes pair w for every sample)
-  if (!(gu_msplit<G>(a) ? wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)
-          : wait_flags(a, flag_base(a, s, l, kPhGu) + half * (kGuItems / 2) + ksp * 32, 32, s_flag)))
+  if (!(gu_msplit<G>(a) ? wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, sy)
+          : wait_flags(a, flag_base(a, s, l, kPhGu) + half * (kGuItems / 2) + ksp * 32, 32, sy)))
     return false;
   PHASE_TS(s, l, PH, 2);
   if (wave == 0) load_w1();
@@ -3022,8 +3069,8 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
   unsigned* fpart = fl + kPartFlags + 4 * (grp + NG * half);
   // this quarter's partials are in this XCD's L2: flag them for the group (all four quarters run on
   // this XCD), then wait for the other three; quarter q finishes samples b0 + q, b0 + q + 4, ...
-  publish_local(a, fpart + ksp, a.epoch);
-  if (!wait_flags(a, fpart, kKSplit, s_flag)) return false;
+  publish_local(a, fpart + ksp, sy.epoch);
+  if (!wait_flags(a, fpart, kKSplit, sy)) return false;
   PHASE_TS(s, l, PH, 7);
   {
     const int ft = tid >> 7, frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;
@@ -3078,7 +3125,7 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
     }
   }
   PHASE_TS(s, l, PH, 8);
-  publish(a, fl + (grp + NG * half) * kKSplit + ksp, a.epoch, true);  // the copy wave stored rows too
+  publish(a, fl + (grp + NG * half) * kKSplit + ksp, sy.epoch, true);  // the copy wave stored rows too
   PHASE_TS(s, l, PH, 9);
   return true;
 }
@@ -3090,12 +3137,12 @@ __device__ bool phase_down_pairs(const MegaArgs& a, int s, int l, float* smem, i
 // with both tiles, as phase_gateup_msplit, and stores its partials straight from the accumulators
 // (a lane: columns 4g .. 4g+3 of one row).  The finishers are phase_down_pairs'.
 // =============================================================================================
-__device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, int* s_flag) {
+__device__ bool phase_down_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
   constexpr int PH = kPhDown, NG = kTiles / 2;
   static_assert(KQ == kGuChunks * kGuCk, "a K quarter is one row-split pass");
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
-  const int item = (int)blockIdx.x;
+  const int item = wg_id();
   PHASE_TS(s, l, PH, 0);
   // copy wave: this layer's down_proj weights (region B, the working area) have landed (read after
   // the polls' barrier); then, ahead of the polls, the next layer's qkv tiles
@@ -3117,7 +3164,7 @@ __device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, 
   const size_t slw = (size_t)s * L + l;
   const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
   PHASE_TS(s, l, PH, 1);
-  if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, s_flag)) return false;  // gate_up items 64 q ..
+  if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, sy)) return false;  // gate_up items 64 q ..
   PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // tile nt0's quarter, then nt0 + 1's
   const brsrc rg = make_rsrc(a.act + slw * (size_t)R * kMlp, (size_t)R * kMlp * 2);
@@ -3160,12 +3207,12 @@ __device__ bool phase_down_msplit(const MegaArgs& a, int s, int l, float* smem, 
   unsigned* fl = flag_base(a, s, l, PH);
   unsigned* fpart = fl + kPartFlags + 4 * (grp + NG * half);
   if (copy_wave()) wait_stores();  // publish_local waits for the compute waves' stores only
-  publish_local(a, fpart + ksp, a.epoch);
-  if (!wait_flags(a, fpart, kKSplit, s_flag)) return false;
+  publish_local(a, fpart + ksp, sy.epoch);
+  if (!wait_flags(a, fpart, kKSplit, sy)) return false;
   PHASE_TS(s, l, PH, 7);
   down_pairs_finish(a, s, l, smem + kLdsWork + kDownW1Floats, nt0, ksp, b0, b1, next_g, fpre);
   PHASE_TS(s, l, PH, 8);
-  publish(a, fl + (grp + NG * half) * kKSplit + ksp, a.epoch, true);  // every wave stored rows
+  publish(a, fl + (grp + NG * half) * kKSplit + ksp, sy.epoch, true);  // every wave stored rows
   PHASE_TS(s, l, PH, 9);
   return true;
 }
@@ -3189,35 +3236,38 @@ static_assert(kDownW1Floats + 256 <= kWorkFloatsBatched, "row-split down_proj: s
 // kernel's register allocation (measured +2-3.5 % per one-sample predict), and the batch paths each
 // other's (+1-1.5 %).
 template <bool G, int I>
-__global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args) {
   __shared__ __align__(16) float smem[G ? kLdsFloatsBatched : kLdsFloats];
   __shared__ int s_flag;
+  // this launch's epoch: one past the last finished launch's
+  const Sync sy{(unsigned)__builtin_amdgcn_readfirstlane(ld_u32(args.err + kCtlEpoch)) + 1u, &s_flag};
   // the copy wave: step 0, layer 0 qkv and o_proj weights
-  copy_norm_w<kModeQkv, 0, 32, G>(a, 0, 0, smem);
-  copy_norm_w<kModeQkv, 0, 31, G>(a, 0, 1, smem);
+  copy_norm_w<kModeQkv, 0, 32, G>(kargs(), 0, 0, smem);
+  copy_norm_w<kModeQkv, 0, 31, G>(kargs(), 0, 1, smem);
   bool ok = true;
-  for (int s = 0; s <= a.steps && ok; ++s) {
-    ok = phase_io<G>(a, s, smem, &s_flag);
-    if (!ok || s == a.steps) break;
-    for (int l = 0; l < a.depth && ok; ++l) {
-      ok = (qkv_msplit<G>() ? phase_qkv_msplit(a, s, l, smem, &s_flag)
-            : G             ? phase_qkv_pairs(a, s, l, smem, &s_flag)
-                            : phase_norm_gemm<kModeQkv, G>(a, s, l, smem, &s_flag)) &&
-           phase_attn<G>(a, s, l, smem, &s_flag) &&
-           (G && PI05_INSTANCE_GROUPED && PI05_OPROJ_MSPLIT ? (a.batch <= 4 ? phase_oproj_msplit<4>(a, s, l, smem, &s_flag)
-                                                                             : phase_oproj_msplit<2>(a, s, l, smem, &s_flag))
-            : G                                             ? phase_oproj_pairs(a, s, l, smem, &s_flag)
-                                                            : phase_oproj(a, s, l, smem, &s_flag)) &&
-           (G ? (gu_msplit<G>(a) ? phase_gateup_msplit(a, s, l, smem, &s_flag) : phase_gateup_pairs4(a, s, l, smem, &s_flag))
-              : ((G || a.batch > 1) && PI05_GU_PAIRS ? phase_gateup_pairs<G>(a, s, l, smem, &s_flag)
-                                                     : phase_norm_gemm<kModeGateUp, G>(a, s, l, smem, &s_flag))) &&
-           (G && PI05_INSTANCE_GROUPED && PI05_DOWN_MSPLIT ? phase_down_msplit(a, s, l, smem, &s_flag)
-            : (G || a.batch > 1) && PI05_DOWN_PAIRS       ? phase_down_pairs<G>(a, s, l, smem, &s_flag)
-                                                          : phase_down(a, s, l, smem, &s_flag));
+  for (int s = 0; s <= kargs().steps && ok; ++s) {
+    ok = phase_io<G>(kargs(), s, smem, sy);
+    if (!ok || s == kargs().steps) break;
+    for (int l = 0; l < kargs().depth && ok; ++l) {
+      ok = (qkv_msplit<G>() ? phase_qkv_msplit(kargs(), s, l, smem, sy)
+            : G             ? phase_qkv_pairs(kargs(), s, l, smem, sy)
+                            : phase_norm_gemm<kModeQkv, G>(kargs(), s, l, smem, sy)) &&
+           phase_attn<G>(kargs(), s, l, smem, sy) &&
+           (G && PI05_INSTANCE_GROUPED ? (kargs().batch <= 4 ? phase_oproj_msplit<4>(kargs(), s, l, smem, sy)
+                                                             : phase_oproj_msplit<2>(kargs(), s, l, smem, sy))
+            : G                         ? phase_oproj_pairs(kargs(), s, l, smem, sy)
+                                        : phase_oproj(kargs(), s, l, smem, sy)) &&
+           (G ? (gu_msplit<G>(kargs()) ? phase_gateup_msplit(kargs(), s, l, smem, sy) : phase_gateup_pairs4(kargs(), s, l, smem, sy))
+              : (kargs().batch > 1 ? phase_gateup_pairs<G>(kargs(), s, l, smem, sy)
+                                   : phase_norm_gemm<kModeGateUp, G>(kargs(), s, l, smem, sy))) &&
+           (G && PI05_INSTANCE_GROUPED ? phase_down_msplit(kargs(), s, l, smem, sy)
+            : (G || kargs().batch > 1) ? phase_down_pairs<G>(kargs(), s, l, smem, sy)
+                                       : phase_down(kargs(), s, l, smem, sy));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
   wait_vmcnt<0>();
+  leave_launch(kargs(), sy);
 }
 
 #if PI05_PERSISTENT_INSTANCE == 1
@@ -3247,7 +3297,7 @@ int denoise_loop_threads() { return kThreads; }
 // =============================================================================================
 __global__ __launch_bounds__(256) void shift_bias_kernel(ShiftBiasArgs a) {
   const int l = blockIdx.y;
-  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int j = (unsigned)wg_id() * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (j >= kBiasCols) return;
   constexpr int KSTEPS = kWidth / 32;

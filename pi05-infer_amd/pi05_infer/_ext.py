@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "pi05_denoise",
     "pi05_denoise_status",
     "pi05_debug_set_spin_limit",
+    "pi05_debug_set_epoch",
     "pi05_release_graph",
     "pi05_set_schedule",
     "pi05_get_schedule",
@@ -177,6 +178,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_denoise": (i32, [vp, vp, vp, vp]),
         "pi05_denoise_status": (i32, [vp, vp]),
         "pi05_debug_set_spin_limit": (i32, [vp, i32]),
+        "pi05_debug_set_epoch": (i32, [vp, ctypes.c_uint32]),
         "pi05_release_graph": (i32, [vp]),
         "pi05_set_schedule": (i32, [vp, i32]),
         "pi05_get_schedule": (i32, [vp]),
@@ -441,6 +443,11 @@ class DenoiseContext:
     def set_spin_limit(self, polls: int) -> None:
         """Test hook: polls after which a kernel wait gives up (0 = the default)."""
         self._call(self.lib.pi05_debug_set_spin_limit(self.handle, polls))
+
+    def set_epoch(self, epoch: int) -> None:
+        """Test hook: the epoch of the last finished persistent launch (the next runs as epoch + 1);
+        lets a test cross the 2^31 wrap-around."""
+        self._call(self.lib.pi05_debug_set_epoch(self.handle, epoch))
 
     def release_graph(self) -> None:
         self._call(self.lib.pi05_release_graph(self.handle))

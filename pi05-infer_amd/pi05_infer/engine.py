@@ -123,6 +123,7 @@ class OpenPi0Inference:
         self._torch_compile_mode = None
         self.training = False
         self.schedule: Optional[str] = None  # None: the library's default for the device
+        self._pending_ctx: Optional[_ext.DenoiseContext] = None  # context of the last predict, until its status is read
         self.prefix_lm = None  # optional PrefixLM (prefix.py): prefix embeddings -> KV cache
         self.vision_tower = None  # optional VisionTower (vision.py): camera images -> image embeddings
         # until setup_wrappers installs the checkpoint's transforms: the policy's Outputs slice only
@@ -231,6 +232,7 @@ class OpenPi0Inference:
 
     # ------------------------------------------------------------------ engine contexts
     def _drop_contexts(self) -> None:
+        self._pending_ctx = None
         for c in self._contexts.values():
             c.close()
         self._contexts.clear()
@@ -276,7 +278,15 @@ class OpenPi0Inference:
 
     @torch.no_grad()
     def sample_actions(self, observation, noise: Optional[torch.Tensor] = None) -> dict:
-        """Prefix KV + ``num_steps`` flow_ode Euler steps (engine.py:344-406) -> ``{"actions"}``."""
+        """Prefix KV + ``num_steps`` flow_ode Euler steps (engine.py:344-406) -> ``{"actions"}``.
+
+        Random draws match the reference's: the initial noise when none is passed, then one
+        ``sample_noise`` of the action shape per Euler step (its flow_ode update adds
+        ``sample_noise * std`` with std = 0, and the graph path draws the same tensor "so RNG
+        consumption matches the eager path", engine.py:389-405), so a generator seeded once gives
+        the reference's noise on every later predict too.  Like the reference's, the call only
+        enqueues GPU work; ``output_transform`` (or ``predict_action_batch``) waits for it and
+        raises ``Pi05Error`` if the launch failed."""
         actions, _ = self._run(observation, noise, trace=False)
         return {"actions": actions}
 
@@ -315,7 +325,18 @@ class OpenPi0Inference:
         if trace:
             tr = torch.empty((cfg.num_steps, bsize, cfg.action_horizon, cfg.action_dim), dtype=torch.float32, device=device)
         ctx.denoise(x, tr)
+        self._pending_ctx = ctx
+        # the reference's per-step draws (engine.py:391-397, 399-403): discarded, generator only
+        for _ in range(cfg.num_steps):
+            self.sample_noise(x.shape, device)
         return x, tr
+
+    def _raise_pending_error(self) -> None:
+        """Raise ``Pi05Error`` (PI05_E_HIP) if the last predict's launch failed; the caller has just
+        waited for the GPU (a device-to-host copy), so the status read adds no wait."""
+        ctx, self._pending_ctx = self._pending_ctx, None
+        if ctx is not None and ctx.handle is not None:
+            ctx.status()
 
     def set_schedule(self, name: Optional[str]) -> None:
         """Execution schedule of the denoise loop: ``"persistent"`` (the whole loop is one
@@ -329,9 +350,12 @@ class OpenPi0Inference:
                 c.set_schedule(name)
 
     def capture_cuda_graph(self, train_batch_size: int, eval_batch_size: int):
-        """The engine always runs its whole Euler loop as one launch (a persistent kernel, or a
-        hipGraph captured lazily per (B, P, num_steps) signature in the graph schedule); this
-        only records that graph use was requested."""
+        """Request graph execution (engine.py:831-860).  The engine already runs its whole Euler
+        loop as one launch: one cooperative kernel (the persistent schedule), or, in the graph
+        schedule, a hipGraph of per-layer kernels captured lazily per (B, P, num_steps) signature.
+        A caller may also capture ``sample_actions`` itself (``torch.cuda.graph``) in the
+        persistent schedule and replay it: the launch carries no per-call state.  The graph
+        schedule refuses capture (``Pi05Error`` PI05_E_STATE), its loop being a hipGraph already."""
         self.cuda_graph_manager = {"eval_batch_size": eval_batch_size}
 
     def is_cuda_graph_enabled(self) -> bool:
@@ -368,6 +392,7 @@ class OpenPi0Inference:
         env action dims), applied on the host like the reference, then the first ``action_chunk``
         actions."""
         host = {k: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for k, v in outputs.items()}
+        self._raise_pending_error()
         out = self._output_transform(host)
         out["actions"] = out["actions"][:, : self.config.action_chunk]
         return out
@@ -385,6 +410,7 @@ class OpenPi0Inference:
         return self.output_transform({"actions": outputs["actions"], "state": obs.state})["actions"]
 
     def close(self) -> None:
+        self._pending_ctx = None
         self._drop_contexts()
         if self.prefix_lm is not None:
             self.prefix_lm.close()

@@ -353,10 +353,102 @@ def test_timeout_is_reported_and_the_next_predict_recovers(full_weights):
     torch.cuda.synchronize()
     with pytest.raises(_ext.Pi05Error, match="PI05_E_HIP"):
         model.sample_actions(obs, x1)
+    # predict_action_batch waits for its actions (the host copy of output_transform) and raises
+    # for the timed-out launch itself, as the reference's synchronising copy would
+    with pytest.raises(_ext.Pi05Error, match="PI05_E_HIP"):
+        model.predict_action_batch(obs, noise=x1)
     ctx.set_spin_limit(0)
     again = model.sample_actions(obs, x1)["actions"]
     ctx.status()
     assert torch.equal(again, good)
+    assert torch.equal(model.predict_action_batch(obs, noise=x1), good.cpu()[:, :5, :7])
+    model.close()
+
+
+def _small_model(full_weights, depth=2, steps=3):
+    g = replace(S.ExpertGeometry(), depth=depth)
+    w = {k: v for k, v in full_weights.items() if ".layers." not in k or int(k.split(".layers.")[1].split(".")[0]) < depth}
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), g)
+    model.load_state_dict(w)
+    model.to("cuda")
+    return g, model
+
+
+def test_seeded_predicts_draw_noise_like_the_reference(full_weights):
+    """Seeded once, two predicts without noise equal predicts fed the noises the reference would
+    draw from that generator: x1, then num_steps discarded draws (one per Euler step,
+    engine.py:391-403), then the next predict's x1."""
+    steps = 3
+    g, model = _small_model(full_weights, steps=steps)
+    k, v = S.make_prefix_kv(g, 64)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(64).cuda())
+    torch.manual_seed(1234)
+    a1 = model.sample_actions(obs)["actions"].clone()
+    a2 = model.sample_actions(obs)["actions"].clone()
+    torch.manual_seed(1234)
+    shape = (1, g.action_horizon, g.action_dim)
+    draws = [torch.normal(0.0, 1.0, size=shape, device="cuda") for _ in range(2 + steps)]
+    b1 = model.sample_actions(obs, draws[0])["actions"]
+    b2 = model.sample_actions(obs, draws[1 + steps])["actions"]
+    torch.cuda.synchronize()
+    assert torch.equal(a1, b1) and torch.equal(a2, b2) and not torch.equal(a1, a2)
+    model.close()
+
+
+def test_captured_predict_replays_match_uncaptured(full_weights):
+    """sample_actions captured with torch.cuda.graph (persistent schedule) and replayed: each
+    replay, with eager predicts and host synchronisations between the replays, equals the
+    uncaptured predict of the same noise bit for bit (the kernel takes its flag epoch from device
+    memory, so a replay never meets flags of its own epoch).  The graph schedule refuses capture."""
+    from pi05_infer import _ext
+
+    g, model = _small_model(full_weights, depth=2, steps=3)
+    k, v = S.make_prefix_kv(g, 64)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(64).cuda())
+    xs = [S.make_noise(g, seed=sd).cuda() for sd in (2, 3)]
+    refs = [model.sample_actions(obs, x)["actions"].clone() for x in xs]
+    torch.cuda.synchronize()
+    x_static = xs[0].clone()
+    graph = torch.cuda.CUDAGraph()
+    print("capturing sample_actions (persistent schedule)", flush=True)
+    with torch.cuda.graph(graph):
+        out = model.sample_actions(obs, x_static)["actions"]
+    torch.cuda.synchronize()
+    for i in (0, 1, 0, 1):
+        x_static.copy_(xs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, refs[i]), f"replay of noise {i}"
+        eager = model.sample_actions(obs, xs[1 - i])["actions"]
+        torch.cuda.synchronize()
+        assert torch.equal(eager, refs[1 - i])
+    model._context(1, 64, 3).status()
+    del graph
+    model.set_schedule("graph")
+    model.sample_actions(obs, xs[0])  # builds the schedule's own graph outside any capture
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(_ext.Pi05Error, match="PI05_E_STATE"):
+        with torch.cuda.graph(g2):
+            model.sample_actions(obs, x_static)
+    model.close()
+
+
+def test_epoch_wraparound_keeps_predicts_exact(full_weights):
+    """The launch whose epoch reaches 2^31 zeroes the flags and the next runs as epoch 1: the
+    predicts on either side of the wrap equal the first one bit for bit."""
+    g, model = _small_model(full_weights, depth=2, steps=3)
+    k, v = S.make_prefix_kv(g, 96)
+    obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(96).cuda())
+    x1 = S.make_noise(g).cuda()
+    good = model.sample_actions(obs, x1)["actions"].clone()
+    ctx = model._context(1, 96, 3)
+    ctx.set_epoch(2**31 - 2)
+    for i in range(4):  # epochs 2^31 - 1, 2^31 (zeroes the flags), 1, 2
+        got = model.sample_actions(obs, x1)["actions"]
+        torch.cuda.synchronize()
+        assert torch.equal(got, good), f"predict {i} after the epoch was set"
+    ctx.status()
     model.close()
 
 

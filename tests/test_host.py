@@ -92,6 +92,42 @@ def test_engine_requires_gpu_and_pi05():
         m.sample_actions(obs, S.make_noise(SMALL))
 
 
+def test_sample_actions_draws_noise_like_the_reference(monkeypatch):
+    """The reference draws the initial noise when none is passed (engine.py:350-354) and then one
+    sample_noise of the action shape per Euler step, on the eager and the graph path alike
+    (engine.py:391-397, 399-403).  With the GPU context stubbed out, the denoise input must be the
+    first draw of a seeded generator and the next predict's the (2 + num_steps)-th: 1 + num_steps
+    draws per predict without noise, num_steps with it."""
+    steps = 4
+    m = build_model("random:0", "pi05_libero", geometry=SMALL, num_steps=steps)
+    seen = []
+
+    class FakeContext:
+        def prime_prefix(self, ks, vs, pad):
+            pass
+
+        def denoise(self, x, trace):
+            seen.append(x.clone())
+
+    monkeypatch.setattr(m, "_context", lambda *args: FakeContext())
+    calls = []
+    draw = m.sample_noise
+    monkeypatch.setattr(m, "sample_noise", lambda shape, device: calls.append(tuple(shape)) or draw(shape, device))
+    k, v = S.make_prefix_kv(SMALL, 8)
+    obs = Observation(k, v, S.full_prefix_pad(8))
+    shape = (1, SMALL.action_horizon, SMALL.action_dim)
+    torch.manual_seed(7)
+    m.sample_actions(obs)
+    m.sample_actions(obs)
+    assert calls == [shape] * (2 * (1 + steps))
+    torch.manual_seed(7)
+    stream = [torch.normal(0.0, 1.0, size=shape) for _ in range(2 * (1 + steps))]
+    assert torch.equal(seen[0], stream[0]) and torch.equal(seen[1], stream[1 + steps])
+    calls.clear()
+    m.sample_actions(obs, stream[0])
+    assert calls == [shape] * steps
+
+
 def test_observation_from_dynamic_cache_dict():
     k, v = S.make_prefix_kv(SMALL, 8)
     kv = [(k[:, i : i + 1], v[:, i : i + 1]) for i in range(SMALL.depth)]
