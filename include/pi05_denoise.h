@@ -177,6 +177,14 @@ int pi05_denoise_status(pi05_ctx* ctx, void* stream);
  * every workgroup still leaves the kernel normally.  No counterpart in the reference. */
 int pi05_debug_set_spin_limit(pi05_ctx* ctx, int polls);
 
+/* Test hook: every persistent launch checks that its workgroups were dealt round-robin over the
+ * 8 XCDs (workgroup w on XCD (w + d) mod 8, one d per launch), which its intra-XCD hand-offs
+ * assume, and a launch that finds otherwise is reported as PI05_E_HIP by the next pi05_denoise or
+ * pi05_denoise_status.  A skew of 1..7 is added to the offset the odd workgroups compute (their
+ * placement and the kernel's work are unchanged), so that the report can be exercised; 0 (the
+ * default) restores the plain check.  No counterpart in the reference. */
+int pi05_debug_skew_placement_check(pi05_ctx* ctx, int skew);
+
 /* Test hook: set the epoch of the last finished persistent launch (the next launch runs as
  * epoch + 1; the launch that reaches 2^31 zeroes the flags and the next one runs as epoch 1), so
  * that the wrap-around can be exercised without 2^31 launches.  Synchronises the device;

@@ -7,6 +7,7 @@ benchmark driver ``denoise_bench``.
   a denoise-only process never loads hipBLASLt.
 
     python pi05-infer_amd/build_lib.py [--verbose]
+    python pi05-infer_amd/build_lib.py --stamps   (the profiling build phase_stamps.py reads)
 """
 
 from __future__ import annotations
@@ -24,6 +25,7 @@ SOURCES = ["pi05_kernels.hip", "pi05_persistent.hip", "pi05_persistent_batched.h
 PREFIX_OUT = os.path.join(HERE, "pi05_infer", "libpi05_prefix.so")
 PREFIX_SOURCES = ["pi05_prefill.hip", "pi05_siglip.hip"]
 PREFIX_LIBS = ["-lhipblaslt"]  # the plain GEMMs of the prefill and the vision tower
+STAMPS_OUT = os.path.join(HERE, "pi05_infer", "stamps", "libpi05_denoise.so")  # profiling build (phase_stamps.py)
 BENCH_SRC = "denoise_bench.hip"
 BENCH_OUT = os.path.join(HERE, "pi05_infer", "denoise_bench")
 
@@ -70,5 +72,19 @@ def build(verbose: bool = False) -> str:
     return OUT
 
 
+def build_stamps(verbose: bool = False) -> str:
+    """The denoise library with per-phase s_memrealtime stamps (-DPI05_PHASE_TIMESTAMPS, ~1 % slower;
+    exports pi05_debug_phase_timestamps), next to the package in pi05_infer/stamps/ -- a profiling
+    build that phase_stamps.py loads instead of the product library."""
+    os.makedirs(os.path.dirname(STAMPS_OUT), exist_ok=True)
+    _run([hipcc(), *HIPCC_FLAGS, "-DPI05_PHASE_TIMESTAMPS", f"-I{INCLUDE}", f"-I{CSRC}", *[os.path.join(CSRC, s) for s in SOURCES],
+          "-o", STAMPS_OUT + ".tmp"], verbose)
+    os.replace(STAMPS_OUT + ".tmp", STAMPS_OUT)
+    return STAMPS_OUT
+
+
 if __name__ == "__main__":
-    print(build(verbose="--verbose" in sys.argv))
+    if "--stamps" in sys.argv:
+        print(build_stamps(verbose="--verbose" in sys.argv))
+    else:
+        print(build(verbose="--verbose" in sys.argv))

@@ -5,6 +5,8 @@
 //   denoise_bench [--prefix P] [--batch B] [--predicts K] [--warmup W] [--schedule persistent|graph]
 //   denoise_bench --copy-bytes N   (one plain N-byte device copy kernel: calibrates HBM byte
 //                                   counters such as FETCH_SIZE / WRITE_SIZE against a known size)
+//   denoise_bench ... --with-copy N (the predicts, then that copy kernel in the same process, so
+//                                   one counter run measures both)
 //
 // Weights are random-init on the device (N(0, 0.02)-scaled uniform noise, seed fixed), prefix
 // KV uniform in [-1.7, 1.7] bf16 (unit variance), all prefix keys valid, noise N(0,1)-scaled
@@ -104,6 +106,7 @@ float* dev_f32(size_t n, float stddev) {
 
 int main(int argc, char** argv) {
   int prefix = 968, batch = 1, predicts = 20, warmup = 3;
+  size_t copy_bytes = 0;
   std::string schedule = "persistent";
   for (int i = 1; i + 1 < argc; i += 2) {
     const std::string k = argv[i];
@@ -113,6 +116,7 @@ int main(int argc, char** argv) {
     else if (k == "--predicts") predicts = atoi(argv[i + 1]);
     else if (k == "--warmup") warmup = atoi(argv[i + 1]);
     else if (k == "--schedule") schedule = argv[i + 1];
+    else if (k == "--with-copy") copy_bytes = strtoull(argv[i + 1], nullptr, 10);
     else {
       fprintf(stderr, "unknown option %s\n", argv[i]);
       return 1;
@@ -186,6 +190,7 @@ int main(int argc, char** argv) {
   for (int i = 0; i < predicts; ++i) PI(ctx, pi05_denoise(ctx, x, nullptr, nullptr));
   CK(hipEventRecord(e1, nullptr));
   CK(hipEventSynchronize(e1));
+  PI(ctx, pi05_denoise_status(ctx, nullptr));  // no launch timed out or ran misplaced
   float ms = 0.f;
   CK(hipEventElapsedTime(&ms, e0, e1));
   std::vector<float> hx(xn);
@@ -206,5 +211,5 @@ int main(int argc, char** argv) {
   CK(hipFree(pad));
   CK(hipFree(noise));
   CK(hipFree(x));
-  return 0;
+  return copy_bytes ? copy_calibration(copy_bytes) : 0;
 }

@@ -333,8 +333,10 @@ struct pi05_ctx {
   // persistent schedule
   char* pbase = nullptr;  // one allocation, carved by carve_persistent()
   MegaArgs mega{};
-  unsigned* host_err = nullptr;  // pinned host word: count of launches whose waits timed out
-  unsigned reported = 0;         // the count already reported to the caller
+  unsigned* host_err = nullptr;  // pinned host words: launches whose waits timed out, launches misplaced over the XCDs
+  unsigned reported = 0;         // the timeout count already reported to the caller
+  unsigned reported_placement = 0;  // the placement count already reported
+  unsigned xcd_skew = 0;         // test hook (pi05_debug_skew_placement_check)
   int spin_limit = kDefaultSpinLimit;
 
   bool weights_ready = false;
@@ -698,13 +700,16 @@ extern "C" {
 int pi05_adarms_table_noalloc(const pi05_dims* dims, const float* tin_w, const float* tin_b, const float* tout_w,
                               const float* tout_b, const float* const* dense_w, const float* const* dense_b, float* table_out,
                               void* stream) {
+  // the scratch bound first: it holds kMaxSteps steps of the time MLP, and a caller that sizes
+  // its own tables may ask for more than the scratch was built for
+  if (dims && dims->num_steps > kMaxSteps) {
+    g_last_error = "num_steps " + std::to_string(dims->num_steps) + " exceeds the no-alloc scratch maximum of " +
+                   std::to_string(kMaxSteps) + " steps";
+    return PI05_E_INVALID;
+  }
   std::string msg;
   if (!check_dims_msg(dims, &msg)) {
     g_last_error = msg;
-    return PI05_E_INVALID;
-  }
-  if (dims->num_steps > kMaxSteps) {
-    g_last_error = "num_steps exceeds the no-alloc scratch maximum";
     return PI05_E_INVALID;
   }
   if (!tin_w || !tin_b || !tout_w || !tout_b || !dense_w || !dense_b || !table_out) {
@@ -826,8 +831,8 @@ int pi05_ctx_create(const pi05_dims* dims, pi05_ctx** out) {
   ALLOC(inv_freq, p.invf);
 #undef ALLOC
   if (ae == hipSuccess) {
-    ae = hipHostMalloc(reinterpret_cast<void**>(&c->host_err), sizeof(unsigned), hipHostMallocMapped);
-    if (ae == hipSuccess) *c->host_err = 0;
+    ae = hipHostMalloc(reinterpret_cast<void**>(&c->host_err), 2 * sizeof(unsigned), hipHostMallocMapped);
+    if (ae == hipSuccess) c->host_err[kHostTimeouts] = c->host_err[kHostPlacement] = 0;
   }
   // the persistent schedule needs every workgroup of the grid resident at once
   int coop = 0, per_cu = 0;
@@ -1064,7 +1069,15 @@ namespace {
 // seen by a later call or by pi05_denoise_status).
 int take_pending_error(pi05_ctx* c) {
   if (!c->host_err) return PI05_OK;
-  const unsigned n = __atomic_load_n(c->host_err, __ATOMIC_ACQUIRE);
+  const unsigned np = __atomic_load_n(c->host_err + kHostPlacement, __ATOMIC_ACQUIRE);
+  if (np != c->reported_placement) {
+    const unsigned fresh = np - c->reported_placement;
+    c->reported_placement = np;
+    return c->fail(PI05_E_HIP, "%u denoise launch%s on this context ran with workgroups not dealt round-robin over the 8 XCDs "
+                   "(workgroups w and w + 8 on different XCDs); the intra-XCD hand-offs may have read stale data, so %s "
+                   "actions are invalid", fresh, fresh == 1 ? "" : "es", fresh == 1 ? "its" : "their");
+  }
+  const unsigned n = __atomic_load_n(c->host_err + kHostTimeouts, __ATOMIC_ACQUIRE);
   if (n == c->reported) return PI05_OK;
   const unsigned fresh = n - c->reported;
   c->reported = n;
@@ -1090,6 +1103,7 @@ int denoise_persistent(pi05_ctx* c, float* x_inout, float* v_trace, hipStream_t 
   unsigned* host_err_dev = nullptr;
   HIPCHK(c, hipHostGetDevicePointer(reinterpret_cast<void**>(&host_err_dev), c->host_err, 0));
   a.host_err = host_err_dev;
+  a.xcd_skew = c->xcd_skew;
   // enqueue only: a timed-out wait is reported by the next call or by pi05_denoise_status
   HIPCHK(c, launch_denoise_loop(a, c->grid, st));
   return PI05_OK;
@@ -1136,6 +1150,16 @@ int pi05_debug_set_spin_limit(pi05_ctx* c, int polls) {
   }
   if (polls < 0) return c->fail(PI05_E_INVALID, "polls %d < 0", polls);
   c->spin_limit = polls == 0 ? kDefaultSpinLimit : polls;
+  return PI05_OK;
+}
+
+int pi05_debug_skew_placement_check(pi05_ctx* c, int skew) {
+  if (!c) {
+    g_last_error = "ctx is NULL";
+    return PI05_E_INVALID;
+  }
+  if (skew < 0 || skew > 7) return c->fail(PI05_E_INVALID, "skew %d outside 0..7", skew);
+  c->xcd_skew = (unsigned)skew;
   return PI05_OK;
 }
 

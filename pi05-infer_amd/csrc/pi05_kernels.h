@@ -134,11 +134,17 @@ constexpr int kFlagCopies = 32;
 constexpr int kBiasCols = 2560 + 2 * 4096;  // 2560 q|k|v columns, then 4096 gate, then 4096 up
 
 // Launch-control words of a context (one zero-filled 256-byte block, each word on its own 64-byte
-// line): the error word, the epoch of the last launch that finished, and the count of workgroups
-// that have left the running launch.
+// line): the error word, the epoch of the last launch that finished, the count of workgroups that
+// have left the running launch, and the placement word (bit d set by every workgroup whose XCD is
+// (workgroup index + d) mod 8).
 constexpr int kCtlErr = 0;
 constexpr int kCtlEpoch = 16;
 constexpr int kCtlExit = 32;
+constexpr int kCtlXcd = 48;
+// The pinned host words of a context: launches whose waits timed out, launches whose workgroups
+// were not placed round-robin over the XCDs.
+constexpr int kHostTimeouts = 0;
+constexpr int kHostPlacement = 1;
 constexpr unsigned kEpochWrap = 1u << 31;  // a launch with this epoch zeroes the flags; the next runs as epoch 1
 
 struct MegaArgs {
@@ -180,7 +186,8 @@ struct MegaArgs {
   float* x;               // [steps][B*50, a] actions after step s (slot 0 unused)
   float* x_io;            // [B*50, a] caller's buffer: noise on entry, actions on exit
   float* trace;           // [steps][B*50, a] caller's velocity buffer (nullable)
-  unsigned* host_err;     // pinned host word: count of launches whose waits timed out (device-visible mapping)
+  unsigned* host_err;     // pinned host words [kHostTimeouts], [kHostPlacement] (device-visible mapping)
+  unsigned xcd_skew;      // test hook: added to the placement offset of odd workgroups (0 in normal runs)
   size_t flag_bytes;      // size of `flags` (zeroed by the launch that reaches kEpochWrap)
 };
 

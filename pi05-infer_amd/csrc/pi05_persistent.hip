@@ -271,16 +271,38 @@ __device__ void record_error(KArgs& a, unsigned epoch) { st_u32(a.err + kCtlErr,
 // graph of this one) runs with a fresh epoch; the host passes none.  A launch whose waits timed out
 // is counted in the pinned host word (one writer: the last workgroup out of a launch).  The launch
 // that reaches kEpochWrap zeroes the flags and the error word first and restarts the epochs at 1.
+//
+// Placement check.  The down_proj K quarters of a tile hand their partials and flags over through
+// one XCD's L2 (st_l2_16, publish_local), which is correct only if workgroups w and w + 8k run on
+// the same XCD.  The dispatcher deals workgroups to the 8 XCDs round-robin, starting where the
+// previous dispatch stopped, so workgroup w runs on XCD (w + d) mod 8 with one offset d per launch.
+// Before counting itself out, every workgroup sets bit (XCC_ID - w) mod 8 of the placement word
+// (and waits for the or, so it is performed before the count); the last one out counts a launch
+// with more than one bit set in the pinned host word, which the host reports as an error.
 __device__ void leave_launch(KArgs& a, Sync sy) {
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const unsigned w = (unsigned)wg_id();
+    const unsigned d = (xcc - w + (w & 1u) * a.xcd_skew) & 7u;
+    const unsigned prev = __hip_atomic_fetch_or(a.err + kCtlXcd, 1u << d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(prev));  // the or has been performed
     *sy.flag = __hip_atomic_fetch_add(a.err + kCtlExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)wg_count() - 1;
+  }
   __syncthreads();
   if (!*sy.flag) return;
   unsigned last = sy.epoch;
   if (threadIdx.x == 0 && ld_u32(a.err + kCtlErr) == sy.epoch) {
-    const unsigned n = __hip_atomic_load(a.host_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(a.host_err, n + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const unsigned n = __hip_atomic_load(a.host_err + kHostTimeouts, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(a.host_err + kHostTimeouts, n + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (threadIdx.x == 0) {
+    if (__builtin_popcount(ld_u32(a.err + kCtlXcd)) != 1) {
+      const unsigned n = __hip_atomic_load(a.host_err + kHostPlacement, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(a.host_err + kHostPlacement, n + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    st_u32(a.err + kCtlXcd, 0);
   }
   if (sy.epoch >= kEpochWrap) {
     uint4* f = reinterpret_cast<uint4*>(a.flags);

@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "pi05_denoise_status",
     "pi05_debug_set_spin_limit",
     "pi05_debug_set_epoch",
+    "pi05_debug_skew_placement_check",
     "pi05_release_graph",
     "pi05_set_schedule",
     "pi05_get_schedule",
@@ -179,6 +180,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "pi05_denoise_status": (i32, [vp, vp]),
         "pi05_debug_set_spin_limit": (i32, [vp, i32]),
         "pi05_debug_set_epoch": (i32, [vp, ctypes.c_uint32]),
+        "pi05_debug_skew_placement_check": (i32, [vp, i32]),
         "pi05_release_graph": (i32, [vp]),
         "pi05_set_schedule": (i32, [vp, i32]),
         "pi05_get_schedule": (i32, [vp]),
@@ -443,6 +445,10 @@ class DenoiseContext:
     def set_spin_limit(self, polls: int) -> None:
         """Test hook: polls after which a kernel wait gives up (0 = the default)."""
         self._call(self.lib.pi05_debug_set_spin_limit(self.handle, polls))
+
+    def skew_placement_check(self, skew: int) -> None:
+        """Test hook: perturb the kernel's XCD placement check (0 restores it)."""
+        self._call(self.lib.pi05_debug_skew_placement_check(self.handle, int(skew)))
 
     def set_epoch(self, epoch: int) -> None:
         """Test hook: the epoch of the last finished persistent launch (the next runs as epoch + 1);

@@ -140,10 +140,11 @@ def test_batch5_batch_paths(full_weights):
 
 
 def test_batch16_multi_pass_items(full_weights):
-    """B=16: every per-workgroup loop of the batched kernel runs more than once -- gate_up rows four
-    samples per wave, qkv thirds of six samples (two per wave for two waves), down_proj halves of
-    eight (two per wave), o_proj's wave pairs eight iterations, the grouped attention two key
-    splits -- with a ragged prefix."""
+    """B=16: the GEMM phases' per-workgroup loops run more than once -- gate_up rows four samples
+    per wave, qkv thirds of six samples (two per wave for two waves), down_proj halves of eight (two
+    per wave), o_proj's wave pairs eight iterations -- with a ragged prefix.  The grouped attention
+    has two key splits here, 224 items that fill the grid once (test_batch40_grouped_items_wrap
+    covers items that wrap around it)."""
     print("case B=16: depth 2, B=16, P=100, 2 steps", flush=True)
 
     def pad_fn(pad):
@@ -152,6 +153,21 @@ def test_batch16_multi_pass_items(full_weights):
 
     model, _, _, _, ref, got = _run_case(full_weights, depth=2, P=100, B=16, steps=2, pad_fn=pad_fn, schedules=("persistent",))
     _check("B=16", ref, got, 2)
+    model.close()
+
+
+def test_batch40_grouped_items_wrap(full_weights):
+    """B=40: 7 x 40 = 280 grouped attention items (one key split) on 256 workgroups, so workgroups
+    0..23 take a second item and restage their LDS K/V ring for it; every other per-workgroup loop
+    also runs many passes."""
+    print("case B=40: depth 2, B=40, P=64, 2 steps", flush=True)
+
+    def pad_fn(pad):
+        pad[7, 50:] = False
+        pad[33, 0:5] = False
+
+    model, _, _, _, ref, got = _run_case(full_weights, depth=2, P=64, B=40, steps=2, pad_fn=pad_fn, schedules=("persistent",))
+    _check("B=40", ref, got, 2)
     model.close()
 
 
@@ -363,6 +379,36 @@ def test_timeout_is_reported_and_the_next_predict_recovers(full_weights):
     assert torch.equal(again, good)
     assert torch.equal(model.predict_action_batch(obs, noise=x1), good.cpu()[:, :5, :7])
     model.close()
+
+
+def test_placement_check_reports_a_misplaced_launch(full_weights):
+    """Every persistent launch checks that workgroups w and w + 8 ran on one XCD (its intra-XCD
+    hand-offs need it).  With the check's offset skewed for the odd workgroups (the placement and
+    the work stay as they are) the launch is reported as PI05_E_HIP, once; with the skew removed
+    the next predicts are exact and report nothing.  Run at B = 1 and B = 3 (kernel instances 0
+    and 2, which share the check)."""
+    from pi05_infer import _ext
+
+    for B in (1, 3):
+        g, model = _small_model(full_weights)
+        k, v = S.make_prefix_kv(g, 64, B)
+        obs = Observation(k.cuda(), v.cuda(), S.full_prefix_pad(64, B).cuda())
+        x1 = S.make_noise(g, B).cuda()
+        good = model.sample_actions(obs, x1)["actions"].clone()
+        ctx = model._context(B, 64, 3)
+        ctx.status()  # the real placement passes the check
+        print(f"skewing the placement check (B={B})", flush=True)
+        ctx.skew_placement_check(3)
+        got = model.sample_actions(obs, x1)["actions"]
+        with pytest.raises(_ext.Pi05Error, match="XCD"):
+            ctx.status()
+        ctx.status()  # reported once
+        assert torch.equal(got, good)  # the work itself ran as usual
+        ctx.skew_placement_check(0)
+        again = model.sample_actions(obs, x1)["actions"]
+        ctx.status()
+        assert torch.equal(again, good)
+        model.close()
 
 
 def _small_model(full_weights, depth=2, steps=3):

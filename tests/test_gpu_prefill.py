@@ -239,3 +239,51 @@ def test_full_depth_prefill_then_denoise_c5_geometry():
         _close(vs_ref[s], vs[s], f"depth-18 prefill->denoise step {s} velocity")
     _close(act_ref, act, "depth-18 prefill->denoise actions")
     model.close()
+
+
+def test_full_vocabulary_prompt_embed_prefill_denoise():
+    """Token ids across Gemma's whole vocabulary (0 .. 257151, both ends included) through
+    embed_tokens with a 257,152-row table, the prefill (depth 2) and the denoise (depth 2, 3 steps):
+    the embeddings equal the oracle's bit for bit, and the actions meet the parity bar against the
+    oracle chain on the same embeddings."""
+    print("case full vocabulary: 257152-row table, 40 tokens (5 padded), prefill depth 2 -> denoise depth 2", flush=True)
+    from pi05_infer.engine import Observation, OpenPi0InferConfig, OpenPi0Inference
+    from pi05_infer.prefix import EMBED_NAME, PrefixGeometry, PrefixLM, layer_param_names
+
+    vocab, T, steps = 257152, 40, 3
+    gen = torch.Generator().manual_seed(12)
+    table = torch.randn(vocab, G.width, generator=gen).to(torch.bfloat16)
+    ids = torch.randint(0, vocab, (1, T), generator=gen)
+    ids[0, :6] = torch.tensor([0, 1, vocab - 1, vocab - 2, 131072, 65535])
+    pad = torch.ones(1, T, dtype=torch.bool)
+    pad[0, 35:] = False
+    layers = PO.random_layers(G, 2, seed=13)
+    plm = PrefixLM(PrefixGeometry(depth=2))
+    sd = {layer_param_names(i)[k]: lw[k] for i, lw in enumerate(layers) for k in lw}
+    sd[EMBED_NAME] = table
+    plm.load_state_dict(sd, strict=True)
+    plm.to("cuda")
+    got = plm.embed_language_tokens(ids.cuda(), prefix_len=T)
+    torch.cuda.synchronize()
+    ref = PO.embed_tokens(ids, table.float(), G.width)
+    assert torch.equal(got.float().cpu(), ref), "token embeddings differ from the oracle's"
+    print("  embeddings equal the oracle's", flush=True)
+    ref_cache = PO.prefill(layers, G, ref, pad)
+    k_ref = torch.cat([k for k, _ in ref_cache], dim=1)
+    v_ref = torch.cat([v for _, v in ref_cache], dim=1)
+    eg = replace(S.ExpertGeometry(), depth=2)
+    w = S.make_weights(eg)
+    x1 = S.make_noise(eg, 1)
+    og = O.geometry_from(eg)
+    act_ref, vs_ref = O.sample_actions(w, og, k_ref, v_ref, pad, x1, steps, O.adarms_table(w, og, steps))
+    model = OpenPi0Inference(OpenPi0InferConfig(num_steps=steps), eg)
+    model.load_state_dict(w)
+    model.to("cuda")
+    model.attach_prefix_lm(plm)
+    obs = Observation(None, None, pad.cuda(), prefix_embs=got)
+    act, vs = model.sample_actions_with_velocities(obs, x1.cuda())
+    torch.cuda.synchronize()
+    for s in range(steps):
+        _close(vs_ref[s], vs[s], f"full-vocabulary chain step {s} velocity")
+    _close(act_ref, act, "full-vocabulary chain actions")
+    model.close()
