@@ -46,21 +46,43 @@ namespace pi05 {
 
 // Phase timestamps for profiling builds (-DPI05_PHASE_TIMESTAMPS): thread 0 of every workgroup
 // records s_memrealtime (100 MHz) at fixed points of every phase of Euler step 1, layers 0..3,
-// into pi05_phase_ts[workgroup][layer*7 + phase][event].  Compiled out otherwise.
+// into pi05_phase_ts[workgroup][layer*7 + phase][event].  The stamps go to LDS while the kernel
+// runs (an LDS write completes in a few cycles, where a global store would hold back the next
+// barrier's implicit vmcnt(0) by its write acknowledgement) and are copied out at kernel exit.
+// Compiled out otherwise.
 #ifdef PI05_PHASE_TIMESTAMPS
 __device__ unsigned long long pi05_phase_ts[256 * 4 * 7 * 16];
+__shared__ unsigned long long pi05_phase_ts_lds[4 * 7 * 16];
 #define PHASE_TS(s, l, ph, ev)                                                                  \
   do {                                                                                          \
     if ((s) == 1 && (l) < 4 && threadIdx.x == 0 && blockIdx.x < 256)                           \
-      pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
+      pi05_phase_ts_lds[((l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime();      \
   } while (0)
 // the same, recorded by the first lane of wave w
 #define PHASE_TS_W(w, s, l, ph, ev)                                                             \
   do {                                                                                          \
     if ((s) == 1 && (l) < 4 && threadIdx.x == 64 * (w) && blockIdx.x < 256)                    \
-      pi05_phase_ts[((size_t)blockIdx.x * 28 + (l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime(); \
+      pi05_phase_ts_lds[((l) * 7 + (ph)) * 16 + (ev)] = __builtin_amdgcn_s_memrealtime();      \
+  } while (0)
+#define PHASE_TS_INIT()                                                                         \
+  do {                                                                                          \
+    for (int i_ = threadIdx.x; i_ < 4 * 7 * 16; i_ += blockDim.x) pi05_phase_ts_lds[i_] = 0;    \
+    __syncthreads();                                                                            \
+  } while (0)
+#define PHASE_TS_FLUSH()                                                                        \
+  do {                                                                                          \
+    __syncthreads();                                                                            \
+    if (blockIdx.x < 256)                                                                       \
+      for (int i_ = threadIdx.x; i_ < 4 * 7 * 16; i_ += blockDim.x)                             \
+        pi05_phase_ts[(size_t)blockIdx.x * 448 + i_] = pi05_phase_ts_lds[i_];                  \
   } while (0)
 #else
+#define PHASE_TS_INIT() \
+  do {                  \
+  } while (0)
+#define PHASE_TS_FLUSH() \
+  do {                   \
+  } while (0)
 #define PHASE_TS(s, l, ph, ev) \
   do {                         \
   } while (0)
@@ -202,8 +224,10 @@ __device__ __forceinline__ void buf_f32(float& v, brsrc r, int off) { v = __uint
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // MFMA steps S2.. of an operand block af[4][KSW]: step s2 reads its NT weight fragments from
-// LDS (wk(t, s2)) and accumulates the four m-tiles.
-template <int KSW, int NT, int S2, int MT, class WK>
+// LDS (wk(t, s2)) and accumulates the four m-tiles.  WT: the products are formed as W . A^T, so
+// lane l ends with output columns 4 (l / 16) .. + 3 of row l % 16 (the A . W form: rows
+// 4 (l / 16) .. + 3 of column l % 16).
+template <int KSW, int NT, int S2, int MT, bool WT = false, class WK>
 __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[MT][NT], bf16x8 (&af)[MT][KSW], WK wk) {
   if constexpr (S2 < KSW) {
     bf16x8 wf[NT];
@@ -212,9 +236,15 @@ __device__ __forceinline__ void mfma_steps(f32x4 (&acc)[MT][NT], bf16x8 (&af)[MT
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[mt][t] = mfma16x16x32(af[mt][S2], wf[t], acc[mt][t]);
-    mfma_steps<KSW, NT, S2 + 1, MT>(acc, af, wk);
+      for (int t = 0; t < NT; ++t)
+        acc[mt][t] = WT ? mfma16x16x32(wf[t], af[mt][S2], acc[mt][t]) : mfma16x16x32(af[mt][S2], wf[t], acc[mt][t]);
+    mfma_steps<KSW, NT, S2 + 1, MT, WT>(acc, af, wk);
   }
+}
+
+// Four bf16 (8 bytes, write-through) at element idx of base (idx a multiple of 4).
+__device__ __forceinline__ void st_bf16x4(u16* base, size_t idx, const u16 (&v)[4]) {
+  st_wt8(base, (uint32_t)(idx * 2), (uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16));
 }
 
 // What every phase's waits and publishes need: this launch's epoch (read from the context's
@@ -830,7 +860,7 @@ __device__ bool phase_io(KArgs& a, int s, float* smem, Sync sy) {
 // =============================================================================================
 template <int MODE, bool G>
 __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
-  constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32, TS = 33;
+  constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32;
   // m-tiles per item: qkv items are one half of a sample's rows (m-tiles 2h, 2h+1), gate_up all four
   constexpr int MT = MODE == kModeQkv ? 2 : 4;
   constexpr int PH = MODE == kModeQkv ? kPhQkv : kPhGu;
@@ -875,24 +905,37 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
     gin = a.gmid + slw * R * kWidth;
     ssin = a.ssmid + slw * kTiles * R;
   }
+  // the products: W . A^T for gate_up and the RoPE pairs (a lane then holds 4 consecutive columns
+  // of one row: GeGLU and RoPE, which pairs column d of the two tiles, are lane-local, and the
+  // stores are 8 bytes), A . W for the v pairs (a lane holds 4 rows of one column in each m-tile:
+  // with the two m-tiles, the 8 keys of one 16-byte chunk of the permuted V layout)
+  const bool wt = MODE != kModeQkv || rotated;
   float* s_rstd = smem + kLdsWork;  // [64] (item rows)
   float* s_bias = s_rstd + 64;      // [32] shift . W^T of the item's two tiles
   float* s_rs = s_bias + 32;        // [3][64] row sums of squares over tiles 22w .. 22w+21
   float* red = s_rs + 192;          // [3 waves][MT m-tiles][NT][64 lanes][4]
-  float* T = red + kCompWaves * MT * NT * 256;  // [16 MT][TS] (item rows)
-  // static operands, loaded ahead of the polls by waves 1 and 2 (wave 0 polls, so it issues
-  // nothing before them): wave 2's qkv tile-1 fragment of k-step 31 (not in LDS), and the RoPE
-  // cos/sin chunks of the first sample for the epilogue threads 64..163 (row, half)
+  // epilogue threads.  gate_up: every thread, m-tile tid / 64, lane tid % 64.  qkv: waves 1 and 2
+  // (wave 0 polls, so it issues nothing ahead of its polls), e = tid - 64: RoPE pairs m-tile e / 64,
+  // lane e % 64; v pairs tile e / 64, lane e % 64 (both m-tiles)
+  const int e = MODE == kModeQkv ? tid - 64 : tid;
+  const bool ep_thread = e >= 0 && e < 64 * (MODE == kModeQkv ? 2 : MT);
+  const int emt = e >> 6, eln = e & 63;
+  const int erow = 16 * emt + (eln & 15);   // W . A^T: the thread's row within the item
+  const int ecol = 4 * (eln >> 4);          // W . A^T: its first column within each tile
+  // static operands, loaded ahead of the polls by waves 1 and 2: wave 2's qkv tile-1 fragment of
+  // k-step 31 (not in LDS), and the RoPE cos/sin of the epilogue thread's row and 4 columns
   bf16x8 w31 = {};
-  u16x8 rcs[4] = {};
-  const int et = tid - 64;  // RoPE epilogue thread: item row et/2, half et%2
-  const bool rope_thread = MODE == kModeQkv && rotated && et >= 0 && et < 2 * nrow;
+  uint32_t rcs[4][2] = {};
+  const bool rope_thread = MODE == kModeQkv && rotated && ep_thread && erow < nrow;
   auto load_rope = [&](int b) {
-    const size_t cr = (size_t)(b * kHorizon + rb + (et >> 1)) * kHeadDim + dt * 16 + (et & 1) * 8;
-    rcs[0] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr);
-    rcs[1] = *reinterpret_cast<const u16x8*>(a.sin_tab + cr);
-    rcs[2] = *reinterpret_cast<const u16x8*>(a.cos_tab + cr + kHalfDim);
-    rcs[3] = *reinterpret_cast<const u16x8*>(a.sin_tab + cr + kHalfDim);
+    const size_t cr = (size_t)(b * kHorizon + rb + erow) * kHeadDim + dt * 16 + ecol;
+    const u16* src[4] = {a.cos_tab + cr, a.sin_tab + cr, a.cos_tab + cr + kHalfDim, a.sin_tab + cr + kHalfDim};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src[k]);
+      rcs[k][0] = v.x;
+      rcs[k][1] = v.y;
+    }
   };
   if constexpr (MODE == kModeQkv) {
     if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(norm_w_tile<kModeQkv>(a, l, 1) + 31 * 512 + lane * 8));
@@ -948,11 +991,13 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
         for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       // zero A for wave 2's surplus step: any finite weights (k-step 31's); qkv tile 1's k-step 31
       // fragment is wave 2's register copy
-      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
+      auto wk = [&](int t, int s2) {
         const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
         if (MODE == kModeQkv && t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
         return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
-      });
+      };
+      if (wt) mfma_steps<KSW, NT, 0, MT, true>(acc, hr, wk);
+      else mfma_steps<KSW, NT, 0, MT, false>(acc, hr, wk);
     }
     if (b == 0) PHASE_TS(s, l, PH, 4);
     __syncthreads();  // every wave is done with region A; the row sums are in LDS
@@ -960,93 +1005,82 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
     if (comp) store_wave_partials<MT, NT>(red, acc, wave, lane);
     if (tid < 16 * MT) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
     __syncthreads();
-    reduce_to_tile<MT, NT, TS>(red, T);
-    __syncthreads();
     if (b == 0) PHASE_TS(s, l, PH, 7);
+    // the three waves' partials of this thread's accumulator positions, added in wave order
+    auto wave_sum = [&](int mt, int t) {
+      f32x4 r[kCompWaves];
+#pragma unroll
+      for (int w = 0; w < kCompWaves; ++w) r[w] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * MT + mt) * NT + t) * 64 + eln) * 4);
+      return (r[0] + r[1]) + r[2];
+    };
     if constexpr (MODE == kModeQkv) {
       if (rotated) {
         // (x*cos) + (rotate_half(x)*sin), rotate_half(x) = cat(-x_hi, x_lo), from the bf16
-        // GEMM values (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216); chunk
-        // (row, half): 8 dims d and their partners d + 128
+        // GEMM values (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216): dims d .. d + 3
+        // of tile 0 and their partners d + 128 .. of tile 1
         if (rope_thread) {
-          const int row = et >> 1, half = et & 1;
           if (b > 0) load_rope(b);
-          const u16x8 cs_lo = rcs[0], sn_lo = rcs[1], cs_hi = rcs[2], sn_hi = rcs[3];
-          const float rstd = s_rstd[row];
-          float tl[8], th[8], bl[8], bh[8];
+          const f32x4 ylo = wave_sum(emt, 0), yhi = wave_sum(emt, 1);
+          const float rstd = s_rstd[erow];
+          u16 olo[4], ohi[4];
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            tl[q] = T[row * TS + half * 8 + q];
-            th[q] = T[row * TS + 16 + half * 8 + q];
-            bl[q] = s_bias[half * 8 + q];
-            bh[q] = s_bias[16 + half * 8 + q];
+          for (int q = 0; q < 4; ++q) {
+            const auto half16 = [&](int k) { return bf2f((u16)(rcs[k][q >> 1] >> (16 * (q & 1)))); };
+            const float x_lo = round_bf(__builtin_fmaf(rstd, ylo[q], s_bias[ecol + q]));
+            const float x_hi = round_bf(__builtin_fmaf(rstd, yhi[q], s_bias[16 + ecol + q]));
+            olo[q] = f2bf(fsub(fmul(x_lo, half16(0)), fmul(x_hi, half16(1))));
+            ohi[q] = f2bf(fadd(fmul(x_hi, half16(2)), fmul(x_lo, half16(3))));
           }
-          sched_fence();
-          u16 olo[8], ohi[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float x_lo = round_bf(__builtin_fmaf(rstd, tl[q], bl[q]));
-            const float x_hi = round_bf(__builtin_fmaf(rstd, th[q], bh[q]));
-            olo[q] = f2bf(fsub(fmul(x_lo, bf2f(cs_lo[q])), fmul(x_hi, bf2f(sn_lo[q]))));
-            ohi[q] = f2bf(fadd(fmul(x_hi, bf2f(cs_hi[q])), fmul(x_lo, bf2f(sn_hi[q]))));
-          }
-          const int d = dt * 16 + half * 8;
+          const int d = dt * 16 + ecol, r = rb + erow;
           if (head < kHeads) {
             u16* qs = a.q + slw * (size_t)R * kQRowsPerTok * kHeadDim;
-            const int qrow = (m0 + rb + row) * kQRowsPerTok + head;
-            st_bf16x8(qs, afrag_index(qrow, d, kHeadDim / 32), olo);
-            st_bf16x8(qs, afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
+            const int qrow = (m0 + r) * kQRowsPerTok + head;
+            st_bf16x4(qs, afrag_index(qrow, d, kHeadDim / 32), olo);
+            st_bf16x4(qs, afrag_index(qrow, d + kHalfDim, kHeadDim / 32), ohi);
           } else {
             u16* kc = a.ksuf + (slw * a.batch + b) * 64 * kHeadDim;
-            st_bf16x8(kc, kfrag_index(rb + row, d), olo);
-            st_bf16x8(kc, kfrag_index(rb + row, d + kHalfDim), ohi);
+            st_bf16x4(kc, kfrag_index(r, d), olo);
+            st_bf16x4(kc, kfrag_index(r, d + kHalfDim), ohi);
           }
         }
-      } else if (comp) {
-        // v: chunk -> (dim dcol of the tile pair, key group (kb, g) of the permuted V fragment);
-        // this item's rows are the keys of 32-key block kb = mh
-        for (int ci = tid; ci < 128; ci += kCompThreads) {
-          const int dcol = ci & 31, kb = mh, gg = ci >> 5;
-          u16 v8[8];
+      } else if (ep_thread) {
+        // v (A . W): this thread = tile e / 64, lane e % 64 -> column dcol of the tile pair, rows
+        // 4 g .. 4 g + 3 of both m-tiles (g = lane / 16): the keys of chunk (kb = mh, g) of the
+        // permuted V fragment, in its order (vkey); keys past the 50 action tokens are zero
+        const int t = emt, g = eln >> 4, dcol = t * 16 + (eln & 15);
+        const f32x4 y0 = wave_sum(0, t), y1 = wave_sum(1, t);
+        u16 v8[8];
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int key = vkey(kb, gg, q);  // key rb + (key - rb) of the sample
-            v8[q] = key < kHorizon ? f2bf(__builtin_fmaf(s_rstd[key - rb], T[(key - rb) * TS + dcol], s_bias[dcol])) : (u16)0;
-          }
-          const int dv = (tile0 - 144) * 16 + dcol;
-          u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
-          st_bf16x8(vc, ((size_t)kb * 16 + (dv >> 4)) * 512 + (size_t)(gg * 16 + (dv & 15)) * 8, v8);
+        for (int q = 0; q < 8; ++q) {
+          const int row = (q < 4 ? 0 : 16) + 4 * g + (q & 3);  // vkey(mh, g, q) - rb
+          const float y = q < 4 ? y0[q] : y1[q - 4];
+          v8[q] = rb + row < kHorizon ? f2bf(__builtin_fmaf(s_rstd[row], y, s_bias[dcol])) : (u16)0;
         }
+        const int dv = (tile0 - 144) * 16 + dcol;
+        u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
+        st_bf16x8(vc, ((size_t)mh * 16 + (dv >> 4)) * 512 + (size_t)(g * 16 + (dv & 15)) * 8, v8);
       }
     } else {
       // GeGLU as the fused reference kernel defines it: bf16(gelu_tanh(bf16(g)) * u), u the fp32
-      // accumulator (rlinf_fused_denoise.py:166-173); chunk = (row, half of the 16 columns)
-      if (tid < 2 * kHorizon) {
-        const int row = tid >> 1, half = tid & 1;
-        const float rstd = s_rstd[row];
-        float tg[8], tu[8], bg[8], bu[8];
+      // accumulator (rlinf_fused_denoise.py:166-173): columns ecol .. ecol + 3 of gate tile j and
+      // of up tile j, row erow
+      if (ep_thread && erow < kHorizon) {
+        const f32x4 yg = wave_sum(emt, 0), yu = wave_sum(emt, 1);
+        const float rstd = s_rstd[erow];
+        u16 o4[4];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          tg[q] = T[row * TS + half * 8 + q];
-          tu[q] = T[row * TS + 16 + half * 8 + q];
-          bg[q] = s_bias[half * 8 + q];
-          bu[q] = s_bias[16 + half * 8 + q];
+        for (int q = 0; q < 4; ++q) {
+          const float gt = round_bf(__builtin_fmaf(rstd, yg[q], s_bias[ecol + q]));
+          const float up = __builtin_fmaf(rstd, yu[q], s_bias[16 + ecol + q]);
+          o4[q] = f2bf(fmul(gelu_tanh(gt), up));
         }
-        sched_fence();
-        u16 o8[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float gt = round_bf(__builtin_fmaf(rstd, tg[q], bg[q]));
-          const float up = __builtin_fmaf(rstd, tu[q], bu[q]);
-          o8[q] = f2bf(fmul(gelu_tanh(gt), up));
-        }
-        st_bf16x8(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + row, tile0 * 16 + half * 8, kMlp / 32), o8);
+        st_bf16x4(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + erow, tile0 * 16 + ecol, kMlp / 32), o4);
       }
     }
-    __syncthreads();  // T and s_rstd are reused by the next sample
+    if (b + 1 < a.batch) __syncthreads();  // red and s_rstd are reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
-  publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
+  publish(a, flag_base(a, s, l, PH) + item, sy.epoch, MODE != kModeQkv);  // gate_up: the copy wave stored rows
   PHASE_TS(s, l, PH, 6);
   return true;
 }
@@ -3263,6 +3297,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
   __shared__ int s_flag;
   // this launch's epoch: one past the last finished launch's
   const Sync sy{(unsigned)__builtin_amdgcn_readfirstlane(ld_u32(args.err + kCtlEpoch)) + 1u, &s_flag};
+  PHASE_TS_INIT();
   // the copy wave: step 0, layer 0 qkv and o_proj weights
   copy_norm_w<kModeQkv, 0, 32, G>(kargs(), 0, 0, smem);
   copy_norm_w<kModeQkv, 0, 31, G>(kargs(), 0, 1, smem);
@@ -3289,6 +3324,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
   wait_vmcnt<0>();
+  PHASE_TS_FLUSH();
   leave_launch(kargs(), sy);
 }
 
