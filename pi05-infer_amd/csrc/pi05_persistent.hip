@@ -2395,7 +2395,7 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   // waves 1 and 2 hold the tile's weights (K halves) and do the MFMA; wave 0 only polls, so
   // nothing it issued before its polls (a wave's vector memory operations complete in issue
   // order) delays seeing the merges; wave 1 also runs the residual epilogue
-  constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / 2, TS = 17;
+  constexpr int KSTEPS = kHeads * kHeadDim / 32, KSW = KSTEPS / 2;
   constexpr int NCH = 4;  // independent accumulation chains per wave
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = (unsigned)wg_id();
@@ -2415,20 +2415,16 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
 #pragma unroll
     for (int s2 = 0; s2 < KSW; ++s2) buf_frag(wf[s2], rw, ((ks0 + s2) * 512 + lane * 8) * 2);
   }
-  // epilogue threads (wave 1, lanes 0..31): row et/2 of the m-tile, columns (et%2)*8 .. +7; gate
-  // and 1 + scale ahead of the polls
-  const int et = tid - 64, erow = et >> 1, ec0 = (et & 1) * 8;
-  const bool ep_thread = et >= 0 && et < 32;
+  // the products are formed as W . A^T, so lane l ends with columns ec = 4 (l / 16) .. + 3 of row
+  // l % 16; the epilogue is wave 1's, lane-local: gate and 1 + scale of its 4 columns ahead of
+  // the polls
+  const bool ep_wave = wave == 1;
+  const int erow = r16, ec = 4 * (lane >> 4);
   const u16* hres = a.h + ((size_t)s * (L + 1) + l) * R * kWidth;
-  float4 g4[2] = {}, s14[2] = {};
-  if (ep_thread) {
-    const float* gmod = a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + ec0;
-    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + ec0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
-      s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
-    }
+  float4 g4 = {}, s14 = {};
+  if (ep_wave) {
+    g4 = *reinterpret_cast<const float4*>(a.table + ((size_t)s * NN + 2 * l) * kModW + 2 * kWidth + col + ec);
+    s14 = *reinterpret_cast<const float4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 1) * kModW + col + ec);
   }
   PHASE_TS(s, l, kPhO, 1);
   const u16* act = a.o + slw * (size_t)R * (KSTEPS * 32);
@@ -2436,12 +2432,9 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   u16* gout = a.gmid + slw * (size_t)R * kWidth;
   float* rout = a.ssmid + slw * kTiles * R;
   const unsigned* fmerge = flag_base(a, s, l, kPhMerge);
-  float* red = smem + kLdsWork;         // [2 MFMA waves][64 lanes][4]
-  float* T = red + 2 * 256;             // [16][TS]
-  float* s_ss = T + 16 * TS;            // [2 halves][16 rows]
-  const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
-                         round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
-  const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
+  float* red = smem + kLdsWork;  // [2 MFMA waves][64 lanes][4]
+  const float gate[4] = {round_bf(g4.x), round_bf(g4.y), round_bf(g4.z), round_bf(g4.w)};
+  const float s1[4] = {s14.x, s14.y, s14.z, s14.w};
   for (int b = 0; b < a.batch; ++b) {
     const int m = 4 * b + mq;  // m-tile of the activations
     // merge flags 4 * bp + hp: the m-tile's row blocks bp = 25 b + 8 mq .. are one contiguous run
@@ -2450,8 +2443,8 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
     // the residual rows: the merges waited for imply every earlier phase of the layer, so the
     // previous layer's down_proj has written them (this workgroup may have had no qkv item)
     const int r = 16 * m + erow;
-    u16x8 hold = {};
-    if (ep_thread && erow < nrow) hold = *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + ec0, kWidth / 32));
+    uint2 hold = {0u, 0u};
+    if (ep_wave && erow < nrow) hold = *reinterpret_cast<const uint2*>(hres + afrag_index(r, col + ec, kWidth / 32));
     if (mw) {
       const brsrc ra = make_rsrc(act, (size_t)R * KSTEPS * 64);
       bf16x8 af[KSW];
@@ -2465,37 +2458,36 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
 #pragma unroll
       for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s2 = 0; s2 < KSW; ++s2) acc[s2 % NCH] = mfma16x16x32(af[s2], wf[s2], acc[s2 % NCH]);
+      for (int s2 = 0; s2 < KSW; ++s2) acc[s2 % NCH] = mfma16x16x32(wf[s2], af[s2], acc[s2 % NCH]);
       *reinterpret_cast<f32x4*>(red + ((size_t)(wave - 1) * 64 + lane) * 4) = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     }
     if (b == 0) PHASE_TS(s, l, kPhO, 4);
     __syncthreads();
-    // the two K halves in order, scattered row-major into T (thread tid < 64: lane tid of the D fragment)
-    if (tid < 64) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(red + (size_t)tid * 4) + *reinterpret_cast<const f32x4*>(red + (size_t)(64 + tid) * 4);
+    if (ep_wave) {
+      // the two K halves in order, then h = bf16(h + bf16(bf16(y) * gate)), g = bf16(h * (1 + scale))
+      // and the row's sum of squares over the tile's 16 columns (the four lanes of the row)
+      const f32x4 y = *reinterpret_cast<const f32x4*>(red + (size_t)lane * 4) + *reinterpret_cast<const f32x4*>(red + (size_t)(64 + lane) * 4);
+      float ss = 0.f;
+      if (erow < nrow) {
+        u16 hn[4], gn[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) T[((tid >> 4) * 4 + i) * TS + (tid & 15)] = v[i];
-    }
-    __syncthreads();
-    float ss = 0.f;
-    if (ep_thread && erow < nrow) {
-      u16 hn[8], gn[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float prod = round_bf(fmul(round_bf(T[erow * TS + ec0 + i]), gate[i]));
-        hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
-        const float hf = bf2f(hn[i]);
-        gn[i] = f2bf(fmul(hf, s1[i]));
-        ss += hf * hf;
+        for (int i = 0; i < 4; ++i) {
+          const u16 hb = (u16)((i < 2 ? hold.x : hold.y) >> (16 * (i & 1)));
+          const float prod = round_bf(fmul(round_bf(y[i]), gate[i]));
+          hn[i] = f2bf(fadd(bf2f(hb), prod));
+          const float hf = bf2f(hn[i]);
+          gn[i] = f2bf(fmul(hf, s1[i]));
+          ss += hf * hf;
+        }
+        st_bf16x4(hout, afrag_index(r, col + ec, kWidth / 32), hn);
+        st_bf16x4(gout, afrag_index(r, col + ec, kWidth / 32), gn);
       }
-      st_bf16x8(hout, afrag_index(r, col + ec0, kWidth / 32), hn);
-      st_bf16x8(gout, afrag_index(r, col + ec0, kWidth / 32), gn);
+      ss += __shfl_xor(ss, 16);
+      ss += __shfl_xor(ss, 32);
+      // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
+      if (lane < 16) st_f32(rout + (size_t)nt * R + 16 * m + lane, ss);
     }
-    if (ep_thread) s_ss[(et & 1) * 16 + erow] = ss;
-    __syncthreads();
-    // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
-    if (tid < 16) st_f32(rout + (size_t)nt * R + 16 * m + tid, s_ss[tid] + s_ss[16 + tid]);
-    __syncthreads();  // red, T and s_ss are reused by the next sample
+    if (b + 1 < a.batch) __syncthreads();  // red is reused by the next sample
   }
   PHASE_TS(s, l, kPhO, 5);
   publish(a, flag_base(a, s, l, kPhO) + item, sy.epoch);
@@ -2503,6 +2495,7 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   return true;
 }
 
+// =============================================================================================
 // o_proj of both batch instances: one wait for every sample's merges (which finish in one pass of
 // the grid), then two wave pairs, (1, 2) and (0, 3), each holding the tile's weights in K halves
 // (wave 1 / 0: k-steps 0..31, wave 2 / 3: 32..63), take samples 2i and 2i + 1 of iteration i side
