@@ -2803,8 +2803,9 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
   // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
   // gate and 1 + scale: loaded by waves 0 and 1 right after the polls, used much later
   const u16* hres = a.hmid + slw * (size_t)R * kWidth;
+  // finisher thread: row, first of its 8 columns (the two halves of a row in adjacent lanes)
   const bool fin_thread = ksp == 0 && tid < 128;
-  const int frow = tid & 63, fc0 = ((tid >> 6) & 1) * 8;  // finisher thread: row, first of its 8 columns
+  const int frow = (tid & 127) >> 1, fc0 = (tid & 1) * 8;
   u16x8 hpre = {};
   if (fin_thread) {
     const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
@@ -2884,7 +2885,6 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
     const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
                            round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
     const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
-    float* s_ss = T + 64 * TS;  // [2 halves][64 rows]
     for (int b = 0; b < a.batch; ++b) {
       const int r = b * kRowsPerSample + frow;
       float ss = 0.f;
@@ -2916,11 +2916,9 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
         st_bf16x8(hout, afrag_index(r, col + fc0, kWidth / 32), hn);
         if (next_g) st_bf16x8(gout, afrag_index(r, col + fc0, kWidth / 32), gn);
       }
-      if (fin_thread) s_ss[(fc0 >> 3) * 64 + frow] = ss;
-      __syncthreads();
-      // tile-major statistics: this tile's sums of the sample's 64 rows are one 256-byte run
-      if (tid < 64) st_f32(rout + (size_t)nt * R + r, s_ss[frow] + s_ss[64 + frow]);
-      __syncthreads();  // s_ss is reused by the next sample
+      // tile-major statistics: this tile's sum of the row, columns 0..7 then 8..15 (lanes 2 i, 2 i + 1)
+      const float ss_hi = __shfl_xor(ss, 1);
+      if (fin_thread && fc0 == 0) st_f32(rout + (size_t)nt * R + r, ss + ss_hi);
     }
   }
   PHASE_TS(s, l, PH, 8);
