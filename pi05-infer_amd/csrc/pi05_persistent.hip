@@ -2174,8 +2174,19 @@ __device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
     PHASE_TS(s, l, kPhSplit, 2);
     if (!attn_group_items(a, s, l, smem, sy)) return false;
   }
-  for (int item = attn_grouped<G>(a) ? n_items : wg_id(); item < n_items; item += (unsigned)wg_count()) {
-    const int bp = item % nbp, split = item / nbp;
+  // One sample with 9 key splits (prefixes of 961..1056 keys): split s < 8 of every row block runs
+  // on workgroup 8 bp + s (XCD s, up to the dispatcher's rotation), split 8 of row block bp on
+  // workgroup 8 (25 + bp / 8) + bp mod 8, so each XCD fetches two splits' prefix keys into its L2
+  // instead of all nine (measured on MI355X: the same time per predict, ~1.1 GB less traffic)
+  const bool xcd_splits = !G && nsplit == 9 && nbp == kPairs;
+  for (int item = attn_grouped<G>(a) ? n_items : wg_id(); item < (xcd_splits ? 256 : n_items); item += (unsigned)wg_count()) {
+    int bp = item % nbp, split = item / nbp;
+    if (xcd_splits) {
+      const int x = item & 7, j = item >> 3;
+      split = j < kPairs ? x : 8;
+      bp = j < kPairs ? j : 8 * (j - kPairs) + x;
+      if (bp >= kPairs) continue;
+    }
     const int b = bp / kPairs, pair = bp % kPairs;
     const int rbq = b * (kRowsPerSample / 2) + pair;  // query-row m-tile (16 rows = 2 tokens x 8 heads)
     const u16* kpre = a.kpre + ((size_t)l * a.batch + b) * a.s_pre * kHeadDim;
