@@ -958,7 +958,8 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   }
   PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
-  for (int b = 0; b < a.batch; ++b) {
+  {
+    constexpr int b = 0;  // one sample: the batch instances have their own qkv and gate_up
     const int m0 = b * kRowsPerSample;
     // the row statistics first (wave w: tiles 22w .. 22w+21, lane = item row), then the A
     // fragments (k-step 32 of wave 2 and the padded rows read as zeros), all without branches
@@ -1019,7 +1020,6 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
         // GEMM values (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216): dims d .. d + 3
         // of tile 0 and their partners d + 128 .. of tile 1
         if (rope_thread) {
-          if (b > 0) load_rope(b);
           const f32x4 ylo = wave_sum(emt, 0), yhi = wave_sum(emt, 1);
           const float rstd = s_rstd[erow];
           u16 olo[4], ohi[4];
@@ -1077,148 +1077,10 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
         st_bf16x4(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + erow, tile0 * 16 + ecol, kMlp / 32), o4);
       }
     }
-    if (b + 1 < a.batch) __syncthreads();  // red and s_rstd are reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
   publish(a, flag_base(a, s, l, PH) + item, sy.epoch, MODE != kModeQkv);  // gate_up: the copy wave stored rows
   PHASE_TS(s, l, PH, 6);
-  return true;
-}
-
-// =============================================================================================
-// gate_up at B > 1: two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from registers) for the
-// samples [b0, b1) of half w / 128 (see gu_pair0).  Per sample the three compute waves split K
-// (11 | 11 | 10 k-steps) over four m-tiles and four tiles; the pairs are then reduced and written
-// in turn with the same epilogue as phase_norm_gemm<kModeGateUp>.  The flag of item w covers both
-// pairs and the half's samples.
-// =============================================================================================
-template <bool G>
-__device__ bool phase_gateup_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
-  constexpr int NT = 4, KSW = 11, KSTEPS = kWidth / 32, TS = 33, MT = 4;
-  const int L = a.depth, R = a.R;
-  const int item = wg_id();
-  PHASE_TS(s, l, kPhGu, 0);
-  // copy wave: pair p0's weights (region A) and everything issued before them have landed; with
-  // grouped attention (which used region B) down(l)'s weights go to B now
-  if (copy_wave()) {
-    wait_vmcnt<0>();
-    if (attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);
-  }
-  const int half = item / (kGuItems / 2), p0 = gu_pair0(a), p1 = p0 + 1;
-  const int bh = (a.batch + 1) / 2, b0 = half * bh, b1 = b0 + bh < a.batch ? b0 + bh : a.batch;
-  if (item >= kGuItems) return true;
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
-  const bool comp = tid < kCompThreads;
-  const int r16 = lane & 15;
-  const int ks0 = wave * KSW;  // this wave's k-steps [ks0, ks0 + KSW) (wave 2: the last one past K)
-  const size_t slw = (size_t)s * L + l;
-  const u16* gin = a.gmid + slw * R * kWidth;
-  const float* ssin = a.ssmid + slw * kTiles * R;
-  const float* bias = a.bias + slw * kBiasCols;
-  float* s_rstd = smem + kLdsWork;  // [64] (sample rows)
-  float* s_bias = s_rstd + 64;      // [64] shift . W^T: gate p0, up p0, gate p1, up p1 (16 each)
-  float* s_rs = s_bias + 64;        // [3][64]
-  float* red = s_rs + 192;          // [3 waves][4 m-tiles][2 tiles][64 lanes][4] (one pair at a time)
-  float* T = red + kCompWaves * MT * 2 * 256;  // [64][TS]
-  // pair p1's weight fragments of this wave's k-steps (gate, up): waves 1 and 2 ahead of the
-  // polls, wave 0 (which polls) after them
-  const u16* wl = a.wpack + (size_t)l * kLayerElems;
-  bf16x8 w1[2][KSW];
-  auto load_w1 = [&]() {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s2 = 0; s2 < KSW; ++s2) {
-        const int ks = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;  // the surplus step multiplies zeros
-        w1[t][s2] = *reinterpret_cast<const bf16x8*>(wl + (t == 0 ? kOffGate : kOffUp) + ((size_t)p1 * KSTEPS + ks) * 512 + lane * 8);
-      }
-  };
-  if (wave == 1 || wave == 2) load_w1();
-  if (tid >= 64 && tid < 128) {
-    const int c = tid - 64, pr = c >> 5, gu = (c >> 4) & 1, n = c & 15;
-    s_bias[c] = bias[kQkvCols + gu * kMlp + (p0 + pr) * 16 + n];
-  }
-  PHASE_TS(s, l, kPhGu, 1);
-  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, sy)) return false;
-  PHASE_TS(s, l, kPhGu, 2);
-  if (wave == 0) load_w1();
-  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
-  for (int b = b0; b < b1; ++b) {
-    const int m0 = b * kRowsPerSample;
-    f32x4 acc[MT][NT];
-    if (comp) {
-      const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
-      const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
-      float st[22];
-#pragma unroll
-      for (int t = 0; t < 22; ++t) {
-        const int tile = 22 * wave + t;
-        buf_f32(st[t], rsrc_s, tile < kTiles ? ((tile * R + m0 + lane) * 4) : kOob);
-      }
-      bf16x8 hr[MT][KSW];
-#pragma unroll
-      for (int s2 = 0; s2 < KSW; ++s2)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const bool ok = r16 < kHorizon - mt * 16 && ks0 + s2 < KSTEPS;
-          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
-        }
-      sched_fence();
-      float v = 0.f;
-#pragma unroll
-      for (int t = 0; t < 22; ++t) v += st[t];
-      s_rs[wave * 64 + lane] = v;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mfma_steps<KSW, NT, 0, MT>(acc, hr, [&](int t, int s2) {
-        if (t >= 2) return w1[t - 2][s2];
-        const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
-        return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
-      });
-    }
-    __syncthreads();  // the row sums are in LDS
-    if (tid < 64) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
-#pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-      if (comp) {
-        f32x4 accp[MT][2];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) accp[mt][0] = acc[mt][2 * pr], accp[mt][1] = acc[mt][2 * pr + 1];
-        store_wave_partials<MT, 2>(red, accp, wave, lane);
-      }
-      __syncthreads();
-      reduce_to_tile<MT, 2, TS>(red, T);
-      __syncthreads();
-      // GeGLU (rlinf_fused_denoise.py:166-173) of pair p0 + pr; chunk = (row, half of 16 columns)
-      if (tid < 2 * kHorizon) {
-        const int row = tid >> 1, hf = tid & 1;
-        const float rstd = s_rstd[row];
-        float tg[8], tu[8], bgv[8], buv[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          tg[q] = T[row * TS + hf * 8 + q];
-          tu[q] = T[row * TS + 16 + hf * 8 + q];
-          bgv[q] = s_bias[32 * pr + hf * 8 + q];
-          buv[q] = s_bias[32 * pr + 16 + hf * 8 + q];
-        }
-        sched_fence();
-        u16 o8[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float gt = round_bf(__builtin_fmaf(rstd, tg[q], bgv[q]));
-          const float up = __builtin_fmaf(rstd, tu[q], buv[q]);
-          o8[q] = f2bf(fmul(gelu_tanh(gt), up));
-        }
-        st_bf16x8(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + row, (p0 + pr) * 16 + hf * 8, kMlp / 32), o8);
-      }
-      __syncthreads();  // red and T are reused
-    }
-  }
-  PHASE_TS(s, l, kPhGu, 5);
-  publish(a, flag_base(a, s, l, kPhGu) + item, sy.epoch);
-  PHASE_TS(s, l, kPhGu, 6);
   return true;
 }
 
@@ -1669,10 +1531,12 @@ __device__ bool phase_qkv_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
 }
 
 // =============================================================================================
-// gate_up at B = 2 (kernel instance 1): phase_gateup_pairs' items, with the copy wave as a fourth
-// compute wave (its down_proj copy is issued before o_proj instead): K splits 8 k-steps per wave, so
-// a sample's 48 loads per wave stay under the 63 a wave may have in flight and each wave runs 128
-// MFMAs per sample instead of 176; the four partials are added in wave order.
+// gate_up at B = 2 (kernel instance 1): item w computes gate/up tile pairs 2g and 2g + 1,
+// g = w mod 128 (pair 2g from region A, 2g + 1 from registers), for sample half w / 128 (see
+// gu_pair0), with the copy wave as a fourth compute wave (its down_proj copy is issued before
+// o_proj instead): K splits 8 k-steps per wave, so a sample's 48 loads per wave stay under the 63
+// a wave may have in flight and each wave runs 128 MFMAs per sample instead of 176 (three waves);
+// the four partials are added in wave order.
 // =============================================================================================
 __device__ bool phase_gateup_pairs4(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NW = 4, NT = 4, KSW = 8, KSTEPS = kWidth / 32, TS = 33, MT = 4, TPW = kTiles / NW;
@@ -2446,7 +2310,8 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   float* red = smem + kLdsWork;  // [2 MFMA waves][64 lanes][4]
   const float gate[4] = {round_bf(g4.x), round_bf(g4.y), round_bf(g4.z), round_bf(g4.w)};
   const float s1[4] = {s14.x, s14.y, s14.z, s14.w};
-  for (int b = 0; b < a.batch; ++b) {
+  {
+    constexpr int b = 0;  // one sample: the batch instances run phase_oproj_pairs / phase_oproj_msplit
     const int m = 4 * b + mq;  // m-tile of the activations
     // merge flags 4 * bp + hp: the m-tile's row blocks bp = 25 b + 8 mq .. are one contiguous run
     if (!wait_flags(a, fmerge + 4 * (b * kPairs + 8 * mq), 4 * np, sy)) return false;
@@ -2498,7 +2363,6 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
       // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
       if (lane < 16) st_f32(rout + (size_t)nt * R + 16 * m + lane, ss);
     }
-    if (b + 1 < a.batch) __syncthreads();  // red is reused by the next sample
   }
   PHASE_TS(s, l, kPhO, 5);
   publish(a, flag_base(a, s, l, kPhO) + item, sy.epoch);
@@ -2801,14 +2665,8 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
   const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
   PHASE_TS(s, l, PH, 1);
   {
-    // the gate_up items of this quarter's 1024 activation columns: pairs 64 ksp .. 64 ksp + 63,
-    // i.e. items 64 ksp .. at B = 1 and, at B > 1, items 32 ksp .. of both sample halves
-    const unsigned* fgu = flag_base(a, s, l, kPhGu);
-    if (a.batch > 1) {
-      if (!wait_flags(a, fgu + ksp * 32, 32, sy) || !wait_flags(a, fgu + kGuItems / 2 + ksp * 32, 32, sy)) return false;
-    } else if (!wait_flags(a, fgu + ksp * 64, 64, sy)) {
-      return false;
-    }
+    // the gate_up items of this quarter's 1024 activation columns: items 64 ksp .. 64 ksp + 63
+    if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, sy)) return false;
   }
   PHASE_TS(s, l, PH, 2);
   // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
@@ -2834,9 +2692,10 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
   float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;
   float* red = smem + kLdsWork;
   float* T = red + kCompWaves * 4 * 256;  // [64][TS], then the finisher's [2][64] row sums
-  const bool own_lds = ksp == 0 && a.batch == 1;  // the finisher keeps its own partial in T
+  const bool own_lds = ksp == 0;  // the finisher keeps its own partial in T
   const int r16 = lane & 15;
-  for (int b = 0; b < a.batch; ++b) {
+  {
+    constexpr int b = 0;  // one sample: the batch instances run phase_down_pairs / phase_down_msplit
     if (comp) {
       // padded rows and the k-steps past the quarter read as zeros (no branches)
       const brsrc rsrc_a = make_rsrc(act, (size_t)R * KSTEPS * 32 * 2);
@@ -2874,7 +2733,6 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
                  u32x4{__float_as_uint(tr[0]), __float_as_uint(tr[1]), __float_as_uint(tr[2]), __float_as_uint(tr[3])});
       }
     }
-    if (!own_lds || b + 1 < a.batch) __syncthreads();  // T is reused by the next sample
   }
   PHASE_TS(s, l, PH, 5);
   unsigned* fl = flag_base(a, s, l, PH);
@@ -2883,7 +2741,7 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
     publish_local(a, fl + kPartFlags + 4 * nt + (ksp - 1), sy.epoch);
     return true;
   }
-  // ---- the finisher (quarter 0): its own partial stays in LDS at B = 1; it waits for the other
+  // ---- the finisher (quarter 0): its own partial stays in LDS; it waits for the other
   // three, adds the four in quarter order and writes the tile.  Waves 0 and 1: lane = row,
   // columns half*8 .. +7.
   if (!own_lds && comp) wait_stores();  // its own partials, reloaded below
@@ -2896,7 +2754,8 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
     const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
                            round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
     const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
-    for (int b = 0; b < a.batch; ++b) {
+    {
+      constexpr int b = 0;
       const int r = b * kRowsPerSample + frow;
       float ss = 0.f;
       if (fin_thread && frow < kHorizon) {
@@ -2913,7 +2772,7 @@ __device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
             pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
           }
         }
-        const u16x8 hold = b == 0 ? hpre : *reinterpret_cast<const u16x8*>(hres + afrag_index(r, col + fc0, kWidth / 32));
+        const u16x8 hold = hpre;
         u16 hn[8], gn[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -3317,11 +3176,10 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
             : G                         ? phase_oproj_pairs(kargs(), s, l, smem, sy)
                                         : phase_oproj(kargs(), s, l, smem, sy)) &&
            (G ? (gu_msplit<G>(kargs()) ? phase_gateup_msplit(kargs(), s, l, smem, sy) : phase_gateup_pairs4(kargs(), s, l, smem, sy))
-              : (kargs().batch > 1 ? phase_gateup_pairs<G>(kargs(), s, l, smem, sy)
-                                   : phase_norm_gemm<kModeGateUp, G>(kargs(), s, l, smem, sy))) &&
+              : phase_norm_gemm<kModeGateUp, G>(kargs(), s, l, smem, sy)) &&
            (G && PI05_INSTANCE_GROUPED ? phase_down_msplit(kargs(), s, l, smem, sy)
-            : (G || kargs().batch > 1) ? phase_down_pairs<G>(kargs(), s, l, smem, sy)
-                                       : phase_down(kargs(), s, l, smem, sy));
+            : G                         ? phase_down_pairs<G>(kargs(), s, l, smem, sy)
+                                        : phase_down(kargs(), s, l, smem, sy));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released
