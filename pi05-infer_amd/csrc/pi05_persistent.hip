@@ -134,7 +134,12 @@ typedef __amdgpu_buffer_rsrc_t brsrc;
 constexpr int kOob = 0x7fffff00;  // an offset past every resource
 constexpr int kAuxNt = 2;         // buffer-instruction cache-policy bits: nt (non-temporal)
 __device__ __forceinline__ brsrc make_rsrc(const void* base, size_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  // the size and flag words pass through empty asm statements so that the compiler builds them
+  // where the resource is used: hoisted out of the step / layer loops as loop-invariant
+  // constants, dozens of them would stay live across every phase and be spilled
+  int nrec = (int)bytes, flags = 0x00020000;
+  asm volatile("" : "+s"(nrec), "+s"(flags));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nrec, flags);
 }
 // A pointer every lane holds the same value of, moved to scalar registers.
 template <class T>
@@ -193,7 +198,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__device__ __forceinline__ bool copy_wave() { return threadIdx.x >= kCompThreads; }
+__device__ __forceinline__ bool copy_wave() { return phase_tid() >= kCompThreads; }
 
 // s_waitcnt vmcnt(0) that is also a compiler barrier for memory operations: every store issued
 // before it in program order stays before it, so its completion is what the wait observes.
@@ -353,8 +358,8 @@ __device__ void leave_launch(KArgs& a, Sync sy) {
 // barrier; returns false (uniformly) after a timeout or another workgroup's error.
 __device__ bool wait_flags(KArgs& a, const unsigned* f, int n, Sync sy) {
   f += (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+  if (phase_tid() < 64) {
+    const int lane = phase_tid();
     const unsigned ep = sy.epoch;
     int ok = 1;
     // one coherent (sc1) 16-byte poll in flight at a time: measured on MI355X, keeping a second
@@ -392,8 +397,8 @@ __device__ bool wait_flags(KArgs& a, const unsigned* f, int n, Sync sy) {
 // per sample would cost a memory round trip each.
 __device__ bool wait_flag_runs(KArgs& a, const unsigned* f, int n, int stride, int cnt, Sync sy) {
   f += (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
+  if (phase_tid() < 64) {
+    const int lane = phase_tid();
     const unsigned ep = sy.epoch;
     const int cpr = (n + 3) >> 2, nch = cpr * cnt;  // 4-word chunks per run, in all
     int ok = 1;
@@ -431,7 +436,8 @@ __device__ bool wait_flag_runs(KArgs& a, const unsigned* f, int n, int stride, i
 __device__ __forceinline__ void publish(KArgs& a, unsigned* flag, unsigned epoch, bool copy_stores = false) {
   if (!copy_wave() || copy_stores) wait_stores();
   wg_barrier();
-  if (threadIdx.x < kFlagCopies) st_u32(flag + (size_t)threadIdx.x * a.fstride, epoch);
+  const int t = phase_tid();
+  if (t < kFlagCopies) st_u32(flag + (size_t)t * a.fstride, epoch);
 }
 
 // The same for a flag that only workgroups of this XCD poll, after data stored with st_l2_16:
@@ -440,7 +446,7 @@ __device__ __forceinline__ void publish(KArgs& a, unsigned* flag, unsigned epoch
 __device__ __forceinline__ void publish_local(KArgs& a, unsigned* flag, unsigned epoch) {
   if (!copy_wave()) wait_stores();
   wg_barrier();
-  if (threadIdx.x == 0) {
+  if (phase_tid() == 0) {
     const brsrc r = make_rsrc(uniform_ptr(flag + (size_t)((unsigned)wg_id() % kFlagCopies) * a.fstride), 4);
     __builtin_amdgcn_raw_buffer_store_b32(epoch, r, 0, 0, 0);
   }
@@ -496,7 +502,7 @@ __device__ __forceinline__ void lds_burst(float* dst, const u16* src) {
   if (!copy_wave()) return;
   wait_vmcnt<63 - N>();
   const brsrc r = make_rsrc(src, (size_t)N * 1024);
-  const unsigned vo = (threadIdx.x & 63) * 16;
+  const unsigned vo = (phase_tid() & 63) * 16;
   lds_u16* d = lds_addr(dst);
 #pragma unroll
   for (int f = 0; f < N; ++f) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, d + f * 512, 16, vo, f * 1024, 0, kAuxNt);
@@ -631,7 +637,7 @@ __device__ __forceinline__ void store_wave_partials(float* red, const f32x4 (&ac
 // copy wave takes m-tile 3: LDS work only).
 template <int MT, int NT, int TS>
 __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
-  const int tid = threadIdx.x;
+  const int tid = phase_tid();
   const int mt = tid >> 6, ln = tid & 63;
   if (mt >= MT) return;
   f32x4 r[kCompWaves][NT];
@@ -653,7 +659,7 @@ __device__ __forceinline__ void reduce_to_tile(const float* red, float* T) {
 // The same over NW waves' partials (red[wave][mt][t][lane], NW * MT * NT fragments).
 template <int NW, int MT, int NT, int TS>
 __device__ __forceinline__ void reduce_to_tile_n(const float* red, float* T) {
-  const int tid = threadIdx.x;
+  const int tid = phase_tid();
   const int mt = tid >> 6, ln = tid & 63;
   if (mt >= MT) return;
   f32x4 r[NW][NT];
