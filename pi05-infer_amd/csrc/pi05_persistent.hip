@@ -283,6 +283,7 @@ constexpr int kPairs = kHorizon / 2; // 25 two-token attention row blocks per sa
 // tile for its finisher (quarter 0)
 constexpr int kPartFlags = 256;
 constexpr int kOItems = kTiles * (kRowsPerSample / 16);  // o_proj items: (m-tile of a sample, tile)
+constexpr int kDownItems1 = kTiles * (kRowsPerSample / 16);  // one-sample down_proj items: (tile, m-tile)
 // Batches of kAttnGroupMinBatch and more (in kernel instance 2): grouped attention items
 // (attn_group_items), which stage K/V blocks in region B as well, so down(l)'s weights are copied
 // to B before o_proj(l) instead of at qkv(l).  G: a batched instance.
@@ -307,9 +308,10 @@ __device__ void record_error(KArgs& a, unsigned epoch) { st_u32(a.err + kCtlErr,
 // is counted in the pinned host word (one writer: the last workgroup out of a launch).  The launch
 // that reaches kEpochWrap zeroes the flags and the error word first and restarts the epochs at 1.
 //
-// Placement check.  The down_proj K quarters of a tile hand their partials and flags over through
-// one XCD's L2 (st_l2_16, publish_local), which is correct only if workgroups w and w + 8k run on
-// the same XCD.  The dispatcher deals workgroups to the 8 XCDs round-robin, starting where the
+// Placement check.  In the batch instances the down_proj K quarters of a tile hand their partials
+// and flags over through one XCD's L2 (st_l2_16, publish_local), which is correct only if
+// workgroups w and w + 8k run on the same XCD (the one-sample kernel has no such hand-off; its
+// launches are checked all the same).  The dispatcher deals workgroups to the 8 XCDs round-robin, starting where the
 // previous dispatch stopped, so workgroup w runs on XCD (w + d) mod 8 with one offset d per launch.
 // Before counting itself out, every workgroup sets bit (XCC_ID - w) mod 8 of the placement word
 // (and waits for the or, so it is performed before the count); the last one out counts a launch
@@ -573,13 +575,14 @@ __device__ void copy_norm_w(KArgs& a, int l, int which, float* smem) {
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE, G>(a, l, which) + F0 * 512);
 }
 
-// down_proj weights of item (unsigned)wg_id() = (tile, K quarter) -> region B.
-// down_proj items.  B = 1: workgroup w = (tile w mod 64, K quarter w / 64).  B > 1: workgroup
+// down_proj weights of workgroup (unsigned)wg_id(): (tile, K quarter) -> region B.
+// down_proj items.  B = 1 (phase_down_rows): workgroup w = (tile w mod 64, m-tile w / 64) over
+// the whole K; its copy wave multiplies K quarter w / 64, which region B holds.  B > 1: workgroup
 // w = 64 q + 32 h + g computes tiles 2g and 2g + 1 over K quarter q for half h of the samples --
-// half the activation bytes per XCD, as for gate_up.  Either way the quarters of a tile (group)
-// run on one XCD (w mod 8 is the same for all four) and poll one flag replica (w mod 32), and the
-// finishers (quarter 0) are workgroups 0..63, which hold no qkv item.  Region B holds the first
-// tile's quarter; at B > 1 the compute waves hold the second one in registers.
+// half the activation bytes per XCD, as for gate_up; the quarters of a group run on one XCD (w mod
+// 8 is the same for all four) and poll one flag replica (w mod 32), and the finishers (quarter 0)
+// are workgroups 0..63, which hold no qkv item.  Region B holds the first tile's quarter; the
+// compute waves hold the second one in registers.
 __device__ __forceinline__ void down_item(KArgs& a, int* nt0, int* ksp, int* half = nullptr) {
   const int w = wg_id();
   *ksp = w / kTiles;
@@ -747,7 +750,7 @@ __device__ bool phase_io(KArgs& a, int s, float* smem, Sync sy) {
       if (tid < 128) load_mod();
     }
     if (has_prev && !waited) {
-      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), G ? kKSplit * kTiles : kTiles, sy)) return false;
+      if (!wait_flags(a, flag_base(a, s - 1, L - 1, kPhDown), kKSplit * kTiles, sy)) return false;  // every down_proj item (256 either way)
       waited = true;
     }
     if (has_prev && tid < 64) {
@@ -959,7 +962,7 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   PHASE_TS(s, l, PH, 1);
   {
     const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
-    const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kTiles) : kOItems;
+    const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kDownItems1) : kOItems;
     if (!wait_flags(a, dep, ndep, sy)) return false;
   }
   PHASE_TS(s, l, PH, 2);
@@ -2635,170 +2638,122 @@ __device__ bool phase_oproj_msplit(KArgs& a, int s, int l, float* smem, Sync sy)
 }
 
 // =============================================================================================
-// down_proj (K = 4096): item = (16-column tile, K quarter), 3 compute waves split the quarter.
-// Quarters 1..3 store their partial and flag it; quarter 0 (the finisher, on the same XCD) keeps
-// its own, waits for the other three, adds the four in quarter order and applies the gated
-// residual h = bf16(h + bf16(bf16(y) * gate)) (modeling_gemma.py:231-249, 511), then writes the
-// new residual rows, g = bf16(h * (1 + scale)) of the next layer's first norm, and the tile's row
-// sums of squares.  (Without the K split, 128 k-steps of weights and a 16-row A block per item
-// measured slower: the loads queue behind each other in the workgroup.)
+// down_proj at one sample without a K split: item = (16-column tile nt, m-tile mq), 256 items, so
+// no partial sum leaves the workgroup and no finisher hand-off follows.  The four waves each take
+// a K quarter (32 k-steps): the copy wave takes quarter mq from region B (it put it there during
+// qkv), so it issues no register loads next to its copies; waves 1 and 2 take quarters mq + 2 and
+// mq + 3 (mod 4) with their weight fragments loaded into registers ahead of the polls; wave 0, the
+// poller, takes quarter mq + 1 and loads its fragments after the polls (the other m-tiles' items
+// of the tile, on the same XCD, have brought that quarter into L2 by then).  The products are formed as W . A^T (a lane ends with 4 consecutive columns of one row);
+// the quarters are added in quarter order in LDS and wave 1 runs the finisher's epilogue:
+// h = bf16(hmid + bf16(bf16(y) * gate)) (modeling_gemma.py:503), g = bf16(h * (1 + scale)) of the
+// next layer's first norm, and the tile's row sums of squares of h.
 // =============================================================================================
-__device__ bool phase_down(KArgs& a, int s, int l, float* smem, Sync sy) {
-  constexpr int KSTEPS = kMlp / 32;
-  constexpr int KQ = KSTEPS / kKSplit, KSW = (KQ + kCompWaves - 1) / kCompWaves, TS = 17;
+// The copy wave's burst at down_proj(l): the next layer's qkv tiles -> region A.
+__device__ __forceinline__ void down_next_qkv_copies(KArgs& a, int s, int l, float* smem) {
+  int ln;
+  if (next_layer(a, s, l, &ln)) {
+    copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
+    copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
+  }
+}
+__device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
+  constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
+  constexpr int NCH = 4;  // independent accumulation chains per wave
   constexpr int PH = kPhDown;
-  const int L = a.depth, NN = 2 * L + 1, R = a.R;
+  const int L = a.depth, NN = 2 * L + 1, R = kRowsPerSample;
   const int item = (unsigned)wg_id();
   PHASE_TS(s, l, PH, 0);
-  // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
-  {
-    int ln;
-    if (next_layer(a, s, l, &ln)) {
-      copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
-      copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
-    }
-  }
-  if (item >= kTiles * kKSplit) return true;
-  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
-  const bool comp = tid < kCompThreads;
-  const int nt = item % kTiles, ksp = item / kTiles;
-  const int kw0 = wave * KSW;  // this wave's k-steps in the quarter: [kw0, kw0 + KSW) clipped to KQ
-  const int kstep0 = ksp * KQ + kw0;
-  const size_t slw = (size_t)s * L + l;
-  // wave 0 (lane = row of the sample): gate and 1 + scale of the tile's 16 columns
-  const int col = nt * 16;
-  float4 g4[2] = {}, s14[2] = {};
-  const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
-  PHASE_TS(s, l, PH, 1);
-  {
-    // the gate_up items of this quarter's 1024 activation columns: items 64 ksp .. 64 ksp + 63
-    if (!wait_flags(a, flag_base(a, s, l, kPhGu) + ksp * 64, 64, sy)) return false;
-  }
-  PHASE_TS(s, l, PH, 2);
-  // the finisher's (quarter 0) residual rows (written before anything this phase waited for),
-  // gate and 1 + scale: loaded by waves 0 and 1 right after the polls, used much later
-  const u16* hres = a.hmid + slw * (size_t)R * kWidth;
-  // finisher thread: row, first of its 8 columns (the two halves of a row in adjacent lanes)
-  const bool fin_thread = ksp == 0 && tid < 128;
-  const int frow = (tid & 127) >> 1, fc0 = (tid & 1) * 8;
-  u16x8 hpre = {};
-  if (fin_thread) {
-    const float* gmod = a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + fc0;
-    const float* smod = a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + fc0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      g4[i] = *reinterpret_cast<const float4*>(gmod + 4 * i);
-      if (next_g) s14[i] = *reinterpret_cast<const float4*>(smod + 4 * i);
-    }
-    if (frow < kHorizon) hpre = *reinterpret_cast<const u16x8*>(hres + afrag_index(frow, col + fc0, kWidth / 32));
-  }
-  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // this item's K-quarter fragments
-  const u16* act = a.act + slw * (size_t)R * kMlp;
-  // this phase's K-quarter partials [quarter][tile][row][16] (written once per launch)
-  float* dpart = a.dpart + slw * (size_t)kKSplit * kTiles * R * 16;
-  float* red = smem + kLdsWork;
-  float* T = red + kCompWaves * 4 * 256;  // [64][TS], then the finisher's [2][64] row sums
-  const bool own_lds = ksp == 0;  // the finisher keeps its own partial in T
-  const int r16 = lane & 15;
-  {
-    constexpr int b = 0;  // one sample: the batch instances run phase_down_pairs / phase_down_msplit
-    if (comp) {
-      // padded rows and the k-steps past the quarter read as zeros (no branches)
-      const brsrc rsrc_a = make_rsrc(act, (size_t)R * KSTEPS * 32 * 2);
-      bf16x8 af[4][KSW];
-#pragma unroll
-      for (int s2 = 0; s2 < KSW; ++s2)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const bool ok = r16 < kHorizon - mt * 16 && kw0 + s2 < KQ;
-          buf_frag(af[mt][s2], rsrc_a, ok ? (int)((afrag_offset(b * 4 + mt, kstep0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
-        }
-      sched_fence();
-      f32x4 acc[4][1];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[mt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // zero A for the surplus steps: any finite weights (the quarter's last k-step)
-      mfma_steps<KSW, 1, 0, 4>(acc, af, [&](int, int s2) {
-        const int kc = kw0 + s2 < KQ ? kw0 + s2 : KQ - 1;
-        return *reinterpret_cast<const bf16x8*>(lw + (size_t)kc * 512 + lane * 8);
-      });
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<f32x4*>(red + (((size_t)wave * 4 + mt) * 64 + lane) * 4) = acc[mt][0];
-    }
-    if (b == 0) PHASE_TS(s, l, PH, 4);
-    __syncthreads();
-    reduce_to_tile<4, 1, TS>(red, T);
-    __syncthreads();
-    if (comp && !own_lds) {
-      // partial [quarter][tile][row][16]: 64 rows x 4 float4
-      for (int e = tid; e < 256; e += kCompThreads) {
-        const int row = e >> 2, q4 = e & 3;
-        const float* tr = T + row * TS + 4 * q4;
-        // the tile's finisher (quarter 0) runs on this XCD: the partial stays in its L2
-        st_l2_16(dpart, (uint32_t)(((((size_t)ksp * kTiles + nt) * R + b * kRowsPerSample + row) * 16 + 4 * q4) * 4),
-                 u32x4{__float_as_uint(tr[0]), __float_as_uint(tr[1]), __float_as_uint(tr[2]), __float_as_uint(tr[3])});
-      }
-    }
-  }
-  PHASE_TS(s, l, PH, 5);
-  unsigned* fl = flag_base(a, s, l, PH);
-  if (ksp != 0) {
-    // this quarter's partial is stored: flag it for the tile's finisher (quarter 0, same XCD)
-    publish_local(a, fl + kPartFlags + 4 * nt + (ksp - 1), sy.epoch);
+  if (item >= kDownItems1) {
+    down_next_qkv_copies(a, s, l, smem);
     return true;
   }
-  // ---- the finisher (quarter 0): its own partial stays in LDS; it waits for the other
-  // three, adds the four in quarter order and writes the tile.  Waves 0 and 1: lane = row,
-  // columns half*8 .. +7.
-  if (!own_lds && comp) wait_stores();  // its own partials, reloaded below
-  if (!wait_flags(a, fl + kPartFlags + 4 * nt, kKSplit - 1, sy)) return false;
-  PHASE_TS(s, l, PH, 7);
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const int nt = item % kTiles, mq = item / kTiles;
+  const int kq = (mq + (wave + 1) % 4) & (kKSplit - 1);  // this wave's K quarter
+  const int col = nt * 16, r16 = lane & 15, ec = 4 * (lane >> 4);
+  const int nrow = kHorizon - 16 * mq < 16 ? kHorizon - 16 * mq : 16;  // action rows of the m-tile
+  const size_t slw = (size_t)s * L + l;
+  bf16x8 wf[KQ];
+  const brsrc rw = make_rsrc(a.wpack + (size_t)l * kLayerElems + kOffDown + (size_t)nt * KSTEPS * 512, (size_t)KSTEPS * 1024);
+  auto load_w = [&]() {
+    // (the quarter goes into the per-lane offset: a resource built from it would not be uniform)
+#pragma unroll
+    for (int s2 = 0; s2 < KQ; ++s2) buf_frag(wf[s2], rw, ((kq * KQ + s2) * 512 + lane * 8) * 2);
+  };
+  if (wave == 1 || wave == 2) load_w();
+  // wave 1 (the epilogue's): the gate of norm 2l + 1 and 1 + scale of the next layer's first norm
+  // for its 4 columns, ahead of the polls
+  const bool ep_wave = wave == 1;
+  const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
+  float4 g4 = {}, s14 = {};
+  if (ep_wave) {
+    g4 = *reinterpret_cast<const float4*>(a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + ec);
+    if (next_g) s14 = *reinterpret_cast<const float4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + ec);
+  }
+  // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
+  down_next_qkv_copies(a, s, l, smem);
+  PHASE_TS(s, l, PH, 1);
+  // every gate_up item: the m-tile's rows over the whole K
+  if (!wait_flags(a, flag_base(a, s, l, kPhGu), kGuItems, sy)) return false;
+  PHASE_TS(s, l, PH, 2);
+  const int r = 16 * mq + r16;
+  const u16* hres = a.hmid + slw * (size_t)R * kWidth;
+  uint2 hold = {0u, 0u};
+  if (ep_wave && r16 < nrow) hold = *reinterpret_cast<const uint2*>(hres + afrag_index(r, col + ec, kWidth / 32));
+  float* red = smem + kLdsWork;  // [4 waves][64 lanes][4]
   {
-    u16* hout = a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth;
-    u16* gout = a.g + (slw + 1) * (size_t)R * kWidth;  // slice (s, l + 1); unused after the last layer
-    float* rout = a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R;
-    const float gate[8] = {round_bf(g4[0].x), round_bf(g4[0].y), round_bf(g4[0].z), round_bf(g4[0].w),
-                           round_bf(g4[1].x), round_bf(g4[1].y), round_bf(g4[1].z), round_bf(g4[1].w)};
-    const float s1[8] = {s14[0].x, s14[0].y, s14[0].z, s14[0].w, s14[1].x, s14[1].y, s14[1].z, s14[1].w};
-    {
-      constexpr int b = 0;
-      const int r = b * kRowsPerSample + frow;
-      float ss = 0.f;
-      if (fin_thread && frow < kHorizon) {
-        float pv[kKSplit][8];
+    const brsrc ra = make_rsrc(a.act + slw * (size_t)R * kMlp, (size_t)R * kMlp * 2);
+    bf16x8 af[KQ];
 #pragma unroll
-        for (int q = 0; q < kKSplit; ++q) {
-          if (q == 0 && own_lds) {
+    for (int s2 = 0; s2 < KQ; ++s2)
+      buf_frag(af[s2], ra, r16 < nrow ? (int)((afrag_offset(mq, kq * KQ + s2, KSTEPS) + lane * 8) * 2) : kOob);
+    if (wave == 0) load_w();
+    if (copy_wave()) {
+      const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // quarter mq of the tile
+      wait_vmcnt<0>();  // (and the next layer's copies: loads complete in issue order)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) pv[0][i] = T[frow * TS + fc0 + i];
-          } else {
-            const float* pp = dpart + (((size_t)q * kTiles + nt) * R + r) * 16 + fc0;
-            const float4 v0 = *reinterpret_cast<const float4*>(pp), v1 = *reinterpret_cast<const float4*>(pp + 4);
-            pv[q][0] = v0.x, pv[q][1] = v0.y, pv[q][2] = v0.z, pv[q][3] = v0.w;
-            pv[q][4] = v1.x, pv[q][5] = v1.y, pv[q][6] = v1.z, pv[q][7] = v1.w;
-          }
-        }
-        const u16x8 hold = hpre;
-        u16 hn[8], gn[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float y = ((pv[0][i] + pv[1][i]) + pv[2][i]) + pv[3][i];
-          const float prod = round_bf(fmul(round_bf(y), gate[i]));
-          hn[i] = f2bf(fadd(bf2f(hold[i]), prod));
-          const float hf = bf2f(hn[i]);
-          gn[i] = f2bf(fmul(hf, s1[i]));
-          ss += hf * hf;
-        }
-        st_bf16x8(hout, afrag_index(r, col + fc0, kWidth / 32), hn);
-        if (next_g) st_bf16x8(gout, afrag_index(r, col + fc0, kWidth / 32), gn);
-      }
-      // tile-major statistics: this tile's sum of the row, columns 0..7 then 8..15 (lanes 2 i, 2 i + 1)
-      const float ss_hi = __shfl_xor(ss, 1);
-      if (fin_thread && fc0 == 0) st_f32(rout + (size_t)nt * R + r, ss + ss_hi);
+      for (int s2 = 0; s2 < KQ; ++s2) wf[s2] = *reinterpret_cast<const bf16x8*>(lw + (size_t)s2 * 512 + lane * 8);
     }
+    sched_fence();
+    f32x4 acc[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s2 = 0; s2 < KQ; ++s2) acc[s2 % NCH] = mfma16x16x32(wf[s2], af[s2], acc[s2 % NCH]);
+    *reinterpret_cast<f32x4*>(red + ((size_t)kq * 64 + lane) * 4) = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  PHASE_TS(s, l, PH, 4);
+  __syncthreads();
+  if (ep_wave) {
+    // the quarters in order, then the finisher's epilogue on the lane's row and 4 columns
+    const f32x4 y = ((*reinterpret_cast<const f32x4*>(red + (size_t)lane * 4) + *reinterpret_cast<const f32x4*>(red + (size_t)(64 + lane) * 4)) +
+                     *reinterpret_cast<const f32x4*>(red + (size_t)(128 + lane) * 4)) +
+                    *reinterpret_cast<const f32x4*>(red + (size_t)(192 + lane) * 4);
+    const float gate[4] = {round_bf(g4.x), round_bf(g4.y), round_bf(g4.z), round_bf(g4.w)};
+    const float s1[4] = {s14.x, s14.y, s14.z, s14.w};
+    float ss = 0.f;
+    if (r16 < nrow) {
+      u16 hn[4], gn[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u16 hb = (u16)((i < 2 ? hold.x : hold.y) >> (16 * (i & 1)));
+        const float prod = round_bf(fmul(round_bf(y[i]), gate[i]));
+        hn[i] = f2bf(fadd(bf2f(hb), prod));
+        const float hf = bf2f(hn[i]);
+        gn[i] = f2bf(fmul(hf, s1[i]));
+        ss += hf * hf;
+      }
+      st_bf16x4(a.h + ((size_t)s * (L + 1) + l + 1) * R * kWidth, afrag_index(r, col + ec, kWidth / 32), hn);
+      if (next_g) st_bf16x4(a.g + (slw + 1) * (size_t)R * kWidth, afrag_index(r, col + ec, kWidth / 32), gn);
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
+    if (lane < 16) st_f32(a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R + (size_t)nt * R + 16 * mq + lane, ss);
   }
   PHASE_TS(s, l, PH, 8);
-  publish(a, flag_base(a, s, l, PH) + nt, sy.epoch);
+  publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
   PHASE_TS(s, l, PH, 9);
   return true;
 }
@@ -2894,7 +2849,7 @@ __device__ __forceinline__ void down_pairs_finish(KArgs& a, int s, int l, float*
 // quarter for the samples [b0, b1) of half h (workgroup 64 q + 32 h + g, see down_item).  Every
 // quarter stores its partials of both tiles and flags them for the group (the four quarters run on
 // one XCD); then quarter q finishes samples b0 + q, b0 + q + 4, ... of the half: it adds the four
-// quarters in order and applies the gated residual to both tiles, as phase_down does for one.  Its
+// quarters in order and applies the gated residual (modeling_gemma.py:231-249, 511) to both tiles.  Its
 // flag (index 4 (g + 32 h) + q) covers both tiles and those samples, so the next phase waits for
 // 256 flags.
 // =============================================================================================
@@ -3185,7 +3140,7 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
               : phase_norm_gemm<kModeGateUp, G>(kargs(), s, l, smem, sy)) &&
            (G && PI05_INSTANCE_GROUPED ? phase_down_msplit(kargs(), s, l, smem, sy)
             : G                         ? phase_down_pairs<G>(kargs(), s, l, smem, sy)
-                                        : phase_down(kargs(), s, l, smem, sy));
+                                        : phase_down_rows(kargs(), s, l, smem, sy));
     }
   }
   // no direct-to-LDS copy may still be in flight when the workgroup's LDS is released

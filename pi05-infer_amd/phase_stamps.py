@@ -11,8 +11,8 @@ Events (phase_norm_gemm = qkv and gate_up at B = 1): 0 phase entry, 1 before the
 2 wait done, 4 MFMAs done, 3 after the barrier that follows them, 7 cross-wave reduction done,
 5 before the publish, 6 after it.  Attention splits: 4/7/8/9 waves 0/1/2/3 done attending, 3 the
 waves' partials exchanged, 5 stores issued, 6 published.  Merges: 1, 2, 6.  o_proj: 2 wait done,
-4 MFMAs done, 5/6 publish.  down_proj: 2 wait done, 4 MFMAs done, 5 quarter partial stored,
-7 finisher's wait done, 8/9 finisher publish.
+4 MFMAs done, 5/6 publish.  down_proj: 2 wait done, 4 MFMAs done, 8/9 publish (the batch
+instances, which split K: 5 quarter partial stored, 7 finisher's wait done, 8/9 finisher publish).
 
     python pi05-infer_amd/phase_stamps.py [--batch B] [--prefix P] [--layer L] [--reps K]
 """
