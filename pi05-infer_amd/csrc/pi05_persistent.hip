@@ -542,8 +542,8 @@ template <bool G>
 __device__ __forceinline__ bool gu_msplit(KArgs&) {
   return G && PI05_INSTANCE_GROUPED;
 }
-__device__ __forceinline__ int gu_pair0(KArgs& a) {
-  return a.batch > 1 ? 2 * (wg_id() % (kGuItems / 2)) : wg_id();
+__device__ __forceinline__ int gu_pair0(KArgs&) {
+  return 2 * (wg_id() % (kGuItems / 2));
 }
 // qkv items.  B = 1: item i = qkv_item() computes tile pair i mod 80 over row half i / 80 of the
 // sample.  B = 2 (kernel instance 1): item i computes tile pairs 2 (i mod 40) and 2 (i mod 40) + 1
@@ -863,22 +863,20 @@ __device__ bool phase_io(KArgs& a, int s, float* smem, Sync sy) {
 }
 
 // =============================================================================================
-// adaRMSNorm-folded GEMM tile (K = 1024, 3 compute waves x 11 | 11 | 10 k-steps): qkv and gate_up.
-// A operand g (or gmid) straight from the producer; rstd from the tile sums of squares; the
-// epilogue computes y = bf16(rstd * acc + shift . W^T) and then RoPE (qkv) or GeGLU (gate_up).
+// qkv at one sample: adaRMSNorm-folded GEMM tile (K = 1024, 3 compute waves x 11 | 11 | 10
+// k-steps).  A operand g straight from the producer; rstd from the tile sums of squares; the
+// epilogue computes y = bf16(rstd * acc + shift . W^T) and then RoPE.
 // =============================================================================================
-template <int MODE, bool G>
-__device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
+template <bool G>
+__device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32;
-  // m-tiles per item: qkv items are one half of a sample's rows (m-tiles 2h, 2h+1), gate_up all four
-  constexpr int MT = MODE == kModeQkv ? 2 : 4;
-  constexpr int PH = MODE == kModeQkv ? kPhQkv : kPhGu;
+  constexpr int MT = 2;  // m-tiles per item: one half of the sample's rows (m-tiles 2h, 2h+1)
+  constexpr int PH = kPhQkv;
   const int L = a.depth, R = a.R;
-  const int n_items = MODE == kModeQkv ? kQkvItems : kGuItems;
-  const int item = MODE == kModeQkv ? qkv_item() : wg_id();
-  const bool has_item = item >= 0 && item < n_items;
-  const int p = MODE == kModeQkv ? item % kQkvPairs : item;  // tile pair (qkv) / item
-  const int mh = MODE == kModeQkv ? item / kQkvPairs : 0;    // qkv: half of the rows
+  const int item = qkv_item();
+  const bool has_item = item >= 0 && item < kQkvItems;
+  const int p = item % kQkvPairs;   // tile pair
+  const int mh = item / kQkvPairs;  // half of the rows
   const int rb = 32 * mh;                          // the item's first row within a sample
   const int nrow = MT * 16 < kHorizon - rb ? MT * 16 : kHorizon - rb;  // its action-token rows
   PHASE_TS(s, l, PH, 0);
@@ -886,9 +884,7 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   // then the bursts of this phase start
   if (copy_wave()) {
     wait_vmcnt<0>();
-    if constexpr (MODE == kModeQkv) {
-      if (!attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
-    }
+    if (!attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
   }
   if (!has_item) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -896,38 +892,26 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   const int r16 = lane & 15;
   const int ks0 = wave * KSW;  // this wave's k-steps [ks0, ks0 + KSW) (wave 2: the last one past K)
   const size_t slw = (size_t)s * L + l;
-  int tile0;
-  bool rotated = false;
-  int head = 0, dt = 0;
-  const u16* gin;
-  const float* ssin;
   const float* bias = a.bias + slw * kBiasCols;
-  if constexpr (MODE == kModeQkv) {
-    rotated = p < 72;
-    head = p >> 3;
-    dt = p & 7;
-    tile0 = rotated ? head * 16 + dt : 144 + 2 * (p - 72);
-    gin = a.g + slw * R * kWidth;
-    ssin = a.ss + ((size_t)s * (L + 1) + l) * kTiles * R;
-  } else {
-    tile0 = p;
-    gin = a.gmid + slw * R * kWidth;
-    ssin = a.ssmid + slw * kTiles * R;
-  }
-  // the products: W . A^T for gate_up and the RoPE pairs (a lane then holds 4 consecutive columns
-  // of one row: GeGLU and RoPE, which pairs column d of the two tiles, are lane-local, and the
-  // stores are 8 bytes), A . W for the v pairs (a lane holds 4 rows of one column in each m-tile:
-  // with the two m-tiles, the 8 keys of one 16-byte chunk of the permuted V layout)
-  const bool wt = MODE != kModeQkv || rotated;
+  const bool rotated = p < 72;
+  const int head = p >> 3, dt = p & 7;
+  const int tile0 = rotated ? head * 16 + dt : 144 + 2 * (p - 72);
+  const u16* gin = a.g + slw * R * kWidth;
+  const float* ssin = a.ss + ((size_t)s * (L + 1) + l) * kTiles * R;
+  // the products: W . A^T for the RoPE pairs (a lane then holds 4 consecutive columns of one row:
+  // RoPE, which pairs column d of the two tiles, is lane-local, and the stores are 8 bytes), A . W
+  // for the v pairs (a lane holds 4 rows of one column in each m-tile: with the two m-tiles, the 8
+  // keys of one 16-byte chunk of the permuted V layout)
+  const bool wt = rotated;
   float* s_rstd = smem + kLdsWork;  // [64] (item rows)
   float* s_bias = s_rstd + 64;      // [32] shift . W^T of the item's two tiles
   float* s_rs = s_bias + 32;        // [3][64] row sums of squares over tiles 22w .. 22w+21
   float* red = s_rs + 192;          // [3 waves][MT m-tiles][NT][64 lanes][4]
-  // epilogue threads.  gate_up: every thread, m-tile tid / 64, lane tid % 64.  qkv: waves 1 and 2
-  // (wave 0 polls, so it issues nothing ahead of its polls), e = tid - 64: RoPE pairs m-tile e / 64,
-  // lane e % 64; v pairs tile e / 64, lane e % 64 (both m-tiles)
-  const int e = MODE == kModeQkv ? tid - 64 : tid;
-  const bool ep_thread = e >= 0 && e < 64 * (MODE == kModeQkv ? 2 : MT);
+  // epilogue threads: waves 1 and 2 (wave 0 polls, so it issues nothing ahead of its polls),
+  // e = tid - 64: RoPE pairs m-tile e / 64, lane e % 64; v pairs tile e / 64, lane e % 64 (both
+  // m-tiles)
+  const int e = tid - 64;
+  const bool ep_thread = e >= 0 && e < 128;
   const int emt = e >> 6, eln = e & 63;
   const int erow = 16 * emt + (eln & 15);   // W . A^T: the thread's row within the item
   const int ecol = 4 * (eln >> 4);          // W . A^T: its first column within each tile
@@ -935,7 +919,7 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
   // k-step 31 (not in LDS), and the RoPE cos/sin of the epilogue thread's row and 4 columns
   bf16x8 w31 = {};
   uint32_t rcs[4][2] = {};
-  const bool rope_thread = MODE == kModeQkv && rotated && ep_thread && erow < nrow;
+  const bool rope_thread = rotated && ep_thread && erow < nrow;
   auto load_rope = [&](int b) {
     const size_t cr = (size_t)(b * kHorizon + rb + erow) * kHeadDim + dt * 16 + ecol;
     const u16* src[4] = {a.cos_tab + cr, a.sin_tab + cr, a.cos_tab + cr + kHalfDim, a.sin_tab + cr + kHalfDim};
@@ -946,23 +930,20 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
       rcs[k][1] = v.y;
     }
   };
-  if constexpr (MODE == kModeQkv) {
-    if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(norm_w_tile<kModeQkv>(a, l, 1) + 31 * 512 + lane * 8));
-    if (rope_thread) load_rope(0);
-  }
+  if (wave == 2) w31 = as_bf16x8(*reinterpret_cast<const u16x8*>(norm_w_tile<kModeQkv>(a, l, 1) + 31 * 512 + lane * 8));
+  if (rope_thread) load_rope(0);
   // the item's shift . W^T columns (static within the launch), by wave 1 ahead of the polls and
   // straight into LDS: the work area is free (every wave passed the previous phase's last
   // barrier) and the wait's barrier orders the stores before their readers
   if (tid >= 64 && tid < 96) {
     const int c = tid - 64;
-    const int col = MODE == kModeQkv ? (c < 16 ? tile0 * 16 + c : (rotated ? tile0 + 8 : tile0 + 1) * 16 + c - 16)
-                                     : (c < 16 ? kQkvCols + tile0 * 16 + c : kQkvCols + kMlp + tile0 * 16 + c - 16);
+    const int col = c < 16 ? tile0 * 16 + c : (rotated ? tile0 + 8 : tile0 + 1) * 16 + c - 16;
     s_bias[c] = bias[col];
   }
   PHASE_TS(s, l, PH, 1);
   {
-    const unsigned* dep = MODE == kModeQkv ? (l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown)) : flag_base(a, s, l, kPhO);
-    const int ndep = MODE == kModeQkv ? (l == 0 ? a.batch * kHorizon : kDownItems1) : kOItems;
+    const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
+    const int ndep = l == 0 ? a.batch * kHorizon : kDownItems1;
     if (!wait_flags(a, dep, ndep, sy)) return false;
   }
   PHASE_TS(s, l, PH, 2);
@@ -1003,7 +984,7 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
       // fragment is wave 2's register copy
       auto wk = [&](int t, int s2) {
         const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
-        if (MODE == kModeQkv && t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
+        if (t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
         return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
       };
       if (wt) mfma_steps<KSW, NT, 0, MT, true>(acc, hr, wk);
@@ -1023,7 +1004,7 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
       for (int w = 0; w < kCompWaves; ++w) r[w] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * MT + mt) * NT + t) * 64 + eln) * 4);
       return (r[0] + r[1]) + r[2];
     };
-    if constexpr (MODE == kModeQkv) {
+    {
       if (rotated) {
         // (x*cos) + (rotate_half(x)*sin), rotate_half(x) = cat(-x_hi, x_lo), from the bf16
         // GEMM values (rlinf_fused_denoise.py:264-278; modeling_gemma.py:185-216): dims d .. d + 3
@@ -1069,35 +1050,147 @@ __device__ bool phase_norm_gemm(KArgs& a, int s, int l, float* smem, Sync sy) {
         u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
         st_bf16x8(vc, ((size_t)mh * 16 + (dv >> 4)) * 512 + (size_t)(g * 16 + (dv & 15)) * 8, v8);
       }
-    } else {
-      // GeGLU as the fused reference kernel defines it: bf16(gelu_tanh(bf16(g)) * u), u the fp32
-      // accumulator (rlinf_fused_denoise.py:166-173): columns ecol .. ecol + 3 of gate tile j and
-      // of up tile j, row erow
-      if (ep_thread && erow < kHorizon) {
-        const f32x4 yg = wave_sum(emt, 0), yu = wave_sum(emt, 1);
-        const float rstd = s_rstd[erow];
-        u16 o4[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float gt = round_bf(__builtin_fmaf(rstd, yg[q], s_bias[ecol + q]));
-          const float up = __builtin_fmaf(rstd, yu[q], s_bias[16 + ecol + q]);
-          o4[q] = f2bf(fmul(gelu_tanh(gt), up));
-        }
-        st_bf16x4(a.act + slw * (size_t)R * kMlp, afrag_index(m0 + erow, tile0 * 16 + ecol, kMlp / 32), o4);
-      }
     }
   }
   PHASE_TS(s, l, PH, 5);
-  publish(a, flag_base(a, s, l, PH) + item, sy.epoch, MODE != kModeQkv);  // gate_up: the copy wave stored rows
+  publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
   PHASE_TS(s, l, PH, 6);
   return true;
 }
 
 // =============================================================================================
+// gate_up at one sample, split by rows: item w = tile pairs 2p and 2p + 1 (p = w mod 128) over row
+// half w / 128 (m-tiles 0, 1 or 2, 3), so an item fetches half of gmid after its wait where a
+// one-pair item over all rows fetched all of it.  Pair 2p's tiles come from region A (the copy
+// wave's bursts); waves 1..3 (the copy wave is free in this phase) split K (11/11/10 k-steps) and
+// load pair 2p + 1's fragments of their k-steps into registers ahead of the polls; wave 0 only
+// polls.  Products as W . A^T, the three waves' partials added in LDS by the epilogue threads,
+// GeGLU lane-local (thread t: m-tile (t / 64) mod 2 of pair t / 128).
+// =============================================================================================
+__device__ bool phase_gateup_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
+  constexpr int NT = 4, MT = 2, KSW = 11, KSTEPS = kWidth / 32;
+  constexpr int PH = kPhGu;
+  const int L = a.depth, R = kRowsPerSample;
+  const int item = wg_id();
+  PHASE_TS(s, l, PH, 0);
+  if (copy_wave()) wait_vmcnt<0>();  // this phase's weights (region A) have landed
+  if (item >= kGuItems) return true;
+  const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
+  const bool mw = wave >= 1;  // MFMA waves 1..3
+  const int cw = wave - 1;    // their K share
+  const int r16 = lane & 15;
+  const int ks0 = cw * KSW;   // k-steps [ks0, ks0 + KSW) (wave 3: the last one past K)
+  const size_t slw = (size_t)s * L + l;
+  const int p0 = 2 * (item % (kGuItems / 2)), mh = item / (kGuItems / 2);
+  const int rb = 32 * mh;                                   // the item's first row
+  const int nrow = kHorizon - rb < 32 ? kHorizon - rb : 32;  // its action-token rows
+  const u16* gin = a.gmid + slw * R * kWidth;
+  const float* ssin = a.ssmid + slw * kTiles * R;
+  float* s_rstd = smem + kLdsWork;  // [32] (item rows)
+  float* s_bias = s_rstd + 64;      // [2 pairs][32]: shift . W^T of gate and up tiles
+  float* s_rs = s_bias + 64;        // [3][64] row sums of squares over tiles 22 cw .. 22 cw + 21
+  float* red = s_rs + 192;          // [3 waves][MT][NT][64 lanes][4]
+  // pair p0 + 1 of this wave's k-steps (the surplus step: any finite weights, A reads zeros)
+  bf16x8 w1[2][KSW];
+  if (mw) {
+    const u16* wl = a.wpack + (size_t)l * kLayerElems;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const brsrc rw = make_rsrc(wl + (t == 0 ? kOffGate : kOffUp) + (size_t)(p0 + 1) * KSTEPS * 512, (size_t)KSTEPS * 1024);
+#pragma unroll
+      for (int s2 = 0; s2 < KSW; ++s2) {
+        const int ks = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
+        buf_frag(w1[t][s2], rw, (ks * 512 + lane * 8) * 2);
+      }
+    }
+  }
+  // the items' shift . W^T columns (static within the launch), by the copy wave ahead of the polls
+  if (wave == 3) {
+    const float* bias = a.bias + slw * kBiasCols;
+    const int pr = lane >> 5, c = lane & 31;
+    s_bias[lane] = bias[kQkvCols + (c < 16 ? 0 : kMlp) + (p0 + pr) * 16 + (c & 15)];
+  }
+  PHASE_TS(s, l, PH, 1);
+  if (!wait_flags(a, flag_base(a, s, l, kPhO), kOItems, sy)) return false;
+  PHASE_TS(s, l, PH, 2);
+  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // pair p0: [tile t][k-step] fragments
+  f32x4 acc[MT][NT];
+  if (mw) {
+    const brsrc rsrc_s = make_rsrc(ssin, (size_t)kTiles * R * 4);
+    const brsrc rsrc_g = make_rsrc(gin, (size_t)R * kWidth * 2);
+    float st[22];
+#pragma unroll
+    for (int t = 0; t < 22; ++t) {
+      const int tile = 22 * cw + t;
+      buf_f32(st[t], rsrc_s, tile < kTiles && lane < 32 ? ((tile * R + rb + lane) * 4) : kOob);
+    }
+    bf16x8 hr[MT][KSW];
+#pragma unroll
+    for (int s2 = 0; s2 < KSW; ++s2)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bool ok = r16 < nrow - mt * 16 && ks0 + s2 < KSTEPS;
+        buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(2 * mh + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+      }
+    sched_fence();
+    float v = 0.f;
+#pragma unroll
+    for (int t = 0; t < 22; ++t) v += st[t];
+    s_rs[cw * 64 + lane] = v;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mfma_steps<KSW, NT, 0, MT, true>(acc, hr, [&](int t, int s2) {
+      if (t >= 2) return w1[t - 2][s2];
+      const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
+      return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
+    });
+  }
+  PHASE_TS(s, l, PH, 4);
+  __syncthreads();  // every wave is done with region A; the row sums are in LDS
+  PHASE_TS(s, l, PH, 3);
+  if (mw) store_wave_partials<MT, NT>(red, acc, cw, lane);
+  if (tid < 32) s_rstd[tid] = 1.0f / sqrtf(fadd(((s_rs[tid] + s_rs[64 + tid]) + s_rs[128 + tid]) * (1.0f / kWidth), a.eps));
+  __syncthreads();
+  PHASE_TS(s, l, PH, 7);
+  {
+    // GeGLU as the fused reference kernel defines it: bf16(gelu_tanh(bf16(g)) * u), u the fp32
+    // accumulator (rlinf_fused_denoise.py:166-173): columns ecol .. ecol + 3 of the pair's gate and
+    // up tiles, row erow
+    const int mt = (tid >> 6) & 1, pr = tid >> 7, eln = lane;
+    const int erow = 16 * mt + (eln & 15), ecol = 4 * (eln >> 4);
+    if (erow < nrow) {
+      auto wave_sum = [&](int t) {
+        f32x4 r[kCompWaves];
+#pragma unroll
+        for (int w = 0; w < kCompWaves; ++w) r[w] = *reinterpret_cast<const f32x4*>(red + (((size_t)(w * MT + mt) * NT + t) * 64 + eln) * 4);
+        return (r[0] + r[1]) + r[2];
+      };
+      const f32x4 yg = wave_sum(2 * pr), yu = wave_sum(2 * pr + 1);
+      const float rstd = s_rstd[erow];
+      u16 o4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float gt = round_bf(__builtin_fmaf(rstd, yg[q], s_bias[pr * 32 + ecol + q]));
+        const float up = __builtin_fmaf(rstd, yu[q], s_bias[pr * 32 + 16 + ecol + q]);
+        o4[q] = f2bf(fmul(gelu_tanh(gt), up));
+      }
+      st_bf16x4(a.act + slw * (size_t)R * kMlp, afrag_index(rb + erow, (p0 + pr) * 16 + ecol, kMlp / 32), o4);
+    }
+  }
+  PHASE_TS(s, l, PH, 5);
+  publish(a, flag_base(a, s, l, PH) + item, sy.epoch, true);  // every wave stored rows
+  PHASE_TS(s, l, PH, 6);
+  return true;
+}
+static_assert(64 + 64 + 192 + 3 * 2 * 4 * 256 <= kWorkFloats, "one-sample gate_up working area");
+
+// =============================================================================================
 // qkv at B = 2 (kernel instance 1): two tile pairs (p0 = 2g from region A, p1 = 2g + 1 from
 // registers) over row half mh for the samples [b0, b1) of sample half sh (see qkv_pair0), as
 // gate_up's pair items do; both pairs are RoPE pairs (g < 36) or both v pairs.  The epilogue per
-// pair is phase_norm_gemm's: bf16(rstd * acc + shift . W^T), then RoPE into the query rows or the
+// pair is phase_qkv1's: bf16(rstd * acc + shift . W^T), then RoPE into the query rows or the
 // action-key block, or the permuted V fragments.
 // =============================================================================================
 __device__ bool phase_qkv_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
@@ -1218,7 +1311,7 @@ __device__ bool phase_qkv_pairs(KArgs& a, int s, int l, float* smem, Sync sy) {
       __syncthreads();
       const int p = p0 + pr, tile0 = tile_of(p, 0);
       if (rotated) {
-        // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
+        // (x*cos) + (rotate_half(x)*sin) as phase_qkv1's RoPE epilogue (rlinf_fused_denoise.py:264-278)
         if (rope_thread) {
           const int head = p >> 3, dt = p & 7;
           const int row = et >> 1, half = et & 1;
@@ -1475,7 +1568,7 @@ __device__ bool phase_qkv_msplit(KArgs& a, int s, int l, float* smem, Sync sy) {
     }
     const float rstd_lane = row_rstd(ss4, lane, a.eps);
     if (rotated) {
-      // (x*cos) + (rotate_half(x)*sin) as phase_norm_gemm's RoPE epilogue (rlinf_fused_denoise.py:264-278)
+      // (x*cos) + (rotate_half(x)*sin) as phase_qkv1's RoPE epilogue (rlinf_fused_denoise.py:264-278)
       const int head = p >> 3, d = rope_d;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
@@ -3130,14 +3223,14 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
     for (int l = 0; l < kargs().depth && ok; ++l) {
       ok = (qkv_msplit<G>() ? phase_qkv_msplit(kargs(), s, l, smem, sy)
             : G             ? phase_qkv_pairs(kargs(), s, l, smem, sy)
-                            : phase_norm_gemm<kModeQkv, G>(kargs(), s, l, smem, sy)) &&
+                            : phase_qkv1<G>(kargs(), s, l, smem, sy)) &&
            phase_attn<G>(kargs(), s, l, smem, sy) &&
            (G && PI05_INSTANCE_GROUPED ? (kargs().batch <= 4 ? phase_oproj_msplit<4>(kargs(), s, l, smem, sy)
                                                              : phase_oproj_msplit<2>(kargs(), s, l, smem, sy))
             : G                         ? phase_oproj_pairs(kargs(), s, l, smem, sy)
                                         : phase_oproj(kargs(), s, l, smem, sy)) &&
            (G ? (gu_msplit<G>(kargs()) ? phase_gateup_msplit(kargs(), s, l, smem, sy) : phase_gateup_pairs4(kargs(), s, l, smem, sy))
-              : phase_norm_gemm<kModeGateUp, G>(kargs(), s, l, smem, sy)) &&
+              : phase_gateup_rows(kargs(), s, l, smem, sy)) &&
            (G && PI05_INSTANCE_GROUPED ? phase_down_msplit(kargs(), s, l, smem, sy)
             : G                         ? phase_down_pairs<G>(kargs(), s, l, smem, sy)
                                         : phase_down_rows(kargs(), s, l, smem, sy));

@@ -7,9 +7,9 @@ layers 0..3), runs whole predicts of the chosen workload and prints, for one lay
 event's time after the previous layer's last down_proj publish: median / max / min over the
 workgroups that record it, averaged over the predicts.
 
-Events (phase_norm_gemm = qkv and gate_up at B = 1): 0 phase entry, 1 before the flag wait,
-2 wait done, 4 MFMAs done, 3 after the barrier that follows them, 7 cross-wave reduction done,
-5 before the publish, 6 after it.  Attention splits: 4/7/8/9 waves 0/1/2/3 done attending, 3 the
+Events (qkv and gate_up at B = 1): 0 phase entry, 1 before the flag wait, 2 wait done, 4 MFMAs
+done (gate_up: wave 0, which only polls, passes it right after the wait), 3 after the barrier that
+follows the MFMAs, 7 cross-wave reduction done, 5 before the publish, 6 after it.  Attention splits: 4/7/8/9 waves 0/1/2/3 done attending, 3 the
 waves' partials exchanged, 5 stores issued, 6 published.  Merges: 1, 2, 6.  o_proj: 2 wait done,
 4 MFMAs done, 5/6 publish.  down_proj: 2 wait done, 4 MFMAs done, 8/9 publish (the batch
 instances, which split K: 5 quarter partial stored, 7 finisher's wait done, 8/9 finisher publish).
