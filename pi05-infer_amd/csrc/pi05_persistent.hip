@@ -264,9 +264,9 @@ struct Sync {
 // ---- phases, items and flags ------------------------------------------------------------------
 enum { kPhIo = 0, kPhQkv = 1, kPhSplit = 2, kPhMerge = 3, kPhO = 4, kPhGu = 5, kPhDown = 6, kNumPh = 7 };
 constexpr int kQkvPairs = 80;        // 72 RoPE pairs of q/k tiles + 8 pairs of v tiles
-constexpr int kQkvItems = 2 * kQkvPairs;  // each pair in two items: rows 0..31 and rows 32..49
-// qkv item i runs on workgroup kQkvWg0 + i: not on workgroups 0..63, which finish the previous
-// layer's down_proj tiles (the two items of a pair share an XCD: 80 is a multiple of 8)
+constexpr int kQkvItems = 2 * kQkvPairs;  // B = 2: each pair in two items, rows 0..31 and rows 32..49
+// B = 2: qkv item i runs on workgroup kQkvWg0 + i, not on workgroups 0..63, which finish the
+// previous layer's down_proj tiles (the two items of a pair share an XCD: 80 is a multiple of 8)
 constexpr int kQkvWg0 = 64;
 __device__ __forceinline__ int qkv_item() { return wg_id() - kQkvWg0; }
 constexpr int kTiles = kWidth / 16;  // 64 output tiles of o_proj / down_proj
@@ -525,16 +525,18 @@ template <bool G>
 __device__ __forceinline__ constexpr bool qkv_msplit() {
   return G && PI05_INSTANCE_GROUPED;
 }
-// phase_qkv_msplit's items: tile pair i mod 80 for sample third i / 80, on workgroups 16..255
+// phase_qkv_msplit's items: tile pair i mod 80 for sample third i / 80; phase_qkv1's (one
+// sample): tile pair i mod 80 for row group i / 80 (m-tile 0, m-tile 1, m-tiles 2 and 3); either
+// way on workgroups 16..255 (the three items of a pair share an XCD: 80 is a multiple of 8)
 constexpr int kQkvItemsRS = 3 * kQkvPairs;
 constexpr int kQkvWg0RS = 256 - kQkvItemsRS;
 template <bool G>
 __device__ __forceinline__ constexpr int n_qkv_items() {
-  return qkv_msplit<G>() ? kQkvItemsRS : kQkvItems;
+  return qkv_msplit<G>() || !G ? kQkvItemsRS : kQkvItems;
 }
 template <bool G>
 __device__ __forceinline__ int qkv_item_of() {
-  return qkv_msplit<G>() ? wg_id() - kQkvWg0RS : qkv_item();
+  return qkv_msplit<G>() || !G ? wg_id() - kQkvWg0RS : qkv_item();
 }
 // The gate_up of kernel instance 2 (phase_gateup_msplit, batches of kRowSplitMinBatch and more):
 // item w = pair w.
@@ -545,8 +547,8 @@ __device__ __forceinline__ bool gu_msplit(KArgs&) {
 __device__ __forceinline__ int gu_pair0(KArgs&) {
   return 2 * (wg_id() % (kGuItems / 2));
 }
-// qkv items.  B = 1: item i = qkv_item() computes tile pair i mod 80 over row half i / 80 of the
-// sample.  B = 2 (kernel instance 1): item i computes tile pairs 2 (i mod 40) and 2 (i mod 40) + 1
+// qkv items.  B = 1: item i = qkv_item_of() computes tile pair i mod 80 over row group i / 80 of
+// the sample.  B = 2 (kernel instance 1): item i computes tile pairs 2 (i mod 40) and 2 (i mod 40) + 1
 // over row half (i / 40) mod 2 for sample half i / 80, as gate_up's pair items do; region A holds
 // the first pair.  Kernel instance 2: item i = tile pair i mod 80 for sample third i / 80.
 template <bool G>
@@ -864,21 +866,23 @@ __device__ bool phase_io(KArgs& a, int s, float* smem, Sync sy) {
 
 // =============================================================================================
 // qkv at one sample: adaRMSNorm-folded GEMM tile (K = 1024, 3 compute waves x 11 | 11 | 10
-// k-steps).  A operand g straight from the producer; rstd from the tile sums of squares; the
-// epilogue computes y = bf16(rstd * acc + shift . W^T) and then RoPE.
+// k-steps) of one tile pair over one row group (m-tile 0, m-tile 1, or m-tiles 2 and 3).  A
+// operand g straight from the producer; rstd from the tile sums of squares; the epilogue computes
+// y = bf16(rstd * acc + shift . W^T) and then RoPE (q, k) or the permuted V layout (v).
 // =============================================================================================
 template <bool G>
 __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int NT = 2, KSW = 11, KSTEPS = kWidth / 32;
-  constexpr int MT = 2;  // m-tiles per item: one half of the sample's rows (m-tiles 2h, 2h+1)
+  constexpr int MT = 2;  // m-tile slots per item (the second used by row group 2 only)
   constexpr int PH = kPhQkv;
   const int L = a.depth, R = a.R;
-  const int item = qkv_item();
-  const bool has_item = item >= 0 && item < kQkvItems;
+  const int item = qkv_item_of<G>();
+  const bool has_item = item >= 0 && item < kQkvItemsRS;
   const int p = item % kQkvPairs;   // tile pair
-  const int mh = item / kQkvPairs;  // half of the rows
-  const int rb = 32 * mh;                          // the item's first row within a sample
-  const int nrow = MT * 16 < kHorizon - rb ? MT * 16 : kHorizon - rb;  // its action-token rows
+  const int rg = item / kQkvPairs;  // row group: m-tile 0, m-tile 1, m-tiles 2 and 3
+  const int mt0 = rg < 2 ? rg : 2;  // its first m-tile
+  const int rb = 16 * mt0;          // its first row within the sample
+  const int nrow = rg < 2 ? 16 : kHorizon - rb;  // its action-token rows (16, 16, 18)
   PHASE_TS(s, l, PH, 0);
   // copy wave: this phase's weights (region A) and everything issued before them have landed;
   // then the bursts of this phase start
@@ -969,7 +973,7 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const bool ok = r16 < nrow - mt * 16 && ks0 + s2 < KSTEPS;
-          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + 2 * mh + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
+          buf_frag(hr[mt][s2], rsrc_g, ok ? (int)((afrag_offset(b * 4 + mt0 + mt, ks0 + s2, KSTEPS) + lane * 8) * 2) : kOob);
         }
       sched_fence();
       float v = 0.f;
@@ -1035,20 +1039,30 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
         }
       } else if (ep_thread) {
         // v (A . W): this thread = tile e / 64, lane e % 64 -> column dcol of the tile pair, rows
-        // 4 g .. 4 g + 3 of both m-tiles (g = lane / 16): the keys of chunk (kb = mh, g) of the
-        // permuted V fragment, in its order (vkey); keys past the 50 action tokens are zero
+        // 4 g .. 4 g + 3 of each m-tile (g = lane / 16).  The permuted V fragment's chunk (kb, g)
+        // holds, in its order (vkey), keys 4 g .. 4 g + 3 of m-tiles 2 kb and 2 kb + 1: row group 2
+        // writes whole chunks of kb = 1 (keys past the 50 action tokens zero), row groups 0 and 1
+        // the first and second halves of the chunks of kb = 0
         const int t = emt, g = eln >> 4, dcol = t * 16 + (eln & 15);
-        const f32x4 y0 = wave_sum(0, t), y1 = wave_sum(1, t);
-        u16 v8[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int row = (q < 4 ? 0 : 16) + 4 * g + (q & 3);  // vkey(mh, g, q) - rb
-          const float y = q < 4 ? y0[q] : y1[q - 4];
-          v8[q] = rb + row < kHorizon ? f2bf(__builtin_fmaf(s_rstd[row], y, s_bias[dcol])) : (u16)0;
-        }
         const int dv = (tile0 - 144) * 16 + dcol;
         u16* vc = a.vsuf + (slw * a.batch + b) * 64 * kHeadDim;
-        st_bf16x8(vc, ((size_t)mh * 16 + (dv >> 4)) * 512 + (size_t)(g * 16 + (dv & 15)) * 8, v8);
+        const f32x4 y0 = wave_sum(0, t);
+        if (rg == 2) {
+          const f32x4 y1 = wave_sum(1, t);
+          u16 v8[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int row = (q < 4 ? 0 : 16) + 4 * g + (q & 3);  // vkey(1, g, q) - rb
+            const float y = q < 4 ? y0[q] : y1[q - 4];
+            v8[q] = rb + row < kHorizon ? f2bf(__builtin_fmaf(s_rstd[row], y, s_bias[dcol])) : (u16)0;
+          }
+          st_bf16x8(vc, ((size_t)16 + (dv >> 4)) * 512 + (size_t)(g * 16 + (dv & 15)) * 8, v8);
+        } else {
+          u16 v4[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v4[q] = f2bf(__builtin_fmaf(s_rstd[4 * g + q], y0[q], s_bias[dcol]));  // vkey(0, g, 4 rg + q) - rb
+          st_bf16x4(vc, (size_t)(dv >> 4) * 512 + (size_t)(g * 16 + (dv & 15)) * 8 + 4 * rg, v4);
+        }
       }
     }
   }
