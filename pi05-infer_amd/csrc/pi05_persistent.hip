@@ -191,6 +191,40 @@ __device__ __forceinline__ int phase_tid() {
   return t;
 }
 
+// Marks values loaded ahead of a poll as used, on a path that leaves the phase without using
+// them: a wait that gave up, or a wave or row that has no use for them.  The compiler's wait
+// counting is path-insensitive, so a load still pending on such a path counts as pending
+// wherever the phases continue, and the next write of its registers then gets a wait -- a full
+// vmcnt(0) once a store is in flight, which also waits for the flag stores of the last publish
+// ahead of the next phase's polls.  Where it is placed (before a publish, which waits for every
+// store, or on the failure path) the wait it asks for costs nothing.  Measured on MI355X, B=1:
+// qkv's and down_proj's preloads consumed, 4.997 -> 4.915 ms per predict; the same for o_proj,
+// gate_up or the attention splits measured slower (register assignment moves the waits).
+template <class T>
+__device__ __forceinline__ void consume(const T& v) {
+  static_assert(sizeof(T) == 16 || sizeof(T) == 8 || sizeof(T) == 4, "one value of whole registers");
+  if constexpr (sizeof(T) == 16) {
+    const u32x4 r = __builtin_bit_cast(u32x4, v);
+    asm volatile("" ::"v"(r));
+  } else if constexpr (sizeof(T) == 8) {
+    const u32x2 r = __builtin_bit_cast(u32x2, v);
+    asm volatile("" ::"v"(r));
+  } else {
+    const uint32_t r = __builtin_bit_cast(uint32_t, v);
+    asm volatile("" ::"v"(r));
+  }
+}
+template <class T, int N>
+__device__ __forceinline__ void consume(const T (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) consume(v[i]);
+}
+template <class T, class... Ts>
+__device__ __forceinline__ void consume(const T& v, const Ts&... vs) {
+  consume(v);
+  if constexpr (sizeof...(Ts) > 0) consume(vs...);
+}
+
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited for), N a compile-time constant < 64.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -948,7 +982,10 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
   {
     const unsigned* dep = l == 0 ? flag_base(a, s, 0, kPhIo) : flag_base(a, s, l - 1, kPhDown);
     const int ndep = l == 0 ? a.batch * kHorizon : kDownItems1;
-    if (!wait_flags(a, dep, ndep, sy)) return false;
+    if (!wait_flags(a, dep, ndep, sy)) {
+      consume(w31, rcs);
+      return false;
+    }
   }
   PHASE_TS(s, l, PH, 2);
   const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
@@ -1067,6 +1104,7 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
     }
   }
   PHASE_TS(s, l, PH, 5);
+  consume(w31, rcs);  // (used by wave 2's last k-step and by the RoPE rows only)
   publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
   PHASE_TS(s, l, PH, 6);
   return true;
@@ -2793,16 +2831,21 @@ __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
   // for its 4 columns, ahead of the polls
   const bool ep_wave = wave == 1;
   const bool next_g = l + 1 < L;  // the last layer's output feeds the final norm only
-  float4 g4 = {}, s14 = {};
+  // (unset in the other waves, which never read them: a zero there would be a register write
+  // that waits for o_proj's loads into the same registers and the flag stores behind them)
+  f32x4 g4, s14;
   if (ep_wave) {
-    g4 = *reinterpret_cast<const float4*>(a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + ec);
-    if (next_g) s14 = *reinterpret_cast<const float4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + ec);
+    g4 = *reinterpret_cast<const f32x4*>(a.table + ((size_t)s * NN + 2 * l + 1) * kModW + 2 * kWidth + col + ec);
+    if (next_g) s14 = *reinterpret_cast<const f32x4*>(a.table_s1 + ((size_t)s * NN + 2 * l + 2) * kModW + col + ec);
   }
   // copy wave, ahead of the polls: the next layer's qkv tiles (this layer's gate_up MFMA is done)
   down_next_qkv_copies(a, s, l, smem);
   PHASE_TS(s, l, PH, 1);
   // every gate_up item: the m-tile's rows over the whole K
-  if (!wait_flags(a, flag_base(a, s, l, kPhGu), kGuItems, sy)) return false;
+  if (!wait_flags(a, flag_base(a, s, l, kPhGu), kGuItems, sy)) {
+    consume(wf, g4, s14);
+    return false;
+  }
   PHASE_TS(s, l, PH, 2);
   const int r = 16 * mq + r16;
   const u16* hres = a.hmid + slw * (size_t)R * kWidth;
@@ -2837,8 +2880,8 @@ __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
     const f32x4 y = ((*reinterpret_cast<const f32x4*>(red + (size_t)lane * 4) + *reinterpret_cast<const f32x4*>(red + (size_t)(64 + lane) * 4)) +
                      *reinterpret_cast<const f32x4*>(red + (size_t)(128 + lane) * 4)) +
                     *reinterpret_cast<const f32x4*>(red + (size_t)(192 + lane) * 4);
-    const float gate[4] = {round_bf(g4.x), round_bf(g4.y), round_bf(g4.z), round_bf(g4.w)};
-    const float s1[4] = {s14.x, s14.y, s14.z, s14.w};
+    const float gate[4] = {round_bf(g4[0]), round_bf(g4[1]), round_bf(g4[2]), round_bf(g4[3])};
+    const float s1[4] = {s14[0], s14[1], s14[2], s14[3]};
     float ss = 0.f;
     if (r16 < nrow) {
       u16 hn[4], gn[4];
@@ -2859,6 +2902,7 @@ __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
     // tile-major statistics: the tile's sums of the m-tile's 16 rows (padded rows: zero)
     if (lane < 16) st_f32(a.ss + ((size_t)s * (L + 1) + l + 1) * kTiles * R + (size_t)nt * R + 16 * mq + lane, ss);
   }
+  consume(hold, g4, s14);  // (used only by the rows the m-tile has)
   PHASE_TS(s, l, PH, 8);
   publish(a, flag_base(a, s, l, PH) + item, sy.epoch);
   PHASE_TS(s, l, PH, 9);
