@@ -497,12 +497,13 @@ __device__ __forceinline__ void publish_local(KArgs& a, unsigned* flag, unsigned
 // later, so every burst is issued just before a flag wait (the copy wave reaches the next barrier
 // while the producers are still working) and never between two compute barriers, where it would
 // hold up the compute waves:
-//   qkv(l) wait      : all copies landed (qkv(l) weights); down(l) -> B (32)
+//   qkv(l) wait      : all copies landed (qkv(l) weights); B > 1: down(l) -> B (32)
 //   attention(l) wait: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's own
 //                      KV block loads
 //   merge(l) wait    : gate_up(l) tile 0 fragments 16..31 (16) and tile 1 (32) -> A
 //   gate_up(l) wait  : all copies landed (gate_up(l) weights)
-//   down(l) wait     : qkv(l+1) tile 0 (32) and tile 1 fragments 0..30 (31) -> A
+//   down(l) wait     : qkv(l+1) tile 0 (32) and tile 1 fragments 0..30 (31) -> A (one sample:
+//                      after the copy wave's own down(l) weight loads)
 // so at most 63 copies are ever in flight and a burst never waits for the one before it.
 constexpr int kLdsA = 0;
 constexpr int kLdsB = kLdsA + 16384;
@@ -922,7 +923,7 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
   // then the bursts of this phase start
   if (copy_wave()) {
     wait_vmcnt<0>();
-    if (!attn_grouped<G>(a)) copy_residual_w<kMlp / 32>(a, l, smem);  // B4 down(l) -> B
+    // (one sample: down_proj's copy wave loads its weights itself, at down_proj)
   }
   if (!has_item) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -2785,11 +2786,13 @@ __device__ bool phase_oproj_msplit(KArgs& a, int s, int l, float* smem, Sync sy)
 // =============================================================================================
 // down_proj at one sample without a K split: item = (16-column tile nt, m-tile mq), 256 items, so
 // no partial sum leaves the workgroup and no finisher hand-off follows.  The four waves each take
-// a K quarter (32 k-steps): the copy wave takes quarter mq from region B (it put it there during
-// qkv), so it issues no register loads next to its copies; waves 1 and 2 take quarters mq + 2 and
-// mq + 3 (mod 4) with their weight fragments loaded into registers ahead of the polls; wave 0, the
-// poller, takes quarter mq + 1 and loads its fragments after the polls (the other m-tiles' items
-// of the tile, on the same XCD, have brought that quarter into L2 by then).  The products are formed as W . A^T (a lane ends with 4 consecutive columns of one row);
+// a K quarter (32 k-steps): the copy wave, waves 1 and 2 take quarters mq, mq + 2 and mq + 3
+// (mod 4) with their weight fragments loaded into registers ahead of the polls (the copy wave's
+// before its burst of the next layer's copies, so they land first); wave 0, the poller, takes
+// quarter mq + 1 and loads its fragments after the polls.  The four m-tiles' items of a tile run
+// on one XCD and read the tile's four quarters at about the same time, so each quarter comes
+// from the memory side once.  (Measured on MI355X: with the copy wave's quarter copied to region
+// B during qkv, 20 us earlier, every quarter was fetched twice, 1.4 GB more per predict.)  The products are formed as W . A^T (a lane ends with 4 consecutive columns of one row);
 // the quarters are added in quarter order in LDS and wave 1 runs the finisher's epilogue:
 // h = bf16(hmid + bf16(bf16(y) * gate)) (modeling_gemma.py:503), g = bf16(h * (1 + scale)) of the
 // next layer's first norm, and the tile's row sums of squares of h.
@@ -2826,7 +2829,7 @@ __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
 #pragma unroll
     for (int s2 = 0; s2 < KQ; ++s2) buf_frag(wf[s2], rw, ((kq * KQ + s2) * 512 + lane * 8) * 2);
   };
-  if (wave == 1 || wave == 2) load_w();
+  if (wave != 0) load_w();
   // wave 1 (the epilogue's): the gate of norm 2l + 1 and 1 + scale of the next layer's first norm
   // for its 4 columns, ahead of the polls
   const bool ep_wave = wave == 1;
@@ -2859,12 +2862,6 @@ __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
     for (int s2 = 0; s2 < KQ; ++s2)
       buf_frag(af[s2], ra, r16 < nrow ? (int)((afrag_offset(mq, kq * KQ + s2, KSTEPS) + lane * 8) * 2) : kOob);
     if (wave == 0) load_w();
-    if (copy_wave()) {
-      const u16* lw = reinterpret_cast<const u16*>(smem + kLdsB);  // quarter mq of the tile
-      wait_vmcnt<0>();  // (and the next layer's copies: loads complete in issue order)
-#pragma unroll
-      for (int s2 = 0; s2 < KQ; ++s2) wf[s2] = *reinterpret_cast<const bf16x8*>(lw + (size_t)s2 * 512 + lane * 8);
-    }
     sched_fence();
     f32x4 acc[NCH];
 #pragma unroll
