@@ -611,6 +611,12 @@ __device__ void copy_norm_w(KArgs& a, int l, int which, float* smem) {
   if (MODE == kModeQkv ? (unsigned)qkv_item_of<G>() >= (unsigned)n_qkv_items<G>() : (unsigned)wg_id() >= kGuItems) return;
   lds_burst<N>(smem + kLdsA + which * 8192 + F0 * 256, norm_w_tile<MODE, G>(a, l, which) + F0 * 512);
 }
+// One sample: qkv(l)'s first tile -> region B, which nothing else uses at one sample (the second
+// tile goes to region A1 at down_proj(l - 1), after gate_up's last read of region A).
+__device__ void copy_qkv_tile0(KArgs& a, int l, float* smem) {
+  if (!copy_wave() || (unsigned)qkv_item_of<false>() >= (unsigned)n_qkv_items<false>()) return;
+  lds_burst<32>(smem + kLdsB, norm_w_tile<kModeQkv, false>(a, l, 0));
+}
 
 // down_proj weights of workgroup (unsigned)wg_id(): (tile, K quarter) -> region B.
 // down_proj items.  B = 1 (phase_down_rows): workgroup w = (tile w mod 64, m-tile w / 64) over
@@ -989,7 +995,8 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
     }
   }
   PHASE_TS(s, l, PH, 2);
-  const u16* lw = reinterpret_cast<const u16*>(smem + kLdsA);  // [tile t][k-step] fragments
+  const u16* lw0 = reinterpret_cast<const u16*>(smem + kLdsB);   // tile 0: [k-step] fragments
+  const u16* lw1 = reinterpret_cast<const u16*>(smem + kLdsA1);  // tile 1
   {
     constexpr int b = 0;  // one sample: the batch instances have their own qkv and gate_up
     const int m0 = b * kRowsPerSample;
@@ -1027,7 +1034,7 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
       auto wk = [&](int t, int s2) {
         const int ksc = ks0 + s2 < KSTEPS ? ks0 + s2 : KSTEPS - 1;
         if (t == 1 && s2 >= KSTEPS - 1 - 2 * KSW && wave == 2) return w31;
-        return *reinterpret_cast<const bf16x8*>(lw + ((size_t)t * KSTEPS + ksc) * 512 + lane * 8);
+        return *reinterpret_cast<const bf16x8*>((t == 0 ? lw0 : lw1) + (size_t)ksc * 512 + lane * 8);
       };
       if (wt) mfma_steps<KSW, NT, 0, MT, true>(acc, hr, wk);
       else mfma_steps<KSW, NT, 0, MT, false>(acc, hr, wk);
@@ -2430,6 +2437,12 @@ __device__ bool phase_oproj(KArgs& a, int s, int l, float* smem, Sync sy) {
   const int L = a.depth, NN = 2 * L + 1, R = a.R;
   const int item = (unsigned)wg_id();
   PHASE_TS(s, l, kPhO, 0);
+  {
+    // copy wave (idle here): the next layer's first qkv tile -> region B, half of the burst that
+    // down_proj's polls would otherwise share the memory side with
+    int ln;
+    if (next_layer(a, s, l, &ln)) copy_qkv_tile0(a, ln, smem);
+  }
   if (item >= kOItems) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
   const bool mw = wave == 1 || wave == 2;  // MFMA waves
@@ -2797,13 +2810,11 @@ __device__ bool phase_oproj_msplit(KArgs& a, int s, int l, float* smem, Sync sy)
 // h = bf16(hmid + bf16(bf16(y) * gate)) (modeling_gemma.py:503), g = bf16(h * (1 + scale)) of the
 // next layer's first norm, and the tile's row sums of squares of h.
 // =============================================================================================
-// The copy wave's burst at down_proj(l): the next layer's qkv tiles -> region A.
+// The copy wave's burst at down_proj(l): the next layer's second qkv tile -> region A1 (its first
+// tile went to region B at o_proj(l)).
 __device__ __forceinline__ void down_next_qkv_copies(KArgs& a, int s, int l, float* smem) {
   int ln;
-  if (next_layer(a, s, l, &ln)) {
-    copy_norm_w<kModeQkv, 0, 32>(a, ln, 0, smem);
-    copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
-  }
+  if (next_layer(a, s, l, &ln)) copy_norm_w<kModeQkv, 0, 31>(a, ln, 1, smem);
 }
 __device__ bool phase_down_rows(KArgs& a, int s, int l, float* smem, Sync sy) {
   constexpr int KSTEPS = kMlp / 32, KQ = KSTEPS / kKSplit;
@@ -3268,8 +3279,9 @@ __global__ __launch_bounds__(kThreads, 1) void denoise_loop_kernel(MegaArgs args
   // this launch's epoch: one past the last finished launch's
   const Sync sy{(unsigned)__builtin_amdgcn_readfirstlane(ld_u32(args.err + kCtlEpoch)) + 1u, &s_flag};
   PHASE_TS_INIT();
-  // the copy wave: step 0, layer 0 qkv and o_proj weights
-  copy_norm_w<kModeQkv, 0, 32, G>(kargs(), 0, 0, smem);
+  // the copy wave: step 0, layer 0 qkv weights (one sample: the first tile in region B)
+  if constexpr (G) copy_norm_w<kModeQkv, 0, 32, G>(kargs(), 0, 0, smem);
+  else copy_qkv_tile0(kargs(), 0, smem);
   copy_norm_w<kModeQkv, 0, 31, G>(kargs(), 0, 1, smem);
   bool ok = true;
   for (int s = 0; s <= kargs().steps && ok; ++s) {
