@@ -497,13 +497,15 @@ __device__ __forceinline__ void publish_local(KArgs& a, unsigned* flag, unsigned
 // later, so every burst is issued just before a flag wait (the copy wave reaches the next barrier
 // while the producers are still working) and never between two compute barriers, where it would
 // hold up the compute waves:
-//   qkv(l) wait      : all copies landed (qkv(l) weights); B > 1: down(l) -> B (32)
-//   attention(l) wait: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's own
-//                      KV block loads
-//   merge(l) wait    : gate_up(l) tile 0 fragments 16..31 (16) and tile 1 (32) -> A
+//   qkv(l) wait      : all copies landed (qkv(l) weights); B > 1: down(l) -> B (32); one sample:
+//                      gate_up(l) tile 0 -> A (32)
+//   attention(l) wait: B > 1: gate_up(l) tile 0 fragments 0..15 -> A (16), after the copy wave's
+//                      own KV block loads
+//   merge(l) wait    : B > 1: gate_up(l) tile 0 fragments 16..31 (16); tile 1 (32) -> A
+//   o_proj(l) wait   : one sample: qkv(l+1) tile 0 -> B (32)
 //   gate_up(l) wait  : all copies landed (gate_up(l) weights)
-//   down(l) wait     : qkv(l+1) tile 0 (32) and tile 1 fragments 0..30 (31) -> A (one sample:
-//                      after the copy wave's own down(l) weight loads)
+//   down(l) wait     : qkv(l+1) tile 1 fragments 0..30 (31) -> A, B > 1: and tile 0 (32) (one
+//                      sample: after the copy wave's own down(l) weight loads)
 // so at most 63 copies are ever in flight and a burst never waits for the one before it.
 constexpr int kLdsA = 0;
 constexpr int kLdsB = kLdsA + 16384;
@@ -929,7 +931,10 @@ __device__ bool phase_qkv1(KArgs& a, int s, int l, float* smem, Sync sy) {
   // then the bursts of this phase start
   if (copy_wave()) {
     wait_vmcnt<0>();
-    // (one sample: down_proj's copy wave loads its weights itself, at down_proj)
+    // gate_up(l)'s first tile -> region A's lower half, free at one sample (qkv's first tile is in
+    // region B), so the attention phases' bursts carry only its second tile.  (down_proj's copy
+    // wave loads its weights itself, at down_proj.)
+    copy_norm_w<kModeGateUp, 0, 32>(a, l, 0, smem);
   }
   if (!has_item) return true;
   const int tid = phase_tid(), lane = tid & 63, wave = tid >> 6;
@@ -2240,8 +2245,8 @@ __device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
     KvBlock blk;
     if (pre) load(blk, kb0);
     if (!burst) {
-      copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
-      burst = true;
+      if constexpr (G) copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);  // gate_up(l) tile 0, fragments 0..15 -> A
+      burst = true;  // (one sample: the whole tile was copied at qkv)
     }
     PHASE_TS(s, l, kPhSplit, 1);
     if (!waited) {
@@ -2350,8 +2355,10 @@ __device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
   }
   // the rest of gate_up(l) -> region A, whose upper half the split items no longer use (the
   // workgroups without a split item: all of it), ahead of the merge polls
-  if (!burst) copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
-  copy_norm_w<kModeGateUp, 16, 16, G>(a, l, 0, smem);
+  if constexpr (G) {
+    if (!burst) copy_norm_w<kModeGateUp, 0, 16, G>(a, l, 0, smem);
+    copy_norm_w<kModeGateUp, 16, 16, G>(a, l, 0, smem);
+  }
   copy_norm_w<kModeGateUp, 0, 32, G>(a, l, 1, smem);
   if (attn_grouped<G>(a)) return attn_group_merges(a, s, l, sy);
   // ---- merges.  Role = hp * nbp + bp runs on workgroup role mod grid, i.e. with the split
