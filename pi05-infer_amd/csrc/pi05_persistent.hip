@@ -2367,7 +2367,6 @@ __device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
   // t owns row t/64 of the head pair (r16 = 2hp + (j&1) + 8*(j>>1)) and dims (t%64)*4 .. +3, and
   // loads every split's (max, sum, O) at once.
   bool first_merge = true;
-  u16* s_ob = reinterpret_cast<u16*>(smem + kLdsWork);  // [4 rows][D] bf16
   for (int role = (unsigned)wg_id(); role < kHeadPairs * nbp; role += (unsigned)wg_count()) {
     const int bp = role % nbp, hp = role / nbp;
     const int b = bp / kPairs, pair = bp % kPairs;
@@ -2402,26 +2401,19 @@ __device__ bool phase_attn(KArgs& a, int s, int l, float* smem, Sync sy) {
         Lb += lc[c] * wc;
         ob += oc[c] * wc;
       }
+      // straight into o_proj's A operand [R, H*D] (no LDS round trip): the thread's 4 dims of row
+      // (token, head) are 8 contiguous bytes of one fragment
       const float inv = 1.0f / Lb;
+      u16 v4[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s_ob[jr * kHeadDim + d0 + i] = f2bf(ob[i] * inv);
-    }
-    __syncthreads();
-    if (tid < 128) {
-      // attention output rows (token, head) -> o_proj A operand [R, H*D]: 4 rows x 32 chunks
+      for (int i = 0; i < 4; ++i) v4[i] = f2bf(ob[i] * inv);
       u16* os = a.o + slw * (size_t)R * (kHeads * kHeadDim);
-      const int j = tid >> 5, d = (tid & 31) * 8;
-      const int rj = 2 * hp + (j & 1) + 8 * (j >> 1);
-      const int r = b * kRowsPerSample + 2 * pair + (rj >> 3), head = rj & 7;
-      u16 v8[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v8[q] = s_ob[j * kHeadDim + d + q];
-      st_bf16x8(os, afrag_index(r, head * kHeadDim + d, kHeads * kHeadDim / 32), v8);
+      const int r = b * kRowsPerSample + 2 * pair + (rr >> 3), head = rr & 7;
+      st_bf16x4(os, afrag_index(r, head * kHeadDim + d0, kHeads * kHeadDim / 32), v4);
     }
     publish(a, fmerge + 4 * bp + hp, sy.epoch);
     if (first_merge) PHASE_TS(s, l, kPhMerge, 6);
     first_merge = false;
-    __syncthreads();  // s_ob is reused by the next role
   }
   return true;
 }
