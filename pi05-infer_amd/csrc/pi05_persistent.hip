@@ -625,7 +625,7 @@ __device__ void copy_qkv_tile0(KArgs& a, int l, float* smem) {
 // the whole K; its copy wave multiplies K quarter w / 64, which region B holds.  B > 1: workgroup
 // w = 64 q + 32 h + g computes tiles 2g and 2g + 1 over K quarter q for half h of the samples --
 // half the activation bytes per XCD, as for gate_up; the quarters of a group run on one XCD (w mod
-// 8 is the same for all four) and poll one flag replica (w mod 32), and the finishers (quarter 0)
+// 8 is the same for all four) and poll one flag replica (w mod kFlagCopies), and the finishers (quarter 0)
 // are workgroups 0..63, which hold no qkv item.  Region B holds the first tile's quarter; the
 // compute waves hold the second one in registers.
 __device__ __forceinline__ void down_item(KArgs& a, int* nt0, int* ksp, int* half = nullptr) {

@@ -98,8 +98,8 @@ def test_device_bytes_covers_weights_and_cache(lib):
     # per-(step, layer) split partials: attention (9 key splits x 25 row blocks x 16 rows x 256
     # fp32) and the down_proj K quarters (4 x 64 tiles x 64 rows x 16 fp32)
     need += 10 * 18 * (9 * 25 * 16 * 256 + 4 * 64 * 64 * 16) * 4
-    # completion flags: (steps + 1) x (depth + 1) x 7 phases x 32 replicas x 512 words
-    need += 11 * 19 * 7 * 32 * 512 * 4
+    # completion flags: (steps + 1) x (depth + 1) x 7 phases x 16 replicas x 512 words
+    need += 11 * 19 * 7 * 16 * 512 * 4
     got = _ext.device_bytes(d)
     assert need <= got <= need + 64 * 2**20
     d8 = _ext.default_dims()
